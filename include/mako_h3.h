@@ -1,0 +1,190 @@
+/*
+ * mako_h3.h — C-ABI of the MI355X (gfx950) kernels for the per-block hot path of mako-video's MiniMax-H3
+ * transformer: the adaLN-modulated RMS norm and the gated residual (`rms_mod_rows`, `gate_add_rows`, fused),
+ * `swiglu_rows`, the `--sparse` cube selector (`cube_pool`, `cube_scores`, `cube_topk`, fused `cube_select`),
+ * the `--int8` weight quantizer (`quant_rows_i8`) and the int8 weight-only fc1 GEMM with its SwiGLU epilogue.
+ *
+ * The reference runs these as Metal kernels looked up by name in mako-common's TransformerRuntime
+ * (`dispatch(enc, name, {buffers}, &args, sizeof args, grid, tg)`, the in-repo instance being
+ * src/video/audio_vae.cpp:151-177 over src/kernels/video.metal:10-36). This header keeps that shape:
+ *   - one entry point per reference kernel name, prefixed `mh3_`;
+ *   - one argument struct of fixed-width fields per entry point, passed by pointer (the reference's setBytes);
+ *   - device buffers as plain pointers, owned by the caller (the reference's reserve()/scratch());
+ *   - an explicit stream (a hipStream_t; NULL is the null stream), the counterpart of the reference's encoder;
+ *   - no allocation, no exceptions: every call returns an int, MH3_OK or a negative MH3_ERR_* code, and an
+ *     invalid call launches nothing (the reference throws std::runtime_error on the host, audio_vae.cpp:231-232).
+ * Calls are asynchronous on the given stream; all entry points are reentrant and may be called from several host
+ * threads on distinct streams.
+ *
+ * Every pointer is a device pointer unless its comment says otherwise. Dense tensors are row-major and contiguous
+ * unless a stride says otherwise. 16-byte vector accesses require the row widths and pointers the comments state.
+ */
+#ifndef MAKO_H3_H
+#define MAKO_H3_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define MH3_ABI_VERSION 1
+
+/* ---- error codes ------------------------------------------------------------------------------------------------ */
+enum {
+    MH3_OK = 0,
+    MH3_ERR_SHAPE = -1,       /* a size is zero where it may not be, too large, or not a required multiple */
+    MH3_ERR_POINTER = -2,     /* a required pointer is NULL */
+    MH3_ERR_ALIGN = -3,       /* a pointer is not aligned as required (16 bytes for vector rows) */
+    MH3_ERR_PARAM = -4,       /* a scalar parameter is outside its domain (dtype, layout, ratio, local, k, eps) */
+    MH3_ERR_HIP = -5,         /* the HIP runtime reported an error launching the kernel */
+    MH3_ERR_UNSUPPORTED = -6, /* a valid request this build has no kernel for (e.g. head_dim != 128) */
+};
+
+/* Element types of activations. */
+enum { MH3_F32 = 0, MH3_BF16 = 1 };
+
+/* A hipStream_t, kept opaque so the header needs no HIP include. */
+typedef void* mh3_stream_t;
+
+/* ---- library ---------------------------------------------------------------------------------------------------- */
+int mh3_abi_version(void);
+/* A static string for an MH3_* code. */
+const char* mh3_strerror(int code);
+/* The last HIP error string seen by a launch on this thread ("" if none). */
+const char* mh3_last_hip_error(void);
+
+/* ---- H3 options (host only, no GPU needed) ---------------------------------------------------------------------- */
+/* The transformer matrices kept as int8 (reference: H3::Int8 mask, engine.hpp:34; parse_int8 called at
+ * tools/mako_video.cpp:110, src/server/video_models.cpp:128, tests/h3_ref_test.cpp:139). */
+enum { MH3_INT8_QKV = 1u, MH3_INT8_OUT = 2u, MH3_INT8_FC1 = 4u, MH3_INT8_FC2 = 8u, MH3_INT8_ALL = 15u };
+/* "none", "all", or a comma list of qkv, out, fc1, fc2 -> *mask (host memory). MH3_ERR_PARAM (mask untouched) for
+ * anything else, as the reference's parse_int8 returns no value. */
+int mh3_parse_int8(const char* text, uint32_t* mask);
+/* H3::set_sparse's domain (reference: src/server/video_models.cpp:117-126): ratio in [0, 1], local in {0, 1, 3}. */
+int mh3_check_sparse(float ratio, uint32_t local);
+/* The cubes a query cube keeps by score: ceil(ratio * cubes), clamped to [0, cubes]; -MH3_ERR_PARAM-style negative
+ * code for a ratio outside [0, 1]. */
+int64_t mh3_topk_k(float ratio, uint32_t cubes);
+
+/* ---- rows: rms_mod_rows, gate_add_rows, fused rms_mod_gate_add_rows ----------------------------------------------
+ * Reference kernels `rms_mod_rows` and `gate_add_rows` (mako-common; named in docs/performance.md:44, semantics in
+ * docs/architecture.md:49-52,61,64-65). A row r uses modulation set s(r) = set_of_row[r] (uint8, device memory) when
+ * set_of_row is non-NULL, else 0. shift, scale and gate are [n_sets][dim] float, w is [dim] float (NULL: all 1).
+ * x, residual, y and out are [rows][dim] of `dtype`. bf16 rows need dim % 8 == 0 and 16-byte aligned pointers;
+ * float rows dim % 4 == 0 and 16-byte alignment. Math is float, the sum of squares accumulated in float, and
+ * bf16 results are rounded to nearest even once, at the store. */
+typedef struct MH3RowsArgs {
+    uint32_t rows;
+    uint32_t dim;
+    uint32_t n_sets; /* >= 1; every set_of_row[r] must be < n_sets */
+    uint32_t dtype;  /* MH3_F32 or MH3_BF16 */
+    float eps;       /* > 0 (H3: 1e-6) */
+    uint32_t reserved[3];
+} MH3RowsArgs;
+
+/* y = x * rsqrt(mean(x^2) + eps) * w * (1 + scale[s]) + shift[s]. y may equal x. */
+int mh3_rms_mod_rows(const MH3RowsArgs* args, const void* x, const float* w, const float* shift, const float* scale,
+                     const uint8_t* set_of_row, void* y, mh3_stream_t stream);
+/* x += gate[s] * y, in place (the reference's residual update after out-proj and after fc2). */
+int mh3_gate_add_rows(const MH3RowsArgs* args, void* x, const void* y, const float* gate, const uint8_t* set_of_row,
+                      mh3_stream_t stream);
+/* out = residual + gate[s] * (x * rsqrt(mean(x^2) + eps) * w * (1 + scale[s]) + shift[s]): the two reference
+ * kernels fused into one HBM pass (reads x and residual once, writes out once). out may equal residual. */
+int mh3_rms_mod_gate_add_rows(const MH3RowsArgs* args, const void* x, const void* residual, const float* w,
+                              const float* shift, const float* scale, const float* gate, const uint8_t* set_of_row,
+                              void* out, mh3_stream_t stream);
+
+/* ---- swiglu_rows -------------------------------------------------------------------------------------------------
+ * Reference kernel `swiglu_rows` (mako-common; docs/architecture.md:65,112-114): out = silu(gate) * up with
+ * silu(g) = g / (1 + exp(-g)), float math, out rounded once. fc1's row is [gate (dim) | up (dim)].
+ *   MH3_SWIGLU_SPLIT: gate and up are separate [rows][dim] tensors.
+ *   MH3_SWIGLU_FUSED: gate points at [rows][2*dim] rows (gate = columns [0, dim), up = [dim, 2*dim)); up is NULL.
+ * out is [rows][dim]. dim % 8 == 0 (bf16) or % 4 == 0 (float); 16-byte aligned pointers. */
+enum { MH3_SWIGLU_SPLIT = 0, MH3_SWIGLU_FUSED = 1 };
+typedef struct MH3SwigluArgs {
+    uint32_t rows;
+    uint32_t dim;
+    uint32_t layout; /* MH3_SWIGLU_SPLIT or MH3_SWIGLU_FUSED */
+    uint32_t dtype;  /* MH3_F32 or MH3_BF16 */
+} MH3SwigluArgs;
+int mh3_swiglu_rows(const MH3SwigluArgs* args, const void* gate, const void* up, void* out, mh3_stream_t stream);
+
+/* ---- the sparse-attention cube selector ---------------------------------------------------------------------------
+ * Reference: H3::Cubes and cube_pool / cube_scores / cube_topk (mako-common; docs/architecture.md:118-133,
+ * README.md:81-87, docs/performance.md:162-181). The generated video rows form a grid of grid_t latent frames x
+ * grid_h patch rows x grid_w patch columns, frame-major then row-major. Cubes are 4x4x4 blocks of it, the grid padded
+ * up to multiples of 4 with rows that are no token; cube c = (ct * ch + cy) * cw + cx with ch = ceil(grid_h / 4),
+ * cw = ceil(grid_w / 4). Q and K are bf16 per head: element (head, row, d) at
+ * head * head_stride + row * row_stride + d, head_dim = 128 contiguous, row_stride and head_stride multiples of 8.
+ *   MH3_CUBES_GRID:     video row (t, y, x) is row row0 + (t * grid_h + y) * grid_w + x (the model's order).
+ *   MH3_CUBES_GATHERED: rows already gathered cube by cube (the reference's heads_partial with the cube map):
+ *                       cube c's 64 rows are rows row0 + 64 c ... + 63, in (dt, dy, dx) order; padding rows are
+ *                       skipped by their grid position, whatever they hold.
+ * cube_pool:  qc[h][c][:] = mean of q over cube c's valid rows (float), same for k; counts[c] = valid rows (int32,
+ *             may be NULL).
+ * cube_scores: s[h][i][j] = qc[h][i] . kc[h][j] / sqrt(head_dim), float [heads][cubes][cubes].
+ * cube_topk:  per (h, query cube i): the k cubes of highest s[h][i][:] (equal scores: lower cube index first),
+ *             united with the local cubes (local 1: i itself; 3: also the cubes of the same (cy, cx) one frame group
+ *             before and after, where they exist), written as ascending int32 cube indices
+ *             idx[h][i][0 .. cnt[h][i]) with idx[h][i][cnt .. out_stride) = -1; cnt[h][i] = k + the local cubes not
+ *             already among the k. out_stride >= k + local.
+ * cube_select: cube_scores and cube_topk fused; the scores stay on chip.
+ * mh3_cube_count() gives the number of cubes of a grid; mh3_topk_k() gives k for a ratio. */
+enum { MH3_CUBES_GRID = 0, MH3_CUBES_GATHERED = 1 };
+typedef struct MH3CubeArgs {
+    uint32_t heads;
+    uint32_t head_dim; /* 128 */
+    uint32_t grid_t, grid_h, grid_w;
+    uint32_t layout;      /* MH3_CUBES_GRID or MH3_CUBES_GATHERED */
+    uint64_t row0;        /* first video row */
+    uint64_t head_stride; /* elements between heads of q / k */
+    uint64_t row_stride;  /* elements between rows of q / k */
+    uint32_t k;           /* cubes kept by score, 1 <= k <= cubes (cube_topk, cube_select) */
+    uint32_t local;       /* 0, 1 or 3 */
+    uint32_t out_stride;  /* int32 entries per (head, query cube) in idx, >= k + local */
+    uint32_t reserved;
+} MH3CubeArgs;
+int64_t mh3_cube_count(uint32_t grid_t, uint32_t grid_h, uint32_t grid_w);
+int mh3_cube_pool(const MH3CubeArgs* args, const uint16_t* q, const uint16_t* k, float* qc, float* kc,
+                  int32_t* counts, mh3_stream_t stream);
+int mh3_cube_scores(const MH3CubeArgs* args, const float* qc, const float* kc, float* s, mh3_stream_t stream);
+int mh3_cube_topk(const MH3CubeArgs* args, const float* s, int32_t* idx, int32_t* cnt, mh3_stream_t stream);
+int mh3_cube_select(const MH3CubeArgs* args, const float* qc, const float* kc, int32_t* idx, int32_t* cnt,
+                    mh3_stream_t stream);
+
+/* ---- int8 weights: quant_rows_i8 (weight side) ---------------------------------------------------------------------
+ * Reference kernel `quant_rows_i8` (mako-common; docs/performance.md:122-123, docs/architecture.md:54-56): each row
+ * of a [rows][cols] matrix (the weight's [out][in] rows) to symmetric int8 with one float scale:
+ * scale = max|row| / 127 (float), q = round-to-nearest-even(w / scale) in [-127, 127]; an all-zero row gets
+ * scale 0 and q 0. w is float or bf16 (`dtype`), cols % 16 == 0, 16-byte aligned. */
+typedef struct MH3QuantArgs {
+    uint32_t rows;
+    uint32_t cols;
+    uint32_t dtype; /* MH3_F32 or MH3_BF16 */
+    uint32_t reserved;
+} MH3QuantArgs;
+int mh3_quant_rows_i8(const MH3QuantArgs* args, const void* w, int8_t* q, float* scale, mh3_stream_t stream);
+
+/* ---- the int8 weight-only fc1 GEMM with the SwiGLU epilogue --------------------------------------------------------
+ * Replaces fc1's `gemm_i8` + `swiglu_rows` pair (mako-common; docs/performance.md:120-136, docs/architecture.md:65).
+ * x is bf16 [m][k]; w is int8 [2n][k], the weight's output-channel rows as quant_rows_i8 leaves them (rows [0, n)
+ * the gate, [n, 2n) the up projection); scale is float [2n]. With W the [k][2n] matrix w^T:
+ *   y = x * (W * diag(scale)) in float accumulation, out = silu(y[:, 0:n]) * y[:, n:2n], bf16 [m][n].
+ * The int8 -> bf16 widening is exact (|w| <= 127); the scale is applied to the float accumulator.
+ * k % 64 == 0, n % 128 == 0, m >= 1; 16-byte aligned pointers. */
+typedef struct MH3GemmArgs {
+    uint32_t m;
+    uint32_t n; /* output columns; w has 2n rows */
+    uint32_t k;
+    uint32_t reserved;
+} MH3GemmArgs;
+int mh3_gemm_w8a16_swiglu(const MH3GemmArgs* args, const uint16_t* x, const int8_t* w, const float* scale,
+                          uint16_t* out, mh3_stream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* MAKO_H3_H */

@@ -1,0 +1,96 @@
+// Shared device and host helpers of the mako_h3 kernels (gfx950, wave64).
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+#include "mako_h3.h"
+
+namespace mh3 {
+
+constexpr int kWave = 64;
+
+// ---- bf16 <-> float ------------------------------------------------------------------------------------------------
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+
+__device__ __forceinline__ float bf16_lo(uint32_t u) { return __uint_as_float(u << 16); }
+__device__ __forceinline__ float bf16_hi(uint32_t u) { return __uint_as_float(u & 0xffff0000u); }
+
+// Two floats to a packed bf16 pair, each rounded to nearest even (v_cvt_pk_bf16_f32 on gfx950).
+__device__ __forceinline__ uint32_t pack_bf16(float lo, float hi)
+{
+    bf16x2_t v = {(__bf16)lo, (__bf16)hi};
+    return __builtin_bit_cast(uint32_t, v);
+}
+
+// ---- wave reductions (64 lanes) ---------------------------------------------------------------------------------------
+__device__ __forceinline__ float wave_sum(float v)
+{
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1)
+        v += __shfl_xor(v, o, kWave);
+    return v;
+}
+
+__device__ __forceinline__ float wave_max(float v)
+{
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1)
+        v = fmaxf(v, __shfl_xor(v, o, kWave));
+    return v;
+}
+
+__device__ __forceinline__ uint32_t wave_min_u32(uint32_t v)
+{
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) {
+        const uint32_t w = __shfl_xor(v, o, kWave);
+        v = w < v ? w : v;
+    }
+    return v;
+}
+
+__device__ __forceinline__ uint32_t wave_max_u32(uint32_t v)
+{
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) {
+        const uint32_t w = __shfl_xor(v, o, kWave);
+        v = w > v ? w : v;
+    }
+    return v;
+}
+
+// Lanes below this one in a 64-bit ballot.
+__device__ __forceinline__ uint64_t lanes_below(int lane) { return (uint64_t(1) << lane) - 1; }
+
+// ---- streaming memory access -----------------------------------------------------------------------------------------
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+
+// 16-byte loads and stores with the non-temporal hint, for data read or written once.
+__device__ __forceinline__ uint4 ld_stream(const uint4* p)
+{
+    const u32x4_t v = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(p));
+    return uint4{v[0], v[1], v[2], v[3]};
+}
+__device__ __forceinline__ void st_stream(uint4* p, const uint4& v)
+{
+    const u32x4_t t = {v.x, v.y, v.z, v.w};
+    __builtin_nontemporal_store(t, reinterpret_cast<u32x4_t*>(p));
+}
+
+} // namespace mh3
+
+// ---- host side ------------------------------------------------------------------------------------------------------
+namespace mh3::host {
+
+// Records the HIP error of the last launch on this thread; returns MH3_ERR_HIP if there was one.
+int check_launch();
+// The CU count of the current device (cached per device).
+int cu_count();
+// How many blocks of `kernel` fit on one CU with `block` threads and `lds` dynamic LDS bytes (cached by the caller).
+int blocks_per_cu(const void* kernel, int block, size_t lds);
+
+inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+} // namespace mh3::host

@@ -1,0 +1,340 @@
+"""Python binding of libmako_h3 (include/mako_h3.h) for torch device tensors.
+
+The op names are the reference's kernel names (mako-common's `rms_mod_rows`, `gate_add_rows`, `swiglu_rows`,
+`cube_pool`, `cube_scores`, `cube_topk`, `quant_rows_i8`; fc1's `gemm_i8` + `swiglu_rows` as `gemm_w8a16_swiglu`),
+and errors raise RuntimeError as the reference's host code throws std::runtime_error on a bad call
+(src/video/audio_vae.cpp:231-232). Every call checks the tensors against the sizes the kernel will touch before it
+reaches the library, launches on torch's current stream, and returns without synchronizing.
+
+torch is used here only for device memory and streams; the compute is the library's HIP kernels. There is no
+fallback: if libmako_h3.so is missing, importing this module raises.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import math
+import os
+from pathlib import Path
+
+import torch
+
+_LIB_PATH = Path(os.environ.get("MAKO_H3_LIB", Path(__file__).resolve().parent.parent / "lib" / "libmako_h3.so"))
+
+OK, ERR_SHAPE, ERR_POINTER, ERR_ALIGN, ERR_PARAM, ERR_HIP, ERR_UNSUPPORTED = 0, -1, -2, -3, -4, -5, -6
+F32, BF16 = 0, 1
+SWIGLU_SPLIT, SWIGLU_FUSED = 0, 1
+CUBES_GRID, CUBES_GATHERED = 0, 1
+INT8_QKV, INT8_OUT, INT8_FC1, INT8_FC2, INT8_ALL = 1, 2, 4, 8, 15
+
+
+class RowsArgs(C.Structure):
+    _fields_ = [("rows", C.c_uint32), ("dim", C.c_uint32), ("n_sets", C.c_uint32), ("dtype", C.c_uint32),
+                ("eps", C.c_float), ("reserved", C.c_uint32 * 3)]
+
+
+class SwigluArgs(C.Structure):
+    _fields_ = [("rows", C.c_uint32), ("dim", C.c_uint32), ("layout", C.c_uint32), ("dtype", C.c_uint32)]
+
+
+class CubeArgs(C.Structure):
+    _fields_ = [("heads", C.c_uint32), ("head_dim", C.c_uint32), ("grid_t", C.c_uint32), ("grid_h", C.c_uint32),
+                ("grid_w", C.c_uint32), ("layout", C.c_uint32), ("row0", C.c_uint64), ("head_stride", C.c_uint64),
+                ("row_stride", C.c_uint64), ("k", C.c_uint32), ("local", C.c_uint32), ("out_stride", C.c_uint32),
+                ("reserved", C.c_uint32)]
+
+
+class QuantArgs(C.Structure):
+    _fields_ = [("rows", C.c_uint32), ("cols", C.c_uint32), ("dtype", C.c_uint32), ("reserved", C.c_uint32)]
+
+
+class GemmArgs(C.Structure):
+    _fields_ = [("m", C.c_uint32), ("n", C.c_uint32), ("k", C.c_uint32), ("reserved", C.c_uint32)]
+
+
+def _load() -> C.CDLL:
+    if not _LIB_PATH.exists():
+        raise ImportError(f"{_LIB_PATH} is not built: run `python mako-video_amd/build.py`")
+    lib = C.CDLL(str(_LIB_PATH))
+    P, U32, I32, I64, F = C.c_void_p, C.c_uint32, C.c_int, C.c_int64, C.c_float
+    sig = {
+        "mh3_abi_version": (I32, []),
+        "mh3_strerror": (C.c_char_p, [I32]),
+        "mh3_last_hip_error": (C.c_char_p, []),
+        "mh3_parse_int8": (I32, [C.c_char_p, C.POINTER(U32)]),
+        "mh3_check_sparse": (I32, [F, U32]),
+        "mh3_topk_k": (I64, [F, U32]),
+        "mh3_cube_count": (I64, [U32, U32, U32]),
+        "mh3_rms_mod_rows": (I32, [C.POINTER(RowsArgs), P, P, P, P, P, P, P]),
+        "mh3_gate_add_rows": (I32, [C.POINTER(RowsArgs), P, P, P, P, P]),
+        "mh3_rms_mod_gate_add_rows": (I32, [C.POINTER(RowsArgs), P, P, P, P, P, P, P, P, P]),
+        "mh3_swiglu_rows": (I32, [C.POINTER(SwigluArgs), P, P, P, P]),
+        "mh3_cube_pool": (I32, [C.POINTER(CubeArgs), P, P, P, P, P, P]),
+        "mh3_cube_scores": (I32, [C.POINTER(CubeArgs), P, P, P, P]),
+        "mh3_cube_topk": (I32, [C.POINTER(CubeArgs), P, P, P, P]),
+        "mh3_cube_select": (I32, [C.POINTER(CubeArgs), P, P, P, P, P]),
+        "mh3_quant_rows_i8": (I32, [C.POINTER(QuantArgs), P, P, P, P]),
+        "mh3_gemm_w8a16_swiglu": (I32, [C.POINTER(GemmArgs), P, P, P, P, P]),
+    }
+    for name, (res, args) in sig.items():
+        f = getattr(lib, name)
+        f.restype, f.argtypes = res, args
+    return lib
+
+
+lib = _load()
+LIB_PATH = _LIB_PATH
+
+
+def strerror(code: int) -> str:
+    return lib.mh3_strerror(code).decode()
+
+
+def _check(rc: int, what: str) -> None:
+    if rc != OK:
+        extra = lib.mh3_last_hip_error().decode() if rc == ERR_HIP else ""
+        raise RuntimeError(f"{what}: {strerror(rc)} ({rc}){': ' + extra if extra else ''}")
+
+
+def _stream() -> int:
+    return torch.cuda.current_stream().cuda_stream
+
+
+def _ptr(t: torch.Tensor | None) -> int | None:
+    return None if t is None else t.data_ptr()
+
+
+def _need(t: torch.Tensor, name: str, dtype: torch.dtype, numel: int) -> None:
+    if not isinstance(t, torch.Tensor):
+        raise TypeError(f"{name}: expected a tensor")
+    if t.device.type != "cuda":
+        raise ValueError(f"{name}: must be on the GPU")
+    if t.dtype != dtype:
+        raise ValueError(f"{name}: dtype {t.dtype}, expected {dtype}")
+    if not t.is_contiguous():
+        raise ValueError(f"{name}: must be contiguous")
+    if t.numel() < numel:
+        raise ValueError(f"{name}: {t.numel()} elements, the call touches {numel}")
+
+
+def _dt(t: torch.Tensor) -> int:
+    if t.dtype == torch.bfloat16:
+        return BF16
+    if t.dtype == torch.float32:
+        return F32
+    raise ValueError(f"unsupported dtype {t.dtype}")
+
+
+# ---- H3 options (host only) ------------------------------------------------------------------------------------------
+
+def parse_int8(text: str) -> int | None:
+    """H3::parse_int8: "none", "all", or a comma list of qkv, out, fc1, fc2 -> mask; None for anything else."""
+    m = C.c_uint32(0)
+    rc = lib.mh3_parse_int8(text.encode(), C.byref(m))
+    return int(m.value) if rc == OK else None
+
+
+def check_sparse(ratio: float, local: int) -> bool:
+    """H3::set_sparse's domain: ratio in [0, 1], local in {0, 1, 3}."""
+    return lib.mh3_check_sparse(float(ratio), int(local)) == OK
+
+
+def topk_k(ratio: float, cubes: int) -> int:
+    k = int(lib.mh3_topk_k(float(ratio), int(cubes)))
+    if k < 0:
+        raise ValueError(f"ratio {ratio} outside [0, 1]")
+    return k
+
+
+def cube_count(grid_t: int, grid_h: int, grid_w: int) -> int:
+    return int(lib.mh3_cube_count(grid_t, grid_h, grid_w))
+
+
+# ---- rows ----------------------------------------------------------------------------------------------------------
+
+def _rows_args(x: torch.Tensor, n_sets: int, eps: float) -> RowsArgs:
+    if x.dim() != 2:
+        raise ValueError("rows must be [rows][dim]")
+    a = RowsArgs()
+    a.rows, a.dim, a.n_sets, a.dtype, a.eps = x.shape[0], x.shape[1], n_sets, _dt(x), eps
+    return a
+
+
+def _mod_params(dim, n_sets, w, shift, scale, gate, set_of_row, rows):
+    if w is not None:
+        _need(w, "w", torch.float32, dim)
+    for name, t in (("shift", shift), ("scale", scale), ("gate", gate)):
+        if t is not None:
+            _need(t, name, torch.float32, n_sets * dim)
+    if set_of_row is not None:
+        _need(set_of_row, "set_of_row", torch.uint8, rows)
+
+
+def rms_mod_rows(x, w, shift, scale, *, eps=1e-6, set_of_row=None, n_sets=1, out=None):
+    """y = x * rsqrt(mean(x^2) + eps) * w * (1 + scale[s]) + shift[s] per row (x: [rows][dim] f32 or bf16)."""
+    a = _rows_args(x, n_sets, eps)
+    _need(x, "x", x.dtype, x.numel())
+    _mod_params(x.shape[1], n_sets, w, shift, scale, None, set_of_row, x.shape[0])
+    out = torch.empty_like(x) if out is None else out
+    _need(out, "out", x.dtype, x.numel())
+    _check(lib.mh3_rms_mod_rows(C.byref(a), _ptr(x), _ptr(w), _ptr(shift), _ptr(scale), _ptr(set_of_row), _ptr(out),
+                                _stream()), "rms_mod_rows")
+    return out
+
+
+def gate_add_rows(x, y, gate, *, set_of_row=None, n_sets=1):
+    """x += gate[s] * y per row, in place; returns x."""
+    a = _rows_args(x, n_sets, 1.0)
+    _need(x, "x", x.dtype, x.numel())
+    _need(y, "y", x.dtype, x.numel())
+    _mod_params(x.shape[1], n_sets, None, None, None, gate, set_of_row, x.shape[0])
+    _check(lib.mh3_gate_add_rows(C.byref(a), _ptr(x), _ptr(y), _ptr(gate), _ptr(set_of_row), _stream()),
+           "gate_add_rows")
+    return x
+
+
+def rms_mod_gate_add_rows(x, residual, w, shift, scale, gate, *, eps=1e-6, set_of_row=None, n_sets=1, out=None):
+    """out = residual + gate[s] * (x * rsqrt(mean(x^2) + eps) * w * (1 + scale[s]) + shift[s]), one HBM pass."""
+    a = _rows_args(x, n_sets, eps)
+    _need(x, "x", x.dtype, x.numel())
+    _need(residual, "residual", x.dtype, x.numel())
+    _mod_params(x.shape[1], n_sets, w, shift, scale, gate, set_of_row, x.shape[0])
+    out = torch.empty_like(x) if out is None else out
+    _need(out, "out", x.dtype, x.numel())
+    _check(lib.mh3_rms_mod_gate_add_rows(C.byref(a), _ptr(x), _ptr(residual), _ptr(w), _ptr(shift), _ptr(scale),
+                                         _ptr(gate), _ptr(set_of_row), _ptr(out), _stream()), "rms_mod_gate_add_rows")
+    return out
+
+
+# ---- swiglu --------------------------------------------------------------------------------------------------------
+
+def swiglu_rows(gate, up=None, *, out=None):
+    """out = silu(gate) * up. With up None, gate is fc1's fused [rows][2 dim] row ([gate | up])."""
+    a = SwigluArgs()
+    if up is None:
+        rows, two = gate.shape
+        if two % 2:
+            raise ValueError("a fused row has an even width")
+        a.rows, a.dim, a.layout = rows, two // 2, SWIGLU_FUSED
+    else:
+        a.rows, a.dim, a.layout = gate.shape[0], gate.shape[1], SWIGLU_SPLIT
+        _need(up, "up", gate.dtype, a.rows * a.dim)
+    a.dtype = _dt(gate)
+    _need(gate, "gate", gate.dtype, gate.numel())
+    out = torch.empty((a.rows, a.dim), dtype=gate.dtype, device=gate.device) if out is None else out
+    _need(out, "out", gate.dtype, a.rows * a.dim)
+    _check(lib.mh3_swiglu_rows(C.byref(a), _ptr(gate), _ptr(up), _ptr(out), _stream()), "swiglu_rows")
+    return out
+
+
+# ---- cubes ---------------------------------------------------------------------------------------------------------
+
+def cube_args(heads, grid, *, layout=CUBES_GRID, row0=0, head_stride=None, row_stride=128, k=0, local=1,
+              out_stride=None, head_dim=128) -> CubeArgs:
+    gt, gh, gw = grid
+    a = CubeArgs()
+    a.heads, a.head_dim, a.grid_t, a.grid_h, a.grid_w, a.layout = heads, head_dim, gt, gh, gw, layout
+    cubes = cube_count(gt, gh, gw)
+    rows = row0 + (cubes * 64 if layout == CUBES_GATHERED else gt * gh * gw)
+    a.row0, a.row_stride = row0, row_stride
+    a.head_stride = rows * row_stride if head_stride is None else head_stride
+    a.k, a.local = k, local
+    a.out_stride = (k + local) if out_stride is None else out_stride
+    return a
+
+
+def _rows_touched(a: CubeArgs) -> int:
+    cubes = cube_count(a.grid_t, a.grid_h, a.grid_w)
+    last = a.row0 + (cubes * 64 - 1 if a.layout == CUBES_GATHERED else a.grid_t * a.grid_h * a.grid_w - 1)
+    return (a.heads - 1) * a.head_stride + last * a.row_stride + a.head_dim
+
+
+def cube_pool(a: CubeArgs, q, k, *, qc=None, kc=None, counts=None):
+    """Per head, the mean of each 4x4x4 cube's q and k rows -> (qc, kc) float [heads][cubes][head_dim]."""
+    cubes = cube_count(a.grid_t, a.grid_h, a.grid_w)
+    n = _rows_touched(a)
+    _need(q, "q", torch.bfloat16, n)
+    _need(k, "k", torch.bfloat16, n)
+    shape = (a.heads, cubes, a.head_dim)
+    qc = torch.empty(shape, dtype=torch.float32, device=q.device) if qc is None else qc
+    kc = torch.empty(shape, dtype=torch.float32, device=q.device) if kc is None else kc
+    _need(qc, "qc", torch.float32, a.heads * cubes * a.head_dim)
+    _need(kc, "kc", torch.float32, a.heads * cubes * a.head_dim)
+    if counts is not None:
+        _need(counts, "counts", torch.int32, cubes)
+    _check(lib.mh3_cube_pool(C.byref(a), _ptr(q), _ptr(k), _ptr(qc), _ptr(kc), _ptr(counts), _stream()), "cube_pool")
+    return qc, kc
+
+
+def cube_scores(a: CubeArgs, qc, kc, *, out=None):
+    """s[h][i][j] = qc[h][i] . kc[h][j] / sqrt(head_dim), float [heads][cubes][cubes]."""
+    cubes = cube_count(a.grid_t, a.grid_h, a.grid_w)
+    _need(qc, "qc", torch.float32, a.heads * cubes * a.head_dim)
+    _need(kc, "kc", torch.float32, a.heads * cubes * a.head_dim)
+    out = torch.empty((a.heads, cubes, cubes), dtype=torch.float32, device=qc.device) if out is None else out
+    _need(out, "scores", torch.float32, a.heads * cubes * cubes)
+    _check(lib.mh3_cube_scores(C.byref(a), _ptr(qc), _ptr(kc), _ptr(out), _stream()), "cube_scores")
+    return out
+
+
+def _topk_out(a: CubeArgs, device, idx, cnt):
+    cubes = cube_count(a.grid_t, a.grid_h, a.grid_w)
+    idx = torch.empty((a.heads, cubes, a.out_stride), dtype=torch.int32, device=device) if idx is None else idx
+    cnt = torch.empty((a.heads, cubes), dtype=torch.int32, device=device) if cnt is None else cnt
+    _need(idx, "idx", torch.int32, a.heads * cubes * a.out_stride)
+    _need(cnt, "cnt", torch.int32, a.heads * cubes)
+    return idx, cnt
+
+
+def cube_topk(a: CubeArgs, scores, *, idx=None, cnt=None):
+    """Per (head, query cube): the top a.k cubes by score plus the local cubes, ascending, padded with -1."""
+    cubes = cube_count(a.grid_t, a.grid_h, a.grid_w)
+    _need(scores, "scores", torch.float32, a.heads * cubes * cubes)
+    idx, cnt = _topk_out(a, scores.device, idx, cnt)
+    _check(lib.mh3_cube_topk(C.byref(a), _ptr(scores), _ptr(idx), _ptr(cnt), _stream()), "cube_topk")
+    return idx, cnt
+
+
+def cube_select(a: CubeArgs, qc, kc, *, idx=None, cnt=None):
+    """cube_scores and cube_topk fused: the scores stay on chip."""
+    cubes = cube_count(a.grid_t, a.grid_h, a.grid_w)
+    _need(qc, "qc", torch.float32, a.heads * cubes * a.head_dim)
+    _need(kc, "kc", torch.float32, a.heads * cubes * a.head_dim)
+    idx, cnt = _topk_out(a, qc.device, idx, cnt)
+    _check(lib.mh3_cube_select(C.byref(a), _ptr(qc), _ptr(kc), _ptr(idx), _ptr(cnt), _stream()), "cube_select")
+    return idx, cnt
+
+
+# ---- int8 ----------------------------------------------------------------------------------------------------------
+
+def quant_rows_i8(w, *, q=None, scale=None):
+    """Each [out][in] row to symmetric int8 with a float scale (max |row| -> 127)."""
+    if w.dim() != 2:
+        raise ValueError("w must be [rows][cols]")
+    a = QuantArgs()
+    a.rows, a.cols, a.dtype = w.shape[0], w.shape[1], _dt(w)
+    _need(w, "w", w.dtype, w.numel())
+    q = torch.empty(w.shape, dtype=torch.int8, device=w.device) if q is None else q
+    scale = torch.empty(w.shape[0], dtype=torch.float32, device=w.device) if scale is None else scale
+    _need(q, "q", torch.int8, w.numel())
+    _need(scale, "scale", torch.float32, w.shape[0])
+    _check(lib.mh3_quant_rows_i8(C.byref(a), _ptr(w), _ptr(q), _ptr(scale), _stream()), "quant_rows_i8")
+    return q, scale
+
+
+def gemm_w8a16_swiglu(x, w, scale, *, out=None):
+    """fc1 + SwiGLU: x bf16 [m][k], w int8 [2n][k] (gate rows then up rows), scale f32 [2n] -> bf16 [m][n]."""
+    m, k = x.shape
+    two_n = w.shape[0]
+    if w.dim() != 2 or w.shape[1] != k or two_n % 2:
+        raise ValueError("w must be [2n][k]")
+    n = two_n // 2
+    _need(x, "x", torch.bfloat16, m * k)
+    _need(w, "w", torch.int8, two_n * k)
+    _need(scale, "scale", torch.float32, two_n)
+    out = torch.empty((m, n), dtype=torch.bfloat16, device=x.device) if out is None else out
+    _need(out, "out", torch.bfloat16, m * n)
+    a = GemmArgs()
+    a.m, a.n, a.k = m, n, k
+    _check(lib.mh3_gemm_w8a16_swiglu(C.byref(a), _ptr(x), _ptr(w), _ptr(scale), _ptr(out), _stream()),
+           "gemm_w8a16_swiglu")
+    return out

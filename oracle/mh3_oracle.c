@@ -1,0 +1,343 @@
+/*
+ * mh3_oracle.c — TEST INFRASTRUCTURE ONLY: the scalar CPU restatement of the H3 per-block hot path that the tests,
+ * the smoke check and bench.py's CPU-baseline leg use as the parity checker. See mh3_oracle.h for what each
+ * function follows in the reference and how it is pinned. Single-threaded, double accumulation, one rounding at the
+ * store (the reference's CPU idiom, src/video/audio_vae.cpp:386-416).
+ */
+#include "mh3_oracle.h"
+
+#include <math.h>
+#include <stdlib.h>
+#include <string.h>
+
+/* ---- bf16 ----------------------------------------------------------------------------------------------------- */
+
+float mh3o_bf16_to_float(uint16_t h)
+{
+    uint32_t u = (uint32_t)h << 16;
+    float f;
+    memcpy(&f, &u, 4);
+    return f;
+}
+
+uint16_t mh3o_bf16_from_float(float f)
+{
+    uint32_t u;
+    memcpy(&u, &f, 4);
+    if ((u & 0x7fffffffu) > 0x7f800000u)
+        return (uint16_t)((u >> 16) | 0x40u); /* NaN stays NaN (quiet) */
+    u += 0x7fffu + ((u >> 16) & 1u);         /* round to nearest, ties to even */
+    return (uint16_t)(u >> 16);
+}
+
+/* Nearest-even bf16 of a double, rounded once (no intermediate float rounding). bf16 keeps 8 significant bits. */
+uint16_t mh3o_bf16_from_double(double d)
+{
+    if (isnan(d))
+        return 0x7fc0u;
+    if (isinf(d) || fabs(d) < 0x1p-126) /* infinities, zeros and the subnormal range: the float path is exact enough */
+        return mh3o_bf16_from_float((float)d);
+    int e;
+    const double m = frexp(d, &e);                /* d = m * 2^e, 0.5 <= |m| < 1 */
+    const double r = nearbyint(ldexp(m, 8));      /* 8 significant bits, ties to even (default rounding mode) */
+    const double v = ldexp(r, e - 8);
+    if (fabs(v) > 0x1.fep127)                     /* beyond bf16's largest finite value */
+        return d > 0 ? 0x7f80u : 0xff80u;
+    const float f = (float)v;                     /* exact: v has <= 8 significant bits */
+    uint32_t u;
+    memcpy(&u, &f, 4);
+    return (uint16_t)(u >> 16);
+}
+
+void mh3o_bf16_to_float_n(const uint16_t* in, float* out, uint64_t n)
+{
+    for (uint64_t i = 0; i < n; ++i)
+        out[i] = mh3o_bf16_to_float(in[i]);
+}
+
+void mh3o_bf16_from_double_n(const double* in, uint16_t* out, uint64_t n)
+{
+    for (uint64_t i = 0; i < n; ++i)
+        out[i] = mh3o_bf16_from_double(in[i]);
+}
+
+static double load(int dtype, const void* p, uint64_t i)
+{
+    return dtype == MH3O_BF16 ? (double)mh3o_bf16_to_float(((const uint16_t*)p)[i]) : (double)((const float*)p)[i];
+}
+
+static void store(int dtype, void* p, uint64_t i, double v)
+{
+    if (dtype == MH3O_BF16)
+        ((uint16_t*)p)[i] = mh3o_bf16_from_double(v);
+    else
+        ((float*)p)[i] = (float)v;
+}
+
+/* ---- rows ------------------------------------------------------------------------------------------------------ */
+
+/* 1 / sqrt(mean(x^2) + eps) of row r, the sum of squares in double. */
+static double inv_rms(uint32_t dim, float eps, int dtype, const void* x, uint64_t r)
+{
+    double ss = 0;
+    for (uint32_t c = 0; c < dim; ++c) {
+        const double v = load(dtype, x, r * dim + c);
+        ss += v * v;
+    }
+    return 1.0 / sqrt(ss / (double)dim + (double)eps);
+}
+
+/* docs/architecture.md:61: "RMS norm with weight times (1 + scale) plus shift, per row"; the row's set through
+ * the offset table (architecture.md:49-52). */
+void mh3o_rms_mod_rows(uint32_t rows, uint32_t dim, float eps, int dtype, const void* x, const float* w,
+                       const float* shift, const float* scale, const uint8_t* set_of_row, void* y)
+{
+    for (uint64_t r = 0; r < rows; ++r) {
+        const double inv = inv_rms(dim, eps, dtype, x, r);
+        const uint64_t s = set_of_row ? set_of_row[r] : 0;
+        const float* sh = shift + s * dim;
+        const float* sc = scale + s * dim;
+        for (uint32_t c = 0; c < dim; ++c) {
+            const double n = load(dtype, x, r * dim + c) * inv * (w ? (double)w[c] : 1.0);
+            store(dtype, y, r * dim + c, n * (1.0 + (double)sc[c]) + (double)sh[c]);
+        }
+    }
+}
+
+/* docs/architecture.md:64-65: "the output projection times the row's gate added back" (and the same after fc2). */
+void mh3o_gate_add_rows(uint32_t rows, uint32_t dim, int dtype, void* x, const void* y, const float* gate,
+                        const uint8_t* set_of_row)
+{
+    for (uint64_t r = 0; r < rows; ++r) {
+        const uint64_t s = set_of_row ? set_of_row[r] : 0;
+        const float* g = gate + s * dim;
+        for (uint32_t c = 0; c < dim; ++c) {
+            const uint64_t i = r * dim + c;
+            store(dtype, x, i, load(dtype, x, i) + (double)g[c] * load(dtype, y, i));
+        }
+    }
+}
+
+/* The fused form: out = residual + gate * modRMS(x), each output rounded once. */
+void mh3o_rms_mod_gate_add_rows(uint32_t rows, uint32_t dim, float eps, int dtype, const void* x, const void* residual,
+                                const float* w, const float* shift, const float* scale, const float* gate,
+                                const uint8_t* set_of_row, void* out)
+{
+    for (uint64_t r = 0; r < rows; ++r) {
+        const double inv = inv_rms(dim, eps, dtype, x, r);
+        const uint64_t s = set_of_row ? set_of_row[r] : 0;
+        const float* sh = shift + s * dim;
+        const float* sc = scale + s * dim;
+        const float* g = gate + s * dim;
+        for (uint32_t c = 0; c < dim; ++c) {
+            const uint64_t i = r * dim + c;
+            const double n = load(dtype, x, i) * inv * (w ? (double)w[c] : 1.0);
+            const double m = n * (1.0 + (double)sc[c]) + (double)sh[c];
+            store(dtype, out, i, load(dtype, residual, i) + (double)g[c] * m);
+        }
+    }
+}
+
+/* ---- swiglu ---------------------------------------------------------------------------------------------------- */
+
+/* docs/architecture.md:65,112-114: fc1's row is [gate; value], SwiGLU = silu(gate) * value. */
+void mh3o_swiglu_rows(uint32_t rows, uint32_t dim, int layout, int dtype, const void* gate, const void* up, void* out)
+{
+    const uint64_t gs = layout == MH3O_SWIGLU_FUSED ? 2ull * dim : dim;
+    const uint64_t uoff = layout == MH3O_SWIGLU_FUSED ? dim : 0;
+    const void* ub = layout == MH3O_SWIGLU_FUSED ? gate : up;
+    for (uint64_t r = 0; r < rows; ++r)
+        for (uint32_t c = 0; c < dim; ++c) {
+            const double g = load(dtype, gate, r * gs + c);
+            const double u = load(dtype, ub, r * gs + uoff + c);
+            store(dtype, out, r * dim + c, g / (1.0 + exp(-g)) * u);
+        }
+}
+
+/* ---- cubes ----------------------------------------------------------------------------------------------------- */
+
+int64_t mh3o_cube_count(uint32_t gt, uint32_t gh, uint32_t gw)
+{
+    return (int64_t)((gt + 3) / 4) * ((gh + 3) / 4) * ((gw + 3) / 4);
+}
+
+/* The row of video position (t, y, x) of cube c's slot (dt, dy, dx), docs/architecture.md:120-125. */
+static uint64_t cube_row(int layout, uint64_t row0, uint32_t gh, uint32_t gw, uint64_t c, uint32_t t, uint32_t y,
+                         uint32_t x, uint32_t dt, uint32_t dy, uint32_t dx)
+{
+    if (layout == MH3O_CUBES_GATHERED)
+        return row0 + c * 64 + (dt * 4 + dy) * 4 + dx;
+    return row0 + ((uint64_t)t * gh + y) * gw + x;
+}
+
+static void pool_one(uint32_t head_dim, uint32_t gt, uint32_t gh, uint32_t gw, int layout, uint64_t row0,
+                     uint64_t head_stride, uint64_t row_stride, const uint16_t* src, uint64_t h, uint64_t c,
+                     double* acc, float* dst, int32_t* count_out)
+{
+    const uint32_t ch = (gh + 3) / 4, cw = (gw + 3) / 4;
+    const uint32_t ct = (uint32_t)(c / ((uint64_t)ch * cw)), cy = (uint32_t)(c / cw % ch), cx = (uint32_t)(c % cw);
+    memset(acc, 0, sizeof(double) * head_dim);
+    int32_t n = 0;
+    for (uint32_t dt = 0; dt < 4; ++dt)
+        for (uint32_t dy = 0; dy < 4; ++dy)
+            for (uint32_t dx = 0; dx < 4; ++dx) {
+                const uint32_t t = ct * 4 + dt, y = cy * 4 + dy, x = cx * 4 + dx;
+                if (t >= gt || y >= gh || x >= gw)
+                    continue; /* padding: no token */
+                const uint64_t row = cube_row(layout, row0, gh, gw, c, t, y, x, dt, dy, dx);
+                const uint16_t* p = src + h * head_stride + row * row_stride;
+                for (uint32_t d = 0; d < head_dim; ++d)
+                    acc[d] += (double)mh3o_bf16_to_float(p[d]);
+                ++n;
+            }
+    for (uint32_t d = 0; d < head_dim; ++d)
+        dst[d] = (float)(acc[d] / (double)n); /* divisor: the cube's token count (architecture.md:124) */
+    if (count_out)
+        *count_out = n;
+}
+
+void mh3o_cube_pool(uint32_t heads, uint32_t head_dim, uint32_t gt, uint32_t gh, uint32_t gw, int layout,
+                    uint64_t row0, uint64_t head_stride, uint64_t row_stride, const uint16_t* q, const uint16_t* k,
+                    float* qc, float* kc, int32_t* counts)
+{
+    const uint64_t C = (uint64_t)mh3o_cube_count(gt, gh, gw);
+    double* acc = (double*)malloc(sizeof(double) * head_dim);
+    for (uint64_t h = 0; h < heads; ++h)
+        for (uint64_t c = 0; c < C; ++c) {
+            int32_t n = 0;
+            pool_one(head_dim, gt, gh, gw, layout, row0, head_stride, row_stride, q, h, c, acc,
+                     qc + (h * C + c) * head_dim, &n);
+            pool_one(head_dim, gt, gh, gw, layout, row0, head_stride, row_stride, k, h, c, acc,
+                     kc + (h * C + c) * head_dim, NULL);
+            if (counts && h == 0)
+                counts[c] = n;
+        }
+    free(acc);
+}
+
+void mh3o_cube_pool_some(uint32_t head_dim, uint32_t gt, uint32_t gh, uint32_t gw, int layout, uint64_t row0,
+                         uint64_t head_stride, uint64_t row_stride, const uint16_t* q, const uint16_t* k,
+                         const int64_t* entries, uint64_t n_entries, float* qc, float* kc)
+{
+    const uint64_t C = (uint64_t)mh3o_cube_count(gt, gh, gw);
+    double* acc = (double*)malloc(sizeof(double) * head_dim);
+    for (uint64_t i = 0; i < n_entries; ++i) {
+        const uint64_t h = (uint64_t)entries[i] / C, c = (uint64_t)entries[i] % C;
+        pool_one(head_dim, gt, gh, gw, layout, row0, head_stride, row_stride, q, h, c, acc, qc + i * head_dim, NULL);
+        pool_one(head_dim, gt, gh, gw, layout, row0, head_stride, row_stride, k, h, c, acc, kc + i * head_dim, NULL);
+    }
+    free(acc);
+}
+
+/* docs/architecture.md:126: "scores every cube pair per head" from the pooled means; scaled by 1/sqrt(head_dim) as
+ * attention scores are (the scale does not change a ranking). */
+void mh3o_cube_scores(uint32_t heads, uint32_t cubes, uint32_t head_dim, const float* qc, const float* kc, double* s)
+{
+    const double scale = 1.0 / sqrt((double)head_dim);
+    for (uint64_t h = 0; h < heads; ++h)
+        for (uint64_t i = 0; i < cubes; ++i) {
+            const float* a = qc + (h * cubes + i) * head_dim;
+            for (uint64_t j = 0; j < cubes; ++j) {
+                const float* b = kc + (h * cubes + j) * head_dim;
+                double acc = 0;
+                for (uint32_t d = 0; d < head_dim; ++d)
+                    acc += (double)a[d] * (double)b[d];
+                s[(h * cubes + i) * cubes + j] = acc * scale;
+            }
+        }
+}
+
+/* docs/architecture.md:126-130, README.md:81-87: for one (head, query cube i) the top k cubes by score (higher first,
+ * equal scores the lower index first), united with the local cubes, as ascending indices; returns the count. O(C^2)
+ * on purpose: a cube j is in the top k iff fewer than k cubes precede it in (score desc, index asc) order. */
+int32_t mh3o_cube_topk_row(uint32_t gt, uint32_t gh, uint32_t gw, uint32_t k, uint32_t local, uint32_t out_stride,
+                           uint64_t i, const double* row, int32_t* out)
+{
+    const uint32_t ch = (gh + 3) / 4, cw = (gw + 3) / 4, cth = (gt + 3) / 4;
+    const uint64_t C = (uint64_t)cth * ch * cw, plane = (uint64_t)ch * cw;
+    unsigned char* sel = (unsigned char*)malloc(C);
+    for (uint64_t j = 0; j < C; ++j) {
+        uint64_t ahead = 0;
+        for (uint64_t o = 0; o < C; ++o)
+            ahead += row[o] > row[j] || (row[o] == row[j] && o < j);
+        sel[j] = ahead < k;
+    }
+    if (local >= 1)
+        sel[i] = 1;
+    if (local == 3) {
+        const uint64_t ct = i / plane;
+        if (ct > 0)
+            sel[i - plane] = 1;
+        if (ct + 1 < cth)
+            sel[i + plane] = 1;
+    }
+    int32_t n = 0;
+    for (uint64_t j = 0; j < C; ++j)
+        if (sel[j])
+            out[n++] = (int32_t)j;
+    for (uint32_t j = (uint32_t)n; j < out_stride; ++j)
+        out[j] = -1;
+    free(sel);
+    return n;
+}
+
+void mh3o_cube_topk(uint32_t heads, uint32_t gt, uint32_t gh, uint32_t gw, uint32_t k, uint32_t local,
+                    uint32_t out_stride, const double* s, int32_t* idx, int32_t* cnt)
+{
+    const uint64_t C = (uint64_t)mh3o_cube_count(gt, gh, gw);
+    for (uint64_t h = 0; h < heads; ++h)
+        for (uint64_t i = 0; i < C; ++i)
+            cnt[h * C + i] = mh3o_cube_topk_row(gt, gh, gw, k, local, out_stride, i, s + (h * C + i) * C,
+                                                idx + (h * C + i) * out_stride);
+}
+
+/* ---- int8 ------------------------------------------------------------------------------------------------------ */
+
+/* docs/performance.md:122-123: "int8 rows with a float scale each (symmetric, the row's maximum at 127)". The scale
+ * and the division are float, as the device computes them; rounding to nearest even. */
+void mh3o_quant_rows_i8(uint32_t rows, uint32_t cols, int dtype, const void* w, int8_t* q, float* scale)
+{
+    for (uint64_t r = 0; r < rows; ++r) {
+        float mx = 0.0f;
+        for (uint32_t c = 0; c < cols; ++c) {
+            const float v = fabsf((float)load(dtype, w, r * cols + c));
+            mx = v > mx ? v : mx;
+        }
+        const float s = mx / 127.0f;
+        scale[r] = s;
+        for (uint32_t c = 0; c < cols; ++c) {
+            if (s == 0.0f) {
+                q[r * cols + c] = 0;
+                continue;
+            }
+            float v = nearbyintf((float)load(dtype, w, r * cols + c) / s);
+            v = v > 127.0f ? 127.0f : (v < -127.0f ? -127.0f : v);
+            q[r * cols + c] = (int8_t)v;
+        }
+    }
+}
+
+/* docs/performance.md:124-126 (the int8 GEMM scaled in the epilogue) and architecture.md:65 (fc1's [gate; value]
+ * rows, then SwiGLU), in the weight-only form: y = x * (W * diag s), out = silu(y_gate) * y_up. */
+void mh3o_gemm_w8a16_swiglu(uint32_t m, uint32_t n, uint32_t k, const uint16_t* x, const int8_t* w,
+                            const float* scale, uint16_t* out)
+{
+    double* xr = (double*)malloc(sizeof(double) * k);
+    for (uint64_t r = 0; r < m; ++r) {
+        for (uint32_t i = 0; i < k; ++i)
+            xr[i] = (double)mh3o_bf16_to_float(x[r * k + i]);
+        for (uint64_t c = 0; c < n; ++c) {
+            const int8_t* wg = w + c * k;
+            const int8_t* wu = w + (n + c) * k;
+            double g = 0, u = 0;
+            for (uint32_t i = 0; i < k; ++i) {
+                g += xr[i] * (double)wg[i];
+                u += xr[i] * (double)wu[i];
+            }
+            g *= (double)scale[c];
+            u *= (double)scale[n + c];
+            out[r * n + c] = mh3o_bf16_from_double(g / (1.0 + exp(-g)) * u);
+        }
+    }
+    free(xr);
+}

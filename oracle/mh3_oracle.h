@@ -1,0 +1,83 @@
+/*
+ * mh3_oracle.h — TEST INFRASTRUCTURE ONLY. A scalar CPU restatement of the H3 per-block hot-path ops, used by
+ * tests/, the smoke check and bench.py's CPU-baseline leg as the parity checker. Nothing in the product links,
+ * loads or calls it.
+ *
+ * The reference's implementation of these ops lives in the un-vendored mako-common submodule (.gitmodules:1-3, empty
+ * at external/mako-common), so this file restates the semantics the reference's documents and call sites fix, in the
+ * reference's CPU idiom (src/video/audio_vae.cpp:386-416: per-row double accumulation, a float store):
+ *   rms_mod_rows / gate_add_rows   docs/architecture.md:49-52,61,64-66
+ *   swiglu_rows                     docs/architecture.md:65,112-114
+ *   cube_pool / _scores / _topk     docs/architecture.md:118-133, README.md:81-87, docs/performance.md:175-181
+ *   quant_rows_i8, W8A16 fc1        docs/performance.md:120-136
+ * bf16 results are rounded to nearest even exactly once, from the double value.
+ *
+ * How each function is pinned (tests/test_oracle.py): no reference vector exists for any of them (the reference
+ * holds no fixture at the kernel level), so each is checked against a library routine or brute force written
+ * independently of it, plus closed forms and invariants:
+ *   mh3o_bf16_from_double      nearest-even property checked exhaustively on neighbours; torch's float->bf16
+ *   mh3o_rms_mod_rows          torch.nn.functional.rms_norm (float64); RMS = 1 at w=1, shift=scale=0
+ *   mh3o_gate_add_rows         closed form in numpy float64; gate = 0 leaves x bit-exact
+ *   mh3o_rms_mod_gate_add_rows composition of the two above; gate = 0 gives residual bit-exact
+ *   mh3o_swiglu_rows           torch.nn.functional.silu (float64); silu(0)=0, large |g| limits; split == fused
+ *   mh3o_cube_pool             numpy reshape-mean over the (t, y, x) grid; brute force on padded grids;
+ *                              permutation invariance inside a cube; gathered layout == grid layout
+ *   mh3o_cube_scores           numpy matmul / sqrt(hd)
+ *   mh3o_cube_topk             numpy lexsort; constructed scores with an analytic answer; ratio 1 selects all
+ *   mh3o_quant_rows_i8         |q| <= 127, the row maximum maps to +-127, |w - q*s| <= s/2, numpy rint
+ *   mh3o_gemm_w8a16_swiglu     torch.matmul in float64; exact integer results for w in {-1,0,1}, s = 1
+ */
+#ifndef MH3_ORACLE_H
+#define MH3_ORACLE_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum { MH3O_F32 = 0, MH3O_BF16 = 1 };
+enum { MH3O_SWIGLU_SPLIT = 0, MH3O_SWIGLU_FUSED = 1 };
+enum { MH3O_CUBES_GRID = 0, MH3O_CUBES_GATHERED = 1 };
+
+float mh3o_bf16_to_float(uint16_t h);
+uint16_t mh3o_bf16_from_float(float f);
+uint16_t mh3o_bf16_from_double(double d);
+/* n values: bf16 -> float and double -> bf16, for the tests. */
+void mh3o_bf16_to_float_n(const uint16_t* in, float* out, uint64_t n);
+void mh3o_bf16_from_double_n(const double* in, uint16_t* out, uint64_t n);
+
+void mh3o_rms_mod_rows(uint32_t rows, uint32_t dim, float eps, int dtype, const void* x, const float* w,
+                       const float* shift, const float* scale, const uint8_t* set_of_row, void* y);
+void mh3o_gate_add_rows(uint32_t rows, uint32_t dim, int dtype, void* x, const void* y, const float* gate,
+                        const uint8_t* set_of_row);
+void mh3o_rms_mod_gate_add_rows(uint32_t rows, uint32_t dim, float eps, int dtype, const void* x, const void* residual,
+                                const float* w, const float* shift, const float* scale, const float* gate,
+                                const uint8_t* set_of_row, void* out);
+
+void mh3o_swiglu_rows(uint32_t rows, uint32_t dim, int layout, int dtype, const void* gate, const void* up, void* out);
+
+int64_t mh3o_cube_count(uint32_t gt, uint32_t gh, uint32_t gw);
+void mh3o_cube_pool(uint32_t heads, uint32_t head_dim, uint32_t gt, uint32_t gh, uint32_t gw, int layout,
+                    uint64_t row0, uint64_t head_stride, uint64_t row_stride, const uint16_t* q, const uint16_t* k,
+                    float* qc, float* kc, int32_t* counts);
+/* Pools only the listed (head, cube) pairs: entries [i] = head * cubes + cube, results to qc/kc[i][head_dim]. */
+void mh3o_cube_pool_some(uint32_t head_dim, uint32_t gt, uint32_t gh, uint32_t gw, int layout, uint64_t row0,
+                         uint64_t head_stride, uint64_t row_stride, const uint16_t* q, const uint16_t* k,
+                         const int64_t* entries, uint64_t n_entries, float* qc, float* kc);
+void mh3o_cube_scores(uint32_t heads, uint32_t cubes, uint32_t head_dim, const float* qc, const float* kc, double* s);
+int32_t mh3o_cube_topk_row(uint32_t gt, uint32_t gh, uint32_t gw, uint32_t k, uint32_t local, uint32_t out_stride,
+                           uint64_t i, const double* row, int32_t* out);
+void mh3o_cube_topk(uint32_t heads, uint32_t gt, uint32_t gh, uint32_t gw, uint32_t k, uint32_t local,
+                    uint32_t out_stride, const double* s, int32_t* idx, int32_t* cnt);
+
+void mh3o_quant_rows_i8(uint32_t rows, uint32_t cols, int dtype, const void* w, int8_t* q, float* scale);
+
+void mh3o_gemm_w8a16_swiglu(uint32_t m, uint32_t n, uint32_t k, const uint16_t* x, const int8_t* w,
+                            const float* scale, uint16_t* out);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif

@@ -1,0 +1,200 @@
+"""TEST INFRASTRUCTURE ONLY: numpy binding of the CPU oracle (mh3_oracle.c), for tests/, the smoke check and
+bench.py's CPU-baseline leg. The product never imports this module.
+
+bf16 arrays are numpy uint16 (the raw bits). Each function mirrors one oracle entry point; see mh3_oracle.h for the
+reference file each follows and how each is pinned.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import subprocess
+from pathlib import Path
+
+import numpy as np
+
+HERE = Path(__file__).resolve().parent
+LIB_PATH = HERE / "libmh3_oracle.so"
+F32, BF16 = 0, 1
+SWIGLU_SPLIT, SWIGLU_FUSED = 0, 1
+CUBES_GRID, CUBES_GATHERED = 0, 1
+
+
+def build() -> Path:
+    subprocess.run(["make", "-s", "-C", str(HERE), "-B", "libmh3_oracle.so"], check=True)
+    return LIB_PATH
+
+
+def _load() -> C.CDLL:
+    if not LIB_PATH.exists():
+        build()
+    return C.CDLL(str(LIB_PATH))
+
+
+_lib = _load()
+_P = C.c_void_p
+_lib.mh3o_bf16_from_double.restype = C.c_uint16
+_lib.mh3o_bf16_from_double.argtypes = [C.c_double]
+_lib.mh3o_bf16_from_float.restype = C.c_uint16
+_lib.mh3o_bf16_from_float.argtypes = [C.c_float]
+_lib.mh3o_cube_count.restype = C.c_int64
+_lib.mh3o_cube_count.argtypes = [C.c_uint32] * 3
+_lib.mh3o_cube_topk_row.restype = C.c_int32
+_lib.mh3o_cube_topk_row.argtypes = [C.c_uint32] * 6 + [C.c_uint64, _P, _P]
+_lib.mh3o_rms_mod_rows.argtypes = [C.c_uint32, C.c_uint32, C.c_float, C.c_int] + [_P] * 6
+_lib.mh3o_gate_add_rows.argtypes = [C.c_uint32, C.c_uint32, C.c_int] + [_P] * 4
+_lib.mh3o_rms_mod_gate_add_rows.argtypes = [C.c_uint32, C.c_uint32, C.c_float, C.c_int] + [_P] * 8
+_lib.mh3o_swiglu_rows.argtypes = [C.c_uint32, C.c_uint32, C.c_int, C.c_int] + [_P] * 3
+_lib.mh3o_cube_pool.argtypes = [C.c_uint32] * 5 + [C.c_int, C.c_uint64, C.c_uint64, C.c_uint64] + [_P] * 5
+_lib.mh3o_cube_pool_some.argtypes = [C.c_uint32] * 4 + [C.c_int, C.c_uint64, C.c_uint64, C.c_uint64] + \
+    [_P, _P, _P, C.c_uint64, _P, _P]
+_lib.mh3o_cube_scores.argtypes = [C.c_uint32] * 3 + [_P] * 3
+_lib.mh3o_cube_topk.argtypes = [C.c_uint32] * 7 + [_P] * 3
+_lib.mh3o_quant_rows_i8.argtypes = [C.c_uint32, C.c_uint32, C.c_int] + [_P] * 3
+_lib.mh3o_gemm_w8a16_swiglu.argtypes = [C.c_uint32] * 3 + [_P] * 4
+_lib.mh3o_bf16_to_float_n.argtypes = [_P, _P, C.c_uint64]
+_lib.mh3o_bf16_from_double_n.argtypes = [_P, _P, C.c_uint64]
+
+
+def _p(a: np.ndarray | None):
+    if a is None:
+        return None
+    assert a.flags["C_CONTIGUOUS"], "oracle arrays must be C-contiguous"
+    return a.ctypes.data
+
+
+def _dtype_code(a: np.ndarray) -> int:
+    if a.dtype == np.uint16:
+        return BF16
+    if a.dtype == np.float32:
+        return F32
+    raise ValueError(f"oracle rows are float32 or bf16 bits (uint16), not {a.dtype}")
+
+
+# ---- bf16 ------------------------------------------------------------------------------------------------------------
+
+def bf16_to_f32(a: np.ndarray) -> np.ndarray:
+    a = np.ascontiguousarray(a, dtype=np.uint16)
+    out = np.empty(a.shape, np.float32)
+    _lib.mh3o_bf16_to_float_n(_p(a), _p(out), a.size)
+    return out
+
+
+def bf16_from_f64(a: np.ndarray) -> np.ndarray:
+    a = np.ascontiguousarray(a, dtype=np.float64)
+    out = np.empty(a.shape, np.uint16)
+    _lib.mh3o_bf16_from_double_n(_p(a), _p(out), a.size)
+    return out
+
+
+def bf16_from_float(f: float) -> int:
+    return int(_lib.mh3o_bf16_from_float(C.c_float(f)))
+
+
+# ---- rows ------------------------------------------------------------------------------------------------------------
+
+def rms_mod_rows(x, w, shift, scale, eps=1e-6, set_of_row=None):
+    rows, dim = x.shape
+    y = np.empty_like(x)
+    _lib.mh3o_rms_mod_rows(rows, dim, eps, _dtype_code(x), _p(x), _p(w), _p(shift), _p(scale), _p(set_of_row), _p(y))
+    return y
+
+
+def gate_add_rows(x, y, gate, set_of_row=None):
+    x = x.copy()
+    rows, dim = x.shape
+    _lib.mh3o_gate_add_rows(rows, dim, _dtype_code(x), _p(x), _p(y), _p(gate), _p(set_of_row))
+    return x
+
+
+def rms_mod_gate_add_rows(x, residual, w, shift, scale, gate, eps=1e-6, set_of_row=None):
+    rows, dim = x.shape
+    out = np.empty_like(x)
+    _lib.mh3o_rms_mod_gate_add_rows(rows, dim, eps, _dtype_code(x), _p(x), _p(residual), _p(w), _p(shift), _p(scale),
+                                    _p(gate), _p(set_of_row), _p(out))
+    return out
+
+
+def swiglu_rows(gate, up=None):
+    if up is None:
+        rows, two = gate.shape
+        dim, layout = two // 2, SWIGLU_FUSED
+    else:
+        rows, dim = gate.shape
+        layout = SWIGLU_SPLIT
+    out = np.empty((rows, dim), gate.dtype)
+    _lib.mh3o_swiglu_rows(rows, dim, layout, _dtype_code(gate), _p(gate), _p(up), _p(out))
+    return out
+
+
+# ---- cubes -----------------------------------------------------------------------------------------------------------
+
+def cube_count(gt, gh, gw) -> int:
+    return int(_lib.mh3o_cube_count(gt, gh, gw))
+
+
+def cube_pool(q, k, heads, grid, layout=CUBES_GRID, row0=0, head_stride=None, row_stride=128, head_dim=128):
+    gt, gh, gw = grid
+    C_ = cube_count(gt, gh, gw)
+    if head_stride is None:
+        rows = row0 + (C_ * 64 if layout == CUBES_GATHERED else gt * gh * gw)
+        head_stride = rows * row_stride
+    qc = np.empty((heads, C_, head_dim), np.float32)
+    kc = np.empty((heads, C_, head_dim), np.float32)
+    counts = np.empty(C_, np.int32)
+    _lib.mh3o_cube_pool(heads, head_dim, gt, gh, gw, layout, row0, head_stride, row_stride, _p(q), _p(k), _p(qc),
+                        _p(kc), _p(counts))
+    return qc, kc, counts
+
+
+def cube_pool_some(q, k, entries, grid, head_stride, layout=CUBES_GRID, row0=0, row_stride=128, head_dim=128):
+    gt, gh, gw = grid
+    entries = np.ascontiguousarray(entries, dtype=np.int64)
+    qc = np.empty((len(entries), head_dim), np.float32)
+    kc = np.empty((len(entries), head_dim), np.float32)
+    _lib.mh3o_cube_pool_some(head_dim, gt, gh, gw, layout, row0, head_stride, row_stride, _p(q), _p(k), _p(entries),
+                             len(entries), _p(qc), _p(kc))
+    return qc, kc
+
+
+def cube_scores(qc, kc):
+    heads, cubes, hd = qc.shape
+    s = np.empty((heads, cubes, cubes), np.float64)
+    _lib.mh3o_cube_scores(heads, cubes, hd, _p(np.ascontiguousarray(qc)), _p(np.ascontiguousarray(kc)), _p(s))
+    return s
+
+
+def cube_topk(s, grid, k, local, out_stride=None):
+    heads, cubes, _ = s.shape
+    out_stride = k + local if out_stride is None else out_stride
+    idx = np.empty((heads, cubes, out_stride), np.int32)
+    cnt = np.empty((heads, cubes), np.int32)
+    _lib.mh3o_cube_topk(heads, *grid, k, local, out_stride, _p(np.ascontiguousarray(s, dtype=np.float64)), _p(idx),
+                        _p(cnt))
+    return idx, cnt
+
+
+def cube_topk_row(row_scores, i, grid, k, local, out_stride=None):
+    out_stride = k + local if out_stride is None else out_stride
+    row = np.ascontiguousarray(row_scores, dtype=np.float64)
+    out = np.empty(out_stride, np.int32)
+    n = _lib.mh3o_cube_topk_row(*grid, k, local, out_stride, i, _p(row), _p(out))
+    return out, int(n)
+
+
+# ---- int8 ------------------------------------------------------------------------------------------------------------
+
+def quant_rows_i8(w):
+    rows, cols = w.shape
+    q = np.empty((rows, cols), np.int8)
+    s = np.empty(rows, np.float32)
+    _lib.mh3o_quant_rows_i8(rows, cols, _dtype_code(w), _p(w), _p(q), _p(s))
+    return q, s
+
+
+def gemm_w8a16_swiglu(x, w, scale):
+    m, k = x.shape
+    n = w.shape[0] // 2
+    out = np.empty((m, n), np.uint16)
+    _lib.mh3o_gemm_w8a16_swiglu(m, n, k, _p(np.ascontiguousarray(x)), _p(np.ascontiguousarray(w)),
+                                _p(np.ascontiguousarray(scale)), _p(out))
+    return out

@@ -1,0 +1,154 @@
+"""The C-ABI without a GPU: libmako_h3.so loads, exports every entry point include/mako_h3.h declares, parses H3's
+options as the reference does, and refuses invalid calls with the right code before launching anything (the calls
+below never reach a kernel, so they run on a machine without a GPU)."""
+import ctypes as C
+import re
+from pathlib import Path
+
+import pytest
+
+import mako_h3 as mh
+
+HEADER = Path(__file__).resolve().parent.parent / "include" / "mako_h3.h"
+
+
+def declared():
+    text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
+    return sorted(set(re.findall(r"\b(mh3_\w+)\s*\(", text)))
+
+
+def test_every_declared_symbol_is_exported():
+    names = declared()
+    assert len(names) >= 17
+    for n in names:
+        assert hasattr(mh.lib, n), f"{n} declared in mako_h3.h but not exported"
+
+
+def test_abi_version_and_strings():
+    assert mh.lib.mh3_abi_version() == 1
+    assert mh.strerror(mh.ERR_SHAPE) == "bad shape"
+    assert mh.strerror(123) == "unknown error"
+
+
+@pytest.mark.parametrize("text,mask", [("none", 0), ("all", 15), ("qkv", 1), ("out", 2), ("fc1", 4), ("fc2", 8),
+                                       ("fc1,fc2", 12), ("qkv,out,fc1,fc2", 15), ("fc2,qkv", 9)])
+def test_parse_int8_accepts(text, mask):
+    assert mh.parse_int8(text) == mask
+
+
+@pytest.mark.parametrize("text", ["", "None", "fc3", "fc1,", ",fc1", "fc1,,fc2", "all,fc1", "fc1 ", "qkv;out"])
+def test_parse_int8_refuses(text):
+    assert mh.parse_int8(text) is None
+
+
+def test_sparse_domain():
+    """src/server/video_models.cpp:117-126: ratio in [0, 1], local in {0, 1, 3}."""
+    assert mh.check_sparse(0.0, 1) and mh.check_sparse(1.0, 3) and mh.check_sparse(0.1, 0)
+    for r, l in ((-0.01, 1), (1.01, 1), (float("nan"), 1), (0.1, 2), (0.1, 4)):
+        assert not mh.check_sparse(r, l)
+
+
+def test_topk_k_and_cube_count():
+    assert mh.cube_count(32, 48, 84) == 2016
+    assert mh.cube_count(37, 24, 42) == 10 * 6 * 11          # padded to 40 x 24 x 44
+    assert mh.topk_k(0.1, 2016) == 202
+    assert mh.topk_k(1.0, 2016) == 2016 and mh.topk_k(0.0, 2016) == 0
+    assert mh.topk_k(0.5, 2016) == 1008
+    with pytest.raises(ValueError):
+        mh.topk_k(1.5, 10)
+
+
+FAKE = C.c_void_p(0x1000)        # aligned; never dereferenced: every call below fails validation first
+ODD = C.c_void_p(0x1008)
+
+
+def rows_args(**kw):
+    a = mh.RowsArgs()
+    a.rows, a.dim, a.n_sets, a.dtype, a.eps = 4, 5120, 1, mh.BF16, 1e-6
+    for k, v in kw.items():
+        setattr(a, k, v)
+    return a
+
+
+@pytest.mark.parametrize("kw,code", [({"dtype": 7}, mh.ERR_PARAM), ({"eps": 0.0}, mh.ERR_PARAM),
+                                     ({"dim": 5121}, mh.ERR_SHAPE), ({"dim": 0}, mh.ERR_SHAPE),
+                                     ({"n_sets": 0}, mh.ERR_SHAPE), ({"dim": 16384 * 8}, mh.ERR_UNSUPPORTED)])
+def test_rows_validation(kw, code):
+    a = rows_args(**kw)
+    rc = mh.lib.mh3_rms_mod_gate_add_rows(C.byref(a), FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, None, FAKE, None)
+    assert rc == code
+
+
+def test_rows_pointer_checks():
+    a = rows_args()
+    assert mh.lib.mh3_rms_mod_gate_add_rows(None, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, None, FAKE, None) == \
+        mh.ERR_POINTER
+    assert mh.lib.mh3_rms_mod_gate_add_rows(C.byref(a), None, FAKE, FAKE, FAKE, FAKE, FAKE, None, FAKE, None) == \
+        mh.ERR_POINTER
+    assert mh.lib.mh3_rms_mod_gate_add_rows(C.byref(a), ODD, FAKE, FAKE, FAKE, FAKE, FAKE, None, FAKE, None) == \
+        mh.ERR_ALIGN
+    z = rows_args(rows=0)
+    assert mh.lib.mh3_rms_mod_gate_add_rows(C.byref(z), None, None, None, None, None, None, None, None, None) == mh.OK
+    assert mh.lib.mh3_rms_mod_rows(C.byref(a), FAKE, None, None, FAKE, None, FAKE, None) == mh.ERR_POINTER
+    assert mh.lib.mh3_gate_add_rows(C.byref(rows_args(eps=0.0)), FAKE, ODD, FAKE, None, None) == mh.ERR_ALIGN
+
+
+def test_swiglu_validation():
+    a = mh.SwigluArgs()
+    a.rows, a.dim, a.layout, a.dtype = 4, 13824, mh.SWIGLU_FUSED, mh.BF16
+    assert mh.lib.mh3_swiglu_rows(C.byref(a), FAKE, FAKE, FAKE, None) == mh.ERR_PARAM     # fused takes no `up`
+    a.layout = 5
+    assert mh.lib.mh3_swiglu_rows(C.byref(a), FAKE, None, FAKE, None) == mh.ERR_PARAM
+    a.layout, a.dim = mh.SWIGLU_SPLIT, 13825
+    assert mh.lib.mh3_swiglu_rows(C.byref(a), FAKE, FAKE, FAKE, None) == mh.ERR_SHAPE
+    a.dim = 13824
+    assert mh.lib.mh3_swiglu_rows(C.byref(a), FAKE, None, FAKE, None) == mh.ERR_POINTER
+    assert mh.lib.mh3_swiglu_rows(C.byref(a), FAKE, ODD, FAKE, None) == mh.ERR_ALIGN
+    a.rows = 2**31
+    assert mh.lib.mh3_swiglu_rows(C.byref(a), FAKE, FAKE, FAKE, None) == mh.ERR_SHAPE
+
+
+def test_cube_validation():
+    a = mh.cube_args(40, (32, 48, 84), k=202, local=1)
+    bad = mh.cube_args(40, (32, 48, 84), k=202, local=2)
+    assert mh.lib.mh3_cube_select(C.byref(bad), FAKE, FAKE, FAKE, FAKE, None) == mh.ERR_PARAM
+    bad = mh.cube_args(40, (32, 48, 84), k=0, local=1)
+    assert mh.lib.mh3_cube_topk(C.byref(bad), FAKE, FAKE, FAKE, None) == mh.ERR_PARAM
+    bad = mh.cube_args(40, (32, 48, 84), k=2017, local=1)
+    assert mh.lib.mh3_cube_topk(C.byref(bad), FAKE, FAKE, FAKE, None) == mh.ERR_PARAM
+    bad = mh.cube_args(40, (32, 48, 84), k=202, local=1, out_stride=202)
+    assert mh.lib.mh3_cube_select(C.byref(bad), FAKE, FAKE, FAKE, FAKE, None) == mh.ERR_SHAPE
+    bad = mh.cube_args(40, (32, 48, 84), head_dim=64)
+    assert mh.lib.mh3_cube_pool(C.byref(bad), FAKE, FAKE, FAKE, FAKE, None, None) == mh.ERR_UNSUPPORTED
+    bad = mh.cube_args(40, (0, 48, 84))
+    assert mh.lib.mh3_cube_pool(C.byref(bad), FAKE, FAKE, FAKE, FAKE, None, None) == mh.ERR_SHAPE
+    bad = mh.cube_args(40, (32, 48, 84), row_stride=100)
+    assert mh.lib.mh3_cube_pool(C.byref(bad), FAKE, FAKE, FAKE, FAKE, None, None) == mh.ERR_ALIGN
+    assert mh.lib.mh3_cube_pool(C.byref(a), FAKE, None, FAKE, FAKE, None, None) == mh.ERR_POINTER
+    big = mh.cube_args(1, (400, 400, 400), k=10, local=1)                 # 10^6 cubes: top-k beyond 4096 cubes
+    assert mh.lib.mh3_cube_topk(C.byref(big), FAKE, FAKE, FAKE, None) == mh.ERR_UNSUPPORTED
+
+
+def test_quant_and_gemm_validation():
+    q = mh.QuantArgs()
+    q.rows, q.cols, q.dtype = 4, 100, mh.BF16
+    assert mh.lib.mh3_quant_rows_i8(C.byref(q), FAKE, FAKE, FAKE, None) == mh.ERR_SHAPE
+    q.cols, q.dtype = 128, 9
+    assert mh.lib.mh3_quant_rows_i8(C.byref(q), FAKE, FAKE, FAKE, None) == mh.ERR_PARAM
+    g = mh.GemmArgs()
+    g.m, g.n, g.k = 100, 13824, 5120
+    assert mh.lib.mh3_gemm_w8a16_swiglu(C.byref(g), FAKE, FAKE, None, FAKE, None) == mh.ERR_POINTER
+    assert mh.lib.mh3_gemm_w8a16_swiglu(C.byref(g), ODD, FAKE, FAKE, FAKE, None) == mh.ERR_ALIGN
+    g.k = 5000
+    assert mh.lib.mh3_gemm_w8a16_swiglu(C.byref(g), FAKE, FAKE, FAKE, FAKE, None) == mh.ERR_SHAPE
+    g.k, g.n = 5120, 100
+    assert mh.lib.mh3_gemm_w8a16_swiglu(C.byref(g), FAKE, FAKE, FAKE, FAKE, None) == mh.ERR_SHAPE
+    g.n, g.m = 128, 0
+    assert mh.lib.mh3_gemm_w8a16_swiglu(C.byref(g), FAKE, FAKE, FAKE, FAKE, None) == mh.ERR_SHAPE
+
+
+def test_python_wrapper_checks_sizes_before_the_library():
+    import torch
+    x = torch.zeros((4, 5120), dtype=torch.bfloat16)      # host tensor: refused before any call
+    with pytest.raises(ValueError):
+        mh.rms_mod_gate_add_rows(x, x, None, x, x, x)

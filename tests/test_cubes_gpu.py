@@ -1,0 +1,191 @@
+"""Parity of the cube selector (cube_pool, cube_scores, cube_topk, cube_select) with the CPU oracle.
+
+- Pooled means are float: 1e-5 relative (plus 1e-6 absolute, means of 64 N(0,1) values being ~0.1).
+- Scores: 1e-5 relative to the row's score scale against the oracle's float64 scores.
+- The GPU's top-k over its own float scores must equal the oracle's top-k over the same scores exactly (same ranking
+  rule, integer output); against the oracle's float64 scores the selected sets must be identical except where the
+  swapped cubes' scores tie with the k-th within 1e-3 relative.
+"""
+import math
+
+import numpy as np
+import pytest
+import torch
+
+import mako_h3 as mh
+import oracle as orc
+from helpers import assert_close, check_selection, from_bits, randn_bf16_bits, to_bits
+
+pytestmark = pytest.mark.gpu
+
+
+def make_qk(rng, heads, rows, row_stride=128):
+    q = randn_bf16_bits(rng, (heads, rows, row_stride))
+    k = randn_bf16_bits(rng, (heads, rows, row_stride))
+    return q, k
+
+
+def pooled(dev, a, q, k):
+    qc, kc = mh.cube_pool(a, from_bits(q, dev), from_bits(k, dev))
+    return qc.cpu().numpy(), kc.cpu().numpy()
+
+
+@pytest.mark.parametrize("grid", [(8, 8, 12), (5, 7, 9), (4, 4, 4), (1, 1, 1), (9, 13, 6)])
+@pytest.mark.parametrize("layout", [mh.CUBES_GRID, mh.CUBES_GATHERED])
+def test_cube_pool(dev, grid, layout):
+    rng = np.random.default_rng(sum(grid))
+    heads, row0 = 3, 5
+    cubes = mh.cube_count(*grid)
+    rows = row0 + (cubes * 64 if layout == mh.CUBES_GATHERED else grid[0] * grid[1] * grid[2]) + 3
+    q, k = make_qk(rng, heads, rows)
+    a = mh.cube_args(heads, grid, layout=layout, row0=row0, head_stride=rows * 128)
+    counts = torch.empty(cubes, dtype=torch.int32, device=dev)
+    qc, kc = mh.cube_pool(a, from_bits(q, dev), from_bits(k, dev), counts=counts)
+    wq, wk, wc = orc.cube_pool(q, k, heads, grid, layout=layout, row0=row0, head_stride=rows * 128)
+    assert_close(qc.cpu().numpy(), wq, 1e-5, 1e-6, "qc")
+    assert_close(kc.cpu().numpy(), wk, 1e-5, 1e-6, "kc")
+    assert (counts.cpu().numpy() == wc).all()
+
+
+def test_cube_pool_interleaved_heads(dev):
+    """q and k as a QKV projection leaves them: row-major [rows][heads * 128] (row_stride = heads * 128)."""
+    rng = np.random.default_rng(11)
+    heads, grid = 4, (8, 4, 8)
+    rows = grid[0] * grid[1] * grid[2]
+    q = randn_bf16_bits(rng, (rows, heads * 128))
+    k = randn_bf16_bits(rng, (rows, heads * 128))
+    a = mh.cube_args(heads, grid, head_stride=128, row_stride=heads * 128)
+    qc, kc = mh.cube_pool(a, from_bits(q, dev), from_bits(k, dev))
+    wq, wk, _ = orc.cube_pool(q, k, heads, grid, head_stride=128, row_stride=heads * 128)
+    assert_close(qc.cpu().numpy(), wq, 1e-5, 1e-6, "qc interleaved")
+    assert_close(kc.cpu().numpy(), wk, 1e-5, 1e-6, "kc interleaved")
+
+
+@pytest.mark.parametrize("cubes_grid", [(8, 8, 12), (5, 7, 9), (12, 24, 44)])
+def test_cube_scores(dev, cubes_grid):
+    rng = np.random.default_rng(3)
+    heads = 2
+    cubes = mh.cube_count(*cubes_grid)
+    qc = rng.standard_normal((heads, cubes, 128)).astype(np.float32)
+    kc = rng.standard_normal((heads, cubes, 128)).astype(np.float32)
+    a = mh.cube_args(heads, cubes_grid)
+    s = mh.cube_scores(a, torch.from_numpy(qc).to(dev), torch.from_numpy(kc).to(dev)).cpu().numpy()
+    want = orc.cube_scores(qc, kc)
+    scale = np.abs(want).max(axis=2, keepdims=True)
+    assert (np.abs(s - want) <= 1e-5 * scale).all()
+
+
+@pytest.mark.parametrize("grid", [(8, 8, 12), (5, 7, 9), (16, 16, 16)])
+@pytest.mark.parametrize("local", [0, 1, 3])
+@pytest.mark.parametrize("ratio", [0.0001, 0.1, 0.25, 0.9, 1.0])
+def test_topk_and_select_match_oracle_on_gpu_scores(dev, grid, local, ratio):
+    """The GPU's selection over its own float scores is the oracle's over the same scores, bit for bit; the fused
+    cube_select equals cube_scores + cube_topk; and against float64 scores only near-ties may differ."""
+    rng = np.random.default_rng(int(ratio * 1000) + local)
+    heads = 2
+    cubes = mh.cube_count(*grid)
+    k = mh.topk_k(ratio, cubes)
+    qc = rng.standard_normal((heads, cubes, 128)).astype(np.float32)
+    kc = rng.standard_normal((heads, cubes, 128)).astype(np.float32)
+    a = mh.cube_args(heads, grid, k=k, local=local, out_stride=k + local + 2)
+    tq, tk = torch.from_numpy(qc).to(dev), torch.from_numpy(kc).to(dev)
+    s = mh.cube_scores(a, tq, tk)
+    idx, cnt = mh.cube_topk(a, s)
+    sidx, scnt = mh.cube_select(a, tq, tk)
+    s_np = s.cpu().numpy().astype(np.float64)
+    widx, wcnt = orc.cube_topk(s_np, grid, k, local, out_stride=k + local + 2)
+    assert (cnt.cpu().numpy() == wcnt).all()
+    assert (idx.cpu().numpy() == widx).all()
+    assert (scnt.cpu().numpy() == wcnt).all()
+    assert (sidx.cpu().numpy() == widx).all()
+    s64 = orc.cube_scores(qc, kc)
+    oidx, ocnt = orc.cube_topk(s64, grid, k, local, out_stride=k + local + 2)
+    check_selection(idx.cpu().numpy(), cnt.cpu().numpy(), s64, oidx, ocnt, k)
+    if ratio == 1.0:
+        assert (cnt.cpu().numpy() == cubes).all()
+        assert (idx.cpu().numpy()[:, :, :cubes] == np.arange(cubes)).all()
+
+
+def test_select_constructed_ranking_and_ties(dev):
+    """Cube-constant q and k with an analytic answer: every query cube's pooled q is e0 and cube j's pooled k is
+    floor(j / 2) e0 / 16 (exact in bf16), so scores rise with j in equal pairs. The top k are the highest indices;
+    at an odd k the boundary pair splits and the lower index of the pair is kept."""
+    grid = (8, 8, 12)
+    cubes = mh.cube_count(*grid)
+    heads = 1
+    rows = grid[0] * grid[1] * grid[2]
+    q = np.zeros((heads, rows, 128), np.float32)
+    k = np.zeros((heads, rows, 128), np.float32)
+    t, y, x = np.meshgrid(np.arange(grid[0]), np.arange(grid[1]), np.arange(grid[2]), indexing="ij")
+    cube = ((t // 4) * (grid[1] // 4) + y // 4) * (grid[2] // 4) + x // 4
+    q[0, :, 0] = 1.0
+    k[0, :, 0] = (cube.reshape(-1) // 2) / 16.0
+    qb = torch.from_numpy(q).to(torch.bfloat16).to(dev)
+    kb = torch.from_numpy(k).to(torch.bfloat16).to(dev)
+    for kk in (1, 5, 6, 12):
+        a = mh.cube_args(heads, grid, k=kk, local=0)
+        qc, kc = mh.cube_pool(a, qb, kb)
+        idx, cnt = mh.cube_select(a, qc, kc)
+        top = cubes - 1 - np.arange(kk)               # descending score pairs (c-1, c-2), (c-3, c-4)...
+        if kk % 2:                                     # the split pair keeps its lower index
+            top[-1] = top[-1] - 1
+        want = np.sort(top)
+        assert (cnt.cpu().numpy() == kk).all()
+        assert (idx.cpu().numpy()[0] == want).all(), f"k={kk}"
+
+
+def smooth_qk(dev, heads, grid, alpha, seed):
+    """Q, K ~ N(0,1) + alpha * sum_j u_{h,j} cos(2 pi f_j . (t/T, y/Y, x/X) + phi_j): per-head random unit u,
+    low integer frequencies f_j in {0..2}^3, so cube means separate above the pooled noise."""
+    T, Y, X = grid
+    gen = torch.Generator(device=dev).manual_seed(seed)
+    rng = np.random.default_rng(seed)
+    tt = torch.arange(T, device=dev, dtype=torch.float32).view(T, 1, 1) / T
+    yy = torch.arange(Y, device=dev, dtype=torch.float32).view(1, Y, 1) / Y
+    xx = torch.arange(X, device=dev, dtype=torch.float32).view(1, 1, X) / X
+    out = []
+    for _ in range(2):
+        t = torch.empty((heads, T * Y * X, 128), dtype=torch.bfloat16, device=dev)
+        for h in range(heads):
+            acc = torch.randn((T * Y * X, 128), generator=gen, device=dev)
+            for _j in range(4):
+                f = rng.integers(0, 3, 3)
+                phi = rng.uniform(0, 2 * math.pi)
+                u = rng.standard_normal(128)
+                u = torch.from_numpy(u / np.linalg.norm(u)).float().to(dev)
+                wave = torch.cos(2 * math.pi * (f[0] * tt + f[1] * yy + f[2] * xx) + phi).reshape(-1, 1)
+                acc += alpha * wave * u
+            t[h] = acc.to(torch.bfloat16)
+        out.append(t)
+    return out
+
+
+def test_select_768p_sampled_heads(dev):
+    """Q, K bf16 [40, 129,024, 128] on the 32x48x84 grid with the smooth component (alpha 0.5), 2016 cubes, ratio 0.1
+    (k = 202), local 1. The oracle pools two whole heads (compared for every cube) and ranks 48 query cubes of each."""
+    heads, grid = 40, (32, 48, 84)
+    q, k = smooth_qk(dev, heads, grid, 0.5, seed=0)
+    cubes = mh.cube_count(*grid)
+    kk = mh.topk_k(0.1, cubes)
+    assert cubes == 2016 and kk == 202
+    a = mh.cube_args(heads, grid, k=kk, local=1)
+    qc, kc = mh.cube_pool(a, q, k)
+    idx, cnt = mh.cube_select(a, qc, kc)
+    torch.cuda.synchronize()
+    c = cnt.cpu().numpy()
+    assert ((c == kk) | (c == kk + 1)).all()
+    rng = np.random.default_rng(0)
+    for h in (0, heads - 1):
+        qh, kh = to_bits(q[h]).reshape(1, -1, 128), to_bits(k[h]).reshape(1, -1, 128)
+        wq, wk, _ = orc.cube_pool(qh, kh, 1, grid)
+        assert_close(qc[h].cpu().numpy(), wq[0], 1e-5, 1e-6, f"qc head {h}")
+        assert_close(kc[h].cpu().numpy(), wk[0], 1e-5, 1e-6, f"kc head {h}")
+        rows = np.unique(np.concatenate([[0, cubes - 1], rng.integers(0, cubes, 46)]))
+        s64 = (wq[0][rows].astype(np.float64) @ wk[0].astype(np.float64).T) / math.sqrt(128)
+        oidx = np.empty((len(rows), kk + 1), np.int32)
+        ocnt = np.empty(len(rows), np.int32)
+        for n, i in enumerate(rows):
+            oidx[n], ocnt[n] = orc.cube_topk_row(s64[n], int(i), grid, kk, 1)
+        gi = idx[h].cpu().numpy()[rows]
+        gc = c[h][rows]
+        check_selection(gi, gc, s64, oidx, ocnt, kk)

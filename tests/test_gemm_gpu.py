@@ -1,0 +1,82 @@
+"""Parity of quant_rows_i8 (bit-exact) and the W8A16 fc1 GEMM + SwiGLU epilogue (bf16 at 1e-2) with the oracle."""
+import numpy as np
+import pytest
+import torch
+
+import mako_h3 as mh
+import oracle as orc
+from helpers import assert_close, bits_to_f64, diff, from_bits, randn_bf16_bits, to_bits
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.mark.parametrize("dtype", ["bf16", "f32"])
+@pytest.mark.parametrize("rows,cols", [(1, 16), (7, 5120), (300, 208)])
+def test_quant_rows_i8_bit_exact(dev, dtype, rows, cols):
+    rng = np.random.default_rng(rows + cols)
+    if dtype == "bf16":
+        w = randn_bf16_bits(rng, (rows, cols), 0.02)
+        w[0, :] = 0                                        # an all-zero row: scale 0, q 0
+        tw = from_bits(w, dev)
+    else:
+        w = (rng.standard_normal((rows, cols)) * 0.02).astype(np.float32)
+        w[0, :] = 0
+        if rows > 1:
+            w[1, 3] = -1.0                                 # the row maximum on the negative side
+        tw = torch.from_numpy(w).to(dev)
+    q, s = mh.quant_rows_i8(tw)
+    wq, ws = orc.quant_rows_i8(w)
+    assert (s.cpu().numpy() == ws).all()
+    assert (q.cpu().numpy() == wq).all()
+
+
+def fc1_inputs(rng, m, n, k):
+    x = randn_bf16_bits(rng, (m, k))
+    w = rng.integers(-127, 128, (2 * n, k), dtype=np.int8)
+    s = rng.uniform(0.5e-3, 2e-3, 2 * n).astype(np.float32)
+    return x, w, s
+
+
+@pytest.mark.parametrize("m,n,k", [(1, 128, 64), (37, 128, 128), (256, 256, 512), (300, 384, 320), (513, 128, 5120)])
+def test_gemm_w8a16_swiglu(dev, m, n, k):
+    rng = np.random.default_rng(m + n + k)
+    x, w, s = fc1_inputs(rng, m, n, k)
+    want = orc.gemm_w8a16_swiglu(x, w, s)
+    got = mh.gemm_w8a16_swiglu(from_bits(x, dev), torch.from_numpy(w).to(dev), torch.from_numpy(s).to(dev))
+    g, wv = bits_to_f64(to_bits(got)), bits_to_f64(want)
+    assert_close(g, wv, 1e-2, 1e-4, f"fc1 {m}x{n}x{k}")
+    rel, cos = diff(g, wv, n)
+    assert rel < 3e-3 and cos > 0.9999
+
+
+def test_gemm_quantized_weights_end_to_end(dev):
+    """quant_rows_i8 on bf16 weights, then the GEMM: equals the oracle run on the oracle's own quantization."""
+    rng = np.random.default_rng(9)
+    m, n, k = 100, 256, 1024
+    x = randn_bf16_bits(rng, (m, k))
+    wf = randn_bf16_bits(rng, (2 * n, k), 0.02)
+    q, s = mh.quant_rows_i8(from_bits(wf, dev))
+    got = mh.gemm_w8a16_swiglu(from_bits(x, dev), q, s)
+    wq, ws = orc.quant_rows_i8(wf)
+    want = orc.gemm_w8a16_swiglu(x, wq, ws)
+    assert_close(bits_to_f64(to_bits(got)), bits_to_f64(want), 1e-2, 1e-6, "quantized fc1")
+
+
+def test_gemm_768p_sampled_rows(dev):
+    """X bf16 [129,536 x 5120] ~ N(0,1), W int8 [27,648 x 5120] uniform in [-127,127], per-output-channel scales
+    U(0.5e-3, 2e-3): all outputs finite; 6 rows (both ends included) against the oracle over all 13,824 columns."""
+    m, n, k = 129536, 13824, 5120
+    gen = torch.Generator(device=dev).manual_seed(2)
+    x = torch.randn((m, k), generator=gen, device=dev).to(torch.bfloat16)
+    w = torch.randint(-127, 128, (2 * n, k), generator=gen, device=dev, dtype=torch.int8)
+    s = (torch.rand(2 * n, generator=gen, device=dev) * 1.5e-3 + 0.5e-3).float()
+    out = mh.gemm_w8a16_swiglu(x, w, s)
+    torch.cuda.synchronize()
+    assert torch.isfinite(out.float()).all()
+    rows = np.array([0, 1, 255, 256, 77777, m - 1])
+    ti = torch.from_numpy(rows).to(dev)
+    want = orc.gemm_w8a16_swiglu(to_bits(x[ti]), w.cpu().numpy(), s.cpu().numpy())
+    g = bits_to_f64(to_bits(out[ti]))
+    assert_close(g, bits_to_f64(want), 1e-2, 1e-4, "fc1 768p")
+    rel, cos = diff(g, bits_to_f64(want), n)
+    assert rel < 3e-3 and cos > 0.9999
