@@ -77,6 +77,15 @@ def bench_fused(mh, dev, steps, warmup):
             HBM_PEAK_GBS, "shape": [ROWS, DIM]}
 
 
+def bench_copy(dev, steps, warmup):
+    """Calibration: a plain device-to-device copy of a 768p-sized bf16 tensor (read + write, 2.65 GB)."""
+    src = torch.empty((ROWS, DIM), dtype=torch.bfloat16, device=dev).fill_(1.0)
+    dst = torch.empty_like(src)
+    ms, _ = time_launches(lambda: dst.copy_(src), steps, warmup)
+    nbytes = ROWS * DIM * 4
+    return {"ms": ms, "bytes": nbytes, "GBs": nbytes / ms / 1e6, "frac": nbytes / ms / 1e6 / HBM_PEAK_GBS}
+
+
 def bench_rms_f32(mh, dev, steps, warmup):
     g = torch.Generator(device=dev).manual_seed(3)
     x = torch.randn((4096, 1024), generator=g, device=dev)
@@ -142,6 +151,12 @@ def bench_select(mh, dev, steps, warmup):
         mh.cube_pool(a, q, k, qc=qc, kc=kc)
         mh.cube_select(a, qc, kc, idx=idx, cnt=cnt)
     total_ms, _ = time_launches(both, steps, warmup)
+    # The unfused pair, scores through HBM: for comparison with the fused select.
+    del q, k
+    s = torch.empty((HEADS, cubes, cubes), dtype=torch.float32, device=dev)
+    scores_ms, _ = time_launches(lambda: mh.cube_scores(a, qc, kc, out=s), steps, warmup)
+    topk_ms, _ = time_launches(lambda: mh.cube_topk(a, s, idx=idx, cnt=cnt), steps, warmup)
+    del s
     pool_bytes = 2 * HEADS * rows * 128 * 2 + 2 * HEADS * cubes * 128 * 4
     sel_bytes = 2 * HEADS * cubes * 128 * 4 + HEADS * cubes * (kk + 2) * 4
     alg_bytes = 2 * HEADS * rows * 128 * 2 + HEADS * cubes * (kk + 1) * 4
@@ -152,7 +167,7 @@ def bench_select(mh, dev, steps, warmup):
             "frac": alg_bytes / total_ms / 1e6 / HBM_PEAK_GBS,
             "score_gflop": flops / 1e9, "select_TFLOPs": flops / sel_ms / 1e9,
             "select_fp32_mfma_frac": flops / sel_ms / 1e9 / FP32_MFMA_PEAK_TFLOPS,
-            "select_bytes": sel_bytes}
+            "select_bytes": sel_bytes, "unfused_scores_ms": scores_ms, "unfused_topk_ms": topk_ms}
 
 
 def bench_fc1(mh, dev, steps, warmup, compare):
@@ -206,7 +221,7 @@ def main() -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--only", default="fused,swiglu,select,fc1,rms_f32")
+    ap.add_argument("--only", default="fused,copy,swiglu,select,fc1,rms_f32")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-compare", action="store_true")
     args = ap.parse_args()
@@ -221,6 +236,9 @@ def main() -> int:
     report = {}
     if "fused" in ops:
         report["fused_rms_mod_gate_add"] = bench_fused(mh, dev, args.steps, args.warmup)
+        torch.cuda.empty_cache()
+    if "copy" in ops:
+        report["hbm_copy"] = bench_copy(dev, args.steps, args.warmup)
         torch.cuda.empty_cache()
     if "rms_f32" in ops:
         report["rms_mod_f32_4096x1024"] = bench_rms_f32(mh, dev, args.steps, args.warmup)

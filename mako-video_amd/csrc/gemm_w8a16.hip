@@ -26,7 +26,6 @@ constexpr int kGemmThreads = 256;
 constexpr uint32_t kStageChunks = 4096; // 16-byte chunks a stage: A 256 x 8, then B 256 x 8
 constexpr size_t kGemmLds = 2 * kStageChunks * 16;
 constexpr uint32_t kBandM = 4;
-constexpr int kRsrcFlags = 0x00020000; // buffer descriptor word 3 for raw 32-bit-offset access on gfx9
 
 __device__ __forceinline__ uint32_t swz(uint32_t row, uint32_t chunk) { return row * 8u + (chunk ^ (row & 7u)); }
 
@@ -127,26 +126,36 @@ __global__ __launch_bounds__(kGemmThreads) void gemm_w8a16_swiglu_kernel(
     swrite(0);
     __syncthreads();
     const uint32_t half = lane >> 5, r32 = lane & 31u;
+    // LDS chunk of this lane's operand rows: A rows wm*128 + t*32 + r32, B rows (gate) wn*64 + t*32 + r32 and
+    // (up) 128 + wn*64 + (t-2)*32 + r32; the k-chunk (ks*2 + half) is XOR-swizzled by the row.
+    auto load_frags = [&](const uint4* A, const uint4* B, uint32_t ks, bf16x8_t (&fa)[4], bf16x8_t (&fb)[4]) {
+#pragma unroll
+        for (uint32_t t = 0; t < 4; ++t) {
+            const uint32_t row = wm * 128u + t * 32u + r32;
+            fa[t] = __builtin_bit_cast(bf16x8_t, A[swz(row, ks * 2u + half)]);
+            const uint32_t brow = (t < 2 ? wn * 64u + t * 32u : kBN + wn * 64u + (t - 2u) * 32u) + r32;
+            fb[t] = __builtin_bit_cast(bf16x8_t, B[swz(brow, ks * 2u + half)]);
+        }
+    };
     for (uint32_t kt = 0; kt < KT; ++kt) {
         if (kt + 1 < KT)
             gload(kt + 1);
         const uint4* A = smem + (kt & 1u) * kStageChunks;
         const uint4* B = A + kStageChunks / 2;
+        bf16x8_t fa[2][4], fb[2][4];
+        load_frags(A, B, 0, fa[0], fb[0]);
 #pragma unroll
         for (uint32_t ks = 0; ks < kBK / 16u; ++ks) {
-            bf16x8_t af[4], bfr[4];
-#pragma unroll
-            for (uint32_t t = 0; t < 4; ++t) {
-                const uint32_t row = wm * 128u + t * 32u + r32;
-                af[t] = __builtin_bit_cast(bf16x8_t, A[swz(row, ks * 2u + half)]);
-                const uint32_t brow = (t < 2 ? wn * 64u + t * 32u : kBN + wn * 64u + (t - 2u) * 32u) + r32;
-                bfr[t] = __builtin_bit_cast(bf16x8_t, B[swz(brow, ks * 2u + half)]);
-            }
+            // The next sub-step's operands are read from LDS while this sub-step's 16 MFMAs run.
+            if (ks + 1 < kBK / 16u)
+                load_frags(A, B, ks + 1, fa[(ks + 1) & 1u], fb[(ks + 1) & 1u]);
+            __builtin_amdgcn_sched_barrier(0); // keep those reads ahead of this sub-step's MFMAs
 #pragma unroll
             for (int a = 0; a < 4; ++a)
 #pragma unroll
                 for (int b = 0; b < 4; ++b)
-                    acc[a][b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[a], bfr[b], acc[a][b], 0, 0, 0);
+                    acc[a][b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[ks & 1u][a], fb[ks & 1u][b], acc[a][b],
+                                                                         0, 0, 0);
         }
         if (kt + 1 < KT)
             swrite((kt + 1) & 1u);

@@ -61,11 +61,33 @@ __device__ __forceinline__ uint32_t wave_max_u32(uint32_t v)
     return v;
 }
 
+// Sum over each 16-lane row of the wave, through DPP (no LDS): every lane of a row ends with its row's total.
+// quad_perm [1,0,3,2] and [2,3,0,1] sum the quads, row_half_mirror pairs the quads of each half-row and row_mirror
+// the half-rows.
+__device__ __forceinline__ float row16_sum(float v)
+{
+    v += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0xB1, 0xF, 0xF, true));
+    v += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0x4E, 0xF, 0xF, true));
+    v += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0x141, 0xF, 0xF, true));
+    v += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0x140, 0xF, 0xF, true));
+    return v;
+}
+
 // Lanes below this one in a 64-bit ballot.
 __device__ __forceinline__ uint64_t lanes_below(int lane) { return (uint64_t(1) << lane) - 1; }
 
 // ---- streaming memory access -----------------------------------------------------------------------------------------
 typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+
+// Buffer descriptor word 3 for raw (stride 0) buffers with 32-bit byte offsets on gfx9: reads past num_records
+// return zero without touching memory, writes past it are dropped.
+constexpr int kRsrcFlags = 0x00020000;
+constexpr int kNonTemporal = 2; // buffer op cache policy: nt
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(const void* base, uint32_t bytes)
+{
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, int(bytes), kRsrcFlags);
+}
 
 // 16-byte loads and stores with the non-temporal hint, for data read or written once.
 __device__ __forceinline__ uint4 ld_stream(const uint4* p)

@@ -2,12 +2,14 @@
 // (`gate_add_rows`), the two fused into one HBM pass, and `swiglu_rows`. Reference semantics: the mako-common
 // kernels of these names, described in docs/architecture.md:49-52,61-66 and docs/performance.md:44.
 //
-// Design (gfx950): one wavefront owns a row at a time and keeps all of it in VGPRs (16-byte loads, 8 bf16 or 4
-// float a lane per vector), so x is read from HBM once: the sum of squares is a lane-local sum plus a 6-step
-// butterfly, and the second pass runs from registers. The per-column coefficients of a modulation set
-// (a = w (1 + scale) gate, b = shift gate) are folded once per workgroup into LDS and read from there for every row
-// the workgroup's waves stream through (a persistent grid), so the parameter vectors cost no HBM or L2 traffic per
-// row. Streaming data uses non-temporal loads and stores.
+// Design (gfx950): a workgroup owns one row at a time and streams through rows (a persistent grid). Each thread keeps
+// a fixed slice of VPT 16-byte vectors of the row (8 bf16 or 4 float each), so the row is read from HBM once and held
+// in registers; the sum of squares is a lane-local sum, a 6-step wave butterfly and one exchange of per-wave partials
+// through LDS (double-buffered by row parity: one barrier a row). The next row's loads are issued before the current
+// row is reduced and written, so every wave keeps a row's worth of loads in flight. The per-column coefficients of a
+// modulation set (a = w (1 + scale) gate, b = shift gate) are folded once per workgroup: into registers when there is
+// one set (the thread's columns never change), into an LDS table when several sets fit in 64 KiB, else recomputed
+// from the parameter vectors per row. Streaming data uses non-temporal loads and stores.
 #include "mh3_common.hpp"
 
 namespace mh3 {
@@ -26,6 +28,15 @@ struct RowVec<MH3_BF16> {
         f[0] = bf16_lo(r.x), f[1] = bf16_hi(r.x), f[2] = bf16_lo(r.y), f[3] = bf16_hi(r.y);
         f[4] = bf16_lo(r.z), f[5] = bf16_hi(r.z), f[6] = bf16_lo(r.w), f[7] = bf16_hi(r.w);
     }
+    __device__ static void unpack(const u32x4_t& r, float (&f)[8])
+    {
+        f[0] = bf16_lo(r[0]), f[1] = bf16_hi(r[0]), f[2] = bf16_lo(r[1]), f[3] = bf16_hi(r[1]);
+        f[4] = bf16_lo(r[2]), f[5] = bf16_hi(r[2]), f[6] = bf16_lo(r[3]), f[7] = bf16_hi(r[3]);
+    }
+    __device__ static u32x4_t pack4(const float (&f)[8])
+    {
+        return u32x4_t{pack_bf16(f[0], f[1]), pack_bf16(f[2], f[3]), pack_bf16(f[4], f[5]), pack_bf16(f[6], f[7])};
+    }
     __device__ static uint4 pack(const float (&f)[8])
     {
         return uint4{pack_bf16(f[0], f[1]), pack_bf16(f[2], f[3]), pack_bf16(f[4], f[5]), pack_bf16(f[6], f[7])};
@@ -40,6 +51,15 @@ struct RowVec<MH3_F32> {
         f[0] = __uint_as_float(r.x), f[1] = __uint_as_float(r.y), f[2] = __uint_as_float(r.z);
         f[3] = __uint_as_float(r.w);
     }
+    __device__ static void unpack(const u32x4_t& r, float (&f)[4])
+    {
+        f[0] = __uint_as_float(r[0]), f[1] = __uint_as_float(r[1]), f[2] = __uint_as_float(r[2]);
+        f[3] = __uint_as_float(r[3]);
+    }
+    __device__ static u32x4_t pack4(const float (&f)[4])
+    {
+        return u32x4_t{__float_as_uint(f[0]), __float_as_uint(f[1]), __float_as_uint(f[2]), __float_as_uint(f[3])};
+    }
     __device__ static uint4 pack(const float (&f)[4])
     {
         return uint4{__float_as_uint(f[0]), __float_as_uint(f[1]), __float_as_uint(f[2]), __float_as_uint(f[3])};
@@ -47,9 +67,9 @@ struct RowVec<MH3_F32> {
 };
 
 struct RowsParams {
-    const uint4* x;   // rms_mod / fused: the normed input; gate_add: the addend y
-    const uint4* res; // fused: the residual; gate_add: x (in/out)
-    uint4* out;
+    const u32x4_t* x;   // rms_mod / fused: the normed input; gate_add: the addend y
+    const u32x4_t* res; // fused: the residual; gate_add: x (in/out)
+    u32x4_t* out;
     const float* w;
     const float* shift;
     const float* scale;
@@ -57,7 +77,6 @@ struct RowsParams {
     const uint8_t* set_of_row;
     uint32_t rows, dim, nvec, n_sets;
     float eps, inv_dim;
-    int coef_in_lds;
 };
 
 // The per-column coefficients of set s: y = (x * inv) * a + b (rms_mod), out = res + (x * inv) * a + b (fused),
@@ -83,85 +102,135 @@ __device__ __forceinline__ void coef(const RowsParams& p, uint32_t s, uint32_t c
     }
 }
 
-template <int DT, int NV, int OP>
-__global__ __launch_bounds__(512) void rows_kernel(RowsParams p)
+enum CoefSrc { kCoefReg = 0, kCoefLds = 1, kCoefGlobal = 2 };
+
+template <int DT, int VPT, int OP, int SRC>
+__global__ __launch_bounds__(1024) void rows_kernel(RowsParams p)
 {
     using V = RowVec<DT>;
     constexpr int E = V::N;
-    extern __shared__ float lds[]; // a[n_sets][dim], then b[n_sets][dim]
-    const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6, waves = blockDim.x >> 6;
+    // LDS: [2][64] partial sums of squares (4 a wave: one per 16-lane row), by row parity; then, for kCoefLds,
+    // a[n_sets][dim] and b[n_sets][dim].
+    extern __shared__ float smem[];
+    float* ctab = smem + 128;
+    const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6, nparts = (blockDim.x >> 6) * 4u;
+    const uint32_t nthr = blockDim.x;
 
-    if (p.coef_in_lds) {
-        const uint32_t total = p.n_sets * p.dim;
-        for (uint32_t i = threadIdx.x; i < total; i += blockDim.x) {
+    float ca[VPT][E], cb[VPT][E];
+    if constexpr (SRC == kCoefReg) {
+#pragma unroll
+        for (int j = 0; j < VPT; ++j) {
+            const uint32_t v = tid + j * nthr;
+#pragma unroll
+            for (int e = 0; e < E; ++e) {
+                ca[j][e] = cb[j][e] = 0.0f;
+                if (v < p.nvec)
+                    coef<OP>(p, 0, v * E + e, ca[j][e], cb[j][e]);
+            }
+        }
+    }
+    const uint32_t coef_total = p.n_sets * p.dim;
+    if constexpr (SRC == kCoefLds) {
+        for (uint32_t i = tid; i < coef_total; i += nthr) {
             const uint32_t s = i / p.dim, c = i - s * p.dim;
             float a, b;
             coef<OP>(p, s, c, a, b);
-            lds[i] = a;
-            lds[total + i] = b;
+            ctab[i] = a;
+            ctab[coef_total + i] = b;
         }
         __syncthreads();
     }
-    const uint32_t coef_total = p.n_sets * p.dim;
 
-    for (uint32_t row = blockIdx.x * waves + wave; row < p.rows; row += gridDim.x * waves) {
-        const uint32_t set = p.set_of_row ? min(uint32_t(p.set_of_row[row]), p.n_sets - 1u) : 0u;
-        const uint64_t base = uint64_t(row) * p.nvec;
-        uint4 xv[NV], rv[NV];
+    // Row r's vectors of this thread, through a descriptor over the row alone: lanes past the row's last vector and
+    // rows past the last row read zero (no memory traffic), so the loads need no branches.
+    auto load = [&](uint32_t r, u32x4_t (&xv)[VPT], u32x4_t (&rv)[VPT]) {
+        const uint32_t rr = min(r, p.rows - 1u), bytes = r < p.rows ? p.nvec * 16u : 0u;
+        const __amdgpu_buffer_rsrc_t sx = buffer_rsrc(p.x + uint64_t(rr) * p.nvec, bytes);
+        const __amdgpu_buffer_rsrc_t sr = buffer_rsrc(p.res + uint64_t(rr) * p.nvec, bytes);
 #pragma unroll
-        for (int j = 0; j < NV; ++j) {
-            const uint32_t v = lane + 64u * j;
-            if (v < p.nvec) {
-                xv[j] = ld_stream(p.x + base + v);
-                if constexpr (OP != kRmsMod)
-                    rv[j] = ld_stream(p.res + base + v);
-            }
+        for (int j = 0; j < VPT; ++j) {
+            const uint32_t off = (tid + j * nthr) * 16u;
+            xv[j] = __builtin_amdgcn_raw_buffer_load_b128(sx, off, 0, kNonTemporal);
+            if constexpr (OP != kRmsMod)
+                rv[j] = __builtin_amdgcn_raw_buffer_load_b128(sr, off, 0, kNonTemporal);
         }
+    };
+    // Reduces, modulates and writes row r from registers; `parity` picks the LDS partial-sum slot.
+    auto process = [&](uint32_t r, const u32x4_t (&xv)[VPT], const u32x4_t (&rv)[VPT], uint32_t parity) {
         float inv = 1.0f;
         if constexpr (OP != kGateAdd) {
             float ss = 0.0f;
 #pragma unroll
-            for (int j = 0; j < NV; ++j) {
-                const uint32_t v = lane + 64u * j;
-                if (v < p.nvec) {
-                    float f[E];
-                    V::unpack(xv[j], f);
+            for (int j = 0; j < VPT; ++j) {
+                float f[E];
+                V::unpack(xv[j], f);
 #pragma unroll
-                    for (int e = 0; e < E; ++e)
-                        ss = fmaf(f[e], f[e], ss);
-                }
+                for (int e = 0; e < E; ++e)
+                    ss = fmaf(f[e], f[e], ss);
             }
-            ss = wave_sum(ss);
-            inv = 1.0f / sqrtf(fmaf(ss, p.inv_dim, p.eps));
+            ss = row16_sum(ss);
+            float* part = smem + parity * 64u;
+            if ((lane & 15u) == 0)
+                part[wave * 4u + (lane >> 4)] = ss;
+            __syncthreads();
+            float total = 0.0f;
+            for (uint32_t w = 0; w < nparts; ++w)
+                total += part[w];
+            inv = 1.0f / sqrtf(fmaf(total, p.inv_dim, p.eps));
         }
+        const uint32_t set = p.set_of_row ? min(uint32_t(p.set_of_row[r]), p.n_sets - 1u) : 0u;
+        // Stores past the row's last vector are dropped by the descriptor.
+        const __amdgpu_buffer_rsrc_t so = buffer_rsrc(p.out + uint64_t(r) * p.nvec, p.nvec * 16u);
 #pragma unroll
-        for (int j = 0; j < NV; ++j) {
-            const uint32_t v = lane + 64u * j;
-            if (v >= p.nvec)
-                continue;
-            float f[E], r[E], o[E];
+        for (int j = 0; j < VPT; ++j) {
+            const uint32_t v = min(tid + j * nthr, p.nvec - 1u); // clamped for the coefficient reads only
+            float f[E], rr[E], o[E];
             V::unpack(xv[j], f);
             if constexpr (OP != kRmsMod)
-                V::unpack(rv[j], r);
-            const uint32_t c0 = v * E;
+                V::unpack(rv[j], rr);
 #pragma unroll
             for (int e = 0; e < E; ++e) {
                 float a, b;
-                if (p.coef_in_lds) {
-                    a = lds[set * p.dim + c0 + e];
-                    b = lds[coef_total + set * p.dim + c0 + e];
+                if constexpr (SRC == kCoefReg) {
+                    a = ca[j][e];
+                    b = cb[j][e];
+                } else if constexpr (SRC == kCoefLds) {
+                    a = ctab[set * p.dim + v * E + e];
+                    b = ctab[coef_total + set * p.dim + v * E + e];
                 } else {
-                    coef<OP>(p, set, c0 + e, a, b);
+                    coef<OP>(p, set, v * E + e, a, b);
                 }
                 if constexpr (OP == kRmsMod)
                     o[e] = fmaf(f[e] * inv, a, b);
                 else if constexpr (OP == kFused)
-                    o[e] = r[e] + fmaf(f[e] * inv, a, b);
+                    o[e] = rr[e] + fmaf(f[e] * inv, a, b);
                 else
-                    o[e] = fmaf(a, f[e], r[e]);
+                    o[e] = fmaf(a, f[e], rr[e]);
             }
-            st_stream(p.out + base + v, V::pack(o));
+            __builtin_amdgcn_raw_buffer_store_b128(V::pack4(o), so, (tid + j * nthr) * 16u, 0, kNonTemporal);
         }
+    };
+
+    // Two register sets take turns: one row is reduced and written while the next one's loads are in flight. The
+    // loop is unrolled by two so no in-flight load is ever copied between registers (a copy would wait for it).
+    const uint32_t G = gridDim.x;
+    uint32_t row = blockIdx.x;
+    if (row >= p.rows)
+        return;
+    u32x4_t xa[VPT], ra[VPT], xb[VPT], rb[VPT];
+    load(row, xa, ra);
+    while (true) {
+        const uint32_t r1 = row + G;
+        load(r1, xb, rb);
+        process(row, xa, ra, 0u);
+        if (r1 >= p.rows)
+            break;
+        const uint32_t r2 = r1 + G;
+        load(r2, xa, ra);
+        process(r1, xb, rb, 1u);
+        if (r2 >= p.rows)
+            break;
+        row = r2;
     }
 }
 
@@ -234,40 +303,44 @@ namespace {
 
 using namespace mh3;
 
-constexpr int kRowsBlock = 512;
 constexpr size_t kCoefLdsMax = 64 * 1024;
+
+template <int DT, int VPT, int OP>
+const void* pick_rows_kernel(int src)
+{
+    if (src == kCoefReg)
+        return reinterpret_cast<const void*>(&rows_kernel<DT, VPT, OP, kCoefReg>);
+    if (src == kCoefLds)
+        return reinterpret_cast<const void*>(&rows_kernel<DT, VPT, OP, kCoefLds>);
+    return reinterpret_cast<const void*>(&rows_kernel<DT, VPT, OP, kCoefGlobal>);
+}
 
 template <int DT, int OP>
 int launch_rows_dt(const RowsParams& p, hipStream_t stream)
 {
-    const uint32_t need = (p.nvec + 63u) / 64u;
+    // Threads a row: enough for VPT vectors each, rounded up to whole waves.
+    const int src = p.n_sets == 1 ? kCoefReg
+                    : (size_t(p.n_sets) * p.dim * 2 * sizeof(float) <= kCoefLdsMax ? kCoefLds : kCoefGlobal);
     const void* k = nullptr;
-    if (need <= 1)
-        k = reinterpret_cast<const void*>(&rows_kernel<DT, 1, OP>);
-    else if (need <= 2)
-        k = reinterpret_cast<const void*>(&rows_kernel<DT, 2, OP>);
-    else if (need <= 4)
-        k = reinterpret_cast<const void*>(&rows_kernel<DT, 4, OP>);
-    else if (need <= 8)
-        k = reinterpret_cast<const void*>(&rows_kernel<DT, 8, OP>);
-    else if (need <= 10)
-        k = reinterpret_cast<const void*>(&rows_kernel<DT, 10, OP>);
-    else if (need <= 12)
-        k = reinterpret_cast<const void*>(&rows_kernel<DT, 12, OP>);
-    else if (need <= 16)
-        k = reinterpret_cast<const void*>(&rows_kernel<DT, 16, OP>);
-    else
+    uint32_t threads = 0;
+    if ((p.nvec + 1) / 2 <= 1024) {
+        threads = ((p.nvec + 1) / 2 + 63) / 64 * 64;
+        k = pick_rows_kernel<DT, 2, OP>(src);
+    } else if ((p.nvec + 3) / 4 <= 1024) {
+        threads = ((p.nvec + 3) / 4 + 63) / 64 * 64;
+        k = pick_rows_kernel<DT, 4, OP>(src);
+    } else {
         return MH3_ERR_UNSUPPORTED;
-    const size_t lds = p.coef_in_lds ? size_t(p.n_sets) * p.dim * 2 * sizeof(float) : 0;
-    const int per_cu = host::blocks_per_cu(k, kRowsBlock, lds);
-    const uint64_t waves = kRowsBlock / 64;
-    uint64_t blocks = (p.rows + waves - 1) / waves;
+    }
+    const size_t lds = 128 * sizeof(float) + (src == kCoefLds ? size_t(p.n_sets) * p.dim * 2 * sizeof(float) : 0);
+    const int per_cu = host::blocks_per_cu(k, int(threads), lds);
+    uint64_t blocks = p.rows;
     const uint64_t cap = uint64_t(host::cu_count()) * per_cu;
     if (blocks > cap)
         blocks = cap;
     RowsParams arg = p;
     void* args[] = {&arg};
-    if (hipLaunchKernel(k, dim3(uint32_t(blocks)), dim3(kRowsBlock), args, lds, stream) != hipSuccess)
+    if (hipLaunchKernel(k, dim3(uint32_t(blocks)), dim3(threads), args, lds, stream) != hipSuccess)
         return host::check_launch() == MH3_OK ? MH3_ERR_HIP : MH3_ERR_HIP;
     return host::check_launch();
 }
@@ -282,7 +355,6 @@ int launch_rows(const MH3RowsArgs* a, RowsParams p, hipStream_t stream)
     p.n_sets = a->n_sets;
     p.eps = a->eps;
     p.inv_dim = 1.0f / float(a->dim);
-    p.coef_in_lds = size_t(a->n_sets) * a->dim * 2 * sizeof(float) <= kCoefLdsMax;
     return a->dtype == MH3_BF16 ? launch_rows_dt<MH3_BF16, OP>(p, stream) : launch_rows_dt<MH3_F32, OP>(p, stream);
 }
 
@@ -298,7 +370,7 @@ int check_rows(const MH3RowsArgs* a, bool needs_eps)
     const uint32_t e = a->dtype == MH3_BF16 ? 8u : 4u;
     if (a->dim == 0 || a->dim % e != 0 || a->n_sets == 0 || a->n_sets > 256)
         return MH3_ERR_SHAPE;
-    if (a->dim / e > 16u * 64u)
+    if (a->dim / e > 4096u)
         return MH3_ERR_UNSUPPORTED;
     if (a->rows >= (1u << 31))
         return MH3_ERR_SHAPE;
@@ -322,8 +394,8 @@ int mh3_rms_mod_rows(const MH3RowsArgs* args, const void* x, const float* w, con
     if (!host::aligned16(x) || !host::aligned16(y))
         return MH3_ERR_ALIGN;
     RowsParams p{};
-    p.x = static_cast<const uint4*>(x);
-    p.out = static_cast<uint4*>(y);
+    p.x = static_cast<const u32x4_t*>(x);
+    p.out = static_cast<u32x4_t*>(y);
     p.w = w;
     p.shift = shift;
     p.scale = scale;
@@ -344,9 +416,9 @@ int mh3_gate_add_rows(const MH3RowsArgs* args, void* x, const void* y, const flo
     if (!host::aligned16(x) || !host::aligned16(y))
         return MH3_ERR_ALIGN;
     RowsParams p{};
-    p.x = static_cast<const uint4*>(y);
-    p.res = static_cast<const uint4*>(x);
-    p.out = static_cast<uint4*>(x);
+    p.x = static_cast<const u32x4_t*>(y);
+    p.res = static_cast<const u32x4_t*>(x);
+    p.out = static_cast<u32x4_t*>(x);
     p.gate = gate;
     p.set_of_row = set_of_row;
     return launch_rows<kGateAdd>(args, p, static_cast<hipStream_t>(stream));
@@ -366,9 +438,9 @@ int mh3_rms_mod_gate_add_rows(const MH3RowsArgs* args, const void* x, const void
     if (!host::aligned16(x) || !host::aligned16(residual) || !host::aligned16(out))
         return MH3_ERR_ALIGN;
     RowsParams p{};
-    p.x = static_cast<const uint4*>(x);
-    p.res = static_cast<const uint4*>(residual);
-    p.out = static_cast<uint4*>(out);
+    p.x = static_cast<const u32x4_t*>(x);
+    p.res = static_cast<const u32x4_t*>(residual);
+    p.out = static_cast<u32x4_t*>(out);
     p.w = w;
     p.shift = shift;
     p.scale = scale;
