@@ -33,6 +33,16 @@ struct RowVec<MH3_BF16> {
         f[0] = bf16_lo(r[0]), f[1] = bf16_hi(r[0]), f[2] = bf16_lo(r[1]), f[3] = bf16_hi(r[1]);
         f[4] = bf16_lo(r[2]), f[5] = bf16_hi(r[2]), f[6] = bf16_lo(r[3]), f[7] = bf16_hi(r[3]);
     }
+    // acc + the sum of squares of the 8 elements.
+    __device__ static float sumsq(const u32x4_t& r, float acc)
+    {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            acc = fmaf(bf16_lo(r[i]), bf16_lo(r[i]), acc);
+            acc = fmaf(bf16_hi(r[i]), bf16_hi(r[i]), acc);
+        }
+        return acc;
+    }
     __device__ static u32x4_t pack4(const float (&f)[8])
     {
         return u32x4_t{pack_bf16(f[0], f[1]), pack_bf16(f[2], f[3]), pack_bf16(f[4], f[5]), pack_bf16(f[6], f[7])};
@@ -56,6 +66,13 @@ struct RowVec<MH3_F32> {
         f[0] = __uint_as_float(r[0]), f[1] = __uint_as_float(r[1]), f[2] = __uint_as_float(r[2]);
         f[3] = __uint_as_float(r[3]);
     }
+    __device__ static float sumsq(const u32x4_t& r, float acc)
+    {
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+            acc = fmaf(__uint_as_float(r[i]), __uint_as_float(r[i]), acc);
+        return acc;
+    }
     __device__ static u32x4_t pack4(const float (&f)[4])
     {
         return u32x4_t{__float_as_uint(f[0]), __float_as_uint(f[1]), __float_as_uint(f[2]), __float_as_uint(f[3])};
@@ -77,32 +94,54 @@ struct RowsParams {
     const uint8_t* set_of_row;
     uint32_t rows, dim, nvec, n_sets;
     float eps, inv_dim;
+    uint32_t rows_per_wave; // wave kernel: 0 = persistent grid
 };
 
+enum CoefSrc { kCoefReg = 0, kCoefLds = 1, kCoefGlobal = 2 };
+
 // The per-column coefficients of set s: y = (x * inv) * a + b (rms_mod), out = res + (x * inv) * a + b (fused),
-// out = res + a * y (gate_add).
-template <int OP>
-__device__ __forceinline__ void coef(const RowsParams& p, uint32_t s, uint32_t c, float& a, float& b)
+// out = res + a * y (gate_add), for the E columns c0 .. c0 + E - 1 (c0 a multiple of 4), through 16-byte loads.
+template <int OP, int E>
+__device__ __forceinline__ void coef_vec(const RowsParams& p, uint32_t s, uint32_t c0, float (&a)[E], float (&b)[E])
 {
-    const uint64_t i = uint64_t(s) * p.dim + c;
-    if constexpr (OP == kGateAdd) {
-        a = p.gate[i];
-        b = 0.0f;
-    } else {
-        const float w = p.w ? p.w[c] : 1.0f;
-        const float m = w * (1.0f + p.scale[i]);
-        if constexpr (OP == kFused) {
-            const float g = p.gate[i];
-            a = m * g;
-            b = p.shift[i] * g;
-        } else {
-            a = m;
-            b = p.shift[i];
+    const uint64_t i = uint64_t(s) * p.dim + c0;
+#pragma unroll
+    for (int q = 0; q < E / 4; ++q) {
+        float g[4], w[4], sc[4], sh[4];
+        if constexpr (OP != kRmsMod) {
+            const float4 t = *reinterpret_cast<const float4*>(p.gate + i + 4 * q);
+            g[0] = t.x, g[1] = t.y, g[2] = t.z, g[3] = t.w;
+        }
+        if constexpr (OP != kGateAdd) {
+            const float4 ts = *reinterpret_cast<const float4*>(p.scale + i + 4 * q);
+            const float4 th = *reinterpret_cast<const float4*>(p.shift + i + 4 * q);
+            sc[0] = ts.x, sc[1] = ts.y, sc[2] = ts.z, sc[3] = ts.w;
+            sh[0] = th.x, sh[1] = th.y, sh[2] = th.z, sh[3] = th.w;
+            if (p.w) {
+                const float4 tw = *reinterpret_cast<const float4*>(p.w + c0 + 4 * q);
+                w[0] = tw.x, w[1] = tw.y, w[2] = tw.z, w[3] = tw.w;
+            } else {
+                w[0] = w[1] = w[2] = w[3] = 1.0f;
+            }
+        }
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            if constexpr (OP == kGateAdd) {
+                a[4 * q + e] = g[e];
+                b[4 * q + e] = 0.0f;
+            } else {
+                const float m = w[e] * (1.0f + sc[e]);
+                if constexpr (OP == kFused) {
+                    a[4 * q + e] = m * g[e];
+                    b[4 * q + e] = sh[e] * g[e];
+                } else {
+                    a[4 * q + e] = m;
+                    b[4 * q + e] = sh[e];
+                }
+            }
         }
     }
 }
-
-enum CoefSrc { kCoefReg = 0, kCoefLds = 1, kCoefGlobal = 2 };
 
 template <int DT, int VPT, int OP, int SRC>
 __global__ __launch_bounds__(1024) void rows_kernel(RowsParams p)
@@ -119,24 +158,20 @@ __global__ __launch_bounds__(1024) void rows_kernel(RowsParams p)
     float ca[VPT][E], cb[VPT][E];
     if constexpr (SRC == kCoefReg) {
 #pragma unroll
-        for (int j = 0; j < VPT; ++j) {
-            const uint32_t v = tid + j * nthr;
-#pragma unroll
-            for (int e = 0; e < E; ++e) {
-                ca[j][e] = cb[j][e] = 0.0f;
-                if (v < p.nvec)
-                    coef<OP>(p, 0, v * E + e, ca[j][e], cb[j][e]);
-            }
-        }
+        for (int j = 0; j < VPT; ++j)
+            coef_vec<OP, E>(p, 0, min(tid + j * nthr, p.nvec - 1u) * E, ca[j], cb[j]);
     }
     const uint32_t coef_total = p.n_sets * p.dim;
     if constexpr (SRC == kCoefLds) {
-        for (uint32_t i = tid; i < coef_total; i += nthr) {
-            const uint32_t s = i / p.dim, c = i - s * p.dim;
-            float a, b;
-            coef<OP>(p, s, c, a, b);
-            ctab[i] = a;
-            ctab[coef_total + i] = b;
+        for (uint32_t i = tid; i < p.n_sets * p.nvec; i += nthr) {
+            const uint32_t s = i / p.nvec, v = i - s * p.nvec;
+            float a[E], b[E];
+            coef_vec<OP, E>(p, s, v * E, a, b);
+#pragma unroll
+            for (int e = 0; e < E; ++e) {
+                ctab[s * p.dim + v * E + e] = a[e];
+                ctab[coef_total + s * p.dim + v * E + e] = b[e];
+            }
         }
         __syncthreads();
     }
@@ -161,13 +196,8 @@ __global__ __launch_bounds__(1024) void rows_kernel(RowsParams p)
         if constexpr (OP != kGateAdd) {
             float ss = 0.0f;
 #pragma unroll
-            for (int j = 0; j < VPT; ++j) {
-                float f[E];
-                V::unpack(xv[j], f);
-#pragma unroll
-                for (int e = 0; e < E; ++e)
-                    ss = fmaf(f[e], f[e], ss);
-            }
+            for (int j = 0; j < VPT; ++j)
+                ss = V::sumsq(xv[j], ss);
             ss = row16_sum(ss);
             float* part = smem + parity * 64u;
             if ((lane & 15u) == 0)
@@ -188,6 +218,9 @@ __global__ __launch_bounds__(1024) void rows_kernel(RowsParams p)
             V::unpack(xv[j], f);
             if constexpr (OP != kRmsMod)
                 V::unpack(rv[j], rr);
+            float ga[E], gb[E];
+            if constexpr (SRC == kCoefGlobal)
+                coef_vec<OP, E>(p, set, v * E, ga, gb);
 #pragma unroll
             for (int e = 0; e < E; ++e) {
                 float a, b;
@@ -198,7 +231,8 @@ __global__ __launch_bounds__(1024) void rows_kernel(RowsParams p)
                     a = ctab[set * p.dim + v * E + e];
                     b = ctab[coef_total + set * p.dim + v * E + e];
                 } else {
-                    coef<OP>(p, set, v * E + e, a, b);
+                    a = ga[e];
+                    b = gb[e];
                 }
                 if constexpr (OP == kRmsMod)
                     o[e] = fmaf(f[e] * inv, a, b);
@@ -231,6 +265,113 @@ __global__ __launch_bounds__(1024) void rows_kernel(RowsParams p)
         if (r2 >= p.rows)
             break;
         row = r2;
+    }
+}
+
+// One wavefront per row (no cross-wave reduction, so no barrier a row). The workgroup folds the coefficient table
+// of every set into LDS once; each wave holds a whole row (NV 16-byte vectors a lane of x, and of the residual) in
+// registers, reduces it with DPP and three cross-row reads, and streams the outputs one vector at a time, reading
+// that vector's coefficients from LDS just before use.
+#ifndef MH3_WAVE_BLOCK
+#define MH3_WAVE_BLOCK 512 // threads of a wave-kernel workgroup
+#endif
+
+template <int DT, int NV, int OP, int SRC>
+__global__ __launch_bounds__(MH3_WAVE_BLOCK) void rows_wave_kernel(RowsParams p)
+{
+    using V = RowVec<DT>;
+    constexpr int E = V::N;
+    extern __shared__ float ctab[]; // a[n_sets][dim], then b[n_sets][dim]
+    const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
+    // Rows: with rows_per_wave = 0 the grid is persistent and strides over all rows; otherwise workgroup b takes the
+    // contiguous rows [b * waves * rows_per_wave, ...), its waves interleaved over them so they read neighbours.
+    const uint32_t waves = blockDim.x >> 6;
+    const uint32_t first = p.rows_per_wave ? blockIdx.x * waves * p.rows_per_wave + wave : blockIdx.x * waves + wave;
+    const uint32_t step = p.rows_per_wave ? waves : gridDim.x * waves;
+    const uint32_t last = p.rows_per_wave ? min(p.rows, (blockIdx.x + 1) * waves * p.rows_per_wave) : p.rows;
+    // A row's loads go through a descriptor over that row alone; a row past `last` reads zero without traffic.
+    u32x4_t xv[NV], rv[NV];
+    auto load = [&](uint32_t row) {
+        const uint32_t bytes = row < last ? p.nvec * 16u : 0u;
+        const uint32_t rr = min(row, p.rows - 1u);
+        const __amdgpu_buffer_rsrc_t sx = buffer_rsrc(p.x + uint64_t(rr) * p.nvec, bytes);
+        const __amdgpu_buffer_rsrc_t sr = buffer_rsrc(p.res + uint64_t(rr) * p.nvec, bytes);
+#pragma unroll
+        for (int j = 0; j < NV; ++j) {
+            xv[j] = __builtin_amdgcn_raw_buffer_load_b128(sx, (lane + 64u * j) * 16u, 0, kNonTemporal);
+            if constexpr (OP != kRmsMod)
+                rv[j] = __builtin_amdgcn_raw_buffer_load_b128(sr, (lane + 64u * j) * 16u, 0, kNonTemporal);
+        }
+    };
+    const uint32_t coef_total = p.n_sets * p.dim;
+    for (uint32_t i = tid; SRC == kCoefLds && i < p.n_sets * p.nvec; i += blockDim.x) {
+        const uint32_t s = i / p.nvec, v = i - s * p.nvec;
+        float a[E], b[E];
+        coef_vec<OP, E>(p, s, v * E, a, b);
+#pragma unroll
+        for (int e = 0; e < E; ++e) {
+            ctab[s * p.dim + v * E + e] = a[e];
+            ctab[coef_total + s * p.dim + v * E + e] = b[e];
+        }
+    }
+    if constexpr (SRC == kCoefLds)
+        __syncthreads();
+
+    // (Issuing the first row's loads before the table is built is slower: the table's parameter loads would then
+    // complete in order behind them.)
+    for (uint32_t row = first; row < last; row += step) {
+        load(row);
+        const __amdgpu_buffer_rsrc_t so = buffer_rsrc(p.out + uint64_t(row) * p.nvec, p.nvec * 16u);
+        float inv = 1.0f;
+        if constexpr (OP != kGateAdd) {
+            float ss = 0.0f;
+#pragma unroll
+            for (int j = 0; j < NV; ++j)
+                ss = V::sumsq(xv[j], ss);
+            ss = row16_sum(ss);
+            // The output pass unpacks x again rather than keeping the sum pass's unpacked values live.
+#pragma unroll
+            for (int j = 0; j < NV; ++j)
+                asm volatile("" : "+v"(xv[j]));
+            const float total = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(ss), 0)) +
+                                __int_as_float(__builtin_amdgcn_readlane(__float_as_int(ss), 16)) +
+                                __int_as_float(__builtin_amdgcn_readlane(__float_as_int(ss), 32)) +
+                                __int_as_float(__builtin_amdgcn_readlane(__float_as_int(ss), 48));
+            inv = 1.0f / sqrtf(fmaf(total, p.inv_dim, p.eps));
+        }
+        const uint32_t set = p.set_of_row ? min(uint32_t(p.set_of_row[row]), p.n_sets - 1u) : 0u;
+        const float* ta = ctab + set * p.dim;
+        const float* tb = ctab + coef_total + set * p.dim;
+#pragma unroll
+        for (int j = 0; j < NV; ++j) {
+            const uint32_t v = min(lane + 64u * j, p.nvec - 1u);
+            float f[E], rr[E], o[E], a[E], b[E];
+            if constexpr (SRC == kCoefLds) {
+#pragma unroll
+                for (int q = 0; q < E / 4; ++q) {
+                    const float4 ta4 = *reinterpret_cast<const float4*>(ta + v * E + 4 * q);
+                    const float4 tb4 = *reinterpret_cast<const float4*>(tb + v * E + 4 * q);
+                    a[4 * q] = ta4.x, a[4 * q + 1] = ta4.y, a[4 * q + 2] = ta4.z, a[4 * q + 3] = ta4.w;
+                    b[4 * q] = tb4.x, b[4 * q + 1] = tb4.y, b[4 * q + 2] = tb4.z, b[4 * q + 3] = tb4.w;
+                }
+            } else {
+                coef_vec<OP, E>(p, set, v * E, a, b);
+            }
+            V::unpack(xv[j], f);
+            if constexpr (OP != kRmsMod)
+                V::unpack(rv[j], rr);
+#pragma unroll
+            for (int e = 0; e < E; ++e) {
+                if constexpr (OP == kRmsMod)
+                    o[e] = fmaf(f[e] * inv, a[e], b[e]);
+                else if constexpr (OP == kFused)
+                    o[e] = rr[e] + fmaf(f[e] * inv, a[e], b[e]);
+                else
+                    o[e] = fmaf(a[e], f[e], rr[e]);
+            }
+            __builtin_amdgcn_raw_buffer_store_b128(V::pack4(o), so, (lane + 64u * j) * 16u, 0, kNonTemporal);
+            __builtin_amdgcn_sched_barrier(0); // one vector's coefficients live at a time
+        }
     }
 }
 
@@ -304,6 +445,12 @@ namespace {
 using namespace mh3;
 
 constexpr size_t kCoefLdsMax = 64 * 1024;
+#ifndef MH3_ROWS_PER_BLOCK
+#define MH3_ROWS_PER_BLOCK 0 // rows a workgroup streams through; 0: as many as keep every CU's slots busy once
+#endif
+#ifndef MH3_SWIGLU_U
+#define MH3_SWIGLU_U 1 // 16-byte vectors of gate (and of up) a thread has in flight
+#endif
 
 template <int DT, int VPT, int OP>
 const void* pick_rows_kernel(int src)
@@ -315,9 +462,68 @@ const void* pick_rows_kernel(int src)
     return reinterpret_cast<const void*>(&rows_kernel<DT, VPT, OP, kCoefGlobal>);
 }
 
+#ifndef MH3_WAVE_ROWS
+#define MH3_WAVE_ROWS 1 // rows each wavefront of the wave kernel takes; 0: a persistent grid
+#endif
+#ifndef MH3_ROWS_WAVE
+#define MH3_ROWS_WAVE 1 // one wavefront a row when the row fits 12 vectors a lane and the coefficients fit in LDS
+#endif
+
+#ifndef MH3_WAVE_SRC
+#define MH3_WAVE_SRC 1 // the wave kernel's coefficients: 1 an LDS table a workgroup builds, 2 the parameter vectors
+#endif
+
+template <int DT, int NV, int OP>
+const void* pick_wave_kernel(int src)
+{
+    if (src == kCoefLds)
+        return reinterpret_cast<const void*>(&rows_wave_kernel<DT, NV, OP, kCoefLds>);
+    return reinterpret_cast<const void*>(&rows_wave_kernel<DT, NV, OP, kCoefGlobal>);
+}
+
+template <int DT, int OP>
+int launch_rows_wave(const RowsParams& p, hipStream_t stream)
+{
+    const uint32_t need = (p.nvec + 63u) / 64u;
+    const int src = MH3_WAVE_SRC;
+    const void* k = nullptr;
+    if (need <= 2)
+        k = pick_wave_kernel<DT, 2, OP>(src);
+    else if (need <= 4)
+        k = pick_wave_kernel<DT, 4, OP>(src);
+    else if (need <= 8)
+        k = pick_wave_kernel<DT, 8, OP>(src);
+    else if (need <= 10)
+        k = pick_wave_kernel<DT, 10, OP>(src);
+    else
+        k = pick_wave_kernel<DT, 12, OP>(src);
+    const uint32_t threads = MH3_WAVE_BLOCK, waves = threads / 64u;
+    const size_t lds = src == kCoefLds ? size_t(p.n_sets) * p.dim * 2 * sizeof(float) : 0;
+    RowsParams arg = p;
+    uint64_t blocks;
+    constexpr uint32_t kWaveRows = MH3_WAVE_ROWS;
+    if constexpr (kWaveRows > 0) {
+        arg.rows_per_wave = kWaveRows;
+        blocks = (uint64_t(p.rows) + waves * kWaveRows - 1) / (waves * (kWaveRows > 0 ? kWaveRows : 1));
+    } else {
+        arg.rows_per_wave = 0;
+        const int per_cu = host::blocks_per_cu(k, int(threads), lds);
+        blocks = (p.rows + waves - 1) / waves;
+        const uint64_t cap = uint64_t(host::cu_count()) * per_cu;
+        if (blocks > cap)
+            blocks = cap;
+    }
+    void* args[] = {&arg};
+    if (hipLaunchKernel(k, dim3(uint32_t(blocks)), dim3(threads), args, lds, stream) != hipSuccess)
+        return host::check_launch() == MH3_OK ? MH3_ERR_HIP : MH3_ERR_HIP;
+    return host::check_launch();
+}
+
 template <int DT, int OP>
 int launch_rows_dt(const RowsParams& p, hipStream_t stream)
 {
+    if (MH3_ROWS_WAVE && p.nvec <= 12u * 64u && size_t(p.n_sets) * p.dim * 2 * sizeof(float) <= kCoefLdsMax)
+        return launch_rows_wave<DT, OP>(p, stream);
     // Threads a row: enough for VPT vectors each, rounded up to whole waves.
     const int src = p.n_sets == 1 ? kCoefReg
                     : (size_t(p.n_sets) * p.dim * 2 * sizeof(float) <= kCoefLdsMax ? kCoefLds : kCoefGlobal);
@@ -335,9 +541,14 @@ int launch_rows_dt(const RowsParams& p, hipStream_t stream)
     const size_t lds = 128 * sizeof(float) + (src == kCoefLds ? size_t(p.n_sets) * p.dim * 2 * sizeof(float) : 0);
     const int per_cu = host::blocks_per_cu(k, int(threads), lds);
     uint64_t blocks = p.rows;
-    const uint64_t cap = uint64_t(host::cu_count()) * per_cu;
-    if (blocks > cap)
-        blocks = cap;
+    constexpr uint32_t kRowsPerBlock = MH3_ROWS_PER_BLOCK;
+    if constexpr (kRowsPerBlock > 0) {
+        blocks = (p.rows + kRowsPerBlock - 1) / (kRowsPerBlock > 0 ? kRowsPerBlock : 1);
+    } else {
+        const uint64_t cap = uint64_t(host::cu_count()) * per_cu;
+        if (blocks > cap)
+            blocks = cap;
+    }
     RowsParams arg = p;
     void* args[] = {&arg};
     if (hipLaunchKernel(k, dim3(uint32_t(blocks)), dim3(threads), args, lds, stream) != hipSuccess)
@@ -391,7 +602,8 @@ int mh3_rms_mod_rows(const MH3RowsArgs* args, const void* x, const float* w, con
         return MH3_OK;
     if (!x || !shift || !scale || !y)
         return MH3_ERR_POINTER;
-    if (!host::aligned16(x) || !host::aligned16(y))
+    if (!host::aligned16(x) || !host::aligned16(y) || !host::aligned16(w) || !host::aligned16(shift) ||
+        !host::aligned16(scale))
         return MH3_ERR_ALIGN;
     RowsParams p{};
     p.x = static_cast<const u32x4_t*>(x);
@@ -413,7 +625,7 @@ int mh3_gate_add_rows(const MH3RowsArgs* args, void* x, const void* y, const flo
         return MH3_OK;
     if (!x || !y || !gate)
         return MH3_ERR_POINTER;
-    if (!host::aligned16(x) || !host::aligned16(y))
+    if (!host::aligned16(x) || !host::aligned16(y) || !host::aligned16(gate))
         return MH3_ERR_ALIGN;
     RowsParams p{};
     p.x = static_cast<const u32x4_t*>(y);
@@ -435,7 +647,8 @@ int mh3_rms_mod_gate_add_rows(const MH3RowsArgs* args, const void* x, const void
         return MH3_OK;
     if (!x || !residual || !shift || !scale || !gate || !out)
         return MH3_ERR_POINTER;
-    if (!host::aligned16(x) || !host::aligned16(residual) || !host::aligned16(out))
+    if (!host::aligned16(x) || !host::aligned16(residual) || !host::aligned16(out) || !host::aligned16(w) ||
+        !host::aligned16(shift) || !host::aligned16(scale) || !host::aligned16(gate))
         return MH3_ERR_ALIGN;
     RowsParams p{};
     p.x = static_cast<const u32x4_t*>(x);
@@ -475,7 +688,7 @@ int mh3_swiglu_rows(const MH3SwigluArgs* a, const void* gate, const void* up, vo
     const uint4* u = a->layout == MH3_SWIGLU_FUSED ? g + vpr : static_cast<const uint4*>(up);
     const uint32_t stride = a->layout == MH3_SWIGLU_FUSED ? 2u * vpr : vpr;
     const uint32_t total = a->rows * vpr;
-    constexpr int U = 4;
+    constexpr int U = MH3_SWIGLU_U;
     const uint32_t blocks = (total + 256u * U - 1) / (256u * U);
     const FastDiv div = FastDiv::make(vpr);
     hipStream_t s = static_cast<hipStream_t>(stream);
