@@ -3,15 +3,17 @@
 // docs/architecture.md:65: fc1's [gate; value] rows, then SwiGLU).
 //
 // Design (gfx950, v_mfma_f32_32x32x16_bf16):
-// - A workgroup of 4 wavefronts computes a 256-row x 128-column output tile, i.e. the 128 gate columns [n0, n0+128)
-//   and the 128 up columns [n + n0, n + n0 + 128) of y, so the SwiGLU epilogue has both halves in registers. Each
-//   wave owns 128 rows x (64 gate + 64 up) columns: 4 x 4 MFMA tiles of 32 x 32, 256 float accumulators.
-// - K advances 64 at a time through two LDS stages (A 256x64 bf16 and B 256x64 bf16 = 64 KiB a stage). The int8
-//   weights are loaded as 16-byte vectors and widened to bf16 on the way into LDS (exact: |w| <= 127 fits bf16's
-//   8-bit significand), so the dequantization costs no extra HBM or LDS traffic and the scale is applied once to the
-//   float accumulator in the epilogue: x (W diag s) = (x W) diag s.
-// - LDS rows are 128 bytes; the 16-byte chunk c of row r is stored at chunk c ^ (r & 7), so the MFMA operand reads
-//   (32 rows at one chunk per half-wave) hit distinct banks.
+// - A workgroup of 8 wavefronts (2 along rows x 4 along columns) computes a 256-row x 128-column output tile, i.e.
+//   the 128 gate columns [n0, n0+128) and the 128 up columns [n + n0, n + n0 + 128) of y, so the SwiGLU epilogue has
+//   both halves in registers. Each wave owns 128 rows x (32 gate + 32 up) columns: 4 x 2 MFMA tiles of 32 x 32.
+// - K advances 64 at a time. A (x, bf16) streams from HBM straight into a 3-stage LDS ring with buffer loads that
+//   write LDS (no VGPR round trip); B (int8 w) is loaded as 16-byte vectors into registers one K-step ahead and
+//   widened to bf16 into a 2-stage LDS ring (exact: |w| <= 127 fits bf16's 8-bit significand), so dequantization
+//   costs no extra HBM traffic and the scale is applied once to the float accumulator in the epilogue:
+//   x (W diag s) = (x W) diag s. The five stages fill gfx950's 160 KiB of LDS.
+// - LDS rows are 128 bytes; the 16-byte chunk c of row r is stored at chunk c ^ ((r >> 1) & 7), so the MFMA operand
+//   reads (32 rows at one chunk per half-wave) hit distinct banks, and B's 16-byte writes are spread over 8 chunk
+//   columns per 8 lanes by the chunk-to-thread mapping.
 // - Workgroups are mapped XCD-aware: the hardware deals workgroup b to XCD b % 8, so consecutive tiles are renumbered
 //   onto one XCD, and grouped 4 row-tiles a band so the tiles running together on an XCD share x and w in its L2.
 #include "mh3_common.hpp"
@@ -22,24 +24,36 @@ typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef float floatx16 __attribute__((ext_vector_type(16)));
 
 constexpr uint32_t kBM = 256, kBN = 128, kBK = 64;
-constexpr int kGemmThreads = 256;
-constexpr uint32_t kStageChunks = 4096; // 16-byte chunks a stage: A 256 x 8, then B 256 x 8
-constexpr size_t kGemmLds = 2 * kStageChunks * 16;
+// LDS: a ring of 3 A stages (256 rows x 64 k bf16 = 2048 16-byte chunks each), then 2 B stages (256 B-rows x 64 k,
+// widened to bf16: 2048 chunks each): 160 KiB, gfx950's whole LDS.
+constexpr uint32_t kStageChunks = 2048, kAStages = 3, kBStages = 2;
+constexpr uint32_t kBBase = kAStages * kStageChunks;
+constexpr size_t kGemmLds = size_t(kAStages + kBStages) * kStageChunks * 16;
 constexpr uint32_t kBandM = 4;
 
-__device__ __forceinline__ uint32_t swz(uint32_t row, uint32_t chunk) { return row * 8u + (chunk ^ (row & 7u)); }
+typedef __attribute__((address_space(3))) void* lds_ptr_t;
+
+// 16 bytes a lane from a buffer straight into LDS: lane L's bytes land at lds + 16 L (buffer_load_dwordx4 ... lds).
+__device__ __forceinline__ void lds_dma16(__amdgpu_buffer_rsrc_t rsrc, void* lds, uint32_t voffset, int soffset)
+{
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, (lds_ptr_t)lds, 16, voffset, soffset, 0, 0);
+}
+
+// 16-byte chunk c of a 128-byte LDS row r sits at chunk c ^ ((r >> 1) & 7): the 16 rows an MFMA operand read touches
+// per half-wave then cover all 64 banks once.
+__device__ __forceinline__ uint32_t swz(uint32_t row, uint32_t chunk) { return row * 8u + (chunk ^ ((row >> 1) & 7u)); }
 
 // 16 int8 weights (one 16-byte vector) to 16 bf16 (two 16-byte vectors), exactly.
 __device__ __forceinline__ void widen16(const u32x4_t& v, u32x4_t& lo, u32x4_t& hi)
 {
-    const uint32_t w[4] = {v[0], v[1], v[2], v[3]};
     uint32_t o[8];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-        const float f0 = float(int32_t(w[i] << 24) >> 24);
-        const float f1 = float(int32_t(w[i] << 16) >> 24);
-        const float f2 = float(int32_t(w[i] << 8) >> 24);
-        const float f3 = float(int32_t(w[i]) >> 24);
+        const uint32_t w = v[i];
+        const float f0 = float(int32_t(w << 24) >> 24);
+        const float f1 = float(int32_t(w << 16) >> 24);
+        const float f2 = float(int32_t(w << 8) >> 24);
+        const float f3 = float(int32_t(w) >> 24);
         o[2 * i] = (__float_as_uint(f0) >> 16) | (__float_as_uint(f1) & 0xffff0000u);
         o[2 * i + 1] = (__float_as_uint(f2) >> 16) | (__float_as_uint(f3) & 0xffff0000u);
     }
@@ -57,125 +71,198 @@ __device__ __forceinline__ void tile_of(uint32_t mt, uint32_t nt, uint32_t& tm, 
     tn = within / in_band;
 }
 
-__global__ __launch_bounds__(kGemmThreads) void gemm_w8a16_swiglu_kernel(
+// s_waitcnt immediate that waits for vmcnt <= n only (gfx9 encoding: vmcnt in bits 3:0 and 15:14, expcnt 6:4,
+// lgkmcnt 11:8).
+constexpr int waitcnt_vm(int n) { return (n & 0xF) | (((n >> 4) & 3) << 14) | (0x7 << 4) | (0xF << 8); }
+
+// All LDS accesses before it done, then the workgroup barrier; the asm statements keep the compiler from moving
+// memory accesses across it.
+__device__ __forceinline__ void lds_barrier()
+{
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_waitcnt(0xC07F); // lgkmcnt(0), vmcnt and expcnt unconstrained
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+}
+
+#ifndef MH3_GEMM_WM
+#define MH3_GEMM_WM 2 // wavefronts along the tile's rows
+#endif
+#ifndef MH3_GEMM_WN
+#define MH3_GEMM_WN 4 // wavefronts along its columns
+#endif
+
+// WM x WN wavefronts: wave (wm, wn) computes rows wm * (256 / WM) ... of the tile against its TN gate column tiles
+// (32 columns each, from wn * 32 TN) and the TN matching up column tiles.
+template <int WM, int WN>
+__global__ __launch_bounds__(MH3_GEMM_WM * MH3_GEMM_WN * 64) void gemm_w8a16_swiglu_kernel(
     const uint16_t* __restrict__ x, const int8_t* __restrict__ w, const float* __restrict__ scale,
     uint16_t* __restrict__ out, uint32_t M, uint32_t N, uint32_t K, uint32_t mt, uint32_t nt)
 {
-    extern __shared__ uint4 smem[];
+    constexpr uint32_t kThreads = WM * WN * 64, kWaves = WM * WN;
+    constexpr int TM = int(kBM / WM / 32), TN = int(kBN / WN / 32); // MFMA tiles: rows, and gate (= up) columns
+    extern __shared__ u32x4_t smem[];
     uint32_t tm, tn;
     tile_of(mt, nt, tm, tn);
     const uint32_t m0 = tm * kBM, n0 = tn * kBN;
-    const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6, wm = wave >> 1, wn = wave & 1u;
+    const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6, wm = wave / WN, wn = wave % WN;
+    const uint32_t KT = K / kBK;
 
-    // Global -> register assignment, through buffer descriptors based at this tile (32-bit lane offsets; reads past
-    // the descriptor's extent return zero, which covers the rows past M). A: chunk c = tid + 256 i (i < 8) is tile row
-    // c / 8 = tid / 8 + 32 i, k-chunk c % 8 (8 bf16). B: chunk c = tid + 256 i (i < 4) is B-row c / 4 = tid / 4 + 64 i
-    // (0..127 the gate rows n0.., 128..255 the up rows n + n0..), k-chunk c % 4 (16 int8).
+    // A: straight from global memory into the LDS ring (buffer_load ... lds). A stage is 2048 16-byte chunks; each
+    // wave fills 2048 / kWaves of them, 64 a instruction; lane L of instruction i lands in chunk q = (wave * AI + i) *
+    // 64 + L = row * 8 + physical chunk and fetches the logical chunk the swizzle puts there. The descriptor starts
+    // at this tile's first row; rows past M read zero.
+    constexpr int AI = int(kStageChunks / 64 / kWaves);
     const uint64_t a_left = uint64_t(M - m0) * K * 2u;
-    const __amdgpu_buffer_rsrc_t ra_src = __builtin_amdgcn_make_buffer_rsrc(
-        const_cast<uint16_t*>(x + uint64_t(m0) * K), 0, int(a_left < 0x7fffffffu ? a_left : 0x7fffffffu), kRsrcFlags);
-    const __amdgpu_buffer_rsrc_t rg_src = __builtin_amdgcn_make_buffer_rsrc(
-        const_cast<int8_t*>(w + uint64_t(n0) * K), 0, int(kBN * K), kRsrcFlags);
-    const __amdgpu_buffer_rsrc_t ru_src = __builtin_amdgcn_make_buffer_rsrc(
-        const_cast<int8_t*>(w + (uint64_t(N) + n0) * K), 0, int(kBN * K), kRsrcFlags);
-    uint32_t a_off[8];
+    const __amdgpu_buffer_rsrc_t ra =
+        buffer_rsrc(x + uint64_t(m0) * K, uint32_t(a_left < 0x7fffffffu ? a_left : 0x7fffffffu));
+    uint32_t a_off[AI];
 #pragma unroll
-    for (int i = 0; i < 8; ++i)
-        a_off[i] = ((tid >> 3) + 32u * i) * K * 2u + (tid & 7u) * 16u;
-    const uint32_t b_off0 = (tid >> 2) * K + (tid & 3u) * 16u, b_off1 = b_off0 + 64u * K;
-    u32x4_t ra[8], rb[4];
-    auto gload = [&](uint32_t kt) {
-        const int sa = int(kt * kBK * 2u), sb = int(kt * kBK);
+    for (int i = 0; i < AI; ++i) {
+        const uint32_t row = (wave * AI + uint32_t(i)) * 8u + (lane >> 3);
+        const uint32_t c = (lane & 7u) ^ ((row >> 1) & 7u);
+        a_off[i] = (row * K + c * 8u) * 2u;
+    }
+    auto a_issue = [&](uint32_t kt) {
+        u32x4_t* stage = smem + (kt % kAStages) * kStageChunks + wave * AI * 64u;
 #pragma unroll
-        for (int i = 0; i < 8; ++i)
-            ra[i] = __builtin_amdgcn_raw_buffer_load_b128(ra_src, a_off[i], sa, 0);
-        rb[0] = __builtin_amdgcn_raw_buffer_load_b128(rg_src, b_off0, sb, 0);
-        rb[1] = __builtin_amdgcn_raw_buffer_load_b128(rg_src, b_off1, sb, 0);
-        rb[2] = __builtin_amdgcn_raw_buffer_load_b128(ru_src, b_off0, sb, 0);
-        rb[3] = __builtin_amdgcn_raw_buffer_load_b128(ru_src, b_off1, sb, 0);
+        for (int i = 0; i < AI; ++i)
+            lds_dma16(ra, stage + i * 64, a_off[i], int(kt * kBK * 2u));
     };
-    auto swrite = [&](uint32_t stage) {
-        u32x4_t* A = reinterpret_cast<u32x4_t*>(smem) + stage * kStageChunks;
-        u32x4_t* B = A + kStageChunks / 2;
+
+    // B: 16-byte int8 vectors into registers a K-step ahead, widened to bf16 into the B ring. The stage's 1024 int8
+    // chunks (256 B-rows x 4 k-chunks; rows 0..127 the gate rows n0.., 128..255 the up rows n + n0..) go BI to a
+    // thread: chunk q = tid + kThreads i is k-chunk q % 4 of B-row 4 (G / 2) + 2 ((q / 4) % 2) + G % 2, G = q / 8.
+    // Each 8 consecutive lanes thus write two rows whose swizzles differ in parity, i.e. 8 distinct chunk columns.
+    constexpr int BI = int(1024 / kThreads);
+    const __amdgpu_buffer_rsrc_t rw = buffer_rsrc(w, uint32_t(2u * N * K)); // N * K < 2^30 is checked on the host
+    uint32_t b_src[BI], b_lo[BI], b_hi[BI];
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            const uint32_t c = tid + 256u * i;
-            A[swz(c >> 3, c & 7u)] = ra[i];
-        }
+    for (int i = 0; i < BI; ++i) {
+        const uint32_t q = tid + kThreads * uint32_t(i), kc = q & 3u, G = q >> 3;
+        const uint32_t brow = 4u * (G >> 1) + 2u * ((q >> 2) & 1u) + (G & 1u);
+        const uint32_t wrow = brow < kBN ? n0 + brow : N + n0 + (brow - kBN);
+        const uint32_t sx = (brow >> 1) & 7u;
+        b_src[i] = wrow * K + kc * 16u;
+        b_lo[i] = brow * 128u + ((2u * kc) ^ sx) * 16u;
+        b_hi[i] = brow * 128u + ((2u * kc + 1u) ^ sx) * 16u;
+    }
+    auto b_issue = [&](uint32_t kt, u32x4_t (&rb)[BI]) {
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const uint32_t c = tid + 256u * i, brow = c >> 2, kc = c & 3u;
+        for (int i = 0; i < BI; ++i)
+            rb[i] = __builtin_amdgcn_raw_buffer_load_b128(rw, b_src[i], int(kt * kBK), 0);
+    };
+    char* const lds = reinterpret_cast<char*>(smem);
+    auto b_write = [&](uint32_t kt, const u32x4_t (&rb)[BI]) {
+        char* B = lds + (kBBase + (kt % kBStages) * kStageChunks) * 16u;
+#pragma unroll
+        for (int i = 0; i < BI; ++i) {
             u32x4_t lo, hi;
             widen16(rb[i], lo, hi);
-            B[swz(brow, 2u * kc)] = lo;
-            B[swz(brow, 2u * kc + 1u)] = hi;
+            *reinterpret_cast<u32x4_t*>(B + b_lo[i]) = lo;
+            *reinterpret_cast<u32x4_t*>(B + b_hi[i]) = hi;
         }
     };
 
-    floatx16 acc[4][4];
+    // MFMA operands of sub-step ks (16 k) of tile kt: A rows wm*(256/WM) + t*32 + lane%32, B rows (gate)
+    // wn*32TN + t*32 + lane%32 and (up) 128 + the same, k-chunk ks*2 + lane/32. Every row a lane reads has
+    // (row >> 1) & 7 = (lane % 32 >> 1) & 7, so one offset per sub-step serves all tiles; t moves it by 32 rows.
+    const uint32_t half = lane >> 5, r32 = lane & 31u, fsx = (r32 >> 1) & 7u;
+    const uint32_t fa_base = (wm * (kBM / WM) + r32) * 128u, fb_base = (wn * 32u * TN + r32) * 128u;
+    uint32_t fko[4];
 #pragma unroll
-    for (int a = 0; a < 4; ++a)
+    for (uint32_t ks = 0; ks < 4; ++ks)
+        fko[ks] = ((ks * 2u + half) ^ fsx) * 16u;
+    auto frags = [&](uint32_t kt, uint32_t ks, bf16x8_t (&fa)[TM], bf16x8_t (&fb)[2 * TN]) {
+        const char* A = lds + (kt % kAStages) * kStageChunks * 16u + fa_base + fko[ks];
+        const char* B = lds + (kBBase + (kt % kBStages) * kStageChunks) * 16u + fb_base + fko[ks];
 #pragma unroll
-        for (int b = 0; b < 4; ++b)
+        for (int t = 0; t < TM; ++t)
+            fa[t] = *reinterpret_cast<const bf16x8_t*>(A + t * 4096);
+#pragma unroll
+        for (int t = 0; t < TN; ++t) {
+            fb[t] = *reinterpret_cast<const bf16x8_t*>(B + t * 4096);
+            fb[TN + t] = *reinterpret_cast<const bf16x8_t*>(B + kBN * 128 + t * 4096);
+        }
+    };
+
+    floatx16 acc[TM][2 * TN];
+#pragma unroll
+    for (int a = 0; a < TM; ++a)
+#pragma unroll
+        for (int b = 0; b < 2 * TN; ++b)
 #pragma unroll
             for (int e = 0; e < 16; ++e)
                 acc[a][b][e] = 0.0f;
-
-    const uint32_t KT = K / kBK;
-    gload(0);
-    swrite(0);
-    __syncthreads();
-    const uint32_t half = lane >> 5, r32 = lane & 31u;
-    // LDS chunk of this lane's operand rows: A rows wm*128 + t*32 + r32, B rows (gate) wn*64 + t*32 + r32 and
-    // (up) 128 + wn*64 + (t-2)*32 + r32; the k-chunk (ks*2 + half) is XOR-swizzled by the row.
-    auto load_frags = [&](const uint4* A, const uint4* B, uint32_t ks, bf16x8_t (&fa)[4], bf16x8_t (&fb)[4]) {
+    auto mfmas = [&](const bf16x8_t (&fa)[TM], const bf16x8_t (&fb)[2 * TN]) {
 #pragma unroll
-        for (uint32_t t = 0; t < 4; ++t) {
-            const uint32_t row = wm * 128u + t * 32u + r32;
-            fa[t] = __builtin_bit_cast(bf16x8_t, A[swz(row, ks * 2u + half)]);
-            const uint32_t brow = (t < 2 ? wn * 64u + t * 32u : kBN + wn * 64u + (t - 2u) * 32u) + r32;
-            fb[t] = __builtin_bit_cast(bf16x8_t, B[swz(brow, ks * 2u + half)]);
-        }
+        for (int a = 0; a < TM; ++a)
+#pragma unroll
+            for (int b = 0; b < 2 * TN; ++b)
+                acc[a][b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[a], fb[b], acc[a][b], 0, 0, 0);
     };
+
+    // Prologue: tile 0's B widened into LDS and tile 0's A in LDS; tile 1's B in registers and A in flight to LDS.
+    // The explicit wait is needed: the compiler may issue the B loads ahead of the LDS-bound A loads, and then the
+    // waits it places for the B registers leave tile 0's A outstanding.
+    u32x4_t rb[BI];
+    a_issue(0);
+    b_issue(0, rb);
+    __builtin_amdgcn_sched_barrier(0);
+    __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
+    __builtin_amdgcn_sched_barrier(0);
+    b_write(0, rb);
+    if (KT > 1) {
+        b_issue(1, rb);
+        a_issue(1);
+    }
+    lds_barrier();
+    bf16x8_t fa[2][TM], fb[2][2 * TN];
+    frags(0, 0, fa[0], fb[0]);
+
+    // One K-step over tile kt. After the second sub-step, tile kt+1's B is widened from registers into LDS (waiting
+    // for it also waits for tile kt+1's A, issued a step ago right after it), then tile kt+2's B and A loads go out;
+    // a barrier at the end publishes tile kt+1. The compiler does not count the LDS-bound A loads in its own waits,
+    // which is why they are issued last: no wait then covers loads issued within the same step.
     for (uint32_t kt = 0; kt < KT; ++kt) {
-        if (kt + 1 < KT)
-            gload(kt + 1);
-        const uint4* A = smem + (kt & 1u) * kStageChunks;
-        const uint4* B = A + kStageChunks / 2;
-        bf16x8_t fa[2][4], fb[2][4];
-        load_frags(A, B, 0, fa[0], fb[0]);
-#pragma unroll
-        for (uint32_t ks = 0; ks < kBK / 16u; ++ks) {
-            // The next sub-step's operands are read from LDS while this sub-step's 16 MFMAs run.
-            if (ks + 1 < kBK / 16u)
-                load_frags(A, B, ks + 1, fa[(ks + 1) & 1u], fb[(ks + 1) & 1u]);
-            __builtin_amdgcn_sched_barrier(0); // keep those reads ahead of this sub-step's MFMAs
-#pragma unroll
-            for (int a = 0; a < 4; ++a)
-#pragma unroll
-                for (int b = 0; b < 4; ++b)
-                    acc[a][b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[ks & 1u][a], fb[ks & 1u][b], acc[a][b],
-                                                                         0, 0, 0);
+        frags(kt, 1, fa[1], fb[1]);
+        __builtin_amdgcn_sched_barrier(0);
+        mfmas(fa[0], fb[0]);
+        frags(kt, 2, fa[0], fb[0]);
+        __builtin_amdgcn_sched_barrier(0);
+        mfmas(fa[1], fb[1]);
+        if (kt + 1 < KT) {
+            b_write(kt + 1, rb);
+            __builtin_amdgcn_s_waitcnt(waitcnt_vm(0)); // tile kt+1's A complete too (the compiler does not track it)
+            if (kt + 2 < KT) {
+                b_issue(kt + 2, rb);
+                a_issue(kt + 2);
+            }
         }
-        if (kt + 1 < KT)
-            swrite((kt + 1) & 1u);
-        __syncthreads();
+        frags(kt, 3, fa[1], fb[1]);
+        __builtin_amdgcn_sched_barrier(0);
+        mfmas(fa[0], fb[0]);
+        mfmas(fa[1], fb[1]);
+        if (kt + 1 < KT) {
+            lds_barrier();
+            frags(kt + 1, 0, fa[0], fb[0]);
+        }
     }
 
-    // Epilogue: acc[a][b][e] is y[row][col] with row = m0 + wm 128 + a 32 + 8 (e / 4) + 4 (lane / 32) + e % 4 and
-    // col = lane % 32 + 32 b within the wave's columns (b < 2: gate, b >= 2: the matching up columns).
+    // Epilogue: acc[a][b][e] is y[row][col] with row = m0 + wm (256 / WM) + a 32 + 8 (e / 4) + 4 (lane / 32) + e % 4
+    // and col = lane % 32 + 32 b within the wave's gate columns (b < TN; acc[a][TN + b] holds the matching up column).
 #pragma unroll
-    for (int b = 0; b < 2; ++b) {
-        const uint32_t col = n0 + wn * 64u + uint32_t(b) * 32u + r32;
+    for (int b = 0; b < TN; ++b) {
+        const uint32_t col = n0 + wn * 32u * TN + uint32_t(b) * 32u + r32;
         const float sg = scale[col], su = scale[N + col];
 #pragma unroll
-        for (int a = 0; a < 4; ++a) {
+        for (int a = 0; a < TM; ++a) {
 #pragma unroll
             for (int e = 0; e < 16; ++e) {
-                const uint32_t row = m0 + wm * 128u + uint32_t(a) * 32u + 8u * (uint32_t(e) >> 2) + 4u * half +
+                const uint32_t row = m0 + wm * (kBM / WM) + uint32_t(a) * 32u + 8u * (uint32_t(e) >> 2) + 4u * half +
                                      (uint32_t(e) & 3u);
                 if (row < M) {
-                    const float g = acc[a][b][e] * sg, u = acc[a][b + 2][e] * su;
+                    const float g = acc[a][b][e] * sg, u = acc[a][TN + b][e] * su;
                     const float o = g * __builtin_amdgcn_rcpf(1.0f + __expf(-g)) * u;
                     out[uint64_t(row) * N + col] = __builtin_bit_cast(uint16_t, __bf16(o));
                 }
@@ -196,19 +283,22 @@ extern "C" int mh3_gemm_w8a16_swiglu(const MH3GemmArgs* a, const uint16_t* x, co
         return MH3_ERR_SHAPE;
     if (a->m >= (1u << 31) || uint64_t(a->n) * 2u >= (uint64_t(1) << 31))
         return MH3_ERR_SHAPE;
+    if (uint64_t(a->k) * kBM * 2u >= (uint64_t(1) << 31) || uint64_t(a->n) * a->k >= (uint64_t(1) << 30))
+        return MH3_ERR_UNSUPPORTED; // 32-bit buffer offsets: a tile's A rows, and all of w (2 n k bytes)
     if (!x || !w || !scale || !out)
         return MH3_ERR_POINTER;
     if (!host::aligned16(x) || !host::aligned16(w) || !host::aligned16(out))
         return MH3_ERR_ALIGN;
-    static const int lds_ok = hipFuncSetAttribute(reinterpret_cast<const void*>(&gemm_w8a16_swiglu_kernel),
-                                                  hipFuncAttributeMaxDynamicSharedMemorySize, int(kGemmLds));
+    constexpr int WM = MH3_GEMM_WM, WN = MH3_GEMM_WN;
+    const void* kernel = reinterpret_cast<const void*>(&gemm_w8a16_swiglu_kernel<WM, WN>);
+    static const int lds_ok = hipFuncSetAttribute(kernel, hipFuncAttributeMaxDynamicSharedMemorySize, int(kGemmLds));
     if (lds_ok != hipSuccess)
         return MH3_ERR_HIP;
     const uint32_t mt = (a->m + kBM - 1) / kBM, nt = a->n / kBN;
     const uint64_t tiles = uint64_t(mt) * nt;
     if (tiles >= (uint64_t(1) << 31))
         return MH3_ERR_SHAPE;
-    hipLaunchKernelGGL(gemm_w8a16_swiglu_kernel, dim3(uint32_t(tiles)), dim3(kGemmThreads), kGemmLds,
+    hipLaunchKernelGGL((gemm_w8a16_swiglu_kernel<WM, WN>), dim3(uint32_t(tiles)), dim3(WM * WN * 64), kGemmLds,
                        static_cast<hipStream_t>(stream), x, w, scale, out, a->m, a->n, a->k, mt, nt);
     return host::check_launch();
 }
