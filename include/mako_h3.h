@@ -71,14 +71,14 @@ int64_t mh3_topk_k(float ratio, uint32_t cubes);
 /* ---- rows: rms_mod_rows, gate_add_rows, fused rms_mod_gate_add_rows ----------------------------------------------
  * Reference kernels `rms_mod_rows` and `gate_add_rows` (mako-common; named in docs/performance.md:44, semantics in
  * docs/architecture.md:49-52,61,64-65). A row r uses modulation set s(r) = set_of_row[r] (uint8, device memory) when
- * set_of_row is non-NULL, else 0. shift, scale and gate are [n_sets][dim] float, w is [dim] float (NULL: all 1).
- * x, residual, y and out are [rows][dim] of `dtype`. bf16 rows need dim % 8 == 0 and 16-byte aligned pointers;
- * float rows dim % 4 == 0 and 16-byte alignment. Math is float, the sum of squares accumulated in float, and
- * bf16 results are rounded to nearest even once, at the store. */
+ * set_of_row is non-NULL, else 0; a value >= n_sets is read as n_sets - 1. shift, scale and gate are [n_sets][dim]
+ * float, w is [dim] float (NULL: all 1). x, residual, y and out are [rows][dim] of `dtype`. bf16 rows need
+ * dim % 8 == 0, float rows dim % 4 == 0; every pointer, the float vectors included, 16-byte aligned. Math is float,
+ * the sum of squares accumulated in float, and bf16 results are rounded to nearest even once, at the store. */
 typedef struct MH3RowsArgs {
     uint32_t rows;
     uint32_t dim;
-    uint32_t n_sets; /* >= 1; every set_of_row[r] must be < n_sets */
+    uint32_t n_sets; /* 1 .. 256 */
     uint32_t dtype;  /* MH3_F32 or MH3_BF16 */
     float eps;       /* > 0 (H3: 1e-6) */
     uint32_t reserved[3];
@@ -173,7 +173,9 @@ int mh3_quant_rows_i8(const MH3QuantArgs* args, const void* w, int8_t* q, float*
  * the gate, [n, 2n) the up projection); scale is float [2n]. With W the [k][2n] matrix w^T:
  *   y = x * (W * diag(scale)) in float accumulation, out = silu(y[:, 0:n]) * y[:, n:2n], bf16 [m][n].
  * The int8 -> bf16 widening is exact (|w| <= 127); the scale is applied to the float accumulator.
- * k % 64 == 0, n % 128 == 0, m >= 1; 16-byte aligned pointers. */
+ * k % 64 == 0, n % 128 == 0, m >= 1; x, w and out 16-byte aligned. The kernel addresses w and a 256-row block of x
+ * with 32-bit offsets: n * k < 2^30 and k < 2^22, else MH3_ERR_UNSUPPORTED (H3's fc1, n = 14,336 and k = 5376,
+ * uses 7.7e7). */
 typedef struct MH3GemmArgs {
     uint32_t m;
     uint32_t n; /* output columns; w has 2n rows */
