@@ -18,6 +18,8 @@
 //   onto one XCD, and grouped 4 row-tiles a band so the tiles running together on an XCD share x and w in its L2.
 #include "mh3_common.hpp"
 
+#include <type_traits>
+
 namespace mh3 {
 
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
@@ -43,22 +45,22 @@ __device__ __forceinline__ void lds_dma16(__amdgpu_buffer_rsrc_t rsrc, void* lds
 // per half-wave then cover all 64 banks once.
 __device__ __forceinline__ uint32_t swz(uint32_t row, uint32_t chunk) { return row * 8u + (chunk ^ ((row >> 1) & 7u)); }
 
-// 16 int8 weights (one 16-byte vector) to 16 bf16 (two 16-byte vectors), exactly.
-__device__ __forceinline__ void widen16(const u32x4_t& v, u32x4_t& lo, u32x4_t& hi)
+// 8 int8 weights (two dwords) to 8 bf16 (one 16-byte vector), exactly: each byte to float, then the upper halves
+// of two floats are the bf16 pair (|w| <= 127 has at most 8 significant bits, so the truncation is exact).
+__device__ __forceinline__ u32x4_t widen8(uint32_t w0, uint32_t w1)
 {
-    uint32_t o[8];
+    u32x4_t r;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const uint32_t w = v[i];
+    for (int d = 0; d < 2; ++d) {
+        const uint32_t w = d ? w1 : w0;
         const float f0 = float(int32_t(w << 24) >> 24);
         const float f1 = float(int32_t(w << 16) >> 24);
         const float f2 = float(int32_t(w << 8) >> 24);
         const float f3 = float(int32_t(w) >> 24);
-        o[2 * i] = (__float_as_uint(f0) >> 16) | (__float_as_uint(f1) & 0xffff0000u);
-        o[2 * i + 1] = (__float_as_uint(f2) >> 16) | (__float_as_uint(f3) & 0xffff0000u);
+        r[2 * d] = __builtin_amdgcn_perm(__float_as_uint(f1), __float_as_uint(f0), 0x07060302u);
+        r[2 * d + 1] = __builtin_amdgcn_perm(__float_as_uint(f3), __float_as_uint(f2), 0x07060302u);
     }
-    lo = u32x4_t{o[0], o[1], o[2], o[3]};
-    hi = u32x4_t{o[4], o[5], o[6], o[7]};
+    return r;
 }
 
 __device__ __forceinline__ void tile_of(uint32_t mt, uint32_t nt, uint32_t& tm, uint32_t& tn)
@@ -153,15 +155,17 @@ __global__ __launch_bounds__(MH3_GEMM_WM * MH3_GEMM_WN * 64) void gemm_w8a16_swi
             rb[i] = __builtin_amdgcn_raw_buffer_load_b128(rw, b_src[i], int(kt * kBK), 0);
     };
     char* const lds = reinterpret_cast<char*>(smem);
-    auto b_write = [&](uint32_t kt, const u32x4_t (&rb)[BI]) {
+    u32x4_t rb[BI];
+    // Piece p of tile kt's B write: half p % 2 of register chunk p / 2, widened and stored.
+    auto b_piece = [&](uint32_t kt, const u32x4_t (&rb)[BI], int p) {
         char* B = lds + (kBBase + (kt % kBStages) * kStageChunks) * 16u;
+        const int i = p >> 1, h = p & 1;
+        *reinterpret_cast<u32x4_t*>(B + (h ? b_hi[i] : b_lo[i])) = widen8(rb[i][2 * h], rb[i][2 * h + 1]);
+    };
+    auto b_write = [&](uint32_t kt, const u32x4_t (&rb)[BI]) {
 #pragma unroll
-        for (int i = 0; i < BI; ++i) {
-            u32x4_t lo, hi;
-            widen16(rb[i], lo, hi);
-            *reinterpret_cast<u32x4_t*>(B + b_lo[i]) = lo;
-            *reinterpret_cast<u32x4_t*>(B + b_hi[i]) = hi;
-        }
+        for (int p = 0; p < 2 * BI; ++p)
+            b_piece(kt, rb, p);
     };
 
     // MFMA operands of sub-step ks (16 k) of tile kt: A rows wm*(256/WM) + t*32 + lane%32, B rows (gate)
@@ -201,11 +205,25 @@ __global__ __launch_bounds__(MH3_GEMM_WM * MH3_GEMM_WN * 64) void gemm_w8a16_swi
             for (int b = 0; b < 2 * TN; ++b)
                 acc[a][b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[a], fb[b], acc[a][b], 0, 0, 0);
     };
+    // The same MFMAs with B pieces p0 .. p0 + np - 1 of tile kt placed between them, at even spacing, so the
+    // widening's VALU work issues while the matrix core is busy.
+    auto mfmas_b = [&](const bf16x8_t (&fa)[TM], const bf16x8_t (&fb)[2 * TN], uint32_t kt, int p0, int np) {
+        constexpr int n = TM * 2 * TN;
+#pragma unroll
+        for (int j = 0; j < n; ++j) {
+            const int a = j / (2 * TN), b = j % (2 * TN);
+            acc[a][b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[a], fb[b], acc[a][b], 0, 0, 0);
+            __builtin_amdgcn_sched_barrier(0);
+            if (j % (n / np) == 0 && j / (n / np) < np) {
+                b_piece(kt, rb, p0 + j / (n / np));
+                __builtin_amdgcn_sched_barrier(0);
+            }
+        }
+    };
 
     // Prologue: tile 0's B widened into LDS and tile 0's A in LDS; tile 1's B in registers and A in flight to LDS.
     // The explicit wait is needed: the compiler may issue the B loads ahead of the LDS-bound A loads, and then the
     // waits it places for the B registers leave tile 0's A outstanding.
-    u32x4_t rb[BI];
     a_issue(0);
     b_issue(0, rb);
     __builtin_amdgcn_sched_barrier(0);
@@ -216,24 +234,37 @@ __global__ __launch_bounds__(MH3_GEMM_WM * MH3_GEMM_WN * 64) void gemm_w8a16_swi
         b_issue(1, rb);
         a_issue(1);
     }
+    // The epilogue's kernel arguments are read here, before the barrier: a scalar load still in flight at the loop
+    // would turn every LDS wait in it into a full wait (scalar loads complete out of order).
+    asm volatile("" ::"s"(scale), "s"(out));
     lds_barrier();
     bf16x8_t fa[2][TM], fb[2][2 * TN];
     frags(0, 0, fa[0], fb[0]);
 
-    // One K-step over tile kt. After the second sub-step, tile kt+1's B is widened from registers into LDS (waiting
-    // for it also waits for tile kt+1's A, issued a step ago right after it), then tile kt+2's B and A loads go out;
-    // a barrier at the end publishes tile kt+1. The compiler does not count the LDS-bound A loads in its own waits,
-    // which is why they are issued last: no wait then covers loads issued within the same step.
-    for (uint32_t kt = 0; kt < KT; ++kt) {
+    // One K-step over tile kt (four sub-steps of 16 k). Tile kt+1's B is widened from registers into LDS in four
+    // pieces placed between the MFMAs of the first two sub-steps. Then the wave waits for everything it has in
+    // flight (tile kt+1's A, issued a step ago) and tile kt+2's B and A loads go out. The barrier publishing tile kt+1
+    // comes after the third sub-step's MFMAs, and
+    // the fourth sub-step's operands are already in registers: the MFMAs keep running while tile kt+1's first
+    // fragments load. LDS stages written in step kt (A stage (kt+2) % 3, B stage (kt+1) % 2) were last read before
+    // step kt-1's barrier. The last step is a separate instance (kLast) so that the loop body has no branch around
+    // the barrier: at such a join the compiler's LDS wait would also cover tile kt+1's fragment reads.
+    auto kstep = [&](uint32_t kt, auto last) {
+        constexpr bool kLast = decltype(last)::value;
         frags(kt, 1, fa[1], fb[1]);
         __builtin_amdgcn_sched_barrier(0);
-        mfmas(fa[0], fb[0]);
+        if constexpr (kLast)
+            mfmas(fa[0], fb[0]);
+        else
+            mfmas_b(fa[0], fb[0], kt + 1, 0, BI);
         frags(kt, 2, fa[0], fb[0]);
         __builtin_amdgcn_sched_barrier(0);
-        mfmas(fa[1], fb[1]);
-        if (kt + 1 < KT) {
-            b_write(kt + 1, rb);
-            __builtin_amdgcn_s_waitcnt(waitcnt_vm(0)); // tile kt+1's A complete too (the compiler does not track it)
+        if constexpr (kLast)
+            mfmas(fa[1], fb[1]);
+        else
+            mfmas_b(fa[1], fb[1], kt + 1, BI, BI);
+        if constexpr (!kLast) {
+            __builtin_amdgcn_s_waitcnt(waitcnt_vm(0)); // tile kt+1's A complete too
             if (kt + 2 < KT) {
                 b_issue(kt + 2, rb);
                 a_issue(kt + 2);
@@ -242,12 +273,17 @@ __global__ __launch_bounds__(MH3_GEMM_WM * MH3_GEMM_WN * 64) void gemm_w8a16_swi
         frags(kt, 3, fa[1], fb[1]);
         __builtin_amdgcn_sched_barrier(0);
         mfmas(fa[0], fb[0]);
-        mfmas(fa[1], fb[1]);
-        if (kt + 1 < KT) {
+        __builtin_amdgcn_sched_barrier(0);
+        if constexpr (!kLast) {
             lds_barrier();
             frags(kt + 1, 0, fa[0], fb[0]);
         }
-    }
+        __builtin_amdgcn_sched_barrier(0);
+        mfmas(fa[1], fb[1]);
+    };
+    for (uint32_t kt = 0; kt + 1 < KT; ++kt)
+        kstep(kt, std::false_type{});
+    kstep(KT - 1, std::true_type{});
 
     // Epilogue: acc[a][b][e] is y[row][col] with row = m0 + wm (256 / WM) + a 32 + 8 (e / 4) + 4 (lane / 32) + e % 4
     // and col = lane % 32 + 32 b within the wave's gate columns (b < TN; acc[a][TN + b] holds the matching up column).
