@@ -130,7 +130,8 @@ int mh3_swiglu_rows(const MH3SwigluArgs* args, const void* gate, const void* up,
  *             before and after, where they exist), written as ascending int32 cube indices
  *             idx[h][i][0 .. cnt[h][i]) with idx[h][i][cnt .. out_stride) = -1; cnt[h][i] = k + the local cubes not
  *             already among the k. out_stride >= k + local.
- * cube_select: cube_scores and cube_topk fused; the scores stay on chip.
+ * cube_select: cube_scores and cube_topk fused; the scores stay on chip. Up to 2048 cubes (MH3_ERR_UNSUPPORTED
+ *             beyond: use cube_scores + cube_topk, which take up to 4096).
  * mh3_cube_count() gives the number of cubes of a grid; mh3_topk_k() gives k for a ratio. */
 enum { MH3_CUBES_GRID = 0, MH3_CUBES_GATHERED = 1 };
 typedef struct MH3CubeArgs {

@@ -8,11 +8,15 @@
 //   layout); all 32 loads of a lane are in flight at once. Lane sums in float, then a 2-step butterfly.
 // - scores: v_mfma_f32_16x16x4_f32 on 16 x 16 blocks; the 128-long contraction is split over the MFMA's 4 k-lanes
 //   as 4 runs of 32 consecutive dimensions, so every lane's q and k operands are 128 contiguous bytes.
-// - top-k: one wavefront per (head, query cube) holds the row's scores as order-preserving 32-bit keys in VGPRs,
-//   finds the k-th largest key by a wave-uniform binary search over the key range (ballot + popcount counts), then
-//   emits the selection in ascending cube order with a ballot prefix sum; equal keys are taken lowest index first.
+// - top-k: one wavefront per (head, query cube) holds the row's scores as order-preserving 32-bit keys in VGPRs, lane l
+//   owning cubes 32 l ... 32 l + 31. It finds the k-th largest key by a binary search over the key range with
+//   per-lane counts and a DPP wave sum, switching to a one-key-per-lane search once at most 64 keys remain in range.
+//   The selection is a per-lane bit mask; wave prefix sums over lanes rank the ties (lowest index first) and place
+//   each lane's indices, so the output is ascending with no per-element ballots.
 // - cube_select keeps a 16 x C score tile in LDS between the two phases, so the scores never reach HBM.
 #include "mh3_common.hpp"
+
+#include <type_traits>
 
 namespace mh3 {
 
@@ -121,8 +125,20 @@ __device__ __forceinline__ floatx4 score_block(const float (&qa)[32], const floa
 
 constexpr float kScoreScale = 0.08838834764831845f; // 1 / sqrt(128)
 
+// LDS rows for the top-k: cube j of a row sits at word (j / KPL) (KPL + 4) + j % KPL, so the KPL scores of lane l
+// (cubes l KPL ...) are contiguous and 16-byte reads of 16 lanes at a stride of KPL + 4 words hit distinct banks.
+template <int KPL>
+__device__ __forceinline__ uint32_t pad_word(uint32_t j)
+{
+    return (j / KPL) * (KPL + 4) + j % KPL;
+}
+template <int KPL>
+constexpr uint32_t kPaddedRow = 64u * (KPL + 4);
+
 // Scores of query block [i0, i0 + 16) of head h against every key cube; the wave takes key blocks wave, wave + waves...
-// Writes s[r][j] for r < 16, j < cubes into `dst` with row stride `ld` (rows past the last query cube skipped).
+// Writes s[r][j] for r < 16, j < cubes into `dst` at r * ld + j, or at r * ld + pad_word<32>(j) when PAD (rows past
+// the last query cube skipped).
+template <bool PAD>
 __device__ __forceinline__ void score_rows(const CubeGeo& g, const float* __restrict__ qh, const float* __restrict__ kh,
                                            uint32_t i0, float* dst, uint64_t ld, uint32_t wave, uint32_t waves)
 {
@@ -130,30 +146,34 @@ __device__ __forceinline__ void score_rows(const CubeGeo& g, const float* __rest
     float qa[32];
     load_operand(qh, i0, g.cubes, qa);
     const uint32_t kblocks = (g.cubes + 15u) / 16u;
-    uint32_t kb_i = wave;
-    if (kb_i >= kblocks)
-        return;
-    float kb[32];
-    load_operand(kh, kb_i * 16u, g.cubes, kb);
-    while (true) {
-        const uint32_t next = kb_i + waves;
-        float kn[32];
-        if (next < kblocks)
-            load_operand(kh, next * 16u, g.cubes, kn);
-        const floatx4 acc = score_block(qa, kb);
+    auto emit = [&](uint32_t kb_i, const floatx4& acc) {
         const uint32_t j = kb_i * 16u + (lane & 15u);
 #pragma unroll
         for (int v = 0; v < 4; ++v) {
             const uint32_t r = (lane >> 4) * 4u + uint32_t(v);
             if (j < g.cubes && i0 + r < g.cubes)
-                dst[r * ld + j] = acc[v] * kScoreScale;
+                dst[r * ld + (PAD ? pad_word<32>(j) : j)] = acc[v] * kScoreScale;
         }
-        if (next >= kblocks)
+    };
+    // Key blocks wave, wave + waves, ... through a two-block register ring: block b + 2 waves loads while block b's
+    // MFMAs run.
+    float k0[32], k1[32];
+    uint32_t b = wave;
+    if (b < kblocks)
+        load_operand(kh, b * 16u, g.cubes, k0);
+    if (b + waves < kblocks)
+        load_operand(kh, (b + waves) * 16u, g.cubes, k1);
+    for (; b < kblocks; b += 2u * waves) {
+        const floatx4 a0 = score_block(qa, k0);
+        if (b + 2u * waves < kblocks)
+            load_operand(kh, (b + 2u * waves) * 16u, g.cubes, k0);
+        emit(b, a0);
+        if (b + waves >= kblocks)
             break;
-        kb_i = next;
-#pragma unroll
-        for (int i = 0; i < 32; ++i)
-            kb[i] = kn[i];
+        const floatx4 a1 = score_block(qa, k1);
+        if (b + 3u * waves < kblocks)
+            load_operand(kh, (b + 3u * waves) * 16u, g.cubes, k1);
+        emit(b + waves, a1);
     }
 }
 
@@ -162,8 +182,8 @@ __global__ __launch_bounds__(256) void cube_scores_kernel(CubeGeo g, const float
 {
     const uint32_t h = blockIdx.y, i0 = blockIdx.x * 16u;
     const uint64_t plane = uint64_t(g.cubes) * 128u;
-    score_rows(g, qc + h * plane, kc + h * plane, i0, s + (uint64_t(h) * g.cubes + i0) * g.cubes, g.cubes,
-               threadIdx.x >> 6, blockDim.x >> 6);
+    score_rows<false>(g, qc + h * plane, kc + h * plane, i0, s + (uint64_t(h) * g.cubes + i0) * g.cubes, g.cubes,
+                      threadIdx.x >> 6, blockDim.x >> 6);
 }
 
 // Order-preserving key of a float score (larger score, larger key); -0 ranks as +0; key 0 is below every score.
@@ -174,103 +194,172 @@ __device__ __forceinline__ uint32_t score_key(float f)
     return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
 }
 
-// Top-k plus local cubes of one (head, query cube i) row of `cubes` scores, by one wavefront.
+// Keys >= t over the wave: per-lane counts in four independent chains, then one DPP wave sum.
 template <int KPL>
-__device__ __forceinline__ void topk_row(const float* srow, const CubeGeo& g, uint32_t i, uint32_t k, uint32_t local,
-                                         int32_t* __restrict__ out, uint32_t out_stride, int32_t* __restrict__ cnt)
+__device__ __forceinline__ uint32_t count_ge(const uint32_t (&key)[KPL], uint32_t t)
 {
+    uint32_t c[4] = {0u, 0u, 0u, 0u};
+#pragma unroll
+    for (int m = 0; m < KPL; ++m)
+        c[m & 3] += key[m] >= t ? 1u : 0u;
+    return wave_sum_u32((c[0] + c[1]) + (c[2] + c[3]));
+}
+
+// Top-k plus local cubes of one (head, query cube i) row of `cubes` scores, by one wavefront. Lane l holds cubes
+// j = l KPL + m (m < KPL), read from `row` in the padded layout of pad_word; entries with j >= cubes are ignored.
+// `cand` is 64 words of LDS private to the wave.
+// The k-th largest key t is the largest t with #{key >= t} >= k. A binary search over the key range keeps
+// lo (#{key >= lo} = n_lo >= k) and hi (#{key > hi} = n_hi < k); once at most 64 keys lie in [lo, hi] they are
+// compacted one to a lane and the search finishes over them alone (#{key >= m} = n_hi + #{candidates >= m}).
+// The selection is then a per-lane bit mask: keys above t, the first k - #{key > t} keys equal to t in cube order
+// (ranked by a wave prefix sum of per-lane tie counts) and the local cubes; a prefix sum of the per-lane counts gives
+// each lane its output position, so the indices come out ascending.
+template <int KPL>
+__device__ __forceinline__ void topk_row(const float* row, const CubeGeo& g, uint32_t i, uint32_t k, uint32_t local,
+                                         int32_t* __restrict__ out, uint32_t out_stride, int32_t* __restrict__ cnt,
+                                         uint32_t* cand)
+{
+    typedef typename std::conditional<KPL == 32, uint32_t, uint64_t>::type Mask;
     const uint32_t lane = threadIdx.x & 63u;
-    const uint32_t C = g.cubes;
+    const uint32_t C = g.cubes, j0 = lane * KPL;
+    const float4* mine = reinterpret_cast<const float4*>(row + lane * (KPL + 4));
     uint32_t key[KPL];
+    Mask valid = 0;
     uint32_t mn = 0xffffffffu, mx = 0u;
 #pragma unroll
-    for (int m = 0; m < KPL; ++m) {
-        const uint32_t j = lane + 64u * m;
-        key[m] = j < C ? score_key(srow[j]) : 0u;
-        if (j < C) {
-            mn = key[m] < mn ? key[m] : mn;
-            mx = key[m] > mx ? key[m] : mx;
+    for (int v = 0; v < KPL / 4; ++v) {
+        const float4 f = mine[v];
+        const float fv[4] = {f.x, f.y, f.z, f.w};
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+            const int m = 4 * v + c;
+            const bool ok = j0 + uint32_t(m) < C;
+            key[m] = ok ? score_key(fv[c]) : 0u;
+            valid |= ok ? Mask(1) << m : Mask(0);
+            mn = ok && key[m] < mn ? key[m] : mn;
+            mx = ok && key[m] > mx ? key[m] : mx;
         }
     }
     uint32_t lo = wave_min_u32(mn), hi = wave_max_u32(mx);
-    // The k-th largest key: the largest t with #{key >= t} >= k. Invariant: #{key >= lo} >= k.
-    while (lo < hi) {
+    uint32_t n_lo = C, n_hi = 0u; // every valid key is >= the minimum; padding keys (0) are never counted (mid > 0)
+    while (lo < hi && n_lo - n_hi > 64u) {
         const uint32_t d = hi - lo;
         const uint32_t mid = lo + (d >> 1) + (d & 1u);
-        uint32_t n = 0;
+        const uint32_t n = count_ge(key, mid);
+        if (n >= k)
+            lo = mid, n_lo = n;
+        else
+            hi = mid - 1u, n_hi = n;
+    }
+    if (lo < hi) {
+        uint32_t mine_n = 0;
 #pragma unroll
         for (int m = 0; m < KPL; ++m)
-            n += __popcll(__ballot(key[m] >= mid));
-        if (n >= k)
-            lo = mid;
-        else
-            hi = mid - 1u;
+            mine_n += ((valid >> m) & 1u) && key[m] >= lo && key[m] <= hi ? 1u : 0u;
+        uint32_t slot = wave_excl_scan_u32(mine_n); // the candidates number n_lo - n_hi <= 64
+#pragma unroll
+        for (int m = 0; m < KPL; ++m)
+            if (((valid >> m) & 1u) && key[m] >= lo && key[m] <= hi)
+                cand[slot++] = key[m];
+        __builtin_amdgcn_s_waitcnt(0xC07F); // the wave's own LDS writes are visible to its reads after lgkmcnt(0)
+        const uint32_t c = lane < n_lo - n_hi ? cand[lane] : 0u;
+        const uint32_t need = k - n_hi;
+        while (lo < hi) {
+            const uint32_t d = hi - lo;
+            const uint32_t mid = lo + (d >> 1) + (d & 1u);
+            if (uint32_t(__popcll(__ballot(c >= mid))) >= need)
+                lo = mid;
+            else
+                hi = mid - 1u;
+        }
     }
     const uint32_t t = lo;
-    uint32_t above = 0;
-#pragma unroll
-    for (int m = 0; m < KPL; ++m)
-        above += __popcll(__ballot(key[m] > t));
-    const uint32_t need_eq = k - above; // >= 1
-    const uint32_t ct = i / g.plane;
-    const bool prev = local == 3u && ct > 0u, next = local == 3u && ct + 1u < g.cth;
-    const uint64_t below = lanes_below(int(lane));
-    uint32_t pos = 0, eq_seen = 0;
+    Mask gt = 0, eq = 0;
 #pragma unroll
     for (int m = 0; m < KPL; ++m) {
-        const uint32_t j = lane + 64u * m;
-        const bool eq = key[m] == t;
-        const uint64_t eqm = __ballot(eq);
-        const uint32_t rank = eq_seen + uint32_t(__popcll(eqm & below));
-        const bool loc = j < C && ((local >= 1u && j == i) || (prev && j == i - g.plane) || (next && j == i + g.plane));
-        const bool sel = key[m] > t || (eq && rank < need_eq) || loc;
-        const uint64_t selm = __ballot(sel);
-        if (sel)
-            out[pos + uint32_t(__popcll(selm & below))] = int32_t(j);
-        pos += uint32_t(__popcll(selm));
-        eq_seen += uint32_t(__popcll(eqm));
+        gt |= key[m] > t ? Mask(1) << m : Mask(0);
+        eq |= key[m] == t ? Mask(1) << m : Mask(0);
     }
-    for (uint32_t j = pos + lane; j < out_stride; j += 64u)
+    gt &= valid;
+    eq &= valid;
+    const uint32_t n_gt = uint32_t(__popcll(uint64_t(gt))), n_eq = uint32_t(__popcll(uint64_t(eq)));
+    const uint32_t need_eq = k - wave_sum_u32(n_gt); // >= 1
+    const uint32_t eq_before = wave_excl_scan_u32(n_eq);
+    uint32_t take = need_eq > eq_before ? min(need_eq - eq_before, n_eq) : 0u;
+    Mask sel = gt;
+#pragma unroll
+    for (int m = 0; m < KPL; ++m) {
+        const bool tie = (eq >> m) & 1u;
+        sel |= tie && take > 0u ? Mask(1) << m : Mask(0);
+        take -= tie && take > 0u ? 1u : 0u;
+    }
+    const uint32_t ct = i / g.plane;
+    const uint32_t loc[3] = {local >= 1u ? i : 0xffffffffu, local == 3u && ct > 0u ? i - g.plane : 0xffffffffu,
+                             local == 3u && ct + 1u < g.cth ? i + g.plane : 0xffffffffu};
+#pragma unroll
+    for (int e = 0; e < 3; ++e)
+        sel |= loc[e] / KPL == lane ? Mask(1) << (loc[e] % KPL) : Mask(0);
+    const uint32_t n_sel = uint32_t(__popcll(uint64_t(sel)));
+    uint32_t pos = wave_excl_scan_u32(n_sel);
+    const uint32_t total = uint32_t(__builtin_amdgcn_readlane(int(pos + n_sel), 63));
+#pragma unroll
+    for (int m = 0; m < KPL; ++m)
+        if ((sel >> m) & 1u)
+            out[pos++] = int32_t(j0 + uint32_t(m));
+    for (uint32_t j = total + lane; j < out_stride; j += 64u)
         out[j] = -1;
     if (lane == 0)
-        *cnt = int32_t(pos);
+        *cnt = int32_t(total);
 }
 
+// One wavefront per (head, query cube) row of s: the row is staged into LDS in the padded layout (coalesced loads),
+// then ranked.
 template <int KPL>
 __global__ __launch_bounds__(256) void cube_topk_kernel(CubeGeo g, const float* __restrict__ s, uint32_t k,
                                                         uint32_t local, uint32_t out_stride, int32_t* __restrict__ idx,
                                                         int32_t* __restrict__ cnt)
 {
-    const uint32_t item = blockIdx.x * 4u + (threadIdx.x >> 6);
+    extern __shared__ float rows[]; // 4 padded rows, then 64 candidate words per wave
+    const uint32_t wave = threadIdx.x >> 6, lane = threadIdx.x & 63u;
+    float* row = rows + wave * kPaddedRow<KPL>;
+    uint32_t* cand = reinterpret_cast<uint32_t*>(rows + 4u * kPaddedRow<KPL>) + wave * 64u;
+    const uint32_t item = blockIdx.x * 4u + wave;
     if (item >= g.heads * g.cubes)
         return;
-    const uint32_t i = item % g.cubes;
-    topk_row<KPL>(s + uint64_t(item) * g.cubes, g, i, k, local, idx + uint64_t(item) * out_stride, out_stride,
-                  cnt + item);
+    const float* src = s + uint64_t(item) * g.cubes;
+#pragma unroll 8
+    for (uint32_t j = lane; j < g.cubes; j += 64u)
+        row[pad_word<KPL>(j)] = src[j];
+    __builtin_amdgcn_s_waitcnt(0xC07F); // the wave reads only what it wrote itself
+    topk_row<KPL>(row, g, item % g.cubes, k, local, idx + uint64_t(item) * out_stride, out_stride, cnt + item, cand);
 }
 
 constexpr int kSelectThreads = 512;
 constexpr uint32_t kSelectRows = 16;
+constexpr uint32_t kSelectMaxCubes = 2048;
+constexpr size_t kSelectLds = (size_t(kSelectRows) * kPaddedRow<32> + (kSelectThreads / 64) * 64u) * sizeof(float);
 
-template <int KPL>
+// Scores of 16 query cubes against every key cube into a padded LDS tile, then one wavefront per row ranks it.
 __global__ __launch_bounds__(kSelectThreads) void cube_select_kernel(CubeGeo g, const float* __restrict__ qc,
                                                                      const float* __restrict__ kc, uint32_t k,
                                                                      uint32_t local, uint32_t out_stride,
                                                                      int32_t* __restrict__ idx,
                                                                      int32_t* __restrict__ cnt)
 {
-    extern __shared__ float tile[]; // [16][cubes]
+    extern __shared__ float tile[]; // [16][padded row], then 64 candidate words per wave
     const uint32_t h = blockIdx.y, i0 = blockIdx.x * kSelectRows;
     const uint32_t wave = threadIdx.x >> 6, waves = blockDim.x >> 6;
+    uint32_t* cand = reinterpret_cast<uint32_t*>(tile + kSelectRows * kPaddedRow<32>) + wave * 64u;
     const uint64_t plane = uint64_t(g.cubes) * 128u;
-    score_rows(g, qc + h * plane, kc + h * plane, i0, tile, g.cubes, wave, waves);
+    score_rows<true>(g, qc + h * plane, kc + h * plane, i0, tile, kPaddedRow<32>, wave, waves);
     __syncthreads();
     for (uint32_t r = wave; r < kSelectRows; r += waves) {
         const uint32_t i = i0 + r;
         if (i >= g.cubes)
             break;
         const uint64_t item = uint64_t(h) * g.cubes + i;
-        topk_row<KPL>(tile + r * g.cubes, g, i, k, local, idx + item * out_stride, out_stride, cnt + item);
+        topk_row<32>(tile + r * kPaddedRow<32>, g, i, k, local, idx + item * out_stride, out_stride, cnt + item,
+                     cand);
     }
 }
 
@@ -371,12 +460,18 @@ int mh3_cube_topk(const MH3CubeArgs* args, const float* s, int32_t* idx, int32_t
         return MH3_ERR_POINTER;
     const uint32_t items = g.heads * g.cubes;
     hipStream_t st = static_cast<hipStream_t>(stream);
-    if (g.cubes <= 2048)
-        hipLaunchKernelGGL(cube_topk_kernel<32>, dim3((items + 3u) / 4u), dim3(256), 0, st, g, s, args->k,
+    if (g.cubes <= 2048) {
+        constexpr size_t lds = (4u * kPaddedRow<32> + 4u * 64u) * sizeof(float);
+        hipLaunchKernelGGL(cube_topk_kernel<32>, dim3((items + 3u) / 4u), dim3(256), lds, st, g, s, args->k,
                            args->local, args->out_stride, idx, cnt);
-    else
-        hipLaunchKernelGGL(cube_topk_kernel<64>, dim3((items + 3u) / 4u), dim3(256), 0, st, g, s, args->k,
+    } else {
+        constexpr size_t lds = (4u * kPaddedRow<64> + 4u * 64u) * sizeof(float);
+        static const int lds_ok = set_lds_limit(reinterpret_cast<const void*>(&cube_topk_kernel<64>), lds);
+        if (lds_ok != MH3_OK)
+            return lds_ok;
+        hipLaunchKernelGGL(cube_topk_kernel<64>, dim3((items + 3u) / 4u), dim3(256), lds, st, g, s, args->k,
                            args->local, args->out_stride, idx, cnt);
+    }
     return host::check_launch();
 }
 
@@ -393,22 +488,14 @@ int mh3_cube_select(const MH3CubeArgs* args, const float* qc, const float* kc, i
         return MH3_ERR_POINTER;
     if (!host::aligned16(qc) || !host::aligned16(kc))
         return MH3_ERR_ALIGN;
-    const size_t lds = size_t(kSelectRows) * g.cubes * sizeof(float);
-    if (lds > 160 * 1024)
-        return MH3_ERR_UNSUPPORTED; // use cube_scores + cube_topk
+    if (g.cubes > kSelectMaxCubes)
+        return MH3_ERR_UNSUPPORTED; // more cubes than the LDS tile holds: use cube_scores + cube_topk
+    static const int lds_ok = set_lds_limit(reinterpret_cast<const void*>(&cube_select_kernel), kSelectLds);
+    if (lds_ok != MH3_OK)
+        return lds_ok;
     const dim3 grid((g.cubes + kSelectRows - 1) / kSelectRows, g.heads);
-    hipStream_t st = static_cast<hipStream_t>(stream);
-    if (g.cubes <= 2048) {
-        if ((rc = set_lds_limit(reinterpret_cast<const void*>(&cube_select_kernel<32>), lds)) != MH3_OK)
-            return rc;
-        hipLaunchKernelGGL(cube_select_kernel<32>, grid, dim3(kSelectThreads), lds, st, g, qc, kc, args->k,
-                           args->local, args->out_stride, idx, cnt);
-    } else {
-        if ((rc = set_lds_limit(reinterpret_cast<const void*>(&cube_select_kernel<64>), lds)) != MH3_OK)
-            return rc;
-        hipLaunchKernelGGL(cube_select_kernel<64>, grid, dim3(kSelectThreads), lds, st, g, qc, kc, args->k,
-                           args->local, args->out_stride, idx, cnt);
-    }
+    hipLaunchKernelGGL(cube_select_kernel, grid, dim3(kSelectThreads), kSelectLds, static_cast<hipStream_t>(stream), g,
+                       qc, kc, args->k, args->local, args->out_stride, idx, cnt);
     return host::check_launch();
 }
 

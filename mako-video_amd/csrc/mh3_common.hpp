@@ -41,24 +41,40 @@ __device__ __forceinline__ float wave_max(float v)
     return v;
 }
 
+// Wave-uniform minimum / maximum of a uint32 through DPP within 16-lane rows and four readlanes.
 __device__ __forceinline__ uint32_t wave_min_u32(uint32_t v)
 {
-#pragma unroll
-    for (int o = 32; o >= 1; o >>= 1) {
-        const uint32_t w = __shfl_xor(v, o, kWave);
-        v = w < v ? w : v;
-    }
-    return v;
+    v = min(v, uint32_t(__builtin_amdgcn_mov_dpp(int(v), 0xB1, 0xF, 0xF, false)));
+    v = min(v, uint32_t(__builtin_amdgcn_mov_dpp(int(v), 0x4E, 0xF, 0xF, false)));
+    v = min(v, uint32_t(__builtin_amdgcn_mov_dpp(int(v), 0x141, 0xF, 0xF, false)));
+    v = min(v, uint32_t(__builtin_amdgcn_mov_dpp(int(v), 0x140, 0xF, 0xF, false)));
+    return min(min(uint32_t(__builtin_amdgcn_readlane(int(v), 0)), uint32_t(__builtin_amdgcn_readlane(int(v), 16))),
+               min(uint32_t(__builtin_amdgcn_readlane(int(v), 32)), uint32_t(__builtin_amdgcn_readlane(int(v), 48))));
 }
 
 __device__ __forceinline__ uint32_t wave_max_u32(uint32_t v)
 {
-#pragma unroll
-    for (int o = 32; o >= 1; o >>= 1) {
-        const uint32_t w = __shfl_xor(v, o, kWave);
-        v = w > v ? w : v;
-    }
-    return v;
+    v = max(v, uint32_t(__builtin_amdgcn_mov_dpp(int(v), 0xB1, 0xF, 0xF, false)));
+    v = max(v, uint32_t(__builtin_amdgcn_mov_dpp(int(v), 0x4E, 0xF, 0xF, false)));
+    v = max(v, uint32_t(__builtin_amdgcn_mov_dpp(int(v), 0x141, 0xF, 0xF, false)));
+    v = max(v, uint32_t(__builtin_amdgcn_mov_dpp(int(v), 0x140, 0xF, 0xF, false)));
+    return max(max(uint32_t(__builtin_amdgcn_readlane(int(v), 0)), uint32_t(__builtin_amdgcn_readlane(int(v), 16))),
+               max(uint32_t(__builtin_amdgcn_readlane(int(v), 32)), uint32_t(__builtin_amdgcn_readlane(int(v), 48))));
+}
+
+// Exclusive prefix sum over the wave's lanes (lane 0 gets 0), through DPP: row_shr 1, 2, 4, 8 give each 16-lane row
+// its inclusive scan (lanes shifted in from outside the row read 0), row_bcast15 and row_bcast31 carry the totals of
+// rows 0 and 0..1 into the rows above.
+__device__ __forceinline__ uint32_t wave_excl_scan_u32(uint32_t v)
+{
+    uint32_t s = v;
+    s += uint32_t(__builtin_amdgcn_update_dpp(0, int(s), 0x111, 0xF, 0xF, false));
+    s += uint32_t(__builtin_amdgcn_update_dpp(0, int(s), 0x112, 0xF, 0xF, false));
+    s += uint32_t(__builtin_amdgcn_update_dpp(0, int(s), 0x114, 0xF, 0xF, false));
+    s += uint32_t(__builtin_amdgcn_update_dpp(0, int(s), 0x118, 0xF, 0xF, false));
+    s += uint32_t(__builtin_amdgcn_update_dpp(0, int(s), 0x142, 0xA, 0xF, false));
+    s += uint32_t(__builtin_amdgcn_update_dpp(0, int(s), 0x143, 0xC, 0xF, false));
+    return s - v;
 }
 
 // Sum over each 16-lane row of the wave, through DPP (no LDS): every lane of a row ends with its row's total.
@@ -71,6 +87,17 @@ __device__ __forceinline__ float row16_sum(float v)
     v += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0x141, 0xF, 0xF, true));
     v += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0x140, 0xF, 0xF, true));
     return v;
+}
+
+// Integer sum over the whole wave through DPP row sums and four readlanes; the result is wave-uniform.
+__device__ __forceinline__ uint32_t wave_sum_u32(uint32_t v)
+{
+    v += uint32_t(__builtin_amdgcn_mov_dpp(int(v), 0xB1, 0xF, 0xF, true));
+    v += uint32_t(__builtin_amdgcn_mov_dpp(int(v), 0x4E, 0xF, 0xF, true));
+    v += uint32_t(__builtin_amdgcn_mov_dpp(int(v), 0x141, 0xF, 0xF, true));
+    v += uint32_t(__builtin_amdgcn_mov_dpp(int(v), 0x140, 0xF, 0xF, true));
+    return uint32_t(__builtin_amdgcn_readlane(int(v), 0)) + uint32_t(__builtin_amdgcn_readlane(int(v), 16)) +
+           uint32_t(__builtin_amdgcn_readlane(int(v), 32)) + uint32_t(__builtin_amdgcn_readlane(int(v), 48));
 }
 
 // Lanes below this one in a 64-bit ballot.
