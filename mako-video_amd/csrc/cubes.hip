@@ -6,8 +6,8 @@
 // - cube_pool: one wavefront per (head, cube) pools q and k together. The wave's four 16-lane quarters take the cube's
 //   four x positions, so each load instruction reads four adjacent rows (1 KiB contiguous per head in the grid
 //   layout); all 32 loads of a lane are in flight at once. Lane sums in float, then a 2-step butterfly.
-// - scores: v_mfma_f32_16x16x4_f32 on 16 x 16 blocks; the 128-long contraction is split over the MFMA's 4 k-lanes
-//   as 4 runs of 32 consecutive dimensions, so every lane's q and k operands are 128 contiguous bytes.
+// - scores: v_mfma_f32_16x16x4_f32 on 16 x 16 blocks; the 128-long contraction is split over the MFMA's 4 k-lanes so
+//   that each operand load of the wave reads 64 contiguous bytes of each of the block's 16 rows.
 // - top-k: one wavefront per (head, query cube) holds the row's scores as order-preserving 32-bit keys in VGPRs, lane l
 //   owning cubes 32 l ... 32 l + 31. It finds the k-th largest key by a binary search over the key range with
 //   per-lane counts and a DPP wave sum, switching to a one-key-per-lane search once at most 64 keys remain in range.
@@ -98,17 +98,18 @@ __global__ __launch_bounds__(256) void cube_pool_kernel(CubeGeo g, const uint16_
         counts[c] = int32_t(nt * ny * nx);
 }
 
-// The 32 contraction operands of lane l for a 16-row block starting at r0: row r0 + l % 16 (clamped to the last row),
-// dimensions [32 (l / 16), 32 (l / 16) + 32).
+// The 32 contraction operands of lane l for a 16-row block starting at r0: row r0 + l % 16 (clamped to the last row);
+// operand 4 v + u is dimension 16 v + 4 (l / 16) + u. Each 16-byte load of the wave thus reads 64 contiguous bytes of
+// each of the 16 rows (16 cache lines, not 64), and the 32 MFMA steps still cover all 128 dimensions once.
 __device__ __forceinline__ void load_operand(const float* __restrict__ base, uint32_t r0, uint32_t rows, float (&v)[32])
 {
     const uint32_t lane = threadIdx.x & 63u;
     uint32_t r = r0 + (lane & 15u);
     r = r < rows ? r : rows - 1u;
-    const float4* p = reinterpret_cast<const float4*>(base + uint64_t(r) * 128u + (lane >> 4) * 32u);
+    const float* p = base + uint64_t(r) * 128u + (lane >> 4) * 4u;
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
-        const float4 t = p[i];
+        const float4 t = *reinterpret_cast<const float4*>(p + 16 * i);
         v[4 * i] = t.x, v[4 * i + 1] = t.y, v[4 * i + 2] = t.z, v[4 * i + 3] = t.w;
     }
 }
