@@ -77,6 +77,25 @@ def bench_fused(mh, dev, steps, warmup):
             HBM_PEAK_GBS, "shape": [ROWS, DIM]}
 
 
+def bench_block_order(mh, dev, steps, warmup):
+    """The block's own order in one pass: x += gate * y, h = modulated RMS norm of the new x (8 bytes an element:
+    read x and y, write x and h), against the two kernels it replaces (10 bytes an element)."""
+    g = torch.Generator(device=dev).manual_seed(2)
+    x = torch.randn((ROWS, DIM), generator=g, device=dev).to(torch.bfloat16)
+    y = torch.randn((ROWS, DIM), generator=g, device=dev).to(torch.bfloat16)
+    w, shift, scale, gate = mod_params(dev, DIM, 3)
+    h = torch.empty_like(x)
+    ms, _ = time_launches(lambda: mh.gate_add_rms_mod_rows(x, y, gate, w, shift, scale, h=h), steps, warmup)
+
+    def two():
+        mh.gate_add_rows(x, y, gate)
+        mh.rms_mod_rows(x, w, shift, scale, out=h)
+    ms2, _ = time_launches(two, steps, warmup)
+    nbytes = ROWS * DIM * 8
+    return {"ms": ms, "bytes": nbytes, "GBs": nbytes / ms / 1e6, "frac": nbytes / ms / 1e6 / HBM_PEAK_GBS,
+            "two_kernel_ms": ms2, "two_kernel_bytes": ROWS * DIM * 10, "shape": [ROWS, DIM]}
+
+
 def bench_copy(dev, steps, warmup):
     """Calibration: a plain device-to-device copy of a 768p-sized bf16 tensor (read + write, 2.65 GB)."""
     src = torch.empty((ROWS, DIM), dtype=torch.bfloat16, device=dev).fill_(1.0)
@@ -221,7 +240,7 @@ def main() -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--only", default="fused,copy,swiglu,select,fc1,rms_f32")
+    ap.add_argument("--only", default="fused,block_order,copy,swiglu,select,fc1,rms_f32")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-compare", action="store_true")
     args = ap.parse_args()
@@ -236,6 +255,9 @@ def main() -> int:
     report = {}
     if "fused" in ops:
         report["fused_rms_mod_gate_add"] = bench_fused(mh, dev, args.steps, args.warmup)
+        torch.cuda.empty_cache()
+    if "block_order" in ops:
+        report["gate_add_rms_mod"] = bench_block_order(mh, dev, args.steps, args.warmup)
         torch.cuda.empty_cache()
     if "copy" in ops:
         report["hbm_copy"] = bench_copy(dev, args.steps, args.warmup)

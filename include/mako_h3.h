@@ -95,6 +95,13 @@ int mh3_gate_add_rows(const MH3RowsArgs* args, void* x, const void* y, const flo
 int mh3_rms_mod_gate_add_rows(const MH3RowsArgs* args, const void* x, const void* residual, const float* w,
                               const float* shift, const float* scale, const float* gate, const uint8_t* set_of_row,
                               void* out, mh3_stream_t stream);
+/* The block's own order after the out projection and after fc2 (docs/architecture.md:61-66): x += gate[s] * y,
+ * then h = the modulated RMS norm of the updated x with this half's w, shift[s] and scale[s], as the next GEMM's
+ * input. One HBM pass (reads x and y, writes x and h) with the same results, bit for bit, as mh3_gate_add_rows
+ * followed by mh3_rms_mod_rows on the updated x. h must not alias x or y. */
+int mh3_gate_add_rms_mod_rows(const MH3RowsArgs* args, void* x, const void* y, const float* gate, const float* w,
+                              const float* shift, const float* scale, const uint8_t* set_of_row, void* h,
+                              mh3_stream_t stream);
 
 /* ---- swiglu_rows -------------------------------------------------------------------------------------------------
  * Reference kernel `swiglu_rows` (mako-common; docs/architecture.md:65,112-114): out = silu(gate) * up with

@@ -14,7 +14,11 @@
 
 namespace mh3 {
 
-enum RowOp { kRmsMod = 0, kGateAdd = 1, kFused = 2 };
+// kGateAddMod is the block's own order: x += gate * y, then h = the modulated norm of the updated (stored) x.
+enum RowOp { kRmsMod = 0, kGateAdd = 1, kFused = 2, kGateAddMod = 3 };
+// Coefficient planes of an op: a and b; kGateAddMod adds c (the gate).
+template <int OP>
+constexpr uint32_t kPlanes = OP == kGateAddMod ? 3u : 2u;
 
 // A 16-byte vector of row elements.
 template <int DT>
@@ -84,9 +88,10 @@ struct RowVec<MH3_F32> {
 };
 
 struct RowsParams {
-    const u32x4_t* x;   // rms_mod / fused: the normed input; gate_add: the addend y
-    const u32x4_t* res; // fused: the residual; gate_add: x (in/out)
-    u32x4_t* out;
+    const u32x4_t* x;   // rms_mod / fused: the normed input; gate_add, gate_add_mod: the addend y
+    const u32x4_t* res; // fused: the residual; gate_add, gate_add_mod: x (in/out)
+    u32x4_t* out;       // gate_add_mod: h
+    u32x4_t* out2;      // gate_add_mod: the updated x
     const float* w;
     const float* shift;
     const float* scale;
@@ -100,9 +105,11 @@ struct RowsParams {
 enum CoefSrc { kCoefReg = 0, kCoefLds = 1, kCoefGlobal = 2 };
 
 // The per-column coefficients of set s: y = (x * inv) * a + b (rms_mod), out = res + (x * inv) * a + b (fused),
-// out = res + a * y (gate_add), for the E columns c0 .. c0 + E - 1 (c0 a multiple of 4), through 16-byte loads.
+// out = res + a * y (gate_add), x' = x + c * y and h = (x' * inv) * a + b (gate_add_mod), for the E columns
+// c0 .. c0 + E - 1 (c0 a multiple of 4), through 16-byte loads.
 template <int OP, int E>
-__device__ __forceinline__ void coef_vec(const RowsParams& p, uint32_t s, uint32_t c0, float (&a)[E], float (&b)[E])
+__device__ __forceinline__ void coef_vec(const RowsParams& p, uint32_t s, uint32_t c0, float (&a)[E], float (&b)[E],
+                                         float (&c)[E])
 {
     const uint64_t i = uint64_t(s) * p.dim + c0;
 #pragma unroll
@@ -138,6 +145,8 @@ __device__ __forceinline__ void coef_vec(const RowsParams& p, uint32_t s, uint32
                     a[4 * q + e] = m;
                     b[4 * q + e] = sh[e];
                 }
+                if constexpr (OP == kGateAddMod)
+                    c[4 * q + e] = g[e];
             }
         }
     }
@@ -155,22 +164,24 @@ __global__ __launch_bounds__(1024) void rows_kernel(RowsParams p)
     const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6, nparts = (blockDim.x >> 6) * 4u;
     const uint32_t nthr = blockDim.x;
 
-    float ca[VPT][E], cb[VPT][E];
+    float ca[VPT][E], cb[VPT][E], cc[VPT][E];
     if constexpr (SRC == kCoefReg) {
 #pragma unroll
         for (int j = 0; j < VPT; ++j)
-            coef_vec<OP, E>(p, 0, min(tid + j * nthr, p.nvec - 1u) * E, ca[j], cb[j]);
+            coef_vec<OP, E>(p, 0, min(tid + j * nthr, p.nvec - 1u) * E, ca[j], cb[j], cc[j]);
     }
     const uint32_t coef_total = p.n_sets * p.dim;
     if constexpr (SRC == kCoefLds) {
         for (uint32_t i = tid; i < p.n_sets * p.nvec; i += nthr) {
             const uint32_t s = i / p.nvec, v = i - s * p.nvec;
-            float a[E], b[E];
-            coef_vec<OP, E>(p, s, v * E, a, b);
+            float a[E], b[E], c[E];
+            coef_vec<OP, E>(p, s, v * E, a, b, c);
 #pragma unroll
             for (int e = 0; e < E; ++e) {
                 ctab[s * p.dim + v * E + e] = a[e];
                 ctab[coef_total + s * p.dim + v * E + e] = b[e];
+                if constexpr (OP == kGateAddMod)
+                    ctab[2 * coef_total + s * p.dim + v * E + e] = c[e];
             }
         }
         __syncthreads();
@@ -191,7 +202,34 @@ __global__ __launch_bounds__(1024) void rows_kernel(RowsParams p)
         }
     };
     // Reduces, modulates and writes row r from registers; `parity` picks the LDS partial-sum slot.
-    auto process = [&](uint32_t r, const u32x4_t (&xv)[VPT], const u32x4_t (&rv)[VPT], uint32_t parity) {
+    auto process = [&](uint32_t r, const u32x4_t (&xin)[VPT], const u32x4_t (&rv)[VPT], uint32_t parity) {
+        const uint32_t set = p.set_of_row ? min(uint32_t(p.set_of_row[r]), p.n_sets - 1u) : 0u;
+        // gate_add_mod: the updated x, rounded and stored first; the norm is of the stored values.
+        u32x4_t xn[VPT];
+        if constexpr (OP == kGateAddMod) {
+            const __amdgpu_buffer_rsrc_t sx = buffer_rsrc(p.out2 + uint64_t(r) * p.nvec, p.nvec * 16u);
+#pragma unroll
+            for (int j = 0; j < VPT; ++j) {
+                const uint32_t v = min(tid + j * nthr, p.nvec - 1u);
+                float f[E], rr[E], o[E], gc[E];
+                V::unpack(xin[j], f);
+                V::unpack(rv[j], rr);
+                if constexpr (SRC == kCoefGlobal) {
+                    float ga[E], gb[E];
+                    coef_vec<OP, E>(p, set, v * E, ga, gb, gc);
+                }
+#pragma unroll
+                for (int e = 0; e < E; ++e) {
+                    const float g = SRC == kCoefReg ? cc[j][e]
+                                    : SRC == kCoefLds ? ctab[2 * coef_total + set * p.dim + v * E + e]
+                                                      : gc[e];
+                    o[e] = fmaf(g, f[e], rr[e]);
+                }
+                xn[j] = V::pack4(o);
+                __builtin_amdgcn_raw_buffer_store_b128(xn[j], sx, (tid + j * nthr) * 16u, 0, kNonTemporal);
+            }
+        }
+        const u32x4_t(&xv)[VPT] = OP == kGateAddMod ? xn : xin;
         float inv = 1.0f;
         if constexpr (OP != kGateAdd) {
             float ss = 0.0f;
@@ -208,7 +246,6 @@ __global__ __launch_bounds__(1024) void rows_kernel(RowsParams p)
                 total += part[w];
             inv = 1.0f / sqrtf(fmaf(total, p.inv_dim, p.eps));
         }
-        const uint32_t set = p.set_of_row ? min(uint32_t(p.set_of_row[r]), p.n_sets - 1u) : 0u;
         // Stores past the row's last vector are dropped by the descriptor.
         const __amdgpu_buffer_rsrc_t so = buffer_rsrc(p.out + uint64_t(r) * p.nvec, p.nvec * 16u);
 #pragma unroll
@@ -216,11 +253,11 @@ __global__ __launch_bounds__(1024) void rows_kernel(RowsParams p)
             const uint32_t v = min(tid + j * nthr, p.nvec - 1u); // clamped for the coefficient reads only
             float f[E], rr[E], o[E];
             V::unpack(xv[j], f);
-            if constexpr (OP != kRmsMod)
+            if constexpr (OP == kGateAdd || OP == kFused)
                 V::unpack(rv[j], rr);
-            float ga[E], gb[E];
+            float ga[E], gb[E], gc[E];
             if constexpr (SRC == kCoefGlobal)
-                coef_vec<OP, E>(p, set, v * E, ga, gb);
+                coef_vec<OP, E>(p, set, v * E, ga, gb, gc);
 #pragma unroll
             for (int e = 0; e < E; ++e) {
                 float a, b;
@@ -234,7 +271,7 @@ __global__ __launch_bounds__(1024) void rows_kernel(RowsParams p)
                     a = ga[e];
                     b = gb[e];
                 }
-                if constexpr (OP == kRmsMod)
+                if constexpr (OP == kRmsMod || OP == kGateAddMod)
                     o[e] = fmaf(f[e] * inv, a, b);
                 else if constexpr (OP == kFused)
                     o[e] = rr[e] + fmaf(f[e] * inv, a, b);
@@ -306,12 +343,14 @@ __global__ __launch_bounds__(MH3_WAVE_BLOCK) void rows_wave_kernel(RowsParams p)
     const uint32_t coef_total = p.n_sets * p.dim;
     for (uint32_t i = tid; SRC == kCoefLds && i < p.n_sets * p.nvec; i += blockDim.x) {
         const uint32_t s = i / p.nvec, v = i - s * p.nvec;
-        float a[E], b[E];
-        coef_vec<OP, E>(p, s, v * E, a, b);
+        float a[E], b[E], c[E];
+        coef_vec<OP, E>(p, s, v * E, a, b, c);
 #pragma unroll
         for (int e = 0; e < E; ++e) {
             ctab[s * p.dim + v * E + e] = a[e];
             ctab[coef_total + s * p.dim + v * E + e] = b[e];
+            if constexpr (OP == kGateAddMod)
+                ctab[2 * coef_total + s * p.dim + v * E + e] = c[e];
         }
     }
     if constexpr (SRC == kCoefLds)
@@ -322,6 +361,34 @@ __global__ __launch_bounds__(MH3_WAVE_BLOCK) void rows_wave_kernel(RowsParams p)
     for (uint32_t row = first; row < last; row += step) {
         load(row);
         const __amdgpu_buffer_rsrc_t so = buffer_rsrc(p.out + uint64_t(row) * p.nvec, p.nvec * 16u);
+        const uint32_t set = p.set_of_row ? min(uint32_t(p.set_of_row[row]), p.n_sets - 1u) : 0u;
+        if constexpr (OP == kGateAddMod) {
+            // x' = x + gate * y, rounded and stored; it replaces y in xv, and the norm below is of the stored values.
+            const __amdgpu_buffer_rsrc_t sx = buffer_rsrc(p.out2 + uint64_t(row) * p.nvec, p.nvec * 16u);
+            const float* tc = ctab + 2 * coef_total + set * p.dim;
+#pragma unroll
+            for (int j = 0; j < NV; ++j) {
+                const uint32_t v = min(lane + 64u * j, p.nvec - 1u);
+                float f[E], rr[E], o[E], g[E];
+                if constexpr (SRC == kCoefLds) {
+#pragma unroll
+                    for (int q = 0; q < E / 4; ++q) {
+                        const float4 t4 = *reinterpret_cast<const float4*>(tc + v * E + 4 * q);
+                        g[4 * q] = t4.x, g[4 * q + 1] = t4.y, g[4 * q + 2] = t4.z, g[4 * q + 3] = t4.w;
+                    }
+                } else {
+                    float ga[E], gb[E];
+                    coef_vec<OP, E>(p, set, v * E, ga, gb, g);
+                }
+                V::unpack(xv[j], f);
+                V::unpack(rv[j], rr);
+#pragma unroll
+                for (int e = 0; e < E; ++e)
+                    o[e] = fmaf(g[e], f[e], rr[e]);
+                xv[j] = V::pack4(o);
+                __builtin_amdgcn_raw_buffer_store_b128(xv[j], sx, (lane + 64u * j) * 16u, 0, kNonTemporal);
+            }
+        }
         float inv = 1.0f;
         if constexpr (OP != kGateAdd) {
             float ss = 0.0f;
@@ -339,7 +406,6 @@ __global__ __launch_bounds__(MH3_WAVE_BLOCK) void rows_wave_kernel(RowsParams p)
                                 __int_as_float(__builtin_amdgcn_readlane(__float_as_int(ss), 48));
             inv = 1.0f / sqrtf(fmaf(total, p.inv_dim, p.eps));
         }
-        const uint32_t set = p.set_of_row ? min(uint32_t(p.set_of_row[row]), p.n_sets - 1u) : 0u;
         const float* ta = ctab + set * p.dim;
         const float* tb = ctab + coef_total + set * p.dim;
 #pragma unroll
@@ -355,14 +421,15 @@ __global__ __launch_bounds__(MH3_WAVE_BLOCK) void rows_wave_kernel(RowsParams p)
                     b[4 * q] = tb4.x, b[4 * q + 1] = tb4.y, b[4 * q + 2] = tb4.z, b[4 * q + 3] = tb4.w;
                 }
             } else {
-                coef_vec<OP, E>(p, set, v * E, a, b);
+                float c[E];
+                coef_vec<OP, E>(p, set, v * E, a, b, c);
             }
             V::unpack(xv[j], f);
-            if constexpr (OP != kRmsMod)
+            if constexpr (OP == kGateAdd || OP == kFused)
                 V::unpack(rv[j], rr);
 #pragma unroll
             for (int e = 0; e < E; ++e) {
-                if constexpr (OP == kRmsMod)
+                if constexpr (OP == kRmsMod || OP == kGateAddMod)
                     o[e] = fmaf(f[e] * inv, a[e], b[e]);
                 else if constexpr (OP == kFused)
                     o[e] = rr[e] + fmaf(f[e] * inv, a[e], b[e]);
@@ -485,7 +552,9 @@ template <int DT, int OP>
 int launch_rows_wave(const RowsParams& p, hipStream_t stream)
 {
     const uint32_t need = (p.nvec + 63u) / 64u;
-    const int src = MH3_WAVE_SRC;
+    const int src = MH3_WAVE_SRC == kCoefLds && size_t(p.n_sets) * p.dim * kPlanes<OP> * sizeof(float) <= kCoefLdsMax
+                        ? kCoefLds
+                        : kCoefGlobal;
     const void* k = nullptr;
     if (need <= 2)
         k = pick_wave_kernel<DT, 2, OP>(src);
@@ -498,7 +567,7 @@ int launch_rows_wave(const RowsParams& p, hipStream_t stream)
     else
         k = pick_wave_kernel<DT, 12, OP>(src);
     const uint32_t threads = MH3_WAVE_BLOCK, waves = threads / 64u;
-    const size_t lds = src == kCoefLds ? size_t(p.n_sets) * p.dim * 2 * sizeof(float) : 0;
+    const size_t lds = src == kCoefLds ? size_t(p.n_sets) * p.dim * kPlanes<OP> * sizeof(float) : 0;
     RowsParams arg = p;
     uint64_t blocks;
     constexpr uint32_t kWaveRows = MH3_WAVE_ROWS;
@@ -524,9 +593,11 @@ int launch_rows_dt(const RowsParams& p, hipStream_t stream)
 {
     if (MH3_ROWS_WAVE && p.nvec <= 12u * 64u && size_t(p.n_sets) * p.dim * 2 * sizeof(float) <= kCoefLdsMax)
         return launch_rows_wave<DT, OP>(p, stream);
+    // (The choice between the two kernels depends on the two-plane table size for every op, so gate_add_mod reduces
+    // in the same order as rms_mod and their norms agree bit for bit.)
     // Threads a row: enough for VPT vectors each, rounded up to whole waves.
-    const int src = p.n_sets == 1 ? kCoefReg
-                    : (size_t(p.n_sets) * p.dim * 2 * sizeof(float) <= kCoefLdsMax ? kCoefLds : kCoefGlobal);
+    const size_t table = size_t(p.n_sets) * p.dim * kPlanes<OP> * sizeof(float);
+    const int src = p.n_sets == 1 ? kCoefReg : (table <= kCoefLdsMax ? kCoefLds : kCoefGlobal);
     const void* k = nullptr;
     uint32_t threads = 0;
     if ((p.nvec + 1) / 2 <= 1024) {
@@ -538,7 +609,7 @@ int launch_rows_dt(const RowsParams& p, hipStream_t stream)
     } else {
         return MH3_ERR_UNSUPPORTED;
     }
-    const size_t lds = 128 * sizeof(float) + (src == kCoefLds ? size_t(p.n_sets) * p.dim * 2 * sizeof(float) : 0);
+    const size_t lds = 128 * sizeof(float) + (src == kCoefLds ? table : 0);
     const int per_cu = host::blocks_per_cu(k, int(threads), lds);
     uint64_t blocks = p.rows;
     constexpr uint32_t kRowsPerBlock = MH3_ROWS_PER_BLOCK;
@@ -660,6 +731,35 @@ int mh3_rms_mod_gate_add_rows(const MH3RowsArgs* args, const void* x, const void
     p.gate = gate;
     p.set_of_row = set_of_row;
     return launch_rows<kFused>(args, p, static_cast<hipStream_t>(stream));
+}
+
+int mh3_gate_add_rms_mod_rows(const MH3RowsArgs* args, void* x, const void* y, const float* gate, const float* w,
+                              const float* shift, const float* scale, const uint8_t* set_of_row, void* h,
+                              mh3_stream_t stream)
+{
+    int rc = check_rows(args, true);
+    if (rc != MH3_OK)
+        return rc;
+    if (args->rows == 0)
+        return MH3_OK;
+    if (!x || !y || !gate || !shift || !scale || !h)
+        return MH3_ERR_POINTER;
+    if (h == x || h == y)
+        return MH3_ERR_PARAM; // h is a separate tensor
+    if (!host::aligned16(x) || !host::aligned16(y) || !host::aligned16(h) || !host::aligned16(gate) ||
+        !host::aligned16(w) || !host::aligned16(shift) || !host::aligned16(scale))
+        return MH3_ERR_ALIGN;
+    RowsParams p{};
+    p.x = static_cast<const u32x4_t*>(y);
+    p.res = static_cast<const u32x4_t*>(x);
+    p.out2 = static_cast<u32x4_t*>(x);
+    p.out = static_cast<u32x4_t*>(h);
+    p.w = w;
+    p.shift = shift;
+    p.scale = scale;
+    p.gate = gate;
+    p.set_of_row = set_of_row;
+    return launch_rows<kGateAddMod>(args, p, static_cast<hipStream_t>(stream));
 }
 
 int mh3_swiglu_rows(const MH3SwigluArgs* a, const void* gate, const void* up, void* out, mh3_stream_t stream)

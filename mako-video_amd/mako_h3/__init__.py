@@ -67,6 +67,7 @@ def _load() -> C.CDLL:
         "mh3_rms_mod_rows": (I32, [C.POINTER(RowsArgs), P, P, P, P, P, P, P]),
         "mh3_gate_add_rows": (I32, [C.POINTER(RowsArgs), P, P, P, P, P]),
         "mh3_rms_mod_gate_add_rows": (I32, [C.POINTER(RowsArgs), P, P, P, P, P, P, P, P, P]),
+        "mh3_gate_add_rms_mod_rows": (I32, [C.POINTER(RowsArgs), P, P, P, P, P, P, P, P, P]),
         "mh3_swiglu_rows": (I32, [C.POINTER(SwigluArgs), P, P, P, P]),
         "mh3_cube_pool": (I32, [C.POINTER(CubeArgs), P, P, P, P, P, P]),
         "mh3_cube_scores": (I32, [C.POINTER(CubeArgs), P, P, P, P]),
@@ -203,6 +204,20 @@ def rms_mod_gate_add_rows(x, residual, w, shift, scale, gate, *, eps=1e-6, set_o
     _check(lib.mh3_rms_mod_gate_add_rows(C.byref(a), _ptr(x), _ptr(residual), _ptr(w), _ptr(shift), _ptr(scale),
                                          _ptr(gate), _ptr(set_of_row), _ptr(out), _stream()), "rms_mod_gate_add_rows")
     return out
+
+
+def gate_add_rms_mod_rows(x, y, gate, w, shift, scale, *, eps=1e-6, set_of_row=None, n_sets=1, h=None):
+    """The block's order: x += gate[s] * y in place, then h = x * rsqrt(mean(x^2) + eps) * w * (1 + scale[s]) +
+    shift[s] of the updated x; one HBM pass. Returns h."""
+    a = _rows_args(x, n_sets, eps)
+    _need(x, "x", x.dtype, x.numel())
+    _need(y, "y", x.dtype, x.numel())
+    _mod_params(x.shape[1], n_sets, w, shift, scale, gate, set_of_row, x.shape[0])
+    h = torch.empty_like(x) if h is None else h
+    _need(h, "h", x.dtype, x.numel())
+    _check(lib.mh3_gate_add_rms_mod_rows(C.byref(a), _ptr(x), _ptr(y), _ptr(gate), _ptr(w), _ptr(shift), _ptr(scale),
+                                         _ptr(set_of_row), _ptr(h), _stream()), "gate_add_rms_mod_rows")
+    return h
 
 
 # ---- swiglu --------------------------------------------------------------------------------------------------------
