@@ -1,0 +1,219 @@
+// mako_h3.hpp — C++ host layer over the C-ABI in mako_h3.h, for C++ callers of the H3 block's hot-path kernels.
+//
+// The reference drives these kernels from C++ through named dispatch (mako-common's TransformerRuntime; the in-repo
+// instance is src/video/audio_vae.cpp:151-177): the host validates shapes and throws std::runtime_error
+// (audio_vae.cpp:231-232, src/video/engine.cpp:681-682), buffers belong to the caller (reserve()/scratch()), and
+// finish(cb) waits for the queue (audio_vae.cpp:242-247). This layer keeps that shape on MI355X:
+//   - one member function of Kernels per reference kernel name, with the reference's argument meaning;
+//   - errors from the library (MH3_ERR_*) and from HIP become std::runtime_error naming the kernel;
+//   - Kernels::finish() is hipStreamSynchronize on the Kernels' stream;
+//   - DeviceBuffer<T> is caller-owned device memory; no kernel allocates;
+//   - parse_int8 returns std::optional like H3::parse_int8 (tools/mako_video.cpp:110).
+// Header-only; link libmako_h3.so and libamdhip64.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+#include <cstdio>
+#include <optional>
+#include <stdexcept>
+#include <string>
+#include <vector>
+
+#include "mako_h3.h"
+
+namespace mako::h3 {
+
+inline std::runtime_error error(const char* what, int rc)
+{
+    char msg[256];
+    std::snprintf(msg, sizeof msg, "%s: %s%s%s", what, mh3_strerror(rc), rc == MH3_ERR_HIP ? ": " : "",
+                  rc == MH3_ERR_HIP ? mh3_last_hip_error() : "");
+    return std::runtime_error(msg);
+}
+
+inline void check(int rc, const char* what)
+{
+    if (rc != MH3_OK)
+        throw error(what, rc);
+}
+
+inline void check_hip(hipError_t e, const char* what)
+{
+    if (e != hipSuccess)
+        throw std::runtime_error(std::string(what) + ": " + hipGetErrorString(e));
+}
+
+// Caller-owned device memory of n elements of T.
+template <class T>
+class DeviceBuffer {
+public:
+    DeviceBuffer() = default;
+    explicit DeviceBuffer(size_t n) : n_(n)
+    {
+        if (n)
+            check_hip(hipMalloc(reinterpret_cast<void**>(&p_), n * sizeof(T)), "hipMalloc");
+    }
+    explicit DeviceBuffer(const std::vector<T>& host) : DeviceBuffer(host.size()) { upload(host); }
+    DeviceBuffer(const DeviceBuffer&) = delete;
+    DeviceBuffer& operator=(const DeviceBuffer&) = delete;
+    DeviceBuffer(DeviceBuffer&& o) noexcept : p_(o.p_), n_(o.n_) { o.p_ = nullptr, o.n_ = 0; }
+    ~DeviceBuffer()
+    {
+        if (p_)
+            (void)hipFree(p_);
+    }
+    T* get() const { return p_; }
+    size_t size() const { return n_; }
+    void upload(const std::vector<T>& host)
+    {
+        if (host.size() != n_)
+            throw std::runtime_error("DeviceBuffer::upload: size mismatch");
+        check_hip(hipMemcpy(p_, host.data(), n_ * sizeof(T), hipMemcpyHostToDevice), "hipMemcpy");
+    }
+    std::vector<T> download() const
+    {
+        std::vector<T> h(n_);
+        check_hip(hipMemcpy(h.data(), p_, n_ * sizeof(T), hipMemcpyDeviceToHost), "hipMemcpy");
+        return h;
+    }
+
+private:
+    T* p_ = nullptr;
+    size_t n_ = 0;
+};
+
+// The per-row modulation of a row kernel: set s(r) = set_of_row[r] (device; nullptr: set 0) picks row s of the
+// [n_sets][dim] shift, scale and gate vectors; w is the norm's [dim] weight (nullptr: all 1).
+struct Modulation {
+    const float* w = nullptr;
+    const float* shift = nullptr;
+    const float* scale = nullptr;
+    const float* gate = nullptr;
+    const uint8_t* set_of_row = nullptr;
+    uint32_t n_sets = 1;
+};
+
+// The H3 grid of generated video rows and the sparse selector's parameters (H3::Cubes, H3::set_sparse).
+struct Cubes {
+    uint32_t heads = 0, t = 0, h = 0, w = 0;
+    float ratio = 0.1f;
+    uint32_t local = 1;
+    uint32_t layout = MH3_CUBES_GRID;
+    uint64_t row0 = 0, head_stride = 0, row_stride = 128;
+
+    uint32_t count() const { return uint32_t(mh3_cube_count(t, h, w)); }
+    uint32_t k() const
+    {
+        const int64_t k = mh3_topk_k(ratio, count());
+        if (k < 0)
+            throw error("set_sparse", int(k));
+        return uint32_t(k);
+    }
+    uint32_t out_stride() const { return k() + local; }
+    MH3CubeArgs args() const
+    {
+        check(mh3_check_sparse(ratio, local), "set_sparse");
+        return MH3CubeArgs{heads, 128, t, h, w, layout, row0, head_stride ? head_stride : uint64_t(t) * h * w * 128,
+                           row_stride, k(), local, out_stride(), 0};
+    }
+};
+
+inline std::optional<uint32_t> parse_int8(const std::string& text)
+{
+    uint32_t mask = 0;
+    if (mh3_parse_int8(text.c_str(), &mask) != MH3_OK)
+        return std::nullopt;
+    return mask;
+}
+
+// The block's row, sparse-selector and int8 kernels on one stream, asynchronous until finish().
+class Kernels {
+public:
+    explicit Kernels(hipStream_t stream = nullptr) : s_(stream) {}
+    hipStream_t stream() const { return s_; }
+    void finish() const { check_hip(hipStreamSynchronize(s_), "finish"); }
+
+    // y = rmsnorm(x) * w * (1 + scale[s]) + shift[s]
+    void rms_mod_rows(uint32_t rows, uint32_t dim, uint32_t dtype, const void* x, const Modulation& m, void* y,
+                      float eps = 1e-6f) const
+    {
+        const MH3RowsArgs a = rows_args(rows, dim, dtype, m, eps);
+        check(mh3_rms_mod_rows(&a, x, m.w, m.shift, m.scale, m.set_of_row, y, s_), "rms_mod_rows");
+    }
+    // x += gate[s] * y
+    void gate_add_rows(uint32_t rows, uint32_t dim, uint32_t dtype, void* x, const void* y, const Modulation& m) const
+    {
+        const MH3RowsArgs a = rows_args(rows, dim, dtype, m, 1.0f);
+        check(mh3_gate_add_rows(&a, x, y, m.gate, m.set_of_row, s_), "gate_add_rows");
+    }
+    // out = residual + gate[s] * rms_mod(x)
+    void rms_mod_gate_add_rows(uint32_t rows, uint32_t dim, uint32_t dtype, const void* x, const void* residual,
+                               const Modulation& m, void* out, float eps = 1e-6f) const
+    {
+        const MH3RowsArgs a = rows_args(rows, dim, dtype, m, eps);
+        check(mh3_rms_mod_gate_add_rows(&a, x, residual, m.w, m.shift, m.scale, m.gate, m.set_of_row, out, s_),
+              "rms_mod_gate_add_rows");
+    }
+    // x += gate[s] * y; h = rms_mod(x)  (the block's order: gate_add_rows then rms_mod_rows, in one pass)
+    void gate_add_rms_mod_rows(uint32_t rows, uint32_t dim, uint32_t dtype, void* x, const void* y,
+                               const Modulation& m, void* h, float eps = 1e-6f) const
+    {
+        const MH3RowsArgs a = rows_args(rows, dim, dtype, m, eps);
+        check(mh3_gate_add_rms_mod_rows(&a, x, y, m.gate, m.w, m.shift, m.scale, m.set_of_row, h, s_),
+              "gate_add_rms_mod_rows");
+    }
+    // out = silu(gate) * up; up == nullptr: gate is fc1's [rows][2 dim] row [gate | up]
+    void swiglu_rows(uint32_t rows, uint32_t dim, uint32_t dtype, const void* gate, const void* up, void* out) const
+    {
+        const MH3SwigluArgs a{rows, dim, up ? uint32_t(MH3_SWIGLU_SPLIT) : uint32_t(MH3_SWIGLU_FUSED), dtype};
+        check(mh3_swiglu_rows(&a, gate, up, out, s_), "swiglu_rows");
+    }
+
+    void cube_pool(const Cubes& c, const uint16_t* q, const uint16_t* k, float* qc, float* kc,
+                   int32_t* counts = nullptr) const
+    {
+        const MH3CubeArgs a = c.args();
+        check(mh3_cube_pool(&a, q, k, qc, kc, counts, s_), "cube_pool");
+    }
+    void cube_scores(const Cubes& c, const float* qc, const float* kc, float* s) const
+    {
+        const MH3CubeArgs a = c.args();
+        check(mh3_cube_scores(&a, qc, kc, s, s_), "cube_scores");
+    }
+    void cube_topk(const Cubes& c, const float* s, int32_t* idx, int32_t* cnt) const
+    {
+        const MH3CubeArgs a = c.args();
+        check(mh3_cube_topk(&a, s, idx, cnt, s_), "cube_topk");
+    }
+    // cube_scores + cube_topk with the scores on chip
+    void cube_select(const Cubes& c, const float* qc, const float* kc, int32_t* idx, int32_t* cnt) const
+    {
+        const MH3CubeArgs a = c.args();
+        check(mh3_cube_select(&a, qc, kc, idx, cnt, s_), "cube_scores+cube_topk");
+    }
+
+    // Weight rows to int8 with one scale each (at load)
+    void quant_rows_i8(uint32_t rows, uint32_t cols, uint32_t dtype, const void* w, int8_t* q, float* scale) const
+    {
+        const MH3QuantArgs a{rows, cols, dtype, 0};
+        check(mh3_quant_rows_i8(&a, w, q, scale, s_), "quant_rows_i8");
+    }
+    // fc1 with int8 weights [2 ffn][dim] and SwiGLU: out[m][ffn] = silu(x Wg sg) * (x Wu su)
+    void fc1_swiglu_i8(uint32_t m, uint32_t ffn, uint32_t dim, const uint16_t* x, const int8_t* w, const float* scale,
+                       uint16_t* out) const
+    {
+        const MH3GemmArgs a{m, ffn, dim, 0};
+        check(mh3_gemm_w8a16_swiglu(&a, x, w, scale, out, s_), "gemm_i8+swiglu_rows");
+    }
+
+private:
+    static MH3RowsArgs rows_args(uint32_t rows, uint32_t dim, uint32_t dtype, const Modulation& m, float eps)
+    {
+        return MH3RowsArgs{rows, dim, m.n_sets, dtype, eps, {0, 0, 0}};
+    }
+    hipStream_t s_;
+};
+
+} // namespace mako::h3

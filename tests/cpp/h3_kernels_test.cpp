@@ -1,0 +1,302 @@
+// The H3 block's hot-path kernels through the C++ host layer (mako_h3.hpp) on the GPU, against the CPU oracle
+// (oracle/mh3_oracle.h, the checker), reported the way the reference's tests/h3_ref_test.cpp reports: one line per
+// check, "ok" or "FAIL", the relative RMS error and the lowest row cosine of diff() (h3_ref_test.cpp:67-90), and
+// the number of failures as the exit status.
+//   h3_kernels_test [rows | swiglu | cubes | int8 | errors | all]
+#include "mako_h3.hpp"
+#include "mh3_oracle.h"
+
+#include <algorithm>
+#include <cmath>
+#include <cstdio>
+#include <cstring>
+#include <functional>
+#include <string>
+#include <vector>
+
+namespace {
+
+using namespace mako::h3;
+
+int failures = 0;
+
+void check(bool ok, const std::string& what)
+{
+    std::printf("  %-4s %s\n", ok ? "ok" : "FAIL", what.c_str());
+    std::fflush(stdout);
+    failures += !ok;
+}
+
+// Relative RMS error over everything and the lowest cosine similarity of a row of `width` (the reference's diff()).
+struct Diff {
+    double rel = 0, min_cos = 1;
+};
+Diff diff(const std::vector<double>& got, const std::vector<double>& want, size_t width)
+{
+    Diff d;
+    double e = 0, r = 0;
+    for (size_t i = 0; i < want.size(); ++i) {
+        e += (got[i] - want[i]) * (got[i] - want[i]);
+        r += want[i] * want[i];
+    }
+    d.rel = r > 0 ? std::sqrt(e / r) : std::sqrt(e);
+    for (size_t row = 0; row < want.size() / width; ++row) {
+        double gw = 0, gg = 0, ww = 0;
+        for (size_t i = row * width; i < (row + 1) * width; ++i)
+            gw += got[i] * want[i], gg += got[i] * got[i], ww += want[i] * want[i];
+        d.min_cos = std::min(d.min_cos, ww > 0 && gg > 0 ? gw / std::sqrt(gg * ww) : 1.0);
+    }
+    return d;
+}
+
+// Every element within rtol relative (plus atol), and the diff() pair, in one check line.
+void compare(const std::string& what, const std::vector<double>& got, const std::vector<double>& want, size_t width,
+             double rtol, double atol)
+{
+    if (got.size() != want.size()) {
+        check(false, what + ": size mismatch");
+        return;
+    }
+    size_t bad = 0;
+    for (size_t i = 0; i < want.size(); ++i)
+        bad += !(std::fabs(got[i] - want[i]) <= rtol * std::fabs(want[i]) + atol);
+    const Diff d = diff(got, want, width);
+    char msg[256];
+    std::snprintf(msg, sizeof msg, "%s: %zu rows, rel error %.2e, lowest row cosine %.6f, %zu beyond tolerance",
+                  what.c_str(), want.size() / width, d.rel, d.min_cos, bad);
+    check(bad == 0, msg);
+}
+
+// Deterministic inputs: splitmix64 and Box-Muller.
+struct Rng {
+    uint64_t s;
+    explicit Rng(uint64_t seed) : s(seed) {}
+    uint64_t next()
+    {
+        uint64_t z = (s += 0x9E3779B97F4A7C15ull);
+        z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+        z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+        return z ^ (z >> 31);
+    }
+    double uniform() { return (double(next() >> 11) + 0.5) * 0x1.0p-53; }
+    double normal() { return std::sqrt(-2.0 * std::log(uniform())) * std::cos(6.283185307179586 * uniform()); }
+};
+
+std::vector<float> normals(Rng& r, size_t n, double sd = 1.0, double mean = 0.0)
+{
+    std::vector<float> v(n);
+    for (auto& x : v)
+        x = float(mean + sd * r.normal());
+    return v;
+}
+std::vector<uint16_t> bf16_normals(Rng& r, size_t n)
+{
+    std::vector<uint16_t> v(n);
+    for (auto& x : v)
+        x = mh3o_bf16_from_double(r.normal());
+    return v;
+}
+std::vector<double> of_bf16(const std::vector<uint16_t>& v)
+{
+    std::vector<double> d(v.size());
+    for (size_t i = 0; i < v.size(); ++i)
+        d[i] = mh3o_bf16_to_float(v[i]);
+    return d;
+}
+std::vector<double> of_f32(const std::vector<float>& v) { return {v.begin(), v.end()}; }
+
+void rows()
+{
+    std::printf("rows\n");
+    Rng r(0);
+    {
+        // Modulated RMS norm, fp32, 4096 x 1024 (the reference's CPU-runnable case), at 1e-5.
+        const uint32_t n = 4096, d = 1024;
+        auto x = normals(r, size_t(n) * d), shift = normals(r, d, 0.1), scale = normals(r, d, 0.1);
+        auto w = normals(r, d, 0.02, 1.0);
+        DeviceBuffer<float> dx(x), dw(w), dsh(shift), dsc(scale), dy(size_t(n) * d);
+        Kernels k;
+        Modulation m{dw.get(), dsh.get(), dsc.get(), nullptr, nullptr, 1};
+        k.rms_mod_rows(n, d, MH3_F32, dx.get(), m, dy.get());
+        k.finish();
+        std::vector<float> want(x.size());
+        mh3o_rms_mod_rows(n, d, 1e-6f, MH3O_F32, x.data(), w.data(), shift.data(), scale.data(), nullptr, want.data());
+        compare("rms_mod_rows f32 4096x1024", of_f32(dy.download()), of_f32(want), d, 1e-5, 1e-6);
+    }
+    {
+        // Fused modulated norm + gated residual, bf16, three modulation sets picked per row.
+        const uint32_t n = 67, d = 5120, sets = 3;
+        auto x = bf16_normals(r, size_t(n) * d), res = bf16_normals(r, size_t(n) * d);
+        auto shift = normals(r, sets * d, 0.1), scale = normals(r, sets * d, 0.1), gate = normals(r, sets * d, 0.1);
+        auto w = normals(r, d, 0.02, 1.0);
+        std::vector<uint8_t> set(n);
+        for (auto& s : set)
+            s = uint8_t(r.next() % sets);
+        DeviceBuffer<uint16_t> dx(x), dres(res), dout(size_t(n) * d);
+        DeviceBuffer<float> dw(w), dsh(shift), dsc(scale), dg(gate);
+        DeviceBuffer<uint8_t> dset(set);
+        Kernels k;
+        Modulation m{dw.get(), dsh.get(), dsc.get(), dg.get(), dset.get(), sets};
+        k.rms_mod_gate_add_rows(n, d, MH3_BF16, dx.get(), dres.get(), m, dout.get());
+        k.finish();
+        std::vector<uint16_t> want(x.size());
+        mh3o_rms_mod_gate_add_rows(n, d, 1e-6f, MH3O_BF16, x.data(), res.data(), w.data(), shift.data(), scale.data(),
+                                   gate.data(), set.data(), want.data());
+        compare("rms_mod_gate_add_rows bf16 67x5120, 3 sets", of_bf16(dout.download()), of_bf16(want), d, 1e-2, 1e-5);
+
+        // The block's order in one pass equals gate_add_rows then rms_mod_rows, bit for bit.
+        DeviceBuffer<uint16_t> xa(x), xb(x), ha(size_t(n) * d), hb(size_t(n) * d);
+        k.gate_add_rms_mod_rows(n, d, MH3_BF16, xa.get(), dres.get(), m, ha.get());
+        k.gate_add_rows(n, d, MH3_BF16, xb.get(), dres.get(), m);
+        k.rms_mod_rows(n, d, MH3_BF16, xb.get(), m, hb.get());
+        k.finish();
+        check(xa.download() == xb.download() && ha.download() == hb.download(),
+              "gate_add_rms_mod_rows == gate_add_rows then rms_mod_rows, bit for bit");
+        std::vector<uint16_t> want_x = x;
+        mh3o_gate_add_rows(n, d, MH3O_BF16, want_x.data(), res.data(), gate.data(), set.data());
+        compare("gate_add_rows bf16 67x5120, 3 sets", of_bf16(xb.download()), of_bf16(want_x), d, 1e-2, 1e-5);
+    }
+}
+
+void swiglu()
+{
+    std::printf("swiglu\n");
+    Rng r(1);
+    const uint32_t n = 130, d = 1000;
+    auto gu = bf16_normals(r, size_t(n) * 2 * d);
+    std::vector<uint16_t> g(size_t(n) * d), u(size_t(n) * d);
+    for (uint32_t i = 0; i < n; ++i)
+        for (uint32_t c = 0; c < d; ++c)
+            g[size_t(i) * d + c] = gu[size_t(i) * 2 * d + c], u[size_t(i) * d + c] = gu[size_t(i) * 2 * d + d + c];
+    DeviceBuffer<uint16_t> dgu(gu), dg(g), du(u), o1(size_t(n) * d), o2(size_t(n) * d);
+    Kernels k;
+    k.swiglu_rows(n, d, MH3_BF16, dgu.get(), nullptr, o1.get());
+    k.swiglu_rows(n, d, MH3_BF16, dg.get(), du.get(), o2.get());
+    k.finish();
+    std::vector<uint16_t> want(size_t(n) * d);
+    mh3o_swiglu_rows(n, d, MH3O_SWIGLU_FUSED, MH3O_BF16, gu.data(), nullptr, want.data());
+    compare("swiglu_rows fused row bf16 130x1000", of_bf16(o1.download()), of_bf16(want), d, 1e-2, 1e-6);
+    compare("swiglu_rows split bf16 130x1000", of_bf16(o2.download()), of_bf16(want), d, 1e-2, 1e-6);
+}
+
+void cubes()
+{
+    std::printf("cubes\n");
+    Rng r(2);
+    Cubes c;
+    c.heads = 3, c.t = 8, c.h = 8, c.w = 12, c.ratio = 0.25f, c.local = 3;
+    const uint32_t rows = c.t * c.h * c.w, C = c.count(), kk = c.k();
+    auto q = bf16_normals(r, size_t(c.heads) * rows * 128), key = bf16_normals(r, size_t(c.heads) * rows * 128);
+    DeviceBuffer<uint16_t> dq(q), dk(key);
+    DeviceBuffer<float> qc(size_t(c.heads) * C * 128), kc(size_t(c.heads) * C * 128), s(size_t(c.heads) * C * C);
+    DeviceBuffer<int32_t> counts(C), idx(size_t(c.heads) * C * c.out_stride()), cnt(size_t(c.heads) * C);
+    DeviceBuffer<int32_t> idx2(size_t(c.heads) * C * c.out_stride()), cnt2(size_t(c.heads) * C);
+    Kernels k;
+    k.cube_pool(c, dq.get(), dk.get(), qc.get(), kc.get(), counts.get());
+    k.cube_scores(c, qc.get(), kc.get(), s.get());
+    k.cube_topk(c, s.get(), idx.get(), cnt.get());
+    k.cube_select(c, qc.get(), kc.get(), idx2.get(), cnt2.get());
+    k.finish();
+    std::vector<float> wq(qc.size()), wk(kc.size());
+    std::vector<int32_t> wc(C);
+    mh3o_cube_pool(c.heads, 128, c.t, c.h, c.w, MH3O_CUBES_GRID, 0, uint64_t(rows) * 128, 128, q.data(), key.data(),
+                   wq.data(), wk.data(), wc.data());
+    compare("cube_pool q 3 heads, 8x8x12 grid", of_f32(qc.download()), of_f32(wq), 128, 1e-5, 1e-6);
+    compare("cube_pool k 3 heads, 8x8x12 grid", of_f32(kc.download()), of_f32(wk), 128, 1e-5, 1e-6);
+    check(counts.download() == wc, "cube_pool counts");
+    std::vector<double> s64(s.size());
+    mh3o_cube_scores(c.heads, C, 128, qc.download().data(), kc.download().data(), s64.data());
+    const auto sg = s.download();
+    double worst = 0;
+    for (uint32_t row = 0; row < c.heads * C; ++row) {
+        double m = 0;
+        for (uint32_t j = 0; j < C; ++j)
+            m = std::max(m, std::fabs(s64[size_t(row) * C + j]));
+        for (uint32_t j = 0; j < C; ++j)
+            worst = std::max(worst, std::fabs(sg[size_t(row) * C + j] - s64[size_t(row) * C + j]) / m);
+    }
+    check(worst <= 1e-5, "cube_scores within 1e-5 of the row's largest |score|");
+    // The oracle's selection over the GPU's own float scores is the GPU's, bit for bit (fused and not).
+    std::vector<double> sd(sg.begin(), sg.end());
+    std::vector<int32_t> widx(idx.size()), wcnt(cnt.size());
+    mh3o_cube_topk(c.heads, c.t, c.h, c.w, kk, c.local, c.out_stride(), sd.data(), widx.data(), wcnt.data());
+    check(idx.download() == widx && cnt.download() == wcnt, "cube_topk == the oracle's top-k of the same scores");
+    check(idx2.download() == widx && cnt2.download() == wcnt, "cube_select == cube_scores + cube_topk");
+}
+
+void int8()
+{
+    std::printf("int8\n");
+    Rng r(3);
+    const uint32_t m = 300, n = 384, d = 320;
+    auto w = normals(r, size_t(2) * n * d, 0.05);
+    DeviceBuffer<float> dw(w), ds(2 * n);
+    DeviceBuffer<int8_t> dq(size_t(2) * n * d);
+    Kernels k;
+    k.quant_rows_i8(2 * n, d, MH3_F32, dw.get(), dq.get(), ds.get());
+    k.finish();
+    std::vector<int8_t> wq(dq.size());
+    std::vector<float> ws(2 * n);
+    mh3o_quant_rows_i8(2 * n, d, MH3O_F32, w.data(), wq.data(), ws.data());
+    check(dq.download() == wq && ds.download() == ws, "quant_rows_i8 bit for bit, 768x320");
+    auto x = bf16_normals(r, size_t(m) * d);
+    DeviceBuffer<uint16_t> dx(x), out(size_t(m) * n);
+    k.fc1_swiglu_i8(m, n, d, dx.get(), dq.get(), ds.get(), out.get());
+    k.finish();
+    std::vector<uint16_t> want(size_t(m) * n);
+    mh3o_gemm_w8a16_swiglu(m, n, d, x.data(), wq.data(), ws.data(), want.data());
+    compare("fc1 int8 + swiglu 300x320 -> 384", of_bf16(out.download()), of_bf16(want), n, 1e-2, 1e-4);
+}
+
+void errors()
+{
+    std::printf("errors\n");
+    Kernels k;
+    auto throws = [](const std::function<void()>& f) {
+        try {
+            f();
+        } catch (const std::runtime_error&) {
+            return true;
+        }
+        return false;
+    };
+    DeviceBuffer<uint16_t> a(64), b(64);
+    Modulation m;
+    check(throws([&] { k.rms_mod_rows(8, 7, MH3_BF16, a.get(), m, b.get()); }), "a row width not a multiple of 8 throws");
+    check(throws([&] { k.rms_mod_rows(8, 8, 9, a.get(), m, b.get()); }), "an unknown dtype throws");
+    check(throws([&] { k.swiglu_rows(8, 8, MH3_BF16, nullptr, nullptr, b.get()); }), "a null gate throws");
+    Cubes c;
+    c.heads = 1, c.t = 4, c.h = 4, c.w = 4, c.local = 2;
+    check(throws([&] { (void)c.args(); }), "local 2 throws (H3::set_sparse's domain is 0, 1, 3)");
+    check(parse_int8("fc1,qkv") == std::optional<uint32_t>(MH3_INT8_FC1 | MH3_INT8_QKV), "parse_int8 fc1,qkv");
+    check(!parse_int8("fc3"), "parse_int8 fc3 has no value");
+}
+
+} // namespace
+
+int main(int argc, char** argv)
+{
+    const std::string mode = argc > 1 ? argv[1] : "all";
+    int devices = 0;
+    if (hipGetDeviceCount(&devices) != hipSuccess || devices == 0) {
+        std::printf("no GPU: skipped\n");
+        return 77;
+    }
+    try {
+        if (mode == "rows" || mode == "all")
+            rows();
+        if (mode == "swiglu" || mode == "all")
+            swiglu();
+        if (mode == "cubes" || mode == "all")
+            cubes();
+        if (mode == "int8" || mode == "all")
+            int8();
+        if (mode == "errors" || mode == "all")
+            errors();
+    } catch (const std::exception& e) {
+        std::printf("  FAIL %s\n", e.what());
+        ++failures;
+    }
+    std::printf("%d failure%s\n", failures, failures == 1 ? "" : "s");
+    return failures;
+}
