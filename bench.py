@@ -199,14 +199,21 @@ def bench_fc1(mh, dev, steps, warmup, compare):
     flops = 2.0 * ROWS * DIM * 2 * FFN
     res = {"ms": ms, "tflops": flops / ms / 1e9, "mfma_util": flops / ms / 1e9 / BF16_PEAK_TFLOPS,
            "flops": flops, "shape": [ROWS, DIM, 2 * FFN]}
+    # The dense bf16 fc1 the int8 path replaces: this library's bf16 kernel (GEMM + SwiGLU epilogue) and, with
+    # compare, hipBLASLt through torch.matmul (GEMM only, no epilogue).
+    wb = (w.float() * s[:, None]).to(torch.bfloat16)
+    bms, _ = time_launches(lambda: mh.gemm_bf16_swiglu(x, wb, out=out), steps, warmup)
+    res["bf16_fc1_ms"] = bms
+    res["bf16_fc1_tflops"] = flops / bms / 1e9
+    res["bf16_fc1_mfma_util"] = flops / bms / 1e9 / BF16_PEAK_TFLOPS
     if compare:
-        # The dense bf16 fc1 the int8 path replaces (hipBLASLt through torch.matmul), GEMM only, no epilogue.
-        wt = (w.float() * s[:, None]).to(torch.bfloat16).t().contiguous()
+        wt = wb.t().contiguous()
         y = torch.empty((ROWS, 2 * FFN), dtype=torch.bfloat16, device=dev)
         cms, _ = time_launches(lambda: torch.matmul(x, wt, out=y), max(3, steps // 2), 2)
         res["bf16_hipblaslt_gemm_ms"] = cms
         res["bf16_hipblaslt_tflops"] = flops / cms / 1e9
         del wt, y
+    del wb
     return res
 
 

@@ -192,6 +192,12 @@ typedef struct MH3GemmArgs {
 } MH3GemmArgs;
 int mh3_gemm_w8a16_swiglu(const MH3GemmArgs* args, const uint16_t* x, const int8_t* w, const float* scale,
                           uint16_t* out, mh3_stream_t stream);
+/* The dense bf16 fc1 with the same epilogue: the reference's bf16 `Gemm::encode` for fc1 (docs/performance.md:52-69,
+ * the `--int8 none` path) + `swiglu_rows`. w is bf16 [2n][k] (gate rows, then up rows), no scale:
+ *   y = x * w^T in float accumulation, out = silu(y[:, 0:n]) * y[:, n:2n], bf16 [m][n].
+ * Same shape rules as mh3_gemm_w8a16_swiglu, with n * k < 2^29. */
+int mh3_gemm_bf16_swiglu(const MH3GemmArgs* args, const uint16_t* x, const uint16_t* w, uint16_t* out,
+                         mh3_stream_t stream);
 
 #ifdef __cplusplus
 }

@@ -1,6 +1,8 @@
 // fc1 as an int8 weight-only GEMM with the SwiGLU epilogue: out = silu(x Wg sg) * (x Wu su).
 // Replaces the reference's `gemm_i8` + `swiglu_rows` pair for fc1 (mako-common; docs/performance.md:120-136,
-// docs/architecture.md:65: fc1's [gate; value] rows, then SwiGLU).
+// docs/architecture.md:65: fc1's [gate; value] rows, then SwiGLU). The same kernel with bf16 weights (I8 false) is
+// the dense fc1 of the `--int8 none` path (the reference's bf16 `Gemm::encode`, docs/performance.md:52-69): its B
+// tiles then stream into LDS like A's, one K-step ahead, and there is no scale.
 //
 // Design (gfx950, v_mfma_f32_32x32x16_bf16):
 // - A workgroup of 8 wavefronts (2 along rows x 4 along columns) computes a 256-row x 128-column output tile, i.e.
@@ -95,10 +97,11 @@ __device__ __forceinline__ void lds_barrier()
 #endif
 
 // WM x WN wavefronts: wave (wm, wn) computes rows wm * (256 / WM) ... of the tile against its TN gate column tiles
-// (32 columns each, from wn * 32 TN) and the TN matching up column tiles.
-template <int WM, int WN>
-__global__ __launch_bounds__(MH3_GEMM_WM * MH3_GEMM_WN * 64) void gemm_w8a16_swiglu_kernel(
-    const uint16_t* __restrict__ x, const int8_t* __restrict__ w, const float* __restrict__ scale,
+// (32 columns each, from wn * 32 TN) and the TN matching up column tiles. I8: int8 weights with per-row scales;
+// otherwise bf16 weights (the dense fc1), no scale.
+template <int WM, int WN, bool I8>
+__global__ __launch_bounds__(MH3_GEMM_WM * MH3_GEMM_WN * 64) void gemm_swiglu_kernel(
+    const uint16_t* __restrict__ x, const void* __restrict__ wv, const float* __restrict__ scale,
     uint16_t* __restrict__ out, uint32_t M, uint32_t N, uint32_t K, uint32_t mt, uint32_t nt)
 {
     constexpr uint32_t kThreads = WM * WN * 64, kWaves = WM * WN;
@@ -137,10 +140,11 @@ __global__ __launch_bounds__(MH3_GEMM_WM * MH3_GEMM_WN * 64) void gemm_w8a16_swi
     // thread: chunk q = tid + kThreads i is k-chunk q % 4 of B-row 4 (G / 2) + 2 ((q / 4) % 2) + G % 2, G = q / 8.
     // Each 8 consecutive lanes thus write two rows whose swizzles differ in parity, i.e. 8 distinct chunk columns.
     constexpr int BI = int(1024 / kThreads);
-    const __amdgpu_buffer_rsrc_t rw = buffer_rsrc(w, uint32_t(2u * N * K)); // N * K < 2^30 is checked on the host
+    // N * K < 2^30 (int8) or 2^29 (bf16) is checked on the host.
+    const __amdgpu_buffer_rsrc_t rw = buffer_rsrc(wv, uint32_t(2u * N * K * (I8 ? 1u : 2u)));
     uint32_t b_src[BI], b_lo[BI], b_hi[BI];
 #pragma unroll
-    for (int i = 0; i < BI; ++i) {
+    for (int i = 0; i < BI && I8; ++i) {
         const uint32_t q = tid + kThreads * uint32_t(i), kc = q & 3u, G = q >> 3;
         const uint32_t brow = 4u * (G >> 1) + 2u * ((q >> 2) & 1u) + (G & 1u);
         const uint32_t wrow = brow < kBN ? n0 + brow : N + n0 + (brow - kBN);
@@ -166,6 +170,22 @@ __global__ __launch_bounds__(MH3_GEMM_WM * MH3_GEMM_WN * 64) void gemm_w8a16_swi
 #pragma unroll
         for (int p = 0; p < 2 * BI; ++p)
             b_piece(kt, rb, p);
+    };
+    // bf16 weights: B goes straight into its LDS ring like A, B-row r of the tile from weight row n0 + r (gate) or
+    // n + n0 + r - 128 (up), with A's chunk-to-lane assignment and swizzle.
+    uint32_t bd_off[AI];
+#pragma unroll
+    for (int i = 0; i < AI && !I8; ++i) {
+        const uint32_t row = (wave * AI + uint32_t(i)) * 8u + (lane >> 3);
+        const uint32_t c = (lane & 7u) ^ ((row >> 1) & 7u);
+        const uint32_t wrow = row < kBN ? n0 + row : N + n0 + (row - kBN);
+        bd_off[i] = (wrow * K + c * 8u) * 2u;
+    }
+    auto b_dma = [&](uint32_t kt) {
+        u32x4_t* stage = smem + kBBase + (kt % kBStages) * kStageChunks + wave * AI * 64u;
+#pragma unroll
+        for (int i = 0; i < AI; ++i)
+            lds_dma16(rw, stage + i * 64, bd_off[i], int(kt * kBK * 2u));
     };
 
     // MFMA operands of sub-step ks (16 k) of tile kt: A rows wm*(256/WM) + t*32 + lane%32, B rows (gate)
@@ -225,13 +245,18 @@ __global__ __launch_bounds__(MH3_GEMM_WM * MH3_GEMM_WN * 64) void gemm_w8a16_swi
     // The explicit wait is needed: the compiler may issue the B loads ahead of the LDS-bound A loads, and then the
     // waits it places for the B registers leave tile 0's A outstanding.
     a_issue(0);
-    b_issue(0, rb);
+    if constexpr (I8)
+        b_issue(0, rb);
+    else
+        b_dma(0);
     __builtin_amdgcn_sched_barrier(0);
     __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
     __builtin_amdgcn_sched_barrier(0);
-    b_write(0, rb);
+    if constexpr (I8)
+        b_write(0, rb);
     if (KT > 1) {
-        b_issue(1, rb);
+        if constexpr (I8)
+            b_issue(1, rb);
         a_issue(1);
     }
     // The epilogue's kernel arguments are read here, before the barrier: a scalar load still in flight at the loop
@@ -251,22 +276,28 @@ __global__ __launch_bounds__(MH3_GEMM_WM * MH3_GEMM_WN * 64) void gemm_w8a16_swi
     // the barrier: at such a join the compiler's LDS wait would also cover tile kt+1's fragment reads.
     auto kstep = [&](uint32_t kt, auto last) {
         constexpr bool kLast = decltype(last)::value;
+        if constexpr (!I8 && !kLast)
+            b_dma(kt + 1); // into B stage (kt+1) % 2, last read before step kt-1's barrier
         frags(kt, 1, fa[1], fb[1]);
         __builtin_amdgcn_sched_barrier(0);
-        if constexpr (kLast)
+        if constexpr (kLast || !I8)
             mfmas(fa[0], fb[0]);
         else
             mfmas_b(fa[0], fb[0], kt + 1, 0, BI);
         frags(kt, 2, fa[0], fb[0]);
         __builtin_amdgcn_sched_barrier(0);
-        if constexpr (kLast)
+        if constexpr (kLast || !I8)
             mfmas(fa[1], fb[1]);
         else
             mfmas_b(fa[1], fb[1], kt + 1, BI, BI);
         if constexpr (!kLast) {
-            __builtin_amdgcn_s_waitcnt(waitcnt_vm(0)); // tile kt+1's A complete too
-            if (kt + 2 < KT) {
-                b_issue(kt + 2, rb);
+            if constexpr (I8) {
+                __builtin_amdgcn_s_waitcnt(waitcnt_vm(0)); // tile kt+1's A complete too
+                if (kt + 2 < KT) {
+                    b_issue(kt + 2, rb);
+                    a_issue(kt + 2);
+                }
+            } else if (kt + 2 < KT) {
                 a_issue(kt + 2);
             }
         }
@@ -275,6 +306,13 @@ __global__ __launch_bounds__(MH3_GEMM_WM * MH3_GEMM_WN * 64) void gemm_w8a16_swi
         mfmas(fa[0], fb[0]);
         __builtin_amdgcn_sched_barrier(0);
         if constexpr (!kLast) {
+            if constexpr (!I8) {
+                // Loads complete in order: all but tile kt+2's AI A loads means tile kt+1's A and B are in LDS.
+                if (kt + 2 < KT)
+                    __builtin_amdgcn_s_waitcnt(waitcnt_vm(AI));
+                else
+                    __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
+            }
             lds_barrier();
             frags(kt + 1, 0, fa[0], fb[0]);
         }
@@ -290,7 +328,7 @@ __global__ __launch_bounds__(MH3_GEMM_WM * MH3_GEMM_WN * 64) void gemm_w8a16_swi
 #pragma unroll
     for (int b = 0; b < TN; ++b) {
         const uint32_t col = n0 + wn * 32u * TN + uint32_t(b) * 32u + r32;
-        const float sg = scale[col], su = scale[N + col];
+        const float sg = I8 ? scale[col] : 1.0f, su = I8 ? scale[N + col] : 1.0f;
 #pragma unroll
         for (int a = 0; a < TM; ++a) {
 #pragma unroll
@@ -309,8 +347,12 @@ __global__ __launch_bounds__(MH3_GEMM_WM * MH3_GEMM_WN * 64) void gemm_w8a16_swi
 
 } // namespace mh3
 
-extern "C" int mh3_gemm_w8a16_swiglu(const MH3GemmArgs* a, const uint16_t* x, const int8_t* w, const float* scale,
-                                     uint16_t* out, mh3_stream_t stream)
+namespace {
+
+// Shared checks and launch of the two weight types. bytes_per_weight 1 (int8) or 2 (bf16).
+template <bool I8>
+int launch_gemm(const MH3GemmArgs* a, const uint16_t* x, const void* w, const float* scale, uint16_t* out,
+                mh3_stream_t stream)
 {
     using namespace mh3;
     if (!a)
@@ -319,14 +361,15 @@ extern "C" int mh3_gemm_w8a16_swiglu(const MH3GemmArgs* a, const uint16_t* x, co
         return MH3_ERR_SHAPE;
     if (a->m >= (1u << 31) || uint64_t(a->n) * 2u >= (uint64_t(1) << 31))
         return MH3_ERR_SHAPE;
-    if (uint64_t(a->k) * kBM * 2u >= (uint64_t(1) << 31) || uint64_t(a->n) * a->k >= (uint64_t(1) << 30))
-        return MH3_ERR_UNSUPPORTED; // 32-bit buffer offsets: a tile's A rows, and all of w (2 n k bytes)
-    if (!x || !w || !scale || !out)
+    const uint64_t w_limit = uint64_t(1) << (I8 ? 30 : 29);
+    if (uint64_t(a->k) * kBM * 2u >= (uint64_t(1) << 31) || uint64_t(a->n) * a->k >= w_limit)
+        return MH3_ERR_UNSUPPORTED; // 32-bit buffer offsets: a tile's A rows, and all of w
+    if (!x || !w || (I8 && !scale) || !out)
         return MH3_ERR_POINTER;
     if (!host::aligned16(x) || !host::aligned16(w) || !host::aligned16(out))
         return MH3_ERR_ALIGN;
     constexpr int WM = MH3_GEMM_WM, WN = MH3_GEMM_WN;
-    const void* kernel = reinterpret_cast<const void*>(&gemm_w8a16_swiglu_kernel<WM, WN>);
+    const void* kernel = reinterpret_cast<const void*>(&gemm_swiglu_kernel<WM, WN, I8>);
     static const int lds_ok = hipFuncSetAttribute(kernel, hipFuncAttributeMaxDynamicSharedMemorySize, int(kGemmLds));
     if (lds_ok != hipSuccess)
         return MH3_ERR_HIP;
@@ -334,7 +377,21 @@ extern "C" int mh3_gemm_w8a16_swiglu(const MH3GemmArgs* a, const uint16_t* x, co
     const uint64_t tiles = uint64_t(mt) * nt;
     if (tiles >= (uint64_t(1) << 31))
         return MH3_ERR_SHAPE;
-    hipLaunchKernelGGL((gemm_w8a16_swiglu_kernel<WM, WN>), dim3(uint32_t(tiles)), dim3(WM * WN * 64), kGemmLds,
+    hipLaunchKernelGGL((gemm_swiglu_kernel<WM, WN, I8>), dim3(uint32_t(tiles)), dim3(WM * WN * 64), kGemmLds,
                        static_cast<hipStream_t>(stream), x, w, scale, out, a->m, a->n, a->k, mt, nt);
     return host::check_launch();
+}
+
+} // namespace
+
+extern "C" int mh3_gemm_w8a16_swiglu(const MH3GemmArgs* a, const uint16_t* x, const int8_t* w, const float* scale,
+                                     uint16_t* out, mh3_stream_t stream)
+{
+    return launch_gemm<true>(a, x, w, scale, out, stream);
+}
+
+extern "C" int mh3_gemm_bf16_swiglu(const MH3GemmArgs* a, const uint16_t* x, const uint16_t* w, uint16_t* out,
+                                    mh3_stream_t stream)
+{
+    return launch_gemm<false>(a, x, w, nullptr, out, stream);
 }

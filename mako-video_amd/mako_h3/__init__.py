@@ -75,6 +75,7 @@ def _load() -> C.CDLL:
         "mh3_cube_select": (I32, [C.POINTER(CubeArgs), P, P, P, P, P]),
         "mh3_quant_rows_i8": (I32, [C.POINTER(QuantArgs), P, P, P, P]),
         "mh3_gemm_w8a16_swiglu": (I32, [C.POINTER(GemmArgs), P, P, P, P, P]),
+        "mh3_gemm_bf16_swiglu": (I32, [C.POINTER(GemmArgs), P, P, P, P]),
     }
     for name, (res, args) in sig.items():
         f = getattr(lib, name)
@@ -352,4 +353,21 @@ def gemm_w8a16_swiglu(x, w, scale, *, out=None):
     a.m, a.n, a.k = m, n, k
     _check(lib.mh3_gemm_w8a16_swiglu(C.byref(a), _ptr(x), _ptr(w), _ptr(scale), _ptr(out), _stream()),
            "gemm_w8a16_swiglu")
+    return out
+
+
+def gemm_bf16_swiglu(x, w, *, out=None):
+    """The dense bf16 fc1 + SwiGLU: x bf16 [m][k], w bf16 [2n][k] (gate rows then up rows) -> bf16 [m][n]."""
+    m, k = x.shape
+    two_n = w.shape[0]
+    if w.dim() != 2 or w.shape[1] != k or two_n % 2:
+        raise ValueError("w must be [2n][k]")
+    n = two_n // 2
+    _need(x, "x", torch.bfloat16, m * k)
+    _need(w, "w", torch.bfloat16, two_n * k)
+    out = torch.empty((m, n), dtype=torch.bfloat16, device=x.device) if out is None else out
+    _need(out, "out", torch.bfloat16, m * n)
+    a = GemmArgs()
+    a.m, a.n, a.k = m, n, k
+    _check(lib.mh3_gemm_bf16_swiglu(C.byref(a), _ptr(x), _ptr(w), _ptr(out), _stream()), "gemm_bf16_swiglu")
     return out

@@ -341,3 +341,28 @@ void mh3o_gemm_w8a16_swiglu(uint32_t m, uint32_t n, uint32_t k, const uint16_t* 
     }
     free(xr);
 }
+
+void mh3o_gemm_bf16_swiglu(uint32_t m, uint32_t n, uint32_t k, const uint16_t* x, const uint16_t* w, uint16_t* out)
+{
+    double* xr = (double*)malloc(sizeof(double) * k);
+    double* wg = (double*)malloc(sizeof(double) * k);
+    double* wu = (double*)malloc(sizeof(double) * k);
+    for (uint64_t c = 0; c < n; ++c) {
+        for (uint32_t i = 0; i < k; ++i) {
+            wg[i] = (double)mh3o_bf16_to_float(w[c * k + i]);
+            wu[i] = (double)mh3o_bf16_to_float(w[(n + c) * k + i]);
+        }
+        for (uint64_t r = 0; r < m; ++r) {
+            double g = 0, u = 0;
+            for (uint32_t i = 0; i < k; ++i) {
+                const double xv = (double)mh3o_bf16_to_float(x[r * k + i]);
+                g += xv * wg[i];
+                u += xv * wu[i];
+            }
+            out[r * n + c] = mh3o_bf16_from_double(g / (1.0 + exp(-g)) * u);
+        }
+    }
+    free(xr);
+    free(wg);
+    free(wu);
+}

@@ -26,6 +26,7 @@
  *   mh3o_cube_topk             numpy lexsort; constructed scores with an analytic answer; ratio 1 selects all
  *   mh3o_quant_rows_i8         |q| <= 127, the row maximum maps to +-127, |w - q*s| <= s/2, numpy rint
  *   mh3o_gemm_w8a16_swiglu     torch.matmul in float64; exact integer results for w in {-1,0,1}, s = 1
+ *   mh3o_gemm_bf16_swiglu      torch.matmul in float64; exact integer results for w in {-1,0,1}
  */
 #ifndef MH3_ORACLE_H
 #define MH3_ORACLE_H
@@ -75,6 +76,8 @@ void mh3o_quant_rows_i8(uint32_t rows, uint32_t cols, int dtype, const void* w, 
 
 void mh3o_gemm_w8a16_swiglu(uint32_t m, uint32_t n, uint32_t k, const uint16_t* x, const int8_t* w,
                             const float* scale, uint16_t* out);
+/* The dense bf16 fc1 with the SwiGLU epilogue: w bf16 [2n][k] (gate rows, then up rows), no scale. */
+void mh3o_gemm_bf16_swiglu(uint32_t m, uint32_t n, uint32_t k, const uint16_t* x, const uint16_t* w, uint16_t* out);
 
 #ifdef __cplusplus
 }

@@ -51,6 +51,7 @@ _lib.mh3o_cube_scores.argtypes = [C.c_uint32] * 3 + [_P] * 3
 _lib.mh3o_cube_topk.argtypes = [C.c_uint32] * 7 + [_P] * 3
 _lib.mh3o_quant_rows_i8.argtypes = [C.c_uint32, C.c_uint32, C.c_int] + [_P] * 3
 _lib.mh3o_gemm_w8a16_swiglu.argtypes = [C.c_uint32] * 3 + [_P] * 4
+_lib.mh3o_gemm_bf16_swiglu.argtypes = [C.c_uint32] * 3 + [_P] * 3
 _lib.mh3o_bf16_to_float_n.argtypes = [_P, _P, C.c_uint64]
 _lib.mh3o_bf16_from_double_n.argtypes = [_P, _P, C.c_uint64]
 
@@ -189,6 +190,15 @@ def quant_rows_i8(w):
     s = np.empty(rows, np.float32)
     _lib.mh3o_quant_rows_i8(rows, cols, _dtype_code(w), _p(w), _p(q), _p(s))
     return q, s
+
+
+def gemm_bf16_swiglu(x, w):
+    """x bf16 bits [m][k], w bf16 bits [2n][k] -> silu(x w_gate^T) * (x w_up^T), bf16 bits [m][n]."""
+    m, k = x.shape
+    n = w.shape[0] // 2
+    out = np.empty((m, n), np.uint16)
+    _lib.mh3o_gemm_bf16_swiglu(m, n, k, _p(np.ascontiguousarray(x)), _p(np.ascontiguousarray(w)), _p(out))
+    return out
 
 
 def gemm_w8a16_swiglu(x, w, scale):

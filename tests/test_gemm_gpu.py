@@ -80,3 +80,51 @@ def test_gemm_768p_sampled_rows(dev):
     assert_close(g, bits_to_f64(want), 1e-2, 1e-4, "fc1 768p")
     rel, cos = diff(g, bits_to_f64(want), n)
     assert rel < 3e-3 and cos > 0.9999
+
+
+# ---- the dense bf16 fc1 (the --int8 none path) ----------------------------------------------------------------------
+
+@pytest.mark.parametrize("m,n,k", [(1, 128, 64), (37, 128, 128), (300, 384, 320), (513, 128, 5120)])
+def test_gemm_bf16_swiglu(dev, m, n, k):
+    rng = np.random.default_rng(m * 3 + n + k)
+    x = randn_bf16_bits(rng, (m, k))
+    w = randn_bf16_bits(rng, (2 * n, k), 0.05)
+    want = orc.gemm_bf16_swiglu(x, w)
+    got = mh.gemm_bf16_swiglu(from_bits(x, dev), from_bits(w, dev))
+    g, wv = bits_to_f64(to_bits(got)), bits_to_f64(want)
+    assert_close(g, wv, 1e-2, 1e-4, f"bf16 fc1 {m}x{n}x{k}")
+    rel, cos = diff(g, wv, n)
+    assert rel < 3e-3 and cos > 0.9999
+
+
+def test_gemm_bf16_equals_int8_path_on_integer_weights(dev):
+    """Integer weights |w| <= 127 are exact in bf16 and int8, so with unit scales both paths compute the same sums
+    in the same order: identical outputs."""
+    rng = np.random.default_rng(21)
+    m, n, k = 300, 256, 640
+    x = randn_bf16_bits(rng, (m, k))
+    wi = rng.integers(-127, 128, (2 * n, k), dtype=np.int8)
+    tw8 = torch.from_numpy(wi).to(dev)
+    ones = torch.ones(2 * n, dtype=torch.float32, device=dev)
+    a = mh.gemm_w8a16_swiglu(from_bits(x, dev), tw8, ones)
+    b = mh.gemm_bf16_swiglu(from_bits(x, dev), tw8.to(torch.bfloat16))
+    assert torch.equal(a.view(torch.int16), b.view(torch.int16))
+
+
+def test_gemm_bf16_768p_sampled_rows(dev):
+    """X bf16 [129,536 x 5120] ~ N(0,1), W bf16 [27,648 x 5120] ~ N(0, 0.02): all outputs finite; 6 rows against
+    the oracle over all 13,824 columns."""
+    m, n, k = 129536, 13824, 5120
+    gen = torch.Generator(device=dev).manual_seed(4)
+    x = torch.randn((m, k), generator=gen, device=dev).to(torch.bfloat16)
+    w = (0.02 * torch.randn((2 * n, k), generator=gen, device=dev)).to(torch.bfloat16)
+    out = mh.gemm_bf16_swiglu(x, w)
+    torch.cuda.synchronize()
+    assert torch.isfinite(out.float()).all()
+    rows = np.array([0, 1, 255, 256, 77777, m - 1])
+    ti = torch.from_numpy(rows).to(dev)
+    want = orc.gemm_bf16_swiglu(to_bits(x[ti]), to_bits(w))
+    g = bits_to_f64(to_bits(out[ti]))
+    assert_close(g, bits_to_f64(want), 1e-2, 1e-4, "bf16 fc1 768p")
+    rel, cos = diff(g, bits_to_f64(want), n)
+    assert rel < 3e-3 and cos > 0.9999

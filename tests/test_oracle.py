@@ -327,6 +327,33 @@ def test_gemm_exact_integers():
     assert (got == 40 * up).all()
 
 
+def test_gemm_bf16_swiglu_matches_torch_matmul():
+    rng = np.random.default_rng(17)
+    m, n, k = 7, 16, 96
+    x = randn_bf16_bits(rng, (m, k))
+    w = orc.bf16_from_f64(rng.standard_normal((2 * n, k)) * 0.05)
+    got = orc.gemm_bf16_swiglu(x, w)
+    y = torch.from_numpy(bits_to_f64(x)) @ torch.from_numpy(bits_to_f64(w)).T
+    want = torch.nn.functional.silu(y[:, :n]) * y[:, n:]
+    assert (got == orc.bf16_from_f64(want.numpy())).all()
+
+
+def test_gemm_bf16_exact_integers():
+    """As for the int8 GEMM: gate rows giving 40 and up rows in {-1, 0, 1} make out = bf16(40 * y_up) exactly; the
+    gate and up halves must not be swapped (a swap gives silu(y_up) * 40)."""
+    rng = np.random.default_rng(18)
+    m, n, k = 5, 8, 64
+    xf = rng.integers(-2, 3, (m, k)).astype(np.float32)
+    xf[:, 0] = 1.0
+    x = orc.bf16_from_f64(xf.astype(np.float64))
+    wf = np.zeros((2 * n, k))
+    wf[:n, 0] = 40.0
+    wf[n:] = rng.integers(-1, 2, (n, k))
+    got = bits_to_f64(orc.gemm_bf16_swiglu(x, orc.bf16_from_f64(wf)))
+    up = xf.astype(np.float64) @ wf[n:].T
+    assert (got == 40 * up).all()
+
+
 # ---- committed fixtures --------------------------------------------------------------------------------------------
 
 def test_golden_fixtures_reproduce():
