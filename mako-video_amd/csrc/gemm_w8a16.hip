@@ -33,7 +33,10 @@ constexpr uint32_t kBM = 256, kBN = 128, kBK = 64;
 constexpr uint32_t kStageChunks = 2048, kAStages = 3, kBStages = 2;
 constexpr uint32_t kBBase = kAStages * kStageChunks;
 constexpr size_t kGemmLds = size_t(kAStages + kBStages) * kStageChunks * 16;
-constexpr uint32_t kBandM = 4;
+#ifndef MH3_GEMM_BAND
+#define MH3_GEMM_BAND 4 // row tiles an XCD sweeps across all column tiles before moving on
+#endif
+constexpr uint32_t kBandM = MH3_GEMM_BAND;
 
 typedef __attribute__((address_space(3))) void* lds_ptr_t;
 
