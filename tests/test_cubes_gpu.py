@@ -189,3 +189,25 @@ def test_select_768p_sampled_heads(dev):
         gi = idx[h].cpu().numpy()[rows]
         gc = c[h][rows]
         check_selection(gi, gc, s64, oidx, ocnt, kk)
+
+
+@pytest.mark.parametrize("local", [1, 3])
+def test_topk_beyond_2048_cubes(dev, local):
+    """52 x 52 x 52 grid: 13^3 = 2197 cubes, the 64-cubes-a-lane top-k. The GPU's selection over its own scores is the
+    oracle's over the same scores; cube_select refuses more than 2048 cubes (its LDS tile holds 2048)."""
+    rng = np.random.default_rng(31 + local)
+    heads, grid = 1, (52, 52, 52)
+    cubes = mh.cube_count(*grid)
+    assert cubes == 2197
+    kk = mh.topk_k(0.1, cubes)
+    qc = rng.standard_normal((heads, cubes, 128)).astype(np.float32)
+    kc = rng.standard_normal((heads, cubes, 128)).astype(np.float32)
+    a = mh.cube_args(heads, grid, k=kk, local=local)
+    tq, tk = torch.from_numpy(qc).to(dev), torch.from_numpy(kc).to(dev)
+    s = mh.cube_scores(a, tq, tk)
+    idx, cnt = mh.cube_topk(a, s)
+    widx, wcnt = orc.cube_topk(s.cpu().numpy().astype(np.float64), grid, kk, local)
+    assert (cnt.cpu().numpy() == wcnt).all()
+    assert (idx.cpu().numpy() == widx).all()
+    with pytest.raises(RuntimeError):
+        mh.cube_select(a, tq, tk)
