@@ -172,3 +172,31 @@ def test_fused_768p_rows_sampled(dev):
     assert_close(bits_to_f64(os_), bits_to_f64(want), BF16_RTOL, BF16_ATOL, "fused 768p rows")
     rel, cos = diff(bits_to_f64(os_), bits_to_f64(want), dim)
     assert rel < 3e-3 and cos > 0.9999
+
+
+@pytest.mark.parametrize("dim", [20480, 32768])
+def test_wide_rows_four_vectors_a_thread(dev, dim):
+    """Rows of more than 16,384 bf16 (2048 vectors) take the workgroup-per-row kernel with 4 vectors a thread; the
+    widest accepted row is 4096 vectors."""
+    rng = np.random.default_rng(dim)
+    rows = 5
+    x, res = randn_bf16_bits(rng, (rows, dim)), randn_bf16_bits(rng, (rows, dim))
+    w, shift, scale, gate = mod_params(rng, dim)
+    want = orc.rms_mod_gate_add_rows(x, res, w, shift, scale, gate, 1e-6)
+    got = mh.rms_mod_gate_add_rows(from_bits(x, dev), from_bits(res, dev), dev_t(w, dev), dev_t(shift, dev),
+                                   dev_t(scale, dev), dev_t(gate, dev))
+    assert_close(bits_to_f64(to_bits(got)), bits_to_f64(want), BF16_RTOL, BF16_ATOL, f"fused {rows}x{dim}")
+    tx = from_bits(res, dev)
+    h = mh.gate_add_rms_mod_rows(tx, from_bits(x, dev), dev_t(gate, dev), dev_t(w, dev), dev_t(shift, dev),
+                                 dev_t(scale, dev))
+    want_x = orc.gate_add_rows(res, x, gate)
+    assert_close(bits_to_f64(to_bits(tx)), bits_to_f64(want_x), BF16_RTOL, BF16_ATOL, f"block order x {dim}")
+    want_h = orc.rms_mod_rows(to_bits(tx), w, shift, scale, 1e-6)
+    assert_close(bits_to_f64(to_bits(h)), bits_to_f64(want_h), BF16_RTOL, BF16_ATOL, f"block order h {dim}")
+
+
+def test_row_wider_than_4096_vectors_is_unsupported(dev):
+    x = torch.zeros((2, 32776), dtype=torch.bfloat16, device=dev)
+    ones = torch.ones(32776, device=dev)
+    with pytest.raises(RuntimeError):
+        mh.rms_mod_rows(x, ones, ones.view(1, -1), ones.view(1, -1))
