@@ -31,6 +31,7 @@ sys.path.insert(0, str(REPO / "mako-video_amd"))
 
 HBM_PEAK_GBS = 8000.0          # MI355X HBM3E
 BF16_PEAK_TFLOPS = 2500.0      # dense bf16 MFMA
+INT8_PEAK_TOPS = 5000.0        # dense int8 MFMA
 FP32_MFMA_PEAK_TFLOPS = 157.3  # dense fp32 MFMA
 METRIC = "ms/op + achieved HBM GB/s (% peak) at 768p rows; int8 GEMM MFMA util %"
 
@@ -206,14 +207,25 @@ def bench_fc1(mh, dev, steps, warmup, compare):
     res["bf16_fc1_ms"] = bms
     res["bf16_fc1_tflops"] = flops / bms / 1e9
     res["bf16_fc1_mfma_util"] = flops / bms / 1e9 / BF16_PEAK_TFLOPS
+    del wb
+    # The reference's own --int8 form, W8A8: x quantized per row (quant_rows_i8), the int8 GEMM on the int8 MFMA.
+    xq = torch.empty((ROWS, DIM), dtype=torch.int8, device=dev)
+    xs = torch.empty(ROWS, dtype=torch.float32, device=dev)
+    qms, _ = time_launches(lambda: mh.quant_rows_i8(x, q=xq, scale=xs), steps, warmup)
+    ims, _ = time_launches(lambda: mh.gemm_i8_swiglu(xq, xs, w, s, out=out), steps, warmup)
+    res["w8a8_quant_x_ms"] = qms
+    res["w8a8_fc1_ms"] = ims
+    res["w8a8_fc1_tops"] = flops / ims / 1e9
+    res["w8a8_fc1_int8_mfma_util"] = flops / ims / 1e9 / INT8_PEAK_TOPS
+    del xq, xs
     if compare:
+        wb = (w.float() * s[:, None]).to(torch.bfloat16)
         wt = wb.t().contiguous()
         y = torch.empty((ROWS, 2 * FFN), dtype=torch.bfloat16, device=dev)
         cms, _ = time_launches(lambda: torch.matmul(x, wt, out=y), max(3, steps // 2), 2)
         res["bf16_hipblaslt_gemm_ms"] = cms
         res["bf16_hipblaslt_tflops"] = flops / cms / 1e9
-        del wt, y
-    del wb
+        del wt, y, wb
     return res
 
 

@@ -198,6 +198,13 @@ int mh3_gemm_w8a16_swiglu(const MH3GemmArgs* args, const uint16_t* x, const int8
  * Same shape rules as mh3_gemm_w8a16_swiglu, with n * k < 2^29. */
 int mh3_gemm_bf16_swiglu(const MH3GemmArgs* args, const uint16_t* x, const uint16_t* w, uint16_t* out,
                          mh3_stream_t stream);
+/* The reference's own `--int8` fc1 (docs/performance.md:120-133): W8A8 `gemm_i8` on the int8 MFMA with the SwiGLU
+ * epilogue. x is int8 [m][k] with x_scale float [m] (mh3_quant_rows_i8 of the bf16 activations), w int8 [2n][k] with
+ * w_scale float [2n]; int32 accumulation (exact), then
+ *   y = sum * x_scale[row] * w_scale[col] in float, out = silu(y[:, 0:n]) * y[:, n:2n], bf16 [m][n].
+ * k % 128 == 0, n % 128 == 0, m >= 1; x, w and out 16-byte aligned; n * k < 2^30. */
+int mh3_gemm_i8_swiglu(const MH3GemmArgs* args, const int8_t* x, const float* x_scale, const int8_t* w,
+                       const float* w_scale, uint16_t* out, mh3_stream_t stream);
 
 #ifdef __cplusplus
 }

@@ -208,6 +208,21 @@ public:
         check(mh3_gemm_w8a16_swiglu(&a, x, w, scale, out, s_), "gemm_i8+swiglu_rows");
     }
 
+    // The dense fc1 (--int8 none): bf16 weights [2 ffn][dim], no scale
+    void fc1_swiglu_bf16(uint32_t m, uint32_t ffn, uint32_t dim, const uint16_t* x, const uint16_t* w,
+                         uint16_t* out) const
+    {
+        const MH3GemmArgs a{m, ffn, dim, 0};
+        check(mh3_gemm_bf16_swiglu(&a, x, w, out, s_), "Gemm::encode+swiglu_rows");
+    }
+    // The reference's own --int8 fc1: x quantized per row (quant_rows_i8), W8A8 gemm_i8 and SwiGLU
+    void fc1_swiglu_w8a8(uint32_t m, uint32_t ffn, uint32_t dim, const int8_t* xq, const float* x_scale,
+                         const int8_t* w, const float* w_scale, uint16_t* out) const
+    {
+        const MH3GemmArgs a{m, ffn, dim, 0};
+        check(mh3_gemm_i8_swiglu(&a, xq, x_scale, w, w_scale, out, s_), "gemm_i8+swiglu_rows");
+    }
+
 private:
     static MH3RowsArgs rows_args(uint32_t rows, uint32_t dim, uint32_t dtype, const Modulation& m, float eps)
     {

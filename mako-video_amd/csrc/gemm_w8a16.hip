@@ -2,7 +2,9 @@
 // Replaces the reference's `gemm_i8` + `swiglu_rows` pair for fc1 (mako-common; docs/performance.md:120-136,
 // docs/architecture.md:65: fc1's [gate; value] rows, then SwiGLU). The same kernel with bf16 weights (I8 false) is
 // the dense fc1 of the `--int8 none` path (the reference's bf16 `Gemm::encode`, docs/performance.md:52-69): its B
-// tiles then stream into LDS like A's, one K-step ahead, and there is no scale.
+// tiles then stream into LDS like A's, one K-step ahead, and there is no scale. With int8 x as well (W8A8, the
+// reference's own `gemm_i8`: activations quantized per row) both operands stream into LDS and the int8 MFMA
+// (v_mfma_i32_32x32x32_i8, exact int32 sums) takes 128 k a K-step; the epilogue applies both scales.
 //
 // Design (gfx950, v_mfma_f32_32x32x16_bf16):
 // - A workgroup of 8 wavefronts (2 along rows x 4 along columns) computes a 256-row x 128-column output tile, i.e.
@@ -99,14 +101,27 @@ __device__ __forceinline__ void lds_barrier()
 #define MH3_GEMM_WN 4 // wavefronts along its columns
 #endif
 
+// The three fc1 forms: int8 weights widened to bf16 with bf16 activations (weight-only), bf16 weights, and int8
+// weights with int8 activations (each row of x with its own scale) on the int8 MFMA.
+enum GemmMode { kW8A16 = 0, kBf16 = 1, kW8A8 = 2 };
+
+typedef int int32x4 __attribute__((ext_vector_type(4)));
+typedef int int32x16 __attribute__((ext_vector_type(16)));
+
 // WM x WN wavefronts: wave (wm, wn) computes rows wm * (256 / WM) ... of the tile against its TN gate column tiles
-// (32 columns each, from wn * 32 TN) and the TN matching up column tiles. I8: int8 weights with per-row scales;
-// otherwise bf16 weights (the dense fc1), no scale.
-template <int WM, int WN, bool I8>
+// (32 columns each, from wn * 32 TN) and the TN matching up column tiles. Every LDS row holds 128 bytes of k: 64 k of
+// bf16 or 128 k of int8, so a K-step is 64 or 128 k.
+template <int WM, int WN, int MODE>
 __global__ __launch_bounds__(MH3_GEMM_WM * MH3_GEMM_WN * 64) void gemm_swiglu_kernel(
-    const uint16_t* __restrict__ x, const void* __restrict__ wv, const float* __restrict__ scale,
-    uint16_t* __restrict__ out, uint32_t M, uint32_t N, uint32_t K, uint32_t mt, uint32_t nt)
+    const void* __restrict__ xv, const void* __restrict__ wv, const float* __restrict__ scale,
+    const float* __restrict__ xscale, uint16_t* __restrict__ out, uint32_t M, uint32_t N, uint32_t K, uint32_t mt,
+    uint32_t nt)
 {
+    constexpr bool I8 = MODE == kW8A16;                   // B through registers, widened
+    constexpr uint32_t kEA = MODE == kW8A8 ? 1u : 2u;     // bytes of an x element
+    constexpr uint32_t kEB = MODE == kBf16 ? 2u : 1u;     // bytes of a w element
+    constexpr uint32_t kKS = 128u / kEA;                  // k of a K-step
+    using Acc = typename std::conditional<MODE == kW8A8, int32x16, floatx16>::type;
     constexpr uint32_t kThreads = WM * WN * 64, kWaves = WM * WN;
     constexpr int TM = int(kBM / WM / 32), TN = int(kBN / WN / 32); // MFMA tiles: rows, and gate (= up) columns
     extern __shared__ u32x4_t smem[];
@@ -114,28 +129,28 @@ __global__ __launch_bounds__(MH3_GEMM_WM * MH3_GEMM_WN * 64) void gemm_swiglu_ke
     tile_of(mt, nt, tm, tn);
     const uint32_t m0 = tm * kBM, n0 = tn * kBN;
     const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6, wm = wave / WN, wn = wave % WN;
-    const uint32_t KT = K / kBK;
+    const uint32_t KT = K / kKS;
 
     // A: straight from global memory into the LDS ring (buffer_load ... lds). A stage is 2048 16-byte chunks; each
     // wave fills 2048 / kWaves of them, 64 a instruction; lane L of instruction i lands in chunk q = (wave * AI + i) *
     // 64 + L = row * 8 + physical chunk and fetches the logical chunk the swizzle puts there. The descriptor starts
     // at this tile's first row; rows past M read zero.
     constexpr int AI = int(kStageChunks / 64 / kWaves);
-    const uint64_t a_left = uint64_t(M - m0) * K * 2u;
-    const __amdgpu_buffer_rsrc_t ra =
-        buffer_rsrc(x + uint64_t(m0) * K, uint32_t(a_left < 0x7fffffffu ? a_left : 0x7fffffffu));
+    const uint64_t a_left = uint64_t(M - m0) * K * kEA;
+    const __amdgpu_buffer_rsrc_t ra = buffer_rsrc(reinterpret_cast<const char*>(xv) + uint64_t(m0) * K * kEA,
+                                                  uint32_t(a_left < 0x7fffffffu ? a_left : 0x7fffffffu));
     uint32_t a_off[AI];
 #pragma unroll
     for (int i = 0; i < AI; ++i) {
         const uint32_t row = (wave * AI + uint32_t(i)) * 8u + (lane >> 3);
         const uint32_t c = (lane & 7u) ^ ((row >> 1) & 7u);
-        a_off[i] = (row * K + c * 8u) * 2u;
+        a_off[i] = row * K * kEA + c * 16u;
     }
     auto a_issue = [&](uint32_t kt) {
         u32x4_t* stage = smem + (kt % kAStages) * kStageChunks + wave * AI * 64u;
 #pragma unroll
         for (int i = 0; i < AI; ++i)
-            lds_dma16(ra, stage + i * 64, a_off[i], int(kt * kBK * 2u));
+            lds_dma16(ra, stage + i * 64, a_off[i], int(kt * 128u));
     };
 
     // B: 16-byte int8 vectors into registers a K-step ahead, widened to bf16 into the B ring. The stage's 1024 int8
@@ -144,7 +159,7 @@ __global__ __launch_bounds__(MH3_GEMM_WM * MH3_GEMM_WN * 64) void gemm_swiglu_ke
     // Each 8 consecutive lanes thus write two rows whose swizzles differ in parity, i.e. 8 distinct chunk columns.
     constexpr int BI = int(1024 / kThreads);
     // N * K < 2^30 (int8) or 2^29 (bf16) is checked on the host.
-    const __amdgpu_buffer_rsrc_t rw = buffer_rsrc(wv, uint32_t(2u * N * K * (I8 ? 1u : 2u)));
+    const __amdgpu_buffer_rsrc_t rw = buffer_rsrc(wv, uint32_t(2u * N * K * kEB));
     uint32_t b_src[BI], b_lo[BI], b_hi[BI];
 #pragma unroll
     for (int i = 0; i < BI && I8; ++i) {
@@ -174,21 +189,21 @@ __global__ __launch_bounds__(MH3_GEMM_WM * MH3_GEMM_WN * 64) void gemm_swiglu_ke
         for (int p = 0; p < 2 * BI; ++p)
             b_piece(kt, rb, p);
     };
-    // bf16 weights: B goes straight into its LDS ring like A, B-row r of the tile from weight row n0 + r (gate) or
-    // n + n0 + r - 128 (up), with A's chunk-to-lane assignment and swizzle.
+    // bf16 weights, and int8 weights with int8 x: B goes straight into its LDS ring like A, B-row r of the tile from
+    // weight row n0 + r (gate) or n + n0 + r - 128 (up), with A's chunk-to-lane assignment and swizzle.
     uint32_t bd_off[AI];
 #pragma unroll
     for (int i = 0; i < AI && !I8; ++i) {
         const uint32_t row = (wave * AI + uint32_t(i)) * 8u + (lane >> 3);
         const uint32_t c = (lane & 7u) ^ ((row >> 1) & 7u);
         const uint32_t wrow = row < kBN ? n0 + row : N + n0 + (row - kBN);
-        bd_off[i] = (wrow * K + c * 8u) * 2u;
+        bd_off[i] = wrow * K * kEB + c * 16u;
     }
     auto b_dma = [&](uint32_t kt) {
         u32x4_t* stage = smem + kBBase + (kt % kBStages) * kStageChunks + wave * AI * 64u;
 #pragma unroll
         for (int i = 0; i < AI; ++i)
-            lds_dma16(rw, stage + i * 64, bd_off[i], int(kt * kBK * 2u));
+            lds_dma16(rw, stage + i * 64, bd_off[i], int(kt * 128u));
     };
 
     // MFMA operands of sub-step ks (16 k) of tile kt: A rows wm*(256/WM) + t*32 + lane%32, B rows (gate)
@@ -213,20 +228,26 @@ __global__ __launch_bounds__(MH3_GEMM_WM * MH3_GEMM_WN * 64) void gemm_swiglu_ke
         }
     };
 
-    floatx16 acc[TM][2 * TN];
+    Acc acc[TM][2 * TN];
 #pragma unroll
     for (int a = 0; a < TM; ++a)
 #pragma unroll
         for (int b = 0; b < 2 * TN; ++b)
 #pragma unroll
             for (int e = 0; e < 16; ++e)
-                acc[a][b][e] = 0.0f;
+                acc[a][b][e] = 0;
     auto mfmas = [&](const bf16x8_t (&fa)[TM], const bf16x8_t (&fb)[2 * TN]) {
 #pragma unroll
         for (int a = 0; a < TM; ++a)
 #pragma unroll
-            for (int b = 0; b < 2 * TN; ++b)
-                acc[a][b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[a], fb[b], acc[a][b], 0, 0, 0);
+            for (int b = 0; b < 2 * TN; ++b) {
+                if constexpr (MODE == kW8A8)
+                    acc[a][b] = __builtin_amdgcn_mfma_i32_32x32x32_i8(__builtin_bit_cast(int32x4, fa[a]),
+                                                                      __builtin_bit_cast(int32x4, fb[b]), acc[a][b],
+                                                                      0, 0, 0);
+                else
+                    acc[a][b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[a], fb[b], acc[a][b], 0, 0, 0);
+            }
     };
     // The same MFMAs with B pieces p0 .. p0 + np - 1 of tile kt placed between them, at even spacing, so the
     // widening's VALU work issues while the matrix core is busy.
@@ -235,7 +256,8 @@ __global__ __launch_bounds__(MH3_GEMM_WM * MH3_GEMM_WN * 64) void gemm_swiglu_ke
 #pragma unroll
         for (int j = 0; j < n; ++j) {
             const int a = j / (2 * TN), b = j % (2 * TN);
-            acc[a][b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[a], fb[b], acc[a][b], 0, 0, 0);
+            if constexpr (MODE == kW8A16)
+                acc[a][b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[a], fb[b], acc[a][b], 0, 0, 0);
             __builtin_amdgcn_sched_barrier(0);
             if (j % (n / np) == 0 && j / (n / np) < np) {
                 b_piece(kt, rb, p0 + j / (n / np));
@@ -264,7 +286,7 @@ __global__ __launch_bounds__(MH3_GEMM_WM * MH3_GEMM_WN * 64) void gemm_swiglu_ke
     }
     // The epilogue's kernel arguments are read here, before the barrier: a scalar load still in flight at the loop
     // would turn every LDS wait in it into a full wait (scalar loads complete out of order).
-    asm volatile("" ::"s"(scale), "s"(out));
+    asm volatile("" ::"s"(scale), "s"(xscale), "s"(out));
     lds_barrier();
     bf16x8_t fa[2][TM], fb[2][2 * TN];
     frags(0, 0, fa[0], fb[0]);
@@ -331,7 +353,7 @@ __global__ __launch_bounds__(MH3_GEMM_WM * MH3_GEMM_WN * 64) void gemm_swiglu_ke
 #pragma unroll
     for (int b = 0; b < TN; ++b) {
         const uint32_t col = n0 + wn * 32u * TN + uint32_t(b) * 32u + r32;
-        const float sg = I8 ? scale[col] : 1.0f, su = I8 ? scale[N + col] : 1.0f;
+        const float sg = MODE != kBf16 ? scale[col] : 1.0f, su = MODE != kBf16 ? scale[N + col] : 1.0f;
 #pragma unroll
         for (int a = 0; a < TM; ++a) {
 #pragma unroll
@@ -339,7 +361,8 @@ __global__ __launch_bounds__(MH3_GEMM_WM * MH3_GEMM_WN * 64) void gemm_swiglu_ke
                 const uint32_t row = m0 + wm * (kBM / WM) + uint32_t(a) * 32u + 8u * (uint32_t(e) >> 2) + 4u * half +
                                      (uint32_t(e) & 3u);
                 if (row < M) {
-                    const float g = acc[a][b][e] * sg, u = acc[a][TN + b][e] * su;
+                    const float sx = MODE == kW8A8 ? xscale[row] : 1.0f;
+                    const float g = float(acc[a][b][e]) * sg * sx, u = float(acc[a][TN + b][e]) * su * sx;
                     const float o = g * __builtin_amdgcn_rcpf(1.0f + __expf(-g)) * u;
                     out[uint64_t(row) * N + col] = __builtin_bit_cast(uint16_t, __bf16(o));
                 }
@@ -352,27 +375,27 @@ __global__ __launch_bounds__(MH3_GEMM_WM * MH3_GEMM_WN * 64) void gemm_swiglu_ke
 
 namespace {
 
-// Shared checks and launch of the two weight types. bytes_per_weight 1 (int8) or 2 (bf16).
-template <bool I8>
-int launch_gemm(const MH3GemmArgs* a, const uint16_t* x, const void* w, const float* scale, uint16_t* out,
-                mh3_stream_t stream)
+// Shared checks and launch of the three forms.
+template <int MODE>
+int launch_gemm(const MH3GemmArgs* a, const void* x, const void* w, const float* scale, const float* xscale,
+                uint16_t* out, mh3_stream_t stream)
 {
     using namespace mh3;
+    constexpr uint32_t kEA = MODE == kW8A8 ? 1u : 2u, kEB = MODE == kBf16 ? 2u : 1u, kKS = 128u / kEA;
     if (!a)
         return MH3_ERR_POINTER;
-    if (a->m == 0 || a->k == 0 || a->n == 0 || a->k % kBK != 0 || a->n % kBN != 0)
+    if (a->m == 0 || a->k == 0 || a->n == 0 || a->k % kKS != 0 || a->n % kBN != 0)
         return MH3_ERR_SHAPE;
     if (a->m >= (1u << 31) || uint64_t(a->n) * 2u >= (uint64_t(1) << 31))
         return MH3_ERR_SHAPE;
-    const uint64_t w_limit = uint64_t(1) << (I8 ? 30 : 29);
-    if (uint64_t(a->k) * kBM * 2u >= (uint64_t(1) << 31) || uint64_t(a->n) * a->k >= w_limit)
+    if (uint64_t(a->k) * kBM * kEA >= (uint64_t(1) << 31) || uint64_t(a->n) * a->k * 2u * kEB >= (uint64_t(1) << 31))
         return MH3_ERR_UNSUPPORTED; // 32-bit buffer offsets: a tile's A rows, and all of w
-    if (!x || !w || (I8 && !scale) || !out)
+    if (!x || !w || (MODE != kBf16 && !scale) || (MODE == kW8A8 && !xscale) || !out)
         return MH3_ERR_POINTER;
     if (!host::aligned16(x) || !host::aligned16(w) || !host::aligned16(out))
         return MH3_ERR_ALIGN;
     constexpr int WM = MH3_GEMM_WM, WN = MH3_GEMM_WN;
-    const void* kernel = reinterpret_cast<const void*>(&gemm_swiglu_kernel<WM, WN, I8>);
+    const void* kernel = reinterpret_cast<const void*>(&gemm_swiglu_kernel<WM, WN, MODE>);
     static const int lds_ok = hipFuncSetAttribute(kernel, hipFuncAttributeMaxDynamicSharedMemorySize, int(kGemmLds));
     if (lds_ok != hipSuccess)
         return MH3_ERR_HIP;
@@ -380,8 +403,8 @@ int launch_gemm(const MH3GemmArgs* a, const uint16_t* x, const void* w, const fl
     const uint64_t tiles = uint64_t(mt) * nt;
     if (tiles >= (uint64_t(1) << 31))
         return MH3_ERR_SHAPE;
-    hipLaunchKernelGGL((gemm_swiglu_kernel<WM, WN, I8>), dim3(uint32_t(tiles)), dim3(WM * WN * 64), kGemmLds,
-                       static_cast<hipStream_t>(stream), x, w, scale, out, a->m, a->n, a->k, mt, nt);
+    hipLaunchKernelGGL((gemm_swiglu_kernel<WM, WN, MODE>), dim3(uint32_t(tiles)), dim3(WM * WN * 64), kGemmLds,
+                       static_cast<hipStream_t>(stream), x, w, scale, xscale, out, a->m, a->n, a->k, mt, nt);
     return host::check_launch();
 }
 
@@ -390,11 +413,17 @@ int launch_gemm(const MH3GemmArgs* a, const uint16_t* x, const void* w, const fl
 extern "C" int mh3_gemm_w8a16_swiglu(const MH3GemmArgs* a, const uint16_t* x, const int8_t* w, const float* scale,
                                      uint16_t* out, mh3_stream_t stream)
 {
-    return launch_gemm<true>(a, x, w, scale, out, stream);
+    return launch_gemm<mh3::kW8A16>(a, x, w, scale, nullptr, out, stream);
 }
 
 extern "C" int mh3_gemm_bf16_swiglu(const MH3GemmArgs* a, const uint16_t* x, const uint16_t* w, uint16_t* out,
                                     mh3_stream_t stream)
 {
-    return launch_gemm<false>(a, x, w, nullptr, out, stream);
+    return launch_gemm<mh3::kBf16>(a, x, w, nullptr, nullptr, out, stream);
+}
+
+extern "C" int mh3_gemm_i8_swiglu(const MH3GemmArgs* a, const int8_t* x, const float* x_scale, const int8_t* w,
+                                  const float* w_scale, uint16_t* out, mh3_stream_t stream)
+{
+    return launch_gemm<mh3::kW8A8>(a, x, w, w_scale, x_scale, out, stream);
 }

@@ -76,6 +76,7 @@ def _load() -> C.CDLL:
         "mh3_quant_rows_i8": (I32, [C.POINTER(QuantArgs), P, P, P, P]),
         "mh3_gemm_w8a16_swiglu": (I32, [C.POINTER(GemmArgs), P, P, P, P, P]),
         "mh3_gemm_bf16_swiglu": (I32, [C.POINTER(GemmArgs), P, P, P, P]),
+        "mh3_gemm_i8_swiglu": (I32, [C.POINTER(GemmArgs), P, P, P, P, P, P]),
     }
     for name, (res, args) in sig.items():
         f = getattr(lib, name)
@@ -370,4 +371,25 @@ def gemm_bf16_swiglu(x, w, *, out=None):
     a = GemmArgs()
     a.m, a.n, a.k = m, n, k
     _check(lib.mh3_gemm_bf16_swiglu(C.byref(a), _ptr(x), _ptr(w), _ptr(out), _stream()), "gemm_bf16_swiglu")
+    return out
+
+
+def gemm_i8_swiglu(x, x_scale, w, w_scale, *, out=None):
+    """The W8A8 fc1 + SwiGLU: x int8 [m][k] with x_scale f32 [m], w int8 [2n][k] with w_scale f32 [2n] -> bf16 [m][n].
+    quant_rows_i8 of the bf16 activations gives x and x_scale."""
+    m, k = x.shape
+    two_n = w.shape[0]
+    if w.dim() != 2 or w.shape[1] != k or two_n % 2:
+        raise ValueError("w must be [2n][k]")
+    n = two_n // 2
+    _need(x, "x", torch.int8, m * k)
+    _need(x_scale, "x_scale", torch.float32, m)
+    _need(w, "w", torch.int8, two_n * k)
+    _need(w_scale, "w_scale", torch.float32, two_n)
+    out = torch.empty((m, n), dtype=torch.bfloat16, device=x.device) if out is None else out
+    _need(out, "out", torch.bfloat16, m * n)
+    a = GemmArgs()
+    a.m, a.n, a.k = m, n, k
+    _check(lib.mh3_gemm_i8_swiglu(C.byref(a), _ptr(x), _ptr(x_scale), _ptr(w), _ptr(w_scale), _ptr(out), _stream()),
+           "gemm_i8_swiglu")
     return out

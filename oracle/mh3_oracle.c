@@ -366,3 +366,23 @@ void mh3o_gemm_bf16_swiglu(uint32_t m, uint32_t n, uint32_t k, const uint16_t* x
     free(wg);
     free(wu);
 }
+
+void mh3o_gemm_i8_swiglu(uint32_t m, uint32_t n, uint32_t k, const int8_t* x, const float* x_scale, const int8_t* w,
+                         const float* w_scale, uint16_t* out)
+{
+    for (uint64_t r = 0; r < m; ++r) {
+        const int8_t* xr = x + r * k;
+        for (uint64_t c = 0; c < n; ++c) {
+            const int8_t* wg = w + c * k;
+            const int8_t* wu = w + (n + c) * k;
+            int64_t ig = 0, iu = 0;
+            for (uint32_t i = 0; i < k; ++i) {
+                ig += (int64_t)xr[i] * wg[i];
+                iu += (int64_t)xr[i] * wu[i];
+            }
+            const double g = (double)ig * (double)x_scale[r] * (double)w_scale[c];
+            const double u = (double)iu * (double)x_scale[r] * (double)w_scale[n + c];
+            out[r * n + c] = mh3o_bf16_from_double(g / (1.0 + exp(-g)) * u);
+        }
+    }
+}

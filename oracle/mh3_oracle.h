@@ -27,6 +27,8 @@
  *   mh3o_quant_rows_i8         |q| <= 127, the row maximum maps to +-127, |w - q*s| <= s/2, numpy rint
  *   mh3o_gemm_w8a16_swiglu     torch.matmul in float64; exact integer results for w in {-1,0,1}, s = 1
  *   mh3o_gemm_bf16_swiglu      torch.matmul in float64; exact integer results for w in {-1,0,1}
+ *   mh3o_gemm_i8_swiglu        torch.matmul of the int64 operands; exact integer results with unit scales
+ *   (the order in which gemm_i8's epilogue applies the two scales is not documented: parity unpinned for it)
  */
 #ifndef MH3_ORACLE_H
 #define MH3_ORACLE_H
@@ -78,6 +80,10 @@ void mh3o_gemm_w8a16_swiglu(uint32_t m, uint32_t n, uint32_t k, const uint16_t* 
                             const float* scale, uint16_t* out);
 /* The dense bf16 fc1 with the SwiGLU epilogue: w bf16 [2n][k] (gate rows, then up rows), no scale. */
 void mh3o_gemm_bf16_swiglu(uint32_t m, uint32_t n, uint32_t k, const uint16_t* x, const uint16_t* w, uint16_t* out);
+/* The reference's W8A8 `gemm_i8` for fc1 with the SwiGLU epilogue: x int8 [m][k] with a scale per row, w int8 [2n][k]
+ * with a scale per row; exact integer sums, then y = sum * x_scale[r] * w_scale[c] in double. */
+void mh3o_gemm_i8_swiglu(uint32_t m, uint32_t n, uint32_t k, const int8_t* x, const float* x_scale, const int8_t* w,
+                         const float* w_scale, uint16_t* out);
 
 #ifdef __cplusplus
 }

@@ -52,6 +52,7 @@ _lib.mh3o_cube_topk.argtypes = [C.c_uint32] * 7 + [_P] * 3
 _lib.mh3o_quant_rows_i8.argtypes = [C.c_uint32, C.c_uint32, C.c_int] + [_P] * 3
 _lib.mh3o_gemm_w8a16_swiglu.argtypes = [C.c_uint32] * 3 + [_P] * 4
 _lib.mh3o_gemm_bf16_swiglu.argtypes = [C.c_uint32] * 3 + [_P] * 3
+_lib.mh3o_gemm_i8_swiglu.argtypes = [C.c_uint32] * 3 + [_P] * 5
 _lib.mh3o_bf16_to_float_n.argtypes = [_P, _P, C.c_uint64]
 _lib.mh3o_bf16_from_double_n.argtypes = [_P, _P, C.c_uint64]
 
@@ -198,6 +199,16 @@ def gemm_bf16_swiglu(x, w):
     n = w.shape[0] // 2
     out = np.empty((m, n), np.uint16)
     _lib.mh3o_gemm_bf16_swiglu(m, n, k, _p(np.ascontiguousarray(x)), _p(np.ascontiguousarray(w)), _p(out))
+    return out
+
+
+def gemm_i8_swiglu(x, x_scale, w, w_scale):
+    """x int8 [m][k] with x_scale f32 [m], w int8 [2n][k] with w_scale f32 [2n] -> bf16 bits [m][n]."""
+    m, k = x.shape
+    n = w.shape[0] // 2
+    out = np.empty((m, n), np.uint16)
+    _lib.mh3o_gemm_i8_swiglu(m, n, k, _p(np.ascontiguousarray(x)), _p(np.ascontiguousarray(x_scale)),
+                             _p(np.ascontiguousarray(w)), _p(np.ascontiguousarray(w_scale)), _p(out))
     return out
 
 

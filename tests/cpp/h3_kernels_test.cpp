@@ -246,6 +246,33 @@ void int8()
     std::vector<uint16_t> want(size_t(m) * n);
     mh3o_gemm_w8a16_swiglu(m, n, d, x.data(), wq.data(), ws.data(), want.data());
     compare("fc1 int8 + swiglu 300x320 -> 384", of_bf16(out.download()), of_bf16(want), n, 1e-2, 1e-4);
+
+    // The dense bf16 fc1 and the W8A8 fc1 (x quantized per row), against the oracle.
+    std::vector<uint16_t> wb(size_t(2) * n * d);
+    for (size_t i = 0; i < wb.size(); ++i)
+        wb[i] = mh3o_bf16_from_float(w[i]);
+    DeviceBuffer<uint16_t> dwb(wb);
+    k.fc1_swiglu_bf16(m, n, d, dx.get(), dwb.get(), out.get());
+    k.finish();
+    mh3o_gemm_bf16_swiglu(m, n, d, x.data(), wb.data(), want.data());
+    compare("fc1 bf16 + swiglu 300x320 -> 384", of_bf16(out.download()), of_bf16(want), n, 1e-2, 1e-4);
+    const uint32_t d8 = 384; // the W8A8 GEMM takes k in steps of 128
+    auto x8 = bf16_normals(r, size_t(m) * d8);
+    auto w8 = normals(r, size_t(2) * n * d8, 0.05);
+    DeviceBuffer<uint16_t> dx8(x8);
+    DeviceBuffer<float> dw8(w8), dxs(m), dws(2 * n);
+    DeviceBuffer<int8_t> dxq(size_t(m) * d8), dwq(size_t(2) * n * d8);
+    k.quant_rows_i8(m, d8, MH3_BF16, dx8.get(), dxq.get(), dxs.get());
+    k.quant_rows_i8(2 * n, d8, MH3_F32, dw8.get(), dwq.get(), dws.get());
+    k.fc1_swiglu_w8a8(m, n, d8, dxq.get(), dxs.get(), dwq.get(), dws.get(), out.get());
+    k.finish();
+    std::vector<int8_t> oxq(size_t(m) * d8), owq(size_t(2) * n * d8);
+    std::vector<float> oxs(m), ows(2 * n);
+    mh3o_quant_rows_i8(m, d8, MH3O_BF16, x8.data(), oxq.data(), oxs.data());
+    mh3o_quant_rows_i8(2 * n, d8, MH3O_F32, w8.data(), owq.data(), ows.data());
+    check(dxq.download() == oxq && dxs.download() == oxs, "quant_rows_i8 of bf16 activations bit for bit");
+    mh3o_gemm_i8_swiglu(m, n, d8, oxq.data(), oxs.data(), owq.data(), ows.data(), want.data());
+    compare("fc1 W8A8 gemm_i8 + swiglu 300x384 -> 384", of_bf16(out.download()), of_bf16(want), n, 1e-2, 1e-4);
 }
 
 void errors()

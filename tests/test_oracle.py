@@ -354,6 +354,34 @@ def test_gemm_bf16_exact_integers():
     assert (got == 40 * up).all()
 
 
+def test_gemm_i8_swiglu_matches_torch_matmul():
+    rng = np.random.default_rng(19)
+    m, n, k = 6, 16, 96
+    x = rng.integers(-127, 128, (m, k), dtype=np.int8)
+    w = rng.integers(-127, 128, (2 * n, k), dtype=np.int8)
+    sx = rng.uniform(0.005, 0.05, m).astype(np.float32)
+    sw = rng.uniform(0.5e-3, 2e-3, 2 * n).astype(np.float32)
+    got = orc.gemm_i8_swiglu(x, sx, w, sw)
+    y = (torch.from_numpy(x.astype(np.int64)) @ torch.from_numpy(w.astype(np.int64)).T).double()
+    y = y * torch.from_numpy(sx.astype(np.float64))[:, None] * torch.from_numpy(sw.astype(np.float64))[None, :]
+    want = torch.nn.functional.silu(y[:, :n]) * y[:, n:]
+    assert (got == orc.bf16_from_f64(want.numpy())).all()
+
+
+def test_gemm_i8_exact_integers():
+    """Unit scales, gate rows giving 40, up rows in {-1, 0, 1}: out = bf16(40 * y_up) exactly."""
+    rng = np.random.default_rng(20)
+    m, n, k = 5, 8, 128
+    x = rng.integers(-2, 3, (m, k), dtype=np.int8)
+    x[:, 0] = 1
+    w = np.zeros((2 * n, k), np.int8)
+    w[:n, 0] = 40
+    w[n:] = rng.integers(-1, 2, (n, k), dtype=np.int8)
+    got = bits_to_f64(orc.gemm_i8_swiglu(x, np.ones(m, np.float32), w, np.ones(2 * n, np.float32)))
+    up = x.astype(np.float64) @ w[n:].T.astype(np.float64)
+    assert (got == 40 * up).all()
+
+
 # ---- committed fixtures --------------------------------------------------------------------------------------------
 
 def test_golden_fixtures_reproduce():
