@@ -106,6 +106,51 @@ def bench_copy(dev, steps, warmup):
     return {"ms": ms, "bytes": nbytes, "GBs": nbytes / ms / 1e6, "frac": nbytes / ms / 1e6 / HBM_PEAK_GBS}
 
 
+def bench_stream(dev, steps, warmup):
+    """The streaming ceiling: a plain HIP kernel reading, copying, and reading two streams into a third (the fused
+    row op's and SwiGLU's mix), 16-byte non-temporal accesses over 768p-sized bf16 buffers (1.33 GB each), swept
+    over unroll (2, 4, 8 vectors a thread) and grid (flat; 4, 8, 16 workgroups a CU, grid-stride); the best of each
+    mix is reported. Also the MFMA peaks from the device's CU count and peak clock (flops a clock a CU: bf16 4096,
+    int8 8192)."""
+    import ctypes as C
+
+    lib = C.CDLL(str(REPO / "mako-video_amd" / "lib" / "libmh3_stream_probe.so"))
+    lib.mh3_probe_stream.argtypes = [C.c_int, C.c_void_p, C.c_void_p, C.c_void_p, C.c_uint64, C.c_int, C.c_uint32,
+                                     C.c_void_p]
+    lib.mh3_probe_device.argtypes = [C.POINTER(C.c_int), C.POINTER(C.c_int)]
+    cus, khz = C.c_int(0), C.c_int(0)
+    if lib.mh3_probe_device(C.byref(cus), C.byref(khz)) != 0:
+        raise RuntimeError("mh3_probe_device failed")
+    nbytes = ROWS * DIM * 2
+    a = torch.empty(nbytes, dtype=torch.uint8, device=dev).fill_(1)
+    b = torch.empty_like(a).fill_(2)
+    c = torch.empty_like(a)
+    stream = torch.cuda.current_stream().cuda_stream
+    res = {"bytes_per_stream": nbytes}
+    for kind, name, moved in ((0, "read", 1), (1, "copy", 2), (2, "r2w1", 3)):
+        best = None
+        for unroll in (2, 4, 8):
+            for per_cu in (0, 4, 8, 16):
+                blocks = per_cu * cus.value
+
+                def run():
+                    rc = lib.mh3_probe_stream(kind, a.data_ptr(), b.data_ptr(), c.data_ptr(), nbytes // 16, unroll,
+                                              blocks, stream)
+                    if rc != 0:
+                        raise RuntimeError(f"mh3_probe_stream({name}) returned {rc}")
+                ms, _ = time_launches(run, max(5, steps // 2), 2)
+                if best is None or ms < best[0]:
+                    best = (ms, unroll, per_cu)
+        ms, unroll, per_cu = best
+        res[name] = {"ms": ms, "GBs": moved * nbytes / ms / 1e6, "frac": moved * nbytes / ms / 1e6 / HBM_PEAK_GBS,
+                     "unroll": unroll, "grid": "flat" if per_cu == 0 else f"{per_cu} workgroups a CU"}
+    clk = khz.value * 1e3
+    res["device"] = {"cus": cus.value, "peak_clock_mhz": khz.value / 1e3,
+                     "bf16_mfma_peak_tflops": cus.value * clk * 4096 / 1e12,
+                     "int8_mfma_peak_tops": cus.value * clk * 8192 / 1e12}
+    return res
+
+
 def bench_rms_f32(mh, dev, steps, warmup):
     g = torch.Generator(device=dev).manual_seed(3)
     x = torch.randn((4096, 1024), generator=g, device=dev)
@@ -214,6 +259,8 @@ def bench_fc1(mh, dev, steps, warmup, compare):
     qms, _ = time_launches(lambda: mh.quant_rows_i8(x, q=xq, scale=xs), steps, warmup)
     ims, _ = time_launches(lambda: mh.gemm_i8_swiglu(xq, xs, w, s, out=out), steps, warmup)
     res["w8a8_quant_x_ms"] = qms
+    res["w8a8_quant_x_GBs"] = ROWS * (DIM * 3 + 4) / qms / 1e6       # read bf16 x; write int8 x and a scale a row
+    res["w8a8_quant_x_frac"] = res["w8a8_quant_x_GBs"] / HBM_PEAK_GBS
     res["w8a8_fc1_ms"] = ims
     res["w8a8_fc1_tops"] = flops / ims / 1e9
     res["w8a8_fc1_int8_mfma_util"] = flops / ims / 1e9 / INT8_PEAK_TOPS
@@ -249,9 +296,115 @@ def cpu_baseline(seconds: float = 10.0) -> dict:
     n = int(min(ROWS, max(64, 64 * seconds / max(t, 1e-6))))
     t = run(n)
     gbs = n * DIM * 6 / t / 1e9
+    # The same port row-parallel on every core this process may use (the oracle releases the GIL in its C call).
+    cores = len(os.sched_getaffinity(0))
+    x = orc.bf16_from_f64(rng.standard_normal((n, DIM)))
+    r = orc.bf16_from_f64(rng.standard_normal((n, DIM)))
+    w = (1 + 0.02 * rng.standard_normal(DIM)).astype(np.float32)
+    sh, sc, ga = [(0.1 * rng.standard_normal((1, DIM))).astype(np.float32) for _ in range(3)]
+    chunks = np.array_split(np.arange(n), cores)
+    from concurrent.futures import ThreadPoolExecutor
+    with ThreadPoolExecutor(cores) as ex:
+        t0 = time.perf_counter()
+        list(ex.map(lambda c: orc.rms_mod_gate_add_rows(x[c[0]:c[-1] + 1], r[c[0]:c[-1] + 1], w, sh, sc, ga),
+                    [c for c in chunks if len(c)]))
+        tp = time.perf_counter() - t0
     return {"value": gbs, "unit": "GB/s", "cores": 1, "kind": "port",
             "sample": f"fused modulated RMS norm + gated residual over {n} of the {ROWS} rows x {DIM} bf16 "
-                      f"({t:.1f} s), scalar C oracle, one thread on {platform.processor() or platform.machine()}"}
+                      f"({t:.1f} s), scalar C oracle, one thread on {platform.processor() or platform.machine()}",
+            "row_parallel": {"value": n * DIM * 6 / tp / 1e9, "unit": "GB/s", "cores": cores,
+                             "sample": f"the same {n} rows split over {cores} threads ({tp:.2f} s)"}}
+
+
+def _parallel(fn, parts, cores):
+    """Run fn(part) for every part on `cores` threads (the oracle's C calls release the GIL); wall seconds."""
+    from concurrent.futures import ThreadPoolExecutor
+    with ThreadPoolExecutor(cores) as ex:
+        t0 = time.perf_counter()
+        list(ex.map(fn, parts))
+        return time.perf_counter() - t0
+
+
+def cpu_baseline_configs(gpu: dict) -> dict:
+    """The scalar C oracle on the other workloads, one thread and row-parallel on every host core, each on a sample
+    of a few seconds; figures for the full workload are extrapolated linearly from the sample and say so."""
+    sys.path.insert(0, str(REPO / "oracle"))
+    import oracle as orc
+
+    cores = len(os.sched_getaffinity(0))
+    rng = np.random.default_rng(5)
+    out = {}
+
+    def timed(fn):
+        t0 = time.perf_counter()
+        fn()
+        return time.perf_counter() - t0
+
+    # modulated RMS norm, f32 [4096][1024], full size
+    x = rng.standard_normal((4096, 1024)).astype(np.float32)
+    w = (1 + 0.02 * rng.standard_normal(1024)).astype(np.float32)
+    sh, sc = [(0.1 * rng.standard_normal((1, 1024))).astype(np.float32) for _ in range(2)]
+    t1 = timed(lambda: orc.rms_mod_rows(x, w, sh, sc))
+    parts = np.array_split(np.arange(4096), cores)
+    tp = _parallel(lambda c: orc.rms_mod_rows(x[c[0]:c[-1] + 1], w, sh, sc), parts, cores)
+    nb = 4096 * 1024 * 8
+    out["rms_mod_f32_4096x1024"] = {"unit": "GB/s", "single": nb / t1 / 1e9, "row_parallel": nb / tp / 1e9,
+                                    "sample": "full size", "gpu": gpu.get("rms_mod_f32_4096x1024", {}).get("GBs")}
+
+    # SwiGLU, split gate and up [129,536][13,824] bf16: a row sample
+    base = orc.bf16_from_f64(rng.standard_normal((64, FFN)))
+    n1 = 64 * max(1, int(1.0 / max(timed(lambda: orc.swiglu_rows(base, base)), 1e-3) // 1))
+    n1 = min(n1, 4096)
+    g = np.tile(base, (n1 // 64, 1))
+    u = np.roll(g, 1, axis=1)
+    t1 = timed(lambda: orc.swiglu_rows(g, u))
+    gp, up = np.tile(g, (cores, 1)), np.tile(u, (cores, 1))
+    parts = [slice(i * n1, (i + 1) * n1) for i in range(cores)]
+    tp = _parallel(lambda sl: orc.swiglu_rows(gp[sl], up[sl]), parts, cores)
+    single, par = n1 * FFN * 6 / t1 / 1e9, cores * n1 * FFN * 6 / tp / 1e9
+    out["swiglu_129536x13824"] = {"unit": "GB/s", "single": single, "row_parallel": par,
+                                  "full_ms_extrapolated": {"single": ROWS * FFN * 6 / single / 1e6,
+                                                           "row_parallel": ROWS * FFN * 6 / par / 1e6},
+                                  "sample": f"{n1} rows on one thread, {cores} x {n1} rows on {cores} threads",
+                                  "gpu": gpu.get("swiglu", {}).get("split", {}).get("GBs")}
+    del gp, up, g, u
+
+    # cube selector (pool, scores, top-k) per head: one head on one thread, one head a thread on all cores
+    rows_h = GRID[0] * GRID[1] * GRID[2]
+    k = math.ceil(0.1 * (GRID[0] // 4) * (GRID[1] // 4) * (GRID[2] // 4))
+    q0 = orc.bf16_from_f64(rng.standard_normal((1, rows_h, 128)))
+    heads_p = min(cores, HEADS)
+    qs = [np.roll(q0, 7 * h, axis=1) for h in range(heads_p)]
+    ks = [np.roll(q0, 7 * h + 3, axis=1) for h in range(heads_p)]
+
+    def one_head(h):
+        qc, kc, _ = orc.cube_pool(qs[h], ks[h], 1, GRID)
+        orc.cube_topk(orc.cube_scores(qc, kc), GRID, k, 1, sorted_form=True)
+    t1 = timed(lambda: one_head(0))
+    tp = _parallel(one_head, range(heads_p), cores)
+    sel = gpu.get("cube_selector", {})
+    out["cube_selector_40x2016"] = {"unit": "ms for 40 heads (extrapolated)", "single": 1e3 * t1 * HEADS,
+                                    "row_parallel": 1e3 * tp * math.ceil(HEADS / heads_p),
+                                    "sample": f"1 head on one thread; {heads_p} heads, one a thread",
+                                    "gpu": sel.get("ms")}
+    del qs, ks
+
+    # fc1 W8A16 + SwiGLU [129,536] x 5120 x 27,648: a row slice
+    wq = rng.integers(-127, 128, (2 * FFN, DIM), dtype=np.int8)
+    ws = rng.uniform(0.5e-3, 2e-3, 2 * FFN).astype(np.float32)
+    xr = orc.bf16_from_f64(rng.standard_normal((4 * cores, DIM)))
+    t1 = timed(lambda: orc.gemm_w8a16_swiglu(xr[:4], wq, ws))
+    tp = _parallel(lambda i: orc.gemm_w8a16_swiglu(xr[4 * i:4 * i + 4], wq, ws), range(cores), cores)
+    fl = 2 * DIM * 2 * FFN
+    fc = gpu.get("fc1_w8a16_swiglu", {})
+    out["fc1_w8a16_swiglu"] = {"unit": "TFLOP/s", "single": 4 * fl / t1 / 1e12, "row_parallel": 4 * cores * fl / tp / 1e12,
+                               "full_ms_extrapolated": {"single": 1e3 * t1 * ROWS / 4,
+                                                        "row_parallel": 1e3 * tp * ROWS / (4 * cores)},
+                               "sample": f"4 rows on one thread, {cores} x 4 rows on {cores} threads",
+                               "gpu": fc.get("tflops")}
+    out["cores"] = cores
+    out["cpu"] = platform.processor() or platform.machine()
+    return out
 
 
 def main() -> int:
@@ -280,6 +433,10 @@ def main() -> int:
         torch.cuda.empty_cache()
     if "copy" in ops:
         report["hbm_copy"] = bench_copy(dev, args.steps, args.warmup)
+        report["stream_ceiling"] = bench_stream(dev, args.steps, args.warmup)
+        head = report.get("fused_rms_mod_gate_add")
+        if head:
+            report["stream_ceiling"]["fused_vs_r2w1"] = head["GBs"] / report["stream_ceiling"]["r2w1"]["GBs"]
         torch.cuda.empty_cache()
     if "rms_f32" in ops:
         report["rms_mod_f32_4096x1024"] = bench_rms_f32(mh, dev, args.steps, args.warmup)
@@ -320,6 +477,7 @@ def main() -> int:
                             "frac": round(head["frac"], 4), "traffic": traffic}
     if not args.no_cpu:
         line["cpu_baseline"] = cpu_baseline()
+        line["cpu_baseline"]["other_workloads"] = cpu_baseline_configs(report)
     line["ops"] = report
     print(json.dumps(line), flush=True)
     return 0

@@ -1,6 +1,6 @@
 """Builds libmako_h3.so, the gfx950 kernels and their C-ABI (include/mako_h3.h), in-tree with hipcc.
 
-    python mako-video_amd/build.py            # -> mako-video_amd/lib/libmako_h3.so
+    python mako-video_amd/build.py            # -> mako-video_amd/lib/libmako_h3.so, libmh3_stream_probe.so
 
 Every HIP source is compiled for gfx950 only, with packed-FP32 instruction selection switched off (the compiler's
 v_pk_*_f32 forms are not trusted on these boxes), then linked into one shared library that host code binds through
@@ -37,6 +37,9 @@ COMMON = [
     f"-I{CSRC}",
 ]
 SOURCES = ["rows.hip", "cubes.hip", "quant.hip", "gemm_w8a16.hip", "abi.cpp"]
+# The streaming-bandwidth probe bench.py reports beside the kernels: its own library, not part of the C-ABI.
+PROBE_SOURCE = "probe/stream_probe.hip"
+PROBE_LIB = PKG / "lib" / "libmh3_stream_probe.so"
 
 
 def _compile(src: str) -> Path:
@@ -55,21 +58,26 @@ def _compile(src: str) -> Path:
     return out
 
 
+def _link(objs: list[Path], lib: Path, verbose: bool) -> None:
+    tmp = lib.with_suffix(".so.tmp")
+    cmd = [HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(tmp), *map(str, objs)]
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError(f"link failed:\n{r.stderr}")
+    os.replace(tmp, lib)
+    if verbose:
+        print(f"built {lib.relative_to(REPO)}")
+
+
 def build(verbose: bool = True) -> Path:
     if not Path(HIPCC).exists() and shutil.which("hipcc") is None:
         raise RuntimeError("hipcc not found")
     OBJ.mkdir(exist_ok=True)
     LIB.parent.mkdir(exist_ok=True)
     with cf.ThreadPoolExecutor(max_workers=min(8, os.cpu_count() or 4)) as ex:
-        objs = list(ex.map(_compile, SOURCES))
-    tmp = LIB.with_suffix(".so.tmp")
-    cmd = [HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(tmp), *map(str, objs)]
-    r = subprocess.run(cmd, capture_output=True, text=True)
-    if r.returncode != 0:
-        raise RuntimeError(f"link failed:\n{r.stderr}")
-    os.replace(tmp, LIB)
-    if verbose:
-        print(f"built {LIB.relative_to(REPO)}")
+        objs = list(ex.map(_compile, SOURCES + [PROBE_SOURCE]))
+    _link(objs[:-1], LIB, verbose)
+    _link(objs[-1:], PROBE_LIB, verbose)
     return LIB
 
 

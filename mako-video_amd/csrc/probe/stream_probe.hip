@@ -1,0 +1,108 @@
+// HBM streaming probe: the bandwidth a plain streaming kernel reaches on this GPU, as the ceiling against which the
+// row kernels' fractions of the 8 TB/s nameplate are read. Three access mixes over 16-byte vectors:
+//   kind 0 (read):  read a (n vectors); nothing is written unless the XOR of all data equals a fixed value;
+//   kind 1 (copy):  c = a;                                 one read stream, one write stream;
+//   kind 2 (r2w1):  c = a + b (as 32-bit lanes);            two read streams, one write: the fused row op's and
+//                                                           SwiGLU's mix.
+// 256 threads a workgroup; each thread moves U vectors 256 apart per step, non-temporal loads and stores; a flat grid
+// (blocks = 0: one step a thread) or a grid-stride loop over `blocks` workgroups. Every access is i < n. bench.py
+// sweeps U and the grid and reports the best of each mix as the ceiling.
+// This library is a measurement tool beside libmako_h3.so; it has no counterpart in the reference.
+//
+//   int mh3_probe_stream(int kind, const void* a, const void* b, void* c, uint64_t n, int unroll, uint32_t blocks,
+//                        void* stream);   unroll 2, 4 or 8
+//   returns 0, -1 for a bad kind, unroll or null pointer, -2 for misaligned pointers, -3 for a launch failure.
+//   int mh3_probe_device(int* cus, int* max_clock_khz);  the current device's CU count and peak engine clock, from
+//   which the MFMA peak is CUs x clock x flops a clock a CU.
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+namespace {
+
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+constexpr uint32_t kThreads = 256;
+
+template <int KIND, int U>
+__global__ __launch_bounds__(kThreads) void stream_kernel(const u32x4* __restrict__ a, const u32x4* __restrict__ b,
+                                                          u32x4* __restrict__ c, uint64_t n)
+{
+    const uint64_t stride = uint64_t(gridDim.x) * kThreads * U;
+    uint32_t acc = 0;
+    for (uint64_t base = uint64_t(blockIdx.x) * kThreads * U + threadIdx.x; base < n; base += stride) {
+        u32x4 va[U], vb[U];
+#pragma unroll
+        for (int j = 0; j < U; ++j) {
+            const uint64_t i = base + uint64_t(j) * kThreads;
+            va[j] = i < n ? __builtin_nontemporal_load(a + i) : u32x4{0u, 0u, 0u, 0u};
+            if constexpr (KIND == 2)
+                vb[j] = i < n ? __builtin_nontemporal_load(b + i) : u32x4{0u, 0u, 0u, 0u};
+        }
+        if constexpr (KIND == 0) {
+#pragma unroll
+            for (int j = 0; j < U; ++j)
+                acc ^= va[j][0] ^ va[j][1] ^ va[j][2] ^ va[j][3];
+        } else {
+#pragma unroll
+            for (int j = 0; j < U; ++j) {
+                const uint64_t i = base + uint64_t(j) * kThreads;
+                if (i < n)
+                    __builtin_nontemporal_store(KIND == 2 ? va[j] + vb[j] : va[j], c + i);
+            }
+        }
+    }
+    if (KIND == 0 && acc == 0x9E3779B9u)
+        c[0] = u32x4{acc, 0u, 0u, 0u};
+}
+
+template <int KIND>
+void launch(int unroll, dim3 grid, hipStream_t s, const u32x4* a, const u32x4* b, u32x4* c, uint64_t n)
+{
+    if (unroll == 2)
+        hipLaunchKernelGGL((stream_kernel<KIND, 2>), grid, dim3(kThreads), 0, s, a, b, c, n);
+    else if (unroll == 4)
+        hipLaunchKernelGGL((stream_kernel<KIND, 4>), grid, dim3(kThreads), 0, s, a, b, c, n);
+    else
+        hipLaunchKernelGGL((stream_kernel<KIND, 8>), grid, dim3(kThreads), 0, s, a, b, c, n);
+}
+
+} // namespace
+
+extern "C" int mh3_probe_stream(int kind, const void* a, const void* b, void* c, uint64_t n, int unroll,
+                                uint32_t blocks, void* stream)
+{
+    if (kind < 0 || kind > 2 || !a || !c || (kind == 2 && !b) || (unroll != 2 && unroll != 4 && unroll != 8))
+        return -1;
+    if ((reinterpret_cast<uintptr_t>(a) | reinterpret_cast<uintptr_t>(b) | reinterpret_cast<uintptr_t>(c)) & 15u)
+        return -2;
+    if (n == 0)
+        return 0;
+    const uint64_t flat = (n + kThreads * unroll - 1) / (kThreads * unroll);
+    const uint64_t grid_blocks = blocks ? (blocks < flat ? blocks : flat) : flat;
+    if (grid_blocks >= (1ull << 31))
+        return -1;
+    const auto* pa = static_cast<const u32x4*>(a);
+    const auto* pb = static_cast<const u32x4*>(b);
+    auto* pc = static_cast<u32x4*>(c);
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    const dim3 grid{uint32_t(grid_blocks)};
+    if (kind == 0)
+        launch<0>(unroll, grid, s, pa, pb, pc, n);
+    else if (kind == 1)
+        launch<1>(unroll, grid, s, pa, pb, pc, n);
+    else
+        launch<2>(unroll, grid, s, pa, pb, pc, n);
+    return hipGetLastError() == hipSuccess ? 0 : -3;
+}
+
+extern "C" int mh3_probe_device(int* cus, int* max_clock_khz)
+{
+    if (!cus || !max_clock_khz)
+        return -1;
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess ||
+        hipDeviceGetAttribute(cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+        hipDeviceGetAttribute(max_clock_khz, hipDeviceAttributeClockRate, dev) != hipSuccess)
+        return -3;
+    return 0;
+}

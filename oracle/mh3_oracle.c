@@ -291,6 +291,62 @@ void mh3o_cube_topk(uint32_t heads, uint32_t gt, uint32_t gh, uint32_t gw, uint3
                                                 idx + (h * C + i) * out_stride);
 }
 
+/* The same selection by sorting each row once, O(C log C) a row: the form a CPU implementation would take, timed by
+ * bench.py's CPU baseline. (score desc, index asc) is a total order, so it selects exactly what mh3o_cube_topk does. */
+typedef struct {
+    double s;
+    int32_t j;
+} mh3o_scored;
+
+static int mh3o_scored_cmp(const void* pa, const void* pb)
+{
+    const mh3o_scored* a = (const mh3o_scored*)pa;
+    const mh3o_scored* b = (const mh3o_scored*)pb;
+    if (a->s != b->s)
+        return a->s > b->s ? -1 : 1;
+    return a->j < b->j ? -1 : (a->j > b->j);
+}
+
+void mh3o_cube_topk_sorted(uint32_t heads, uint32_t gt, uint32_t gh, uint32_t gw, uint32_t k, uint32_t local,
+                           uint32_t out_stride, const double* s, int32_t* idx, int32_t* cnt)
+{
+    const uint32_t ch = (gh + 3) / 4, cw = (gw + 3) / 4, cth = (gt + 3) / 4;
+    const uint64_t C = (uint64_t)cth * ch * cw, plane = (uint64_t)ch * cw;
+    mh3o_scored* row = (mh3o_scored*)malloc(sizeof(mh3o_scored) * C);
+    unsigned char* sel = (unsigned char*)malloc(C);
+    for (uint64_t h = 0; h < heads; ++h)
+        for (uint64_t i = 0; i < C; ++i) {
+            const double* r = s + (h * C + i) * C;
+            for (uint64_t j = 0; j < C; ++j) {
+                row[j].s = r[j];
+                row[j].j = (int32_t)j;
+                sel[j] = 0;
+            }
+            qsort(row, C, sizeof(mh3o_scored), mh3o_scored_cmp);
+            for (uint64_t j = 0; j < C && j < k; ++j)
+                sel[row[j].j] = 1;
+            if (local >= 1)
+                sel[i] = 1;
+            if (local == 3) {
+                const uint64_t ct = i / plane;
+                if (ct > 0)
+                    sel[i - plane] = 1;
+                if (ct + 1 < cth)
+                    sel[i + plane] = 1;
+            }
+            int32_t* out = idx + (h * C + i) * out_stride;
+            int32_t n = 0;
+            for (uint64_t j = 0; j < C; ++j)
+                if (sel[j])
+                    out[n++] = (int32_t)j;
+            for (uint32_t j = (uint32_t)n; j < out_stride; ++j)
+                out[j] = -1;
+            cnt[h * C + i] = n;
+        }
+    free(sel);
+    free(row);
+}
+
 /* ---- int8 ------------------------------------------------------------------------------------------------------ */
 
 /* docs/performance.md:122-123: "int8 rows with a float scale each (symmetric, the row's maximum at 127)". The scale

@@ -24,6 +24,8 @@
  *                              permutation invariance inside a cube; gathered layout == grid layout
  *   mh3o_cube_scores           numpy matmul / sqrt(hd)
  *   mh3o_cube_topk             numpy lexsort; constructed scores with an analytic answer; ratio 1 selects all
+ *   mh3o_cube_topk_sorted      equals mh3o_cube_topk on random and tie-heavy rows (the form bench.py's CPU
+ *                              baseline times: a sort a row instead of the O(C^2) count)
  *   mh3o_quant_rows_i8         |q| <= 127, the row maximum maps to +-127, |w - q*s| <= s/2, numpy rint
  *   mh3o_gemm_w8a16_swiglu     torch.matmul in float64; exact integer results for w in {-1,0,1}, s = 1
  *   mh3o_gemm_bf16_swiglu      torch.matmul in float64; exact integer results for w in {-1,0,1}
@@ -73,6 +75,8 @@ int32_t mh3o_cube_topk_row(uint32_t gt, uint32_t gh, uint32_t gw, uint32_t k, ui
                            uint64_t i, const double* row, int32_t* out);
 void mh3o_cube_topk(uint32_t heads, uint32_t gt, uint32_t gh, uint32_t gw, uint32_t k, uint32_t local,
                     uint32_t out_stride, const double* s, int32_t* idx, int32_t* cnt);
+void mh3o_cube_topk_sorted(uint32_t heads, uint32_t gt, uint32_t gh, uint32_t gw, uint32_t k, uint32_t local,
+                           uint32_t out_stride, const double* s, int32_t* idx, int32_t* cnt);
 
 void mh3o_quant_rows_i8(uint32_t rows, uint32_t cols, int dtype, const void* w, int8_t* q, float* scale);
 

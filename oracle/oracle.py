@@ -49,6 +49,7 @@ _lib.mh3o_cube_pool_some.argtypes = [C.c_uint32] * 4 + [C.c_int, C.c_uint64, C.c
     [_P, _P, _P, C.c_uint64, _P, _P]
 _lib.mh3o_cube_scores.argtypes = [C.c_uint32] * 3 + [_P] * 3
 _lib.mh3o_cube_topk.argtypes = [C.c_uint32] * 7 + [_P] * 3
+_lib.mh3o_cube_topk_sorted.argtypes = [C.c_uint32] * 7 + [_P] * 3
 _lib.mh3o_quant_rows_i8.argtypes = [C.c_uint32, C.c_uint32, C.c_int] + [_P] * 3
 _lib.mh3o_gemm_w8a16_swiglu.argtypes = [C.c_uint32] * 3 + [_P] * 4
 _lib.mh3o_gemm_bf16_swiglu.argtypes = [C.c_uint32] * 3 + [_P] * 3
@@ -165,13 +166,14 @@ def cube_scores(qc, kc):
     return s
 
 
-def cube_topk(s, grid, k, local, out_stride=None):
+def cube_topk(s, grid, k, local, out_stride=None, sorted_form=False):
+    """sorted_form: the O(C log C) a row selection (mh3o_cube_topk_sorted) instead of the O(C^2) count."""
     heads, cubes, _ = s.shape
     out_stride = k + local if out_stride is None else out_stride
     idx = np.empty((heads, cubes, out_stride), np.int32)
     cnt = np.empty((heads, cubes), np.int32)
-    _lib.mh3o_cube_topk(heads, *grid, k, local, out_stride, _p(np.ascontiguousarray(s, dtype=np.float64)), _p(idx),
-                        _p(cnt))
+    fn = _lib.mh3o_cube_topk_sorted if sorted_form else _lib.mh3o_cube_topk
+    fn(heads, *grid, k, local, out_stride, _p(np.ascontiguousarray(s, dtype=np.float64)), _p(idx), _p(cnt))
     return idx, cnt
 
 

@@ -24,6 +24,22 @@ def test_every_declared_symbol_is_exported():
         assert hasattr(mh.lib, n), f"{n} declared in mako_h3.h but not exported"
 
 
+def test_stream_probe_library_loads_and_refuses_bad_calls():
+    """The measurement probe bench.py loads beside the library: both entry points exist, and a bad kind, a null
+    pointer or a misaligned pointer is refused before any launch."""
+    probe = C.CDLL(str(Path(mh.lib._name).parent / "libmh3_stream_probe.so"))
+    probe.mh3_probe_stream.argtypes = [C.c_int, C.c_void_p, C.c_void_p, C.c_void_p, C.c_uint64, C.c_int, C.c_uint32,
+                                       C.c_void_p]
+    assert hasattr(probe, "mh3_probe_device")
+    buf = C.create_string_buffer(64)
+    a = (C.addressof(buf) + 15) // 16 * 16
+    assert probe.mh3_probe_stream(3, a, a, a, 1, 4, 0, None) == -1
+    assert probe.mh3_probe_stream(2, a, None, a, 1, 4, 0, None) == -1
+    assert probe.mh3_probe_stream(1, a, None, a, 1, 3, 0, None) == -1
+    assert probe.mh3_probe_stream(1, a + 4, None, a, 1, 4, 0, None) == -2
+    assert probe.mh3_probe_stream(1, a, None, a, 0, 4, 0, None) == 0
+
+
 def test_abi_version_and_strings():
     assert mh.lib.mh3_abi_version() == 1
     assert mh.strerror(mh.ERR_SHAPE) == "bad shape"

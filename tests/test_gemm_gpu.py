@@ -11,12 +11,17 @@ pytestmark = pytest.mark.gpu
 
 
 @pytest.mark.parametrize("dtype", ["bf16", "f32"])
-@pytest.mark.parametrize("rows,cols", [(1, 16), (7, 5120), (300, 208)])
+@pytest.mark.parametrize("rows,cols", [(1, 16), (7, 5120), (300, 208), (5, 2048), (6, 4096), (3, 8192), (3, 8208),
+                                       (2, 27648)])
 def test_quant_rows_i8_bit_exact(dev, dtype, rows, cols):
+    """Widths up to 8192 keep the row in registers (2, 4 or 8 chunks of 16 a lane); wider rows take the two-read
+    path. The row's last element carries its maximum in one row, so a dropped tail chunk changes the scale."""
     rng = np.random.default_rng(rows + cols)
     if dtype == "bf16":
         w = randn_bf16_bits(rng, (rows, cols), 0.02)
         w[0, :] = 0                                        # an all-zero row: scale 0, q 0
+        if rows > 1:
+            w[1, -1] = 0x3F80                              # 1.0 at the row's last element: its maximum
         tw = from_bits(w, dev)
     else:
         w = (rng.standard_normal((rows, cols)) * 0.02).astype(np.float32)
@@ -28,6 +33,39 @@ def test_quant_rows_i8_bit_exact(dev, dtype, rows, cols):
     wq, ws = orc.quant_rows_i8(w)
     assert (s.cpu().numpy() == ws).all()
     assert (q.cpu().numpy() == wq).all()
+
+
+@pytest.mark.parametrize("cols", [208, 5120, 27648])
+def test_quant_rows_i8_rounding_and_scale_range(dev, cols):
+    """Bit-exact at the cases where a quotient computed other than by IEEE division would differ: exact ties
+    (k + 0.5 at scale 1 and 0.5, rounding to even), scales on both sides of 2^-100 and 2^100 (the kernel switches its
+    division method there), subnormal elements, and 1024 rows whose magnitudes run from 1e-38 to 1e38."""
+    rng = np.random.default_rng(cols)
+    rows = []
+    ties = np.arange(-126.5, 127.0, 1.0, dtype=np.float32)              # every k + 0.5 in range
+    row = np.resize(ties, cols).astype(np.float32)
+    row[0] = 127.0                                                      # max 127: s = 1, quotients are exact ties
+    rows.append(row)
+    rows.append(row * np.float32(0.5))                                  # s = 0.5
+    for e in (-101, -100, -99, 99, 100, 101):                          # s = mx / 127 around 2^-100 and 2^100
+        for f in (0.999, 1.0, 1.001):
+            r = (rng.standard_normal(cols) * 2.0 ** e).astype(np.float32)
+            r[1] = np.float32(127 * f * 2.0 ** e)
+            rows.append(r)
+    r = (rng.standard_normal(cols) * 1e-39).astype(np.float32)          # every element subnormal
+    rows.append(r)
+    r = (rng.standard_normal(cols)).astype(np.float32)
+    r[::7] = np.float32(1e-42)                                          # subnormals among normal values
+    rows.append(r)
+    mags = 10.0 ** rng.uniform(-38, 38, 1024 if cols <= 5120 else 64)
+    rows += [(rng.standard_normal(cols) * m).astype(np.float32) for m in mags]
+    w = np.stack(rows).astype(np.float32)
+    assert np.isfinite(w).all()
+    q, s = mh.quant_rows_i8(torch.from_numpy(w).to(dev))
+    wq, ws = orc.quant_rows_i8(w)
+    assert np.array_equal(s.cpu().numpy().view(np.uint32), ws.view(np.uint32))
+    bad = np.argwhere(q.cpu().numpy() != wq)
+    assert bad.size == 0, f"{len(bad)} differ, first at {bad[:3].tolist()}"
 
 
 def fc1_inputs(rng, m, n, k):

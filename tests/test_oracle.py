@@ -263,6 +263,17 @@ def test_cube_topk_matches_lexsort(local, k):
             assert (idx[h, i, cnt[h, i]:] == -1).all()
 
 
+@pytest.mark.parametrize("local,k", [(0, 1), (1, 7), (3, 12), (1, 48)])
+def test_cube_topk_sorted_form_equals_count_form(local, k):
+    """The sort-a-row selection the CPU baseline times selects exactly what the O(C^2) count does."""
+    rng = np.random.default_rng(40 + k + local)
+    grid = (12, 16, 16)
+    for s in (rng.integers(-3, 3, (2, 48, 48)).astype(np.float64), rng.standard_normal((2, 48, 48))):
+        a_idx, a_cnt = orc.cube_topk(s, grid, k, local, out_stride=k + 4)
+        b_idx, b_cnt = orc.cube_topk(s, grid, k, local, out_stride=k + 4, sorted_form=True)
+        assert (a_cnt == b_cnt).all() and (a_idx == b_idx).all()
+
+
 def test_cube_topk_ratio_one_selects_everything():
     rng = np.random.default_rng(13)
     grid = (8, 8, 8)
