@@ -81,7 +81,12 @@ typedef struct MH3RowsArgs {
     uint32_t n_sets; /* 1 .. 256 */
     uint32_t dtype;  /* MH3_F32 or MH3_BF16 */
     float eps;       /* > 0 (H3: 1e-6) */
-    uint32_t reserved[3];
+    /* Floats from set s's shift, scale and gate vectors to set s + 1's; 0 means dim (separate [n_sets][dim]
+     * arrays). Otherwise a multiple of 4 and at least dim: shift, scale and gate may then point into one table of
+     * interleaved vectors, such as the reference's [U][3][6][D] modulation table (h3_ref_test.cpp:229-241), whose
+     * (level, tag) sets are 6 D floats apart. */
+    uint32_t set_stride;
+    uint32_t reserved[2];
 } MH3RowsArgs;
 
 /* y = x * rsqrt(mean(x^2) + eps) * w * (1 + scale[s]) + shift[s]. y may equal x. */

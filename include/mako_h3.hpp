@@ -93,6 +93,9 @@ struct Modulation {
     const float* gate = nullptr;
     const uint8_t* set_of_row = nullptr;
     uint32_t n_sets = 1;
+    // Floats from one set's shift / scale / gate vector to the next set's; 0: dim. With the reference's
+    // [U][3][6][D] table, shift = table + i D (i the vector's slot), and set_stride = 6 D.
+    uint32_t set_stride = 0;
 };
 
 // The H3 grid of generated video rows and the sparse selector's parameters (H3::Cubes, H3::set_sparse).
@@ -226,7 +229,7 @@ public:
 private:
     static MH3RowsArgs rows_args(uint32_t rows, uint32_t dim, uint32_t dtype, const Modulation& m, float eps)
     {
-        return MH3RowsArgs{rows, dim, m.n_sets, dtype, eps, {0, 0, 0}};
+        return MH3RowsArgs{rows, dim, m.n_sets, dtype, eps, m.set_stride, {0, 0}};
     }
     hipStream_t s_;
 };

@@ -98,6 +98,7 @@ struct RowsParams {
     const float* gate;
     const uint8_t* set_of_row;
     uint32_t rows, dim, nvec, n_sets;
+    uint32_t set_stride; // floats from one set's shift / scale / gate vector to the next set's
     float eps, inv_dim;
     uint32_t rows_per_wave; // wave kernel: 0 = persistent grid
 };
@@ -111,7 +112,7 @@ template <int OP, int E>
 __device__ __forceinline__ void coef_vec(const RowsParams& p, uint32_t s, uint32_t c0, float (&a)[E], float (&b)[E],
                                          float (&c)[E])
 {
-    const uint64_t i = uint64_t(s) * p.dim + c0;
+    const uint64_t i = uint64_t(s) * p.set_stride + c0;
 #pragma unroll
     for (int q = 0; q < E / 4; ++q) {
         float g[4], w[4], sc[4], sh[4];
@@ -635,6 +636,7 @@ int launch_rows(const MH3RowsArgs* a, RowsParams p, hipStream_t stream)
     p.dim = a->dim;
     p.nvec = a->dim / e;
     p.n_sets = a->n_sets;
+    p.set_stride = a->set_stride ? a->set_stride : a->dim;
     p.eps = a->eps;
     p.inv_dim = 1.0f / float(a->dim);
     return a->dtype == MH3_BF16 ? launch_rows_dt<MH3_BF16, OP>(p, stream) : launch_rows_dt<MH3_F32, OP>(p, stream);
@@ -652,6 +654,8 @@ int check_rows(const MH3RowsArgs* a, bool needs_eps)
     const uint32_t e = a->dtype == MH3_BF16 ? 8u : 4u;
     if (a->dim == 0 || a->dim % e != 0 || a->n_sets == 0 || a->n_sets > 256)
         return MH3_ERR_SHAPE;
+    if (a->set_stride != 0 && (a->set_stride < a->dim || a->set_stride % 4 != 0))
+        return MH3_ERR_PARAM;
     if (a->dim / e > 4096u)
         return MH3_ERR_UNSUPPORTED;
     if (a->rows >= (1u << 31))

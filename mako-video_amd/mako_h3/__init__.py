@@ -29,7 +29,7 @@ INT8_QKV, INT8_OUT, INT8_FC1, INT8_FC2, INT8_ALL = 1, 2, 4, 8, 15
 
 class RowsArgs(C.Structure):
     _fields_ = [("rows", C.c_uint32), ("dim", C.c_uint32), ("n_sets", C.c_uint32), ("dtype", C.c_uint32),
-                ("eps", C.c_float), ("reserved", C.c_uint32 * 3)]
+                ("eps", C.c_float), ("set_stride", C.c_uint32), ("reserved", C.c_uint32 * 2)]
 
 
 class SwigluArgs(C.Structure):
@@ -162,12 +162,35 @@ def _rows_args(x: torch.Tensor, n_sets: int, eps: float) -> RowsArgs:
     return a
 
 
-def _mod_params(dim, n_sets, w, shift, scale, gate, set_of_row, rows):
+def _set_stride(t: torch.Tensor, name: str, dim: int, n_sets: int) -> int:
+    """Floats between consecutive sets of a modulation vector tensor [..., dim]: its leading dimensions must collapse
+    to one stride (a contiguous [n_sets][dim] tensor, or a view into a table such as [U][3][6][D] with one of the six
+    vectors selected) and cover n_sets sets."""
+    if not isinstance(t, torch.Tensor) or t.device.type != "cuda" or t.dtype != torch.float32:
+        raise ValueError(f"{name}: expected a float32 tensor on the GPU")
+    if t.shape[-1] != dim or t.stride(-1) != 1:
+        raise ValueError(f"{name}: the last dimension must be dim ({dim}) and contiguous")
+    lead = [(n, st) for n, st in zip(t.shape[:-1], t.stride()[:-1]) if n != 1]
+    for (n0, s0), (n1, s1) in zip(lead, lead[1:]):
+        if s0 != s1 * n1:
+            raise ValueError(f"{name}: its sets are not evenly spaced")
+    sets = 1
+    for n, _ in lead:
+        sets *= n
+    if sets < n_sets:
+        raise ValueError(f"{name}: {sets} sets, the call uses {n_sets}")
+    return lead[-1][1] if lead else dim
+
+
+def _mod_params(a, dim, n_sets, w, shift, scale, gate, set_of_row, rows):
     if w is not None:
         _need(w, "w", torch.float32, dim)
-    for name, t in (("shift", shift), ("scale", scale), ("gate", gate)):
-        if t is not None:
-            _need(t, name, torch.float32, n_sets * dim)
+    strides = {_set_stride(t, name, dim, n_sets) for name, t in (("shift", shift), ("scale", scale), ("gate", gate))
+               if t is not None}
+    if len(strides) > 1:
+        raise ValueError("shift, scale and gate must share one set stride")
+    if n_sets > 1 and strides:
+        a.set_stride = strides.pop()
     if set_of_row is not None:
         _need(set_of_row, "set_of_row", torch.uint8, rows)
 
@@ -176,7 +199,7 @@ def rms_mod_rows(x, w, shift, scale, *, eps=1e-6, set_of_row=None, n_sets=1, out
     """y = x * rsqrt(mean(x^2) + eps) * w * (1 + scale[s]) + shift[s] per row (x: [rows][dim] f32 or bf16)."""
     a = _rows_args(x, n_sets, eps)
     _need(x, "x", x.dtype, x.numel())
-    _mod_params(x.shape[1], n_sets, w, shift, scale, None, set_of_row, x.shape[0])
+    _mod_params(a, x.shape[1], n_sets, w, shift, scale, None, set_of_row, x.shape[0])
     out = torch.empty_like(x) if out is None else out
     _need(out, "out", x.dtype, x.numel())
     _check(lib.mh3_rms_mod_rows(C.byref(a), _ptr(x), _ptr(w), _ptr(shift), _ptr(scale), _ptr(set_of_row), _ptr(out),
@@ -189,7 +212,7 @@ def gate_add_rows(x, y, gate, *, set_of_row=None, n_sets=1):
     a = _rows_args(x, n_sets, 1.0)
     _need(x, "x", x.dtype, x.numel())
     _need(y, "y", x.dtype, x.numel())
-    _mod_params(x.shape[1], n_sets, None, None, None, gate, set_of_row, x.shape[0])
+    _mod_params(a, x.shape[1], n_sets, None, None, None, gate, set_of_row, x.shape[0])
     _check(lib.mh3_gate_add_rows(C.byref(a), _ptr(x), _ptr(y), _ptr(gate), _ptr(set_of_row), _stream()),
            "gate_add_rows")
     return x
@@ -200,7 +223,7 @@ def rms_mod_gate_add_rows(x, residual, w, shift, scale, gate, *, eps=1e-6, set_o
     a = _rows_args(x, n_sets, eps)
     _need(x, "x", x.dtype, x.numel())
     _need(residual, "residual", x.dtype, x.numel())
-    _mod_params(x.shape[1], n_sets, w, shift, scale, gate, set_of_row, x.shape[0])
+    _mod_params(a, x.shape[1], n_sets, w, shift, scale, gate, set_of_row, x.shape[0])
     out = torch.empty_like(x) if out is None else out
     _need(out, "out", x.dtype, x.numel())
     _check(lib.mh3_rms_mod_gate_add_rows(C.byref(a), _ptr(x), _ptr(residual), _ptr(w), _ptr(shift), _ptr(scale),
@@ -214,7 +237,7 @@ def gate_add_rms_mod_rows(x, y, gate, w, shift, scale, *, eps=1e-6, set_of_row=N
     a = _rows_args(x, n_sets, eps)
     _need(x, "x", x.dtype, x.numel())
     _need(y, "y", x.dtype, x.numel())
-    _mod_params(x.shape[1], n_sets, w, shift, scale, gate, set_of_row, x.shape[0])
+    _mod_params(a, x.shape[1], n_sets, w, shift, scale, gate, set_of_row, x.shape[0])
     h = torch.empty_like(x) if h is None else h
     _need(h, "h", x.dtype, x.numel())
     _check(lib.mh3_gate_add_rms_mod_rows(C.byref(a), _ptr(x), _ptr(y), _ptr(gate), _ptr(w), _ptr(shift), _ptr(scale),

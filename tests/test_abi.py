@@ -88,7 +88,8 @@ def rows_args(**kw):
 
 @pytest.mark.parametrize("kw,code", [({"dtype": 7}, mh.ERR_PARAM), ({"eps": 0.0}, mh.ERR_PARAM),
                                      ({"dim": 5121}, mh.ERR_SHAPE), ({"dim": 0}, mh.ERR_SHAPE),
-                                     ({"n_sets": 0}, mh.ERR_SHAPE), ({"dim": 16384 * 8}, mh.ERR_UNSUPPORTED)])
+                                     ({"n_sets": 0}, mh.ERR_SHAPE), ({"dim": 16384 * 8}, mh.ERR_UNSUPPORTED),
+                                     ({"set_stride": 5116}, mh.ERR_PARAM), ({"set_stride": 5122}, mh.ERR_PARAM)])
 def test_rows_validation(kw, code):
     a = rows_args(**kw)
     rc = mh.lib.mh3_rms_mod_gate_add_rows(C.byref(a), FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, None, FAKE, None)

@@ -200,3 +200,46 @@ def test_row_wider_than_4096_vectors_is_unsupported(dev):
     ones = torch.ones(32776, device=dev)
     with pytest.raises(RuntimeError):
         mh.rms_mod_rows(x, ones, ones.view(1, -1), ones.view(1, -1))
+
+
+@pytest.mark.parametrize("dim", [1024, 5120])
+def test_modulation_table_views(dev, dim):
+    """shift, scale and gate read straight from a [U][3][6][D] modulation table (sets 6 D floats apart; slots 0-2
+    the attention half's shift, scale, gate, 3-5 the MLP half's) give, bit for bit, what contiguous copies of the
+    same vectors give, for all four row ops. 6 sets of 1024 use the LDS coefficient table, 6 of 5120 global memory."""
+    rng = np.random.default_rng(dim + 6)
+    U, rows = 2, 70
+    table = torch.from_numpy((0.1 * rng.standard_normal((U, 3, 6, dim))).astype(np.float32)).to(dev)
+    w = dev_t((1 + 0.02 * rng.standard_normal(dim)).astype(np.float32), dev)
+    sets = dev_t(rng.integers(0, U * 3, rows).astype(np.uint8), dev)
+    x = from_bits(randn_bf16_bits(rng, (rows, dim)), dev)
+    y = from_bits(randn_bf16_bits(rng, (rows, dim)), dev)
+    sh, sc, ga = table[:, :, 3], table[:, :, 4], table[:, :, 5]             # [U][3][D] views, 6 D floats apart
+    c_sh, c_sc, c_ga = [t.reshape(U * 3, dim).contiguous() for t in (sh, sc, ga)]
+    kw = dict(set_of_row=sets, n_sets=U * 3)
+    same = lambda a, b: torch.equal(a.view(torch.int16), b.view(torch.int16))  # noqa: E731
+    assert same(mh.rms_mod_rows(x, w, sh, sc, **kw), mh.rms_mod_rows(x, w, c_sh, c_sc, **kw))
+    assert same(mh.rms_mod_gate_add_rows(x, y, w, sh, sc, ga, **kw), mh.rms_mod_gate_add_rows(x, y, w, c_sh, c_sc,
+                                                                                              c_ga, **kw))
+    x1, x2 = x.clone(), x.clone()
+    mh.gate_add_rows(x1, y, ga, **kw)
+    mh.gate_add_rows(x2, y, c_ga, **kw)
+    assert same(x1, x2)
+    x1, x2 = x.clone(), x.clone()
+    h1 = mh.gate_add_rms_mod_rows(x1, y, ga, w, sh, sc, **kw)
+    h2 = mh.gate_add_rms_mod_rows(x2, y, c_ga, w, c_sh, c_sc, **kw)
+    assert same(x1, x2) and same(h1, h2)
+    want = orc.rms_mod_gate_add_rows(to_bits(x), to_bits(y), w.cpu().numpy(), c_sh.cpu().numpy(), c_sc.cpu().numpy(),
+                                     c_ga.cpu().numpy(), 1e-6, sets.cpu().numpy())
+    got = mh.rms_mod_gate_add_rows(x, y, w, sh, sc, ga, **kw)
+    assert_close(bits_to_f64(to_bits(got)), bits_to_f64(want), BF16_RTOL, BF16_ATOL, "table views vs oracle")
+
+
+def test_modulation_table_views_refused_when_uneven(dev):
+    """Vectors whose sets are not evenly spaced, or whose strides differ, are refused before any launch."""
+    t = torch.zeros((2, 3, 6, 64), device=dev)
+    x = torch.zeros((4, 64), device=dev)
+    with pytest.raises(ValueError):
+        mh.rms_mod_rows(x, None, t[:, :, 0, :].transpose(0, 1), t[:, :, 1, :].transpose(0, 1), n_sets=6)
+    with pytest.raises(ValueError):
+        mh.rms_mod_rows(x, None, t[:, :, 0, :], t.reshape(36, 64)[:6], n_sets=6)
