@@ -167,6 +167,28 @@ int mh3_cube_topk(const MH3CubeArgs* args, const float* s, int32_t* idx, int32_t
 int mh3_cube_select(const MH3CubeArgs* args, const float* qc, const float* kc, int32_t* idx, int32_t* cnt,
                     mh3_stream_t stream);
 
+/* ---- flash_attn_sparse_128 ---------------------------------------------------------------------------------------
+ * Reference kernel `flash_attn_sparse_128` (mako-common; docs/architecture.md:123-130, docs/performance.md:162-181):
+ * flash attention, head_dim 128, over the pass lists of cube_topk / cube_select. Per head h:
+ *   - the queries of cube i attend the tokens of cubes idx[h][i][0 .. cnt[h][i]) and every dense row;
+ *   - a dense row's query attends every token of the grid and every dense row;
+ *   - out[row] = softmax(q[row] . k * scale) v over those keys, bf16, accumulated in float.
+ * q, k, v and out share the cube geometry of `cubes` (rows addressed as for cube_pool, in the grid or gathered
+ * layout); the dense rows are rows dense_row0 .. + n_dense of the same arrays and may not overlap the video rows.
+ * Output rows are written where the queries lie: the grid layout writes the token rows and the dense rows (the
+ * reference's write-back to the model's rows, with no gather or scatter pass); the gathered layout also writes a
+ * cube's padding slots, as zeros. idx entries outside [0, cubes) are skipped; cnt is clamped to [0, out_stride].
+ * out may not be q, k or v. cubes.k and cubes.local are not used. */
+typedef struct MH3AttnArgs {
+    MH3CubeArgs cubes;   /* heads, head_dim (128), grid, layout, row0, head_stride, row_stride; out_stride: idx's
+                            int32 entries per (head, query cube) */
+    uint64_t dense_row0; /* first dense row (text, keyframe and audio rows) */
+    uint32_t n_dense;    /* dense rows; 0 allowed */
+    float scale;         /* score scale; 0 means 1 / sqrt(128) */
+} MH3AttnArgs;
+int mh3_flash_attn_sparse_128(const MH3AttnArgs* args, const uint16_t* q, const uint16_t* k, const uint16_t* v,
+                              const int32_t* idx, const int32_t* cnt, uint16_t* out, mh3_stream_t stream);
+
 /* ---- int8 weights: quant_rows_i8 (weight side) ---------------------------------------------------------------------
  * Reference kernel `quant_rows_i8` (mako-common; docs/performance.md:122-123, docs/architecture.md:54-56): each row
  * of a [rows][cols] matrix (the weight's [out][in] rows) to symmetric int8 with one float scale:

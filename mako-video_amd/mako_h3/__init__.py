@@ -43,6 +43,10 @@ class CubeArgs(C.Structure):
                 ("reserved", C.c_uint32)]
 
 
+class AttnArgs(C.Structure):
+    _fields_ = [("cubes", CubeArgs), ("dense_row0", C.c_uint64), ("n_dense", C.c_uint32), ("scale", C.c_float)]
+
+
 class QuantArgs(C.Structure):
     _fields_ = [("rows", C.c_uint32), ("cols", C.c_uint32), ("dtype", C.c_uint32), ("reserved", C.c_uint32)]
 
@@ -73,6 +77,7 @@ def _load() -> C.CDLL:
         "mh3_cube_scores": (I32, [C.POINTER(CubeArgs), P, P, P, P]),
         "mh3_cube_topk": (I32, [C.POINTER(CubeArgs), P, P, P, P]),
         "mh3_cube_select": (I32, [C.POINTER(CubeArgs), P, P, P, P, P]),
+        "mh3_flash_attn_sparse_128": (I32, [C.POINTER(AttnArgs), P, P, P, P, P, P, P]),
         "mh3_quant_rows_i8": (I32, [C.POINTER(QuantArgs), P, P, P, P]),
         "mh3_gemm_w8a16_swiglu": (I32, [C.POINTER(GemmArgs), P, P, P, P, P]),
         "mh3_gemm_bf16_swiglu": (I32, [C.POINTER(GemmArgs), P, P, P, P]),
@@ -342,6 +347,30 @@ def cube_select(a: CubeArgs, qc, kc, *, idx=None, cnt=None):
     idx, cnt = _topk_out(a, qc.device, idx, cnt)
     _check(lib.mh3_cube_select(C.byref(a), _ptr(qc), _ptr(kc), _ptr(idx), _ptr(cnt), _stream()), "cube_select")
     return idx, cnt
+
+
+# ---- flash_attn_sparse_128 -------------------------------------------------------------------------------------------
+
+def flash_attn_sparse_128(a: CubeArgs, q, k, v, idx, cnt, *, dense_row0=0, n_dense=0, scale=0.0, out=None):
+    """Sparse attention over the pass lists idx / cnt (as cube_select writes them): the queries of cube i attend the
+    tokens of its selected cubes and the dense rows [dense_row0, dense_row0 + n_dense); a dense row's query attends
+    every token. q, k, v (and out) bf16 in the cube geometry `a` (grid or gathered layout); scale 0 is 1/sqrt(128).
+    Rows that are not written keep `out`'s values (zero when out is None)."""
+    cubes = cube_count(a.grid_t, a.grid_h, a.grid_w)
+    n = _rows_touched(a)
+    if n_dense:
+        n = max(n, (a.heads - 1) * a.head_stride + (dense_row0 + n_dense - 1) * a.row_stride + a.head_dim)
+    for name, t in (("q", q), ("k", k), ("v", v)):
+        _need(t, name, torch.bfloat16, n)
+    _need(idx, "idx", torch.int32, a.heads * cubes * a.out_stride)
+    _need(cnt, "cnt", torch.int32, a.heads * cubes)
+    out = torch.zeros_like(q) if out is None else out
+    _need(out, "out", torch.bfloat16, n)
+    args = AttnArgs()
+    args.cubes, args.dense_row0, args.n_dense, args.scale = a, dense_row0, n_dense, scale
+    _check(lib.mh3_flash_attn_sparse_128(C.byref(args), _ptr(q), _ptr(k), _ptr(v), _ptr(idx), _ptr(cnt), _ptr(out),
+                                         _stream()), "flash_attn_sparse_128")
+    return out
 
 
 # ---- int8 ----------------------------------------------------------------------------------------------------------

@@ -442,3 +442,111 @@ void mh3o_gemm_i8_swiglu(uint32_t m, uint32_t n, uint32_t k, const int8_t* x, co
         }
     }
 }
+
+/* ---- flash_attn_sparse_128 -------------------------------------------------------------------------------------- */
+
+/* Row of slot l (0..63) of attention tile `tile`: tiles 0 .. nd-1 are the dense rows in runs of 64 (row
+ * dense_row0 + 64 tile + l, valid below n_dense), tile nd + c is cube c (slot l = (dt, dy, dx) = (l / 16, l / 4 % 4,
+ * l % 4), valid where its grid position is a token). Returns the row, or -1 for a slot that is no token. */
+static int64_t attn_tile_row(uint32_t gt, uint32_t gh, uint32_t gw, int layout, uint64_t row0, uint64_t dense_row0,
+                             uint32_t n_dense, uint64_t tile, uint32_t l)
+{
+    const uint64_t nd = ((uint64_t)n_dense + 63) / 64;
+    if (tile < nd) {
+        const uint64_t r = 64 * tile + l;
+        return r < n_dense ? (int64_t)(dense_row0 + r) : -1;
+    }
+    const uint64_t c = tile - nd;
+    const uint32_t ch = (gh + 3) / 4, cw = (gw + 3) / 4;
+    const uint32_t ct = (uint32_t)(c / ((uint64_t)ch * cw)), cy = (uint32_t)(c / cw % ch), cx = (uint32_t)(c % cw);
+    const uint32_t dt = l / 16, dy = l / 4 % 4, dx = l % 4;
+    const uint32_t t = ct * 4 + dt, y = cy * 4 + dy, x = cx * 4 + dx;
+    if (t >= gt || y >= gh || x >= gw)
+        return -1;
+    return (int64_t)cube_row(layout, row0, gh, gw, c, t, y, x, dt, dy, dx);
+}
+
+/* docs/architecture.md:123-130: flash attention over a pass list. The queries of cube i (head h) attend the rows of
+ * the cubes idx[h][i][0 .. cnt[h][i]) and every dense row; a dense row's query attends every row (all cubes and
+ * dense rows); padding slots are neither keys nor outputs. softmax(q . k * scale) v per query, in double, rounded
+ * to bf16 once. One query tile (the numbering of attn_tile_row) of one head; in the gathered layout a cube's
+ * padding slots are written zero. */
+void mh3o_attn_sparse_tile(uint32_t gt, uint32_t gh, uint32_t gw, int layout, uint64_t row0, uint64_t head_stride,
+                           uint64_t row_stride, uint64_t dense_row0, uint32_t n_dense, double scale,
+                           const uint16_t* q, const uint16_t* k, const uint16_t* v, const int32_t* idx,
+                           const int32_t* cnt, uint32_t out_stride, uint32_t h, uint64_t tile, uint16_t* out)
+{
+    const uint32_t hd = 128;
+    const uint64_t C = (uint64_t)mh3o_cube_count(gt, gh, gw), nd = ((uint64_t)n_dense + 63) / 64;
+    /* the key tiles of this query tile */
+    uint64_t n_kt = 0;
+    uint64_t* kt = (uint64_t*)malloc(sizeof(uint64_t) * (C + nd));
+    if (tile < nd) {
+        for (uint64_t c = 0; c < C; ++c)
+            kt[n_kt++] = nd + c;
+    } else {
+        const uint64_t i = tile - nd;
+        const int32_t* list = idx + ((uint64_t)h * C + i) * out_stride;
+        for (int32_t e = 0; e < cnt[(uint64_t)h * C + i]; ++e)
+            kt[n_kt++] = nd + (uint64_t)list[e];
+    }
+    for (uint64_t d = 0; d < nd; ++d)
+        kt[n_kt++] = d;
+    double* s = (double*)malloc(sizeof(double) * 64 * (n_kt ? n_kt : 1));
+    int64_t* krow = (int64_t*)malloc(sizeof(int64_t) * 64 * (n_kt ? n_kt : 1));
+    uint64_t nk = 0;
+    for (uint64_t e = 0; e < n_kt; ++e)
+        for (uint32_t l = 0; l < 64; ++l) {
+            const int64_t r = attn_tile_row(gt, gh, gw, layout, row0, dense_row0, n_dense, kt[e], l);
+            if (r >= 0)
+                krow[nk++] = r;
+        }
+    double acc[128];
+    for (uint32_t l = 0; l < 64; ++l) {
+        const int64_t qr = attn_tile_row(gt, gh, gw, layout, row0, dense_row0, n_dense, tile, l);
+        if (qr < 0) {
+            if (layout == MH3O_CUBES_GATHERED && tile >= nd) { /* gathered: the padding slot's row exists; it is written zero */
+                uint16_t* o = out + (uint64_t)h * head_stride + (row0 + 64 * (tile - nd) + l) * row_stride;
+                memset(o, 0, sizeof(uint16_t) * hd);
+            }
+            continue;
+        }
+        const uint16_t* qp = q + (uint64_t)h * head_stride + (uint64_t)qr * row_stride;
+        double mx = -INFINITY;
+        for (uint64_t j = 0; j < nk; ++j) {
+            const uint16_t* kp = k + (uint64_t)h * head_stride + (uint64_t)krow[j] * row_stride;
+            double dot = 0;
+            for (uint32_t d = 0; d < hd; ++d)
+                dot += (double)mh3o_bf16_to_float(qp[d]) * (double)mh3o_bf16_to_float(kp[d]);
+            s[j] = dot * scale;
+            mx = s[j] > mx ? s[j] : mx;
+        }
+        double sum = 0;
+        memset(acc, 0, sizeof acc);
+        for (uint64_t j = 0; j < nk; ++j) {
+            const double p = exp(s[j] - mx);
+            const uint16_t* vp = v + (uint64_t)h * head_stride + (uint64_t)krow[j] * row_stride;
+            sum += p;
+            for (uint32_t d = 0; d < hd; ++d)
+                acc[d] += p * (double)mh3o_bf16_to_float(vp[d]);
+        }
+        uint16_t* o = out + (uint64_t)h * head_stride + (uint64_t)qr * row_stride;
+        for (uint32_t d = 0; d < hd; ++d)
+            o[d] = mh3o_bf16_from_double(sum > 0 ? acc[d] / sum : 0.0);
+    }
+    free(krow);
+    free(s);
+    free(kt);
+}
+
+void mh3o_attn_sparse(uint32_t heads, uint32_t gt, uint32_t gh, uint32_t gw, int layout, uint64_t row0,
+                      uint64_t head_stride, uint64_t row_stride, uint64_t dense_row0, uint32_t n_dense, double scale,
+                      const uint16_t* q, const uint16_t* k, const uint16_t* v, const int32_t* idx, const int32_t* cnt,
+                      uint32_t out_stride, uint16_t* out)
+{
+    const uint64_t tiles = ((uint64_t)n_dense + 63) / 64 + (uint64_t)mh3o_cube_count(gt, gh, gw);
+    for (uint32_t h = 0; h < heads; ++h)
+        for (uint64_t t = 0; t < tiles; ++t)
+            mh3o_attn_sparse_tile(gt, gh, gw, layout, row0, head_stride, row_stride, dense_row0, n_dense, scale, q,
+                                  k, v, idx, cnt, out_stride, h, t, out);
+}

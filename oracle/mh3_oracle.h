@@ -26,6 +26,8 @@
  *   mh3o_cube_topk             numpy lexsort; constructed scores with an analytic answer; ratio 1 selects all
  *   mh3o_cube_topk_sorted      equals mh3o_cube_topk on random and tie-heavy rows (the form bench.py's CPU
  *                              baseline times: a sort a row instead of the O(C^2) count)
+ *   mh3o_attn_sparse(_tile)    torch scaled_dot_product_attention in float64 with a boolean mask built in numpy
+ *                              from the pass lists; with every cube selected, the unmasked attention over all rows
  *   mh3o_quant_rows_i8         |q| <= 127, the row maximum maps to +-127, |w - q*s| <= s/2, numpy rint
  *   mh3o_gemm_w8a16_swiglu     torch.matmul in float64; exact integer results for w in {-1,0,1}, s = 1
  *   mh3o_gemm_bf16_swiglu      torch.matmul in float64; exact integer results for w in {-1,0,1}
@@ -77,6 +79,15 @@ void mh3o_cube_topk(uint32_t heads, uint32_t gt, uint32_t gh, uint32_t gw, uint3
                     uint32_t out_stride, const double* s, int32_t* idx, int32_t* cnt);
 void mh3o_cube_topk_sorted(uint32_t heads, uint32_t gt, uint32_t gh, uint32_t gw, uint32_t k, uint32_t local,
                            uint32_t out_stride, const double* s, int32_t* idx, int32_t* cnt);
+
+void mh3o_attn_sparse_tile(uint32_t gt, uint32_t gh, uint32_t gw, int layout, uint64_t row0, uint64_t head_stride,
+                           uint64_t row_stride, uint64_t dense_row0, uint32_t n_dense, double scale,
+                           const uint16_t* q, const uint16_t* k, const uint16_t* v, const int32_t* idx,
+                           const int32_t* cnt, uint32_t out_stride, uint32_t h, uint64_t tile, uint16_t* out);
+void mh3o_attn_sparse(uint32_t heads, uint32_t gt, uint32_t gh, uint32_t gw, int layout, uint64_t row0,
+                      uint64_t head_stride, uint64_t row_stride, uint64_t dense_row0, uint32_t n_dense, double scale,
+                      const uint16_t* q, const uint16_t* k, const uint16_t* v, const int32_t* idx, const int32_t* cnt,
+                      uint32_t out_stride, uint16_t* out);
 
 void mh3o_quant_rows_i8(uint32_t rows, uint32_t cols, int dtype, const void* w, int8_t* q, float* scale);
 

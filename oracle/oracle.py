@@ -50,6 +50,9 @@ _lib.mh3o_cube_pool_some.argtypes = [C.c_uint32] * 4 + [C.c_int, C.c_uint64, C.c
 _lib.mh3o_cube_scores.argtypes = [C.c_uint32] * 3 + [_P] * 3
 _lib.mh3o_cube_topk.argtypes = [C.c_uint32] * 7 + [_P] * 3
 _lib.mh3o_cube_topk_sorted.argtypes = [C.c_uint32] * 7 + [_P] * 3
+_ATTN_GEOM = [C.c_uint32] * 3 + [C.c_int, C.c_uint64, C.c_uint64, C.c_uint64, C.c_uint64, C.c_uint32, C.c_double]
+_lib.mh3o_attn_sparse_tile.argtypes = _ATTN_GEOM + [_P] * 5 + [C.c_uint32, C.c_uint32, C.c_uint64, _P]
+_lib.mh3o_attn_sparse.argtypes = [C.c_uint32] + _ATTN_GEOM + [_P] * 5 + [C.c_uint32, _P]
 _lib.mh3o_quant_rows_i8.argtypes = [C.c_uint32, C.c_uint32, C.c_int] + [_P] * 3
 _lib.mh3o_gemm_w8a16_swiglu.argtypes = [C.c_uint32] * 3 + [_P] * 4
 _lib.mh3o_gemm_bf16_swiglu.argtypes = [C.c_uint32] * 3 + [_P] * 3
@@ -221,3 +224,44 @@ def gemm_w8a16_swiglu(x, w, scale):
     _lib.mh3o_gemm_w8a16_swiglu(m, n, k, _p(np.ascontiguousarray(x)), _p(np.ascontiguousarray(w)),
                                 _p(np.ascontiguousarray(scale)), _p(out))
     return out
+
+
+# ---- flash_attn_sparse_128 ---------------------------------------------------------------------------------------------
+
+def attn_sparse(q, k, v, idx, cnt, grid, dense_row0, n_dense, layout=CUBES_GRID, row0=0, scale=None, tiles=None,
+                out=None):
+    """Sparse attention of q, k, v bf16 bits [heads][rows][128] over the pass lists idx / cnt ([heads][cubes][stride]
+    and [heads][cubes], as cube_topk writes them) plus the dense rows [dense_row0, dense_row0 + n_dense). Every query
+    tile when `tiles` is None, else only the (head, tile) pairs listed (tile numbering: dense runs of 64 first, then
+    cube c as tile nd + c). Rows not written keep `out`'s values (zero when out is None)."""
+    heads, rows, hd = q.shape
+    assert hd == 128 and k.shape == q.shape and v.shape == q.shape
+    scale = 1.0 / np.sqrt(128.0) if scale is None else scale
+    out = np.zeros_like(q) if out is None else out
+    q, k, v = (np.ascontiguousarray(a) for a in (q, k, v))
+    idx, cnt = np.ascontiguousarray(idx, dtype=np.int32), np.ascontiguousarray(cnt, dtype=np.int32)
+    geom = (*grid, layout, row0, rows * 128, 128, dense_row0, n_dense, scale)
+    if tiles is None:
+        _lib.mh3o_attn_sparse(heads, *geom, _p(q), _p(k), _p(v), _p(idx), _p(cnt), idx.shape[2], _p(out))
+    else:
+        for h, t in tiles:
+            _lib.mh3o_attn_sparse_tile(*geom, _p(q), _p(k), _p(v), _p(idx), _p(cnt), idx.shape[2], h, t, _p(out))
+    return out
+
+
+def attn_tile_rows(grid, layout, row0, dense_row0, n_dense, tile):
+    """The rows of attention tile `tile` that are tokens (dense runs of 64 first, then one tile per cube)."""
+    gt, gh, gw = grid
+    nd = (n_dense + 63) // 64
+    if tile < nd:
+        return np.arange(dense_row0 + 64 * tile, dense_row0 + min(n_dense, 64 * tile + 64))
+    c = tile - nd
+    ch, cw = (gh + 3) // 4, (gw + 3) // 4
+    ct, cy, cx = c // (ch * cw), c // cw % ch, c % cw
+    rows = []
+    for l in range(64):
+        dt, dy, dx = l // 16, l // 4 % 4, l % 4
+        t, y, x = 4 * ct + dt, 4 * cy + dy, 4 * cx + dx
+        if t < gt and y < gh and x < gw:
+            rows.append(row0 + 64 * c + l if layout == CUBES_GATHERED else row0 + (t * gh + y) * gw + x)
+    return np.array(rows, dtype=np.int64)

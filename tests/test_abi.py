@@ -169,3 +169,35 @@ def test_python_wrapper_checks_sizes_before_the_library():
     x = torch.zeros((4, 5120), dtype=torch.bfloat16)      # host tensor: refused before any call
     with pytest.raises(ValueError):
         mh.rms_mod_gate_add_rows(x, x, None, x, x, x)
+
+
+def attn_args(**kw):
+    a = mh.AttnArgs()
+    a.cubes = mh.cube_args(2, (8, 8, 12), k=3, local=1)
+    a.dense_row0, a.n_dense, a.scale = 768, 40, 0.0
+    for key, val in kw.items():
+        if hasattr(a.cubes, key) and key not in ("dense_row0", "n_dense", "scale"):
+            setattr(a.cubes, key, val)
+        else:
+            setattr(a, key, val)
+    return a
+
+
+@pytest.mark.parametrize("kw,code", [({"layout": 2}, mh.ERR_PARAM), ({"heads": 0}, mh.ERR_SHAPE),
+                                     ({"head_dim": 64}, mh.ERR_UNSUPPORTED), ({"out_stride": 0}, mh.ERR_SHAPE),
+                                     ({"scale": -1.0}, mh.ERR_PARAM), ({"dense_row0": 700}, mh.ERR_PARAM),
+                                     ({"row_stride": 100}, mh.ERR_ALIGN), ({"grid_w": 0}, mh.ERR_SHAPE)])
+def test_flash_attn_sparse_validation(kw, code):
+    """Bad geometry, a negative scale, dense rows overlapping the video rows and misaligned strides are refused."""
+    a = attn_args(**kw)
+    out = C.c_void_p(0x2000)
+    assert mh.lib.mh3_flash_attn_sparse_128(C.byref(a), FAKE, FAKE, FAKE, FAKE, FAKE, out, None) == code
+
+
+def test_flash_attn_sparse_pointer_checks():
+    a = attn_args()
+    assert mh.lib.mh3_flash_attn_sparse_128(None, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, None) == mh.ERR_POINTER
+    assert mh.lib.mh3_flash_attn_sparse_128(C.byref(a), FAKE, FAKE, None, FAKE, FAKE, FAKE, None) == mh.ERR_POINTER
+    out = C.c_void_p(0x2000)
+    assert mh.lib.mh3_flash_attn_sparse_128(C.byref(a), ODD, FAKE, FAKE, FAKE, FAKE, out, None) == mh.ERR_ALIGN
+    assert mh.lib.mh3_flash_attn_sparse_128(C.byref(a), FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, None) == mh.ERR_PARAM

@@ -1,0 +1,128 @@
+"""Parity of flash_attn_sparse_128 with the oracle (bf16 output; 1e-2 relative, checked per element against the
+row's scale, and the reference's diff() pair: relative RMS error and the lowest row cosine)."""
+import math
+
+import numpy as np
+import pytest
+import torch
+
+import mako_h3 as mh
+import oracle as orc
+from helpers import bits_to_f64, diff, from_bits, randn_bf16_bits, to_bits
+
+pytestmark = pytest.mark.gpu
+
+
+def check(got_bits, want_bits, what):
+    g, w = bits_to_f64(got_bits).reshape(-1, 128), bits_to_f64(want_bits).reshape(-1, 128)
+    scale = np.sqrt((w ** 2).mean(1, keepdims=True)) + 1e-30              # a row's RMS
+    err = np.abs(g - w)
+    assert np.all(err <= 1e-2 * (np.abs(w) + scale)), f"{what}: worst {(err / (np.abs(w) + scale)).max():.3g}"
+    rel, cos = diff(g, w, 128)
+    assert rel < 5e-3 and cos > 0.9999, f"{what}: rel {rel:.3g} cos {cos:.6f}"
+
+
+def run(dev, q, k, v, idx, cnt, grid, layout, row0, dense_row0, n_dense, out_init=None):
+    heads, rows, _ = q.shape
+    a = mh.cube_args(heads, grid, layout=layout, row0=row0, head_stride=rows * 128, out_stride=idx.shape[2])
+    out = None if out_init is None else from_bits(out_init, dev)
+    t = lambda x: torch.from_numpy(np.ascontiguousarray(x)).to(dev)  # noqa: E731
+    got = mh.flash_attn_sparse_128(a, from_bits(q, dev), from_bits(k, dev), from_bits(v, dev), t(idx), t(cnt),
+                                   dense_row0=dense_row0, n_dense=n_dense, out=out)
+    return to_bits(got)
+
+
+CASES = [
+    # grid, layout, row0, dense_row0, n_dense, k, local
+    ((8, 8, 12), orc.CUBES_GRID, 0, 768, 40, 4, 1),
+    ((7, 9, 10), orc.CUBES_GATHERED, 70, 0, 70, 5, 3),
+    ((8, 8, 12), orc.CUBES_GRID, 5, 0, 0, 3, 0),
+    ((4, 5, 4), orc.CUBES_GRID, 64, 0, 64, 1, 1),
+    ((13, 10, 9), orc.CUBES_GRID, 0, 1170, 130, 6, 1),
+]
+
+
+@pytest.mark.parametrize("grid,layout,row0,dense_row0,n_dense,k_sel,local", CASES)
+def test_flash_attn_sparse_matches_oracle(dev, grid, layout, row0, dense_row0, n_dense, k_sel, local):
+    rng = np.random.default_rng(sum(grid) + n_dense + layout)
+    C = orc.cube_count(*grid)
+    video = C * 64 if layout == orc.CUBES_GATHERED else grid[0] * grid[1] * grid[2]
+    rows = max(row0 + video, dense_row0 + n_dense)
+    q, k, v = [randn_bf16_bits(rng, (2, rows, 128)) for _ in range(3)]
+    idx, cnt = orc.cube_topk(rng.standard_normal((2, C, C)), grid, k_sel, local, out_stride=k_sel + 3)
+    want = orc.attn_sparse(q, k, v, idx, cnt, grid, dense_row0, n_dense, layout, row0)
+    got = run(dev, q, k, v, idx, cnt, grid, layout, row0, dense_row0, n_dense)
+    check(got, want, f"attn {grid} layout {layout}")
+    if layout == orc.CUBES_GATHERED:
+        vrow = np.concatenate([orc.attn_tile_rows(grid, layout, row0, dense_row0, n_dense, (n_dense + 63) // 64 + c)
+                               for c in range(C)])
+        pad = np.setdiff1d(np.arange(row0, row0 + 64 * C), vrow)
+        assert len(pad) and (got[:, pad] == 0).all()
+
+
+def test_flash_attn_sparse_every_cube_is_dense_attention(dev):
+    """Every cube selected: each query attends every token, as torch's attention (float32 on the GPU) does."""
+    rng = np.random.default_rng(21)
+    grid = (8, 8, 8)
+    C = orc.cube_count(*grid)
+    q, k, v = [randn_bf16_bits(rng, (2, 542, 128)) for _ in range(3)]
+    idx = np.tile(np.arange(C, dtype=np.int32), (2, C, 1))
+    cnt = np.full((2, C), C, np.int32)
+    got = run(dev, q, k, v, idx, cnt, grid, orc.CUBES_GRID, 0, 512, 30)
+    f = lambda a: torch.from_numpy(bits_to_f64(a)).to(dev, torch.float32)  # noqa: E731
+    want = torch.nn.functional.scaled_dot_product_attention(f(q), f(k), f(v)).to(torch.bfloat16)
+    check(got, to_bits(want), "every cube")
+
+
+def test_flash_attn_sparse_leaves_other_rows_and_skips_bad_entries(dev):
+    """Rows that are neither tokens nor dense rows keep their contents; an idx entry outside the cubes is skipped."""
+    rng = np.random.default_rng(22)
+    grid, row0, dense_row0, n_dense = (8, 8, 12), 3, 800, 20
+    C = orc.cube_count(*grid)
+    rows = 830
+    q, k, v = [randn_bf16_bits(rng, (1, rows, 128)) for _ in range(3)]
+    idx, cnt = orc.cube_topk(rng.standard_normal((1, C, C)), grid, 4, 1, out_stride=8)
+    bad_idx, bad_cnt = idx.copy(), cnt.copy()
+    bad_idx[0, 5, cnt[0, 5]] = C + 7                                    # one entry past the cubes, counted
+    bad_cnt[0, 5] += 1
+    sentinel = np.full((1, rows, 128), 0x3F80, np.uint16)               # 1.0 in bf16
+    got = run(dev, q, k, v, bad_idx, bad_cnt, grid, orc.CUBES_GRID, row0, dense_row0, n_dense, out_init=sentinel)
+    want = orc.attn_sparse(q, k, v, idx, cnt, grid, dense_row0, n_dense, orc.CUBES_GRID, row0, out=sentinel.copy())
+    check(got, want, "bad entry skipped")
+    untouched = np.r_[0:row0, row0 + 768:dense_row0, dense_row0 + n_dense:rows]
+    assert (got[0, untouched] == 0x3F80).all()
+
+
+def test_flash_attn_sparse_768p_sampled(dev):
+    """The 768p shape (grid 32 x 48 x 84: 2016 cubes; 512 text rows after the video rows), two heads, the pass lists
+    from cube_select at ratio 0.1 (k = 202) and local 1 on structured q and k: a dense tile and eight cube tiles
+    a head checked against the oracle."""
+    grid, heads, n_dense = (32, 48, 84), 2, 512
+    video = 32 * 48 * 84
+    rows = video + n_dense
+    g = torch.Generator(device=dev).manual_seed(5)
+    q, k, v = [torch.randn((heads, rows, 128), generator=g, device=dev).to(torch.bfloat16) for _ in range(3)]
+    t = torch.arange(video, device=dev)
+    tt, yy, xx = (t // (48 * 84)).float() / 32, (t // 84 % 48).float() / 48, (t % 84).float() / 84
+    for h in range(heads):                                              # low-frequency structure across cubes
+        for f in range(3):
+            u = torch.randn(128, generator=g, device=dev)
+            wave = torch.cos(2 * math.pi * ((f + 1) * tt + (2 - f) * yy + f * xx))
+            q[h, :video] += (0.5 * wave[:, None] * u[None, :]).to(torch.bfloat16)
+            k[h, :video] += (0.5 * wave[:, None] * u[None, :]).to(torch.bfloat16)
+    C = orc.cube_count(*grid)
+    kk = mh.topk_k(0.1, C)
+    a = mh.cube_args(heads, grid, head_stride=rows * 128, k=kk, local=1)
+    qc, kc = mh.cube_pool(a, q, k)
+    idx, cnt = mh.cube_select(a, qc, kc)
+    out = mh.flash_attn_sparse_128(a, q, k, v, idx, cnt, dense_row0=video, n_dense=n_dense)
+    qb, kb, vb, ob = (to_bits(x) for x in (q, k, v, out))
+    idx_n, cnt_n = idx.cpu().numpy(), cnt.cpu().numpy()
+    nd = n_dense // 64
+    rng = np.random.default_rng(6)
+    tiles = [(h, 0) for h in range(heads)] + [(h, nd + int(c)) for h in range(heads)
+                                              for c in rng.choice(C, 8, replace=False)]
+    want = orc.attn_sparse(qb, kb, vb, idx_n, cnt_n, grid, video, n_dense, tiles=tiles)
+    for h, tile in tiles:
+        r = orc.attn_tile_rows(grid, orc.CUBES_GRID, 0, video, n_dense, tile)
+        check(ob[h, r], want[h, r], f"768p head {h} tile {tile}")
