@@ -180,7 +180,10 @@ def bench_swiglu(mh, dev, steps, warmup):
     return res
 
 
-def bench_select(mh, dev, steps, warmup):
+def selector_qk(dev, extra_rows=0):
+    """q and k [40][rows + extra_rows][128] bf16: N(0,1) plus, on the video rows, four low-frequency waves over
+    (t, y, x) along random unit directions (amplitude 0.5), so cube means separate above the pooled noise; the
+    extra (dense) rows are N(0,1)."""
     T, Y, X = GRID
     rows = T * Y * X
     g = torch.Generator(device=dev).manual_seed(7)
@@ -190,7 +193,7 @@ def bench_select(mh, dev, steps, warmup):
     xx = torch.arange(X, device=dev, dtype=torch.float32).view(1, 1, X) / X
     qk = []
     for _ in range(2):
-        t = torch.empty((HEADS, rows, 128), dtype=torch.bfloat16, device=dev)
+        t = torch.empty((HEADS, rows + extra_rows, 128), dtype=torch.bfloat16, device=dev)
         for h in range(HEADS):
             acc = torch.randn((rows, 128), generator=g, device=dev)
             for _j in range(4):
@@ -199,9 +202,17 @@ def bench_select(mh, dev, steps, warmup):
                 u = torch.from_numpy(u / np.linalg.norm(u)).float().to(dev)
                 wave = torch.cos(2 * math.pi * (f[0] * tt + f[1] * yy + f[2] * xx) + rng.uniform(0, 6.283))
                 acc += 0.5 * wave.reshape(-1, 1) * u
-            t[h] = acc.to(torch.bfloat16)
+            t[h, :rows] = acc.to(torch.bfloat16)
+            if extra_rows:
+                t[h, rows:] = torch.randn((extra_rows, 128), generator=g, device=dev).to(torch.bfloat16)
         qk.append(t)
-    q, k = qk
+    return qk
+
+
+def bench_select(mh, dev, steps, warmup):
+    T, Y, X = GRID
+    rows = T * Y * X
+    q, k = selector_qk(dev)
     cubes = mh.cube_count(*GRID)
     kk = mh.topk_k(0.1, cubes)
     a = mh.cube_args(HEADS, GRID, k=kk, local=1)
@@ -233,6 +244,36 @@ def bench_select(mh, dev, steps, warmup):
             "score_gflop": flops / 1e9, "select_TFLOPs": flops / sel_ms / 1e9,
             "select_fp32_mfma_frac": flops / sel_ms / 1e9 / FP32_MFMA_PEAK_TFLOPS,
             "select_bytes": sel_bytes, "unfused_scores_ms": scores_ms, "unfused_topk_ms": topk_ms}
+
+
+def bench_attn(mh, dev, steps, warmup):
+    """flash_attn_sparse_128 at the 768p shape: 40 heads, grid 32 x 48 x 84 (2016 cubes) in the model's row order,
+    512 text rows after the video rows; the pass lists from cube_pool + cube_select at ratio 0.1 (k = 202), local 1.
+    Algorithmic work: 4 x 128 flops (q.k and p.v) per (query, attended key) pair; K/V bytes: 512 per attended key
+    a query tile (one K and one V row per tile that attends it)."""
+    T, Y, X = GRID
+    video, n_dense = T * Y * X, 512
+    rows = video + n_dense
+    q, k = selector_qk(dev, n_dense)
+    v = torch.randn((HEADS, rows, 128), generator=torch.Generator(device=dev).manual_seed(8),
+                    device=dev).to(torch.bfloat16)
+    cubes = mh.cube_count(*GRID)
+    kk = mh.topk_k(0.1, cubes)
+    a = mh.cube_args(HEADS, GRID, head_stride=rows * 128, k=kk, local=1)
+    qc, kc = mh.cube_pool(a, q, k)
+    idx, cnt = mh.cube_select(a, qc, kc)
+    out = torch.empty_like(q)
+    ms, _ = time_launches(lambda: mh.flash_attn_sparse_128(a, q, k, v, idx, cnt, dense_row0=video, n_dense=n_dense,
+                                                           out=out), steps, warmup)
+    sel = int(cnt.to(torch.int64).sum())
+    pairs = 64 * (sel * 64 + HEADS * cubes * n_dense) + HEADS * n_dense * rows
+    flops = 4.0 * 128 * pairs
+    kv_tile_rows = sel * 64 + HEADS * cubes * n_dense + HEADS * (n_dense // 64) * rows
+    dense_flops = 4.0 * 128 * HEADS * rows * rows
+    return {"ms": ms, "tflops": flops / ms / 1e9, "mfma_util": flops / ms / 1e9 / BF16_PEAK_TFLOPS,
+            "flops": flops, "mean_cubes_selected": sel / (HEADS * cubes), "kv_bytes": kv_tile_rows * 512,
+            "kv_GBs": kv_tile_rows * 512 / ms / 1e6, "dense_equivalent_flops": dense_flops,
+            "shape": {"heads": HEADS, "grid": list(GRID), "cubes": cubes, "dense_rows": n_dense, "k": kk}}
 
 
 def bench_fc1(mh, dev, steps, warmup, compare):
@@ -412,7 +453,7 @@ def main() -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--only", default="fused,block_order,copy,swiglu,select,fc1,rms_f32")
+    ap.add_argument("--only", default="fused,block_order,copy,swiglu,select,attn,fc1,rms_f32")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-compare", action="store_true")
     args = ap.parse_args()
@@ -445,6 +486,9 @@ def main() -> int:
         torch.cuda.empty_cache()
     if "select" in ops:
         report["cube_selector"] = bench_select(mh, dev, args.steps, args.warmup)
+        torch.cuda.empty_cache()
+    if "attn" in ops:
+        report["flash_attn_sparse_128"] = bench_attn(mh, dev, max(3, args.steps // 2), max(1, args.warmup // 2))
         torch.cuda.empty_cache()
     if "fc1" in ops:
         report["fc1_w8a16_swiglu"] = bench_fc1(mh, dev, max(3, args.steps // 2), max(1, args.warmup // 2),

@@ -16,14 +16,21 @@
 //   a query's keys in one lane and its lane + 32 twin, so the softmax's row maximum and sum are in-lane plus one
 //   cross-half exchange, and the rescale of a query's output is one factor per lane.
 // - The output is also transposed, O^T += V^T P^T. P^T is the B operand as the score accumulator leaves it in
-//   registers; the contraction order over keys is free, so V^T is staged in LDS with its key positions in that
-//   order: position p of 16-key chunk c holds key 32 (c / 2) + 16 (c % 2) + 8 (p % 8 / 4) + 4 (p / 8) + p % 4.
-// - Each key tile (64 rows of K and V, 32 KB) is loaded by the 128 threads into registers, then written to LDS: K
-//   row-major with its 16-byte chunks XOR-swizzled by the row (conflict-free fragment reads), V as 8 x 8 blocks
-//   transposed in registers (v_perm) into V^T rows, chunks swizzled by d / 2. The loads' registers are free again
-//   during the MFMAs, which keeps a wave within 256 registers: two waves a SIMD, four workgroups a CU, and one
-//   workgroup's loads overlap the others' MFMAs.
+//   registers; the contraction order over keys is free, so the V^T fragment's key positions follow it: position p of
+//   16-key chunk c is key 32 (c / 2) + 16 (c % 2) + 8 (p % 8 / 4) + 4 (p / 8) + p % 4.
+// - K and V tiles (64 rows each, 32 KB) go from global memory straight into LDS (buffer_load ... lds), one tile
+//   ahead of the MFMAs when two stages fit. Each lane fetches whichever source chunk its LDS slot holds, so the
+//   layouts are free: K in 2 KB blocks of 8 rows interleaved at 16 bytes (8 lanes reading 8 consecutive rows of a
+//   fragment touch 128 contiguous bytes), V in 1 KB blocks of 4 keys interleaved at 16 bytes, read with
+//   ds_read_b64_tr_b16. That instruction hands lane i of a 16-lane group element i & 3 of the 8-byte rows named by
+//   lanes (i >> 2) + 4 j, j = 0..3: with lane L naming key (L >> 2)'s columns d0 + 4 (L & 3) .. + 3, lane i receives
+//   column d0 + i of four keys, a V^T fragment, with no transpose in registers. Every fragment address is a lane
+//   constant plus an immediate. Padding slots are fetched from past the buffer's end, which reads zeros.
+// - Softmax in base 2 with the scale folded into the exponent. A query's running maximum moves only when a tile
+//   raises it by more than 8 (in log2 units): P stays below 2^8, and most tiles skip the rescale of O.
 #include "mh3_common.hpp"
+
+#include <algorithm>
 
 namespace mh3 {
 namespace {
@@ -32,6 +39,13 @@ typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef float floatx16 __attribute__((ext_vector_type(16)));
 
 constexpr uint32_t kAttnThreads = 128;
+#ifndef MH3_ATTN_XCD
+#define MH3_ATTN_XCD 1 // map each XCD to a contiguous eighth of every head's query cubes
+#endif
+#ifndef MH3_ATTN_STAGES
+#define MH3_ATTN_STAGES 1 // K/V stages in LDS (2 overlaps a tile's loads with the previous tile's MFMAs but halves
+                          // the workgroups a CU holds; one stage and two waves a SIMD measured faster)
+#endif
 constexpr uint32_t kNoTile = 0xffffffffu;
 
 struct AttnParams {
@@ -45,7 +59,8 @@ struct AttnParams {
     uint32_t gt, gh, gw, ch, cw, plane; // plane = ch * cw cubes a frame group
     uint32_t cubes, heads, n_dense, nd; // nd: dense tiles of 64 rows
     uint32_t layout, out_stride;
-    float scale_log2; // score scale times log2(e): softmax in base 2
+    uint32_t xcd_slices; // cube tiles mapped to XCDs in eighths of each head (needs 8 | cubes and 8 | nd heads)
+    float scale_log2;    // score scale times log2(e): softmax in base 2
 };
 
 // A tile of 64 slots. kind 0: dense run (slot l is row base + l, a token while l < lim_t); 1: cube in the grid layout
@@ -107,20 +122,46 @@ __device__ __forceinline__ uint4 load16(const uint16_t* p)
     return *reinterpret_cast<const uint4*>(p);
 }
 
-// The key whose V column sits at position j (0..7) of position group pg (0..7: 16-key chunk pg / 2, half pg % 2).
-__device__ __forceinline__ uint32_t vt_key(uint32_t pg, uint32_t j)
+typedef __attribute__((address_space(3))) void* lds_ptr_t;
+typedef short v4i16 __attribute__((ext_vector_type(4)));
+
+// s_waitcnt that waits for vmcnt == 0 only (gfx9 encoding: vmcnt bits 3:0 and 15:14, expcnt 6:4, lgkmcnt 11:8),
+// between scheduling barriers so the compiler moves no memory access across it.
+__device__ __forceinline__ void wait_vm0()
 {
-    return 32u * (pg >> 2) + 16u * ((pg >> 1) & 1u) + 8u * (j >> 2) + 4u * (pg & 1u) + (j & 3u);
+    __builtin_amdgcn_sched_barrier(0);
+    __builtin_amdgcn_s_waitcnt(0x0070 | 0x0F00);
+    __builtin_amdgcn_sched_barrier(0);
 }
 
-__global__ __launch_bounds__(kAttnThreads, 2) void attn_sparse_kernel(AttnParams p)
+__device__ __forceinline__ void lds_barrier()
 {
-    __shared__ uint4 lds_k[64 * 16]; // [key][16-byte chunk]; chunk c of key r at c ^ (r & 15)
-    __shared__ uint4 lds_vt[128 * 8]; // [d][8 chunks of 8 key positions]; chunk c of row d at c ^ ((d >> 1) & 7)
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_waitcnt(0xC07F); // lgkmcnt(0)
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+}
+
+constexpr uint32_t kStageBytes = 32768; // K 16 KB, then V 16 KB
+constexpr uint32_t kPastEnd = 0x80000000u; // a buffer offset past num_records: the load reads zeros
+constexpr uint32_t kRecords = 0x7fffffffu;
+
+__device__ __forceinline__ bool tile_full(const Tile& r)
+{
+    return r.kind == 0 ? r.lim_t == 64u : (r.kind != 3 && r.lim_t == 4u && r.lim_y == 4u && r.lim_x == 4u);
+}
+
+template <int STAGES>
+__global__ __launch_bounds__(kAttnThreads, STAGES == 2 ? 1 : 2) void attn_sparse_kernel(AttnParams p)
+{
+    extern __shared__ __attribute__((aligned(16))) char lds[]; // STAGES x (K stage, V stage)
 
     const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6, n = lane & 31u, hh = lane >> 5;
 
-    // This workgroup's head and query tile.
+    // This workgroup's head and query tile: the dense query tiles of every head first, then the cube tiles. Blocks
+    // go to the 8 XCDs round-robin (block b to XCD b % 8); when the counts allow, XCD x takes the x-th eighth of each
+    // head's cubes in raster order, so the workgroups resident on one XCD are neighbouring query cubes, whose pass
+    // lists overlap and meet in that XCD's L2, while all XCDs stay on the same head.
     uint32_t h, qt;
     {
         const uint32_t b = blockIdx.x, dense_blocks = p.nd * p.heads;
@@ -129,8 +170,14 @@ __global__ __launch_bounds__(kAttnThreads, 2) void attn_sparse_kernel(AttnParams
             qt = b - h * p.nd;
         } else {
             const uint32_t r = b - dense_blocks;
-            h = r / p.cubes;
-            qt = p.nd + (r - h * p.cubes);
+            if (p.xcd_slices) {
+                const uint32_t per = p.cubes / 8u, k = r / 8u;
+                h = k / per;
+                qt = p.nd + (r % 8u) * per + (k - h * per);
+            } else {
+                h = r / p.cubes;
+                qt = p.nd + (r - h * p.cubes);
+            }
         }
     }
     const uint64_t hoff = uint64_t(h) * p.head_stride;
@@ -157,44 +204,49 @@ __global__ __launch_bounds__(kAttnThreads, 2) void attn_sparse_kernel(AttnParams
         return j >= 0 && uint32_t(j) < p.cubes ? p.nd + uint32_t(j) : kNoTile;
     };
 
-    // Loader slots, fixed for the whole kernel: K chunk kc of rows kr(jj) = tid / 16 + 8 jj; V columns 8 dg .. + 7 of
-    // the keys vt_key(pg, j).
-    const uint32_t kc = tid & 15u, pg = tid >> 4, dg = tid & 15u;
-    uint4 kreg[8], vreg[8];
-    uint64_t mask_next = 0;
-    auto load_tile = [&](uint32_t t) {
+    // DMA source offsets of this wave's 8 K and 8 V instructions (instruction i = 8 wave + u of the workgroup's 16),
+    // for cubes in the grid layout (G) and for consecutive rows (L: gathered cubes, dense runs).
+    //   K: instruction i fills half i % 2 of the 2 KB block of rows 8 (i / 2) .. + 7; lane L's LDS position
+    //      P = 64 (i % 2) + L holds chunk P / 8 of row 8 (i / 2) + P % 8.
+    //   V: instruction i fills the 1 KB block of keys 4 i .. + 3; lane L's position holds chunk L / 4 of key
+    //      4 i + L % 4.
+    // Each offset is a lane constant (voffset) plus a term of i alone (soffset): a slot's grid offset
+    // (dt gh + dy) gw + dx splits that way because i fixes dt and, for K, dy's high bit.
+    const uint32_t rs2 = uint32_t(p.row_stride) * 2u, gw_rs2 = p.gw * rs2, plane_rs2 = p.gh * gw_rs2;
+    const uint32_t kL_lane = (lane & 7u) * rs2 + 16u * (lane >> 3);
+    const uint32_t kG_lane = (((lane >> 2) & 1u) * p.gw + (lane & 3u)) * rs2 + 16u * (lane >> 3);
+    const uint32_t v_lane_off = (lane & 3u) * rs2 + 16u * (lane >> 2);
+    // Starts tile t's loads into stage st; returns its key mask (bit l: slot l is a token).
+    auto dma_tile = [&](uint32_t t, uint32_t st) -> uint64_t {
         const Tile tl = make_tile(p, t);
+        const uint64_t row_bytes = (tl.kind == 3 ? 0ull : tl.base) * p.row_stride * 2ull;
+        const __amdgpu_buffer_rsrc_t rk =
+            __builtin_amdgcn_make_buffer_rsrc(reinterpret_cast<char*>(const_cast<uint16_t*>(kh)) + row_bytes, 0,
+                                              int(kRecords), kRsrcFlags);
+        const __amdgpu_buffer_rsrc_t rv =
+            __builtin_amdgcn_make_buffer_rsrc(reinterpret_cast<char*>(const_cast<uint16_t*>(vh)) + row_bytes, 0,
+                                              int(kRecords), kRsrcFlags);
+        char* ks = lds + st * kStageBytes;
+        char* vs = ks + 16384;
+        const bool full = tile_full(tl), grid = tl.kind == 1;
+        const uint32_t k_lane = grid ? kG_lane : kL_lane;
 #pragma unroll
-        for (int j = 0; j < 8; ++j) {
-            const uint32_t ks = (tid >> 4) + 8u * j, vs = vt_key(pg, j);
-            kreg[j] = slot_token(tl, ks) ? load16(kh + slot_row(p, tl, ks) * p.row_stride + kc * 8u)
-                                         : uint4{0u, 0u, 0u, 0u};
-            vreg[j] = slot_token(tl, vs) ? load16(vh + slot_row(p, tl, vs) * p.row_stride + dg * 8u)
-                                         : uint4{0u, 0u, 0u, 0u};
-        }
-        mask_next = __ballot(slot_token(tl, lane));
-    };
-    auto store_tile = [&]() {
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
-            const uint32_t r = (tid >> 4) + 8u * j;
-            lds_k[r * 16u + (kc ^ (r & 15u))] = kreg[j];
-        }
-        // 8 keys x 8 d to 8 d x 8 keys: output dword m of d i pairs keys 2m (low half) and 2m + 1 (high half).
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            const uint32_t sel = (i & 1) ? 0x07060302u : 0x05040100u;
-            uint32_t w[4];
-#pragma unroll
-            for (int m = 0; m < 4; ++m) {
-                const uint4 a = vreg[2 * m], b = vreg[2 * m + 1];
-                const uint32_t wa = (i >> 1) == 0 ? a.x : (i >> 1) == 1 ? a.y : (i >> 1) == 2 ? a.z : a.w;
-                const uint32_t wb = (i >> 1) == 0 ? b.x : (i >> 1) == 1 ? b.y : (i >> 1) == 2 ? b.z : b.w;
-                w[m] = __builtin_amdgcn_perm(wb, wa, sel);
+        for (int u = 0; u < 8; ++u) {
+            const uint32_t i = 8u * wave + uint32_t(u);
+            const uint32_t k_i = grid ? (i >> 2) * plane_rs2 + 2u * ((i >> 1) & 1u) * gw_rs2 + 128u * (i & 1u)
+                                      : 8u * (i >> 1) * rs2 + 128u * (i & 1u);
+            const uint32_t v_i = grid ? ((i >> 2) * p.gh + (i & 3u)) * gw_rs2 : 4u * i * rs2;
+            uint32_t ko = k_lane, vo = v_lane_off;
+            if (!full) {
+                ko = slot_token(tl, 8u * (i >> 1) + (lane & 7u)) ? ko : kPastEnd;
+                vo = slot_token(tl, 4u * i + (lane & 3u)) ? vo : kPastEnd;
             }
-            const uint32_t d = 8u * dg + uint32_t(i);
-            lds_vt[d * 8u + (pg ^ ((d >> 1) & 7u))] = uint4{w[0], w[1], w[2], w[3]};
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rk, (lds_ptr_t)(ks + 1024u * i), 16, ko,
+                                                     int(__builtin_amdgcn_readfirstlane(k_i)), 0, 0);
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rv, (lds_ptr_t)(vs + 1024u * i), 16, vo,
+                                                     int(__builtin_amdgcn_readfirstlane(v_i)), 0, 0);
         }
+        return full ? ~0ull : __ballot(slot_token(tl, lane));
     };
 
     // This wave's 32 queries as the B operand of S^T = K Q^T: lane (n, hh) holds d 16 dc + 8 hh .. + 7 of query n.
@@ -216,72 +268,102 @@ __global__ __launch_bounds__(kAttnThreads, 2) void attn_sparse_kernel(AttnParams
         for (int e = 0; e < 16; ++e)
             o[b][e] = 0.0f;
     float m_run = -__builtin_inff(), l_run = 0.0f;
+    // Fragment addresses: lane constants; the rest is immediates.
+    const uint32_t k_lane = 2048u * (n >> 3) + 128u * hh + 16u * (n & 7u);
+    const uint32_t L = lane & 15u, grp = lane >> 4;
+    const uint32_t v_lane = 1024u * (grp >> 1) + 128u * (grp & 1u) + 64u * ((L & 3u) >> 1) + 16u * (L >> 2) +
+                            8u * (L & 1u);
 
+    uint64_t mask = n_tiles ? dma_tile(key_tile(0), 0) : 0ull;
     for (uint32_t e = 0; e < n_tiles; ++e) {
-        load_tile(key_tile(e));
-        __syncthreads(); // every wave is done with the previous tile's LDS
-        store_tile();
-        const uint64_t mask = mask_next;
-        __syncthreads();
+        const uint32_t st = STAGES == 2 ? (e & 1u) : 0u;
+        wait_vm0();
+        lds_barrier(); // tile e is in LDS for every wave; every wave is done with tile e - 1
+        uint64_t mask_next = 0;
+        if (STAGES == 2 && e + 1 < n_tiles)
+            mask_next = dma_tile(key_tile(e + 1), st ^ 1u);
+        const char* ks = lds + st * kStageBytes + k_lane;
+        const char* vs = lds + st * kStageBytes + 16384u + v_lane;
 
-        // The tile's two 32-key blocks in turn, each an online-softmax step (fewer live registers than one step of
-        // 64 keys). S^T block b: lane (n, hh), element i is key 32 b + 8 (i / 4) + 4 hh + i % 4 of query n.
+        // S^T: lane (n, hh), element i of block b is key 32 b + 8 (i / 4) + 4 hh + i % 4 of query n.
+        floatx16 s[2];
 #pragma unroll
         for (int b = 0; b < 2; ++b) {
-            floatx16 s;
 #pragma unroll
             for (int i = 0; i < 16; ++i)
-                s[i] = 0.0f;
-            const uint32_t r = 32u * b + n;
+                s[b][i] = 0.0f;
 #pragma unroll
             for (int dc = 0; dc < 8; ++dc) {
-                const uint4 a = lds_k[r * 16u + ((2u * dc + hh) ^ (r & 15u))];
-                s = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, a), qf[dc], s, 0, 0, 0);
-            }
-            // Softmax in base 2; padding keys score -inf.
-            float mt = -__builtin_inff();
-            const uint32_t bmask = uint32_t(mask >> (32 * b));
-#pragma unroll
-            for (int i = 0; i < 16; ++i) {
-                float x = s[i] * p.scale_log2;
-                if (bmask != ~0u)
-                    x = (bmask >> (8u * (i >> 2) + 4u * hh + (i & 3))) & 1u ? x : -__builtin_inff();
-                s[i] = x;
-                mt = fmaxf(mt, x);
-            }
-            mt = fmaxf(mt, __shfl_xor(mt, 32, kWave));
-            const float m_new = fmaxf(m_run, mt);
-            const float m_ref = m_new == -__builtin_inff() ? 0.0f : m_new;
-            const float alpha = __builtin_amdgcn_exp2f(m_run - m_ref);
-            m_run = m_new;
-            float ps = 0.0f;
-            uint32_t pw[8];
-#pragma unroll
-            for (int i = 0; i < 16; i += 2) {
-                const float p0 = __builtin_amdgcn_exp2f(s[i] - m_ref);
-                const float p1 = __builtin_amdgcn_exp2f(s[i + 1] - m_ref);
-                ps += p0 + p1;
-                pw[i >> 1] = pack_bf16(p0, p1);
-            }
-            l_run = l_run * alpha + ps;
-#pragma unroll
-            for (int db = 0; db < 4; ++db)
-#pragma unroll
-                for (int i = 0; i < 16; ++i)
-                    o[db][i] *= alpha;
-            // P^T chunk c = 2 b + g holds accumulator elements 8 g .. 8 g + 7 of this block.
-            const bf16x8_t pf0 = __builtin_bit_cast(bf16x8_t, uint4{pw[0], pw[1], pw[2], pw[3]});
-            const bf16x8_t pf1 = __builtin_bit_cast(bf16x8_t, uint4{pw[4], pw[5], pw[6], pw[7]});
-            // O^T (d 32 db + 8 (i / 4) + 4 hh + i % 4 of query n) += V^T P^T over the block's two 16-key chunks.
-#pragma unroll
-            for (int db = 0; db < 4; ++db) {
-                const uint32_t d = 32u * db + n, sw = (d >> 1) & 7u;
-                const uint4 a0 = lds_vt[d * 8u + ((4u * b + hh) ^ sw)];
-                const uint4 a1 = lds_vt[d * 8u + ((4u * b + 2u + hh) ^ sw)];
-                o[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, a0), pf0, o[db], 0, 0, 0);
-                o[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, a1), pf1, o[db], 0, 0, 0);
+                const bf16x8_t a = *reinterpret_cast<const bf16x8_t*>(ks + 8192u * b + 256u * dc);
+                s[b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, qf[dc], s[b], 0, 0, 0);
             }
         }
+        // Online softmax in base 2: padding keys score -inf; the maximum moves only when it rises by more than 8.
+        float mt = -__builtin_inff();
+        if (mask != ~0ull) {
+#pragma unroll
+            for (int b = 0; b < 2; ++b)
+#pragma unroll
+                for (int i = 0; i < 16; ++i) {
+                    const uint32_t key = 32u * b + 8u * (i >> 2) + 4u * hh + (i & 3);
+                    s[b][i] = (mask >> key) & 1ull ? s[b][i] : -__builtin_inff();
+                }
+        }
+#pragma unroll
+        for (int b = 0; b < 2; ++b)
+#pragma unroll
+            for (int i = 0; i < 16; ++i)
+                mt = fmaxf(mt, s[b][i]);
+        mt = fmaxf(mt, __shfl_xor(mt, 32, kWave)) * p.scale_log2;
+        if (__ballot(mt > m_run + 8.0f)) {
+            const float m_new = fmaxf(m_run, mt);
+            const float alpha = m_run == -__builtin_inff() ? 0.0f : __builtin_amdgcn_exp2f(m_run - m_new);
+            m_run = m_new;
+            l_run *= alpha;
+#pragma unroll
+            for (int b = 0; b < 4; ++b)
+#pragma unroll
+                for (int i = 0; i < 16; ++i)
+                    o[b][i] *= alpha;
+        }
+        const float m_ref = m_run == -__builtin_inff() ? 0.0f : m_run;
+        float ps = 0.0f;
+        uint32_t pw[2][8];
+#pragma unroll
+        for (int b = 0; b < 2; ++b)
+#pragma unroll
+            for (int i = 0; i < 16; i += 2) {
+                const float p0 = __builtin_amdgcn_exp2f(fmaf(s[b][i], p.scale_log2, -m_ref));
+                const float p1 = __builtin_amdgcn_exp2f(fmaf(s[b][i + 1], p.scale_log2, -m_ref));
+                ps += p0 + p1;
+                pw[b][i >> 1] = pack_bf16(p0, p1);
+            }
+        l_run += ps;
+        // O^T (d 32 db + 8 (i / 4) + 4 hh + i % 4 of query n) += V^T P^T; P^T chunk c = 2 b + g is accumulator
+        // elements 8 g .. + 7 of block b; its V^T fragment is two transposed reads (positions 0-3, 4-7 of the half).
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+            const int b = c >> 1, g = c & 1;
+            const bf16x8_t pf = __builtin_bit_cast(bf16x8_t, uint4{pw[b][4 * g], pw[b][4 * g + 1], pw[b][4 * g + 2],
+                                                                   pw[b][4 * g + 3]});
+#pragma unroll
+            for (int db = 0; db < 4; ++db) {
+                const uint32_t off = 1024u * (8u * b + 4u * g) + 256u * db;
+                const v4i16 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((v4i16 __attribute__((address_space(3)))*)(
+                    const_cast<char*>(vs) + off));
+                const v4i16 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((v4i16 __attribute__((address_space(3)))*)(
+                    const_cast<char*>(vs) + off + 2048u));
+                const bf16x8_t a = __builtin_bit_cast(
+                    bf16x8_t, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+                o[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, pf, o[db], 0, 0, 0);
+            }
+        }
+        if (STAGES == 1) {
+            lds_barrier(); // every wave is done with the stage before it is refilled
+            if (e + 1 < n_tiles)
+                mask_next = dma_tile(key_tile(e + 1), 0);
+        }
+        mask = mask_next;
     }
 
     // Normalize and write the query rows (a gathered cube's padding slots get zeros; other non-tokens nothing).
@@ -333,8 +415,10 @@ extern "C" int mh3_flash_attn_sparse_128(const MH3AttnArgs* args, const uint16_t
     p.ch = (p.gh + 3u) / 4u, p.cw = (p.gw + 3u) / 4u;
     const uint64_t cth = (p.gt + 3u) / 4u, plane = uint64_t(p.ch) * p.cw, cubes = cth * plane;
     const uint64_t nd = (uint64_t(args->n_dense) + 63u) / 64u;
+    // Row offsets within a tile, in bytes, stay below 2^31 (the DMA's 32-bit buffer offsets).
+    const uint64_t tile_rows = c.layout == MH3_CUBES_GRID ? (3ull * p.gh + 4u) * p.gw : 64u;
     if (cubes * c.heads >= (1ull << 31) || (cubes + nd) * c.heads >= (1ull << 31) ||
-        4ull * p.gh * p.gw >= (1ull << 32))
+        std::max<uint64_t>(tile_rows, 64u) * c.row_stride * 2u >= (1ull << 31))
         return MH3_ERR_SHAPE;
     // The dense rows may not overlap the video rows.
     const uint64_t video = c.layout == MH3_CUBES_GRID ? uint64_t(p.gt) * p.gh * p.gw : 64ull * cubes;
@@ -344,10 +428,16 @@ extern "C" int mh3_flash_attn_sparse_128(const MH3AttnArgs* args, const uint16_t
     p.row0 = c.row0, p.dense_row0 = args->dense_row0, p.head_stride = c.head_stride, p.row_stride = c.row_stride;
     p.plane = uint32_t(plane), p.cubes = uint32_t(cubes), p.heads = c.heads, p.n_dense = args->n_dense;
     p.nd = uint32_t(nd), p.layout = c.layout, p.out_stride = c.out_stride;
+    p.xcd_slices = MH3_ATTN_XCD && cubes % 8u == 0 && (nd * c.heads) % 8u == 0 ? 1u : 0u;
     const float scale = args->scale > 0.0f ? args->scale : 0.08838834764831845f; // 1 / sqrt(128)
     p.scale_log2 = scale * 1.4426950408889634f;
     const uint64_t blocks = (cubes + nd) * c.heads;
-    hipLaunchKernelGGL(attn_sparse_kernel, dim3(uint32_t(blocks)), dim3(kAttnThreads), 0,
+    constexpr int kStages = MH3_ATTN_STAGES;
+    const void* kern = reinterpret_cast<const void*>(&attn_sparse_kernel<kStages>);
+    const size_t lds = size_t(kStages) * kStageBytes;
+    if (hipFuncSetAttribute(kern, hipFuncAttributeMaxDynamicSharedMemorySize, int(lds)) != hipSuccess)
+        return MH3_ERR_HIP;
+    hipLaunchKernelGGL(attn_sparse_kernel<kStages>, dim3(uint32_t(blocks)), dim3(kAttnThreads), lds,
                        static_cast<hipStream_t>(stream), p);
     return host::check_launch();
 }
