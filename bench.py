@@ -1,6 +1,7 @@
 """Benchmark of the H3 per-block hot path on one MI355X.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--only fused,swiglu,select,fc1,rms_f32] [--no-cpu]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--only fused,block_order,copy,swiglu,select,heads,attn,fc1,rms_f32]
+                    [--no-cpu] [--no-compare]
 
 A step is one pass of the headline kernel -- the fused adaLN-modulated RMS norm + gated residual -- over the
 768p-shaped batch (129,536 rows = 32x48x84 video + 512 text, x 5120, bf16), inputs resident in HBM. value is its
@@ -276,6 +277,46 @@ def bench_attn(mh, dev, steps, warmup):
             "shape": {"heads": HEADS, "grid": list(GRID), "cubes": cubes, "dense_rows": n_dense, "k": kk}}
 
 
+def bench_heads(mh, dev, steps, warmup):
+    """heads_partial at the 768p shape: qkv [129,536][3 x 40 x 128] bf16 (the QKV GEMM's rows: 512 text + the
+    32 x 48 x 84 video grid), per-head RMS norm + rotary on 96 of 128 values for q and k, v copied, out as head tiles
+    [40][rows][128]; and the same with the cube map (the gathered order: 2016 cubes x 64 slots + 512 text rows).
+    Algorithmic bytes: 4 per element of q, k and v (read once, written once), plus the rows' cos / sin tables."""
+    g = torch.Generator(device=dev).manual_seed(11)
+    T, Y, X = GRID
+    video, n_dense = T * Y * X, 512
+    rows = ROWS
+    x = torch.randn((rows, 3 * HEADS * 128), generator=g, device=dev).to(torch.bfloat16)
+    ang = torch.rand((rows, 48), generator=g, device=dev) * 6.2831853 - 3.1415927
+    ct, st = torch.cos(ang), torch.sin(ang)
+    qw = 1 + 0.1 * torch.randn(128, generator=g, device=dev)
+    kw = 1 + 0.1 * torch.randn(128, generator=g, device=dev)
+    outs = [torch.empty((HEADS, rows, 128), dtype=torch.bfloat16, device=dev) for _ in range(3)]
+    ms, _ = time_launches(lambda: mh.heads_partial(x, HEADS, qw, kw, ct, st, q=outs[0], k=outs[1], v=outs[2]),
+                          steps, warmup)
+    nbytes = rows * 3 * HEADS * 128 * 4 + rows * 48 * 8
+    res = {"ms": ms, "bytes": nbytes, "GBs": nbytes / ms / 1e6, "frac": nbytes / ms / 1e6 / HBM_PEAK_GBS,
+           "shape": {"rows": rows, "heads": HEADS, "rot": 96}}
+    # Gathered through the cube map: text rows first in the model (rows 0..511), the video grid after them.
+    cubes = mh.cube_count(*GRID)
+    l = torch.arange(64, device=dev)
+    c = torch.arange(cubes, device=dev)[:, None]
+    ch, cw = Y // 4, X // 4
+    t = 4 * (c // (ch * cw)) + l // 16
+    y = 4 * (c // cw % ch) + l // 4 % 4
+    xx = 4 * (c % cw) + l % 4
+    cube_rows = (n_dense + (t * Y + y) * X + xx).reshape(-1)
+    cmap = torch.cat([cube_rows, torch.arange(n_dense, device=dev)]).to(torch.int32)
+    del outs
+    gout = [torch.empty((HEADS, cmap.numel(), 128), dtype=torch.bfloat16, device=dev) for _ in range(3)]
+    gms, _ = time_launches(lambda: mh.heads_partial(x, HEADS, qw, kw, ct, st, map=cmap, q=gout[0], k=gout[1],
+                                                    v=gout[2]), steps, warmup)
+    gbytes = cmap.numel() * 3 * HEADS * 128 * 4 + cmap.numel() * (48 * 8 + 4)
+    res["gathered"] = {"ms": gms, "bytes": gbytes, "GBs": gbytes / gms / 1e6,
+                       "frac": gbytes / gms / 1e6 / HBM_PEAK_GBS, "rows": cmap.numel()}
+    return res
+
+
 def bench_fc1(mh, dev, steps, warmup, compare):
     g = torch.Generator(device=dev).manual_seed(9)
     x = torch.randn((ROWS, DIM), generator=g, device=dev).to(torch.bfloat16)
@@ -453,7 +494,7 @@ def main() -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--only", default="fused,block_order,copy,swiglu,select,attn,fc1,rms_f32")
+    ap.add_argument("--only", default="fused,block_order,copy,swiglu,select,heads,attn,fc1,rms_f32")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-compare", action="store_true")
     args = ap.parse_args()
@@ -486,6 +527,9 @@ def main() -> int:
         torch.cuda.empty_cache()
     if "select" in ops:
         report["cube_selector"] = bench_select(mh, dev, args.steps, args.warmup)
+        torch.cuda.empty_cache()
+    if "heads" in ops:
+        report["heads_partial"] = bench_heads(mh, dev, args.steps, args.warmup)
         torch.cuda.empty_cache()
     if "attn" in ops:
         report["flash_attn_sparse_128"] = bench_attn(mh, dev, max(3, args.steps // 2), max(1, args.warmup // 2))

@@ -167,6 +167,38 @@ int mh3_cube_topk(const MH3CubeArgs* args, const float* s, int32_t* idx, int32_t
 int mh3_cube_select(const MH3CubeArgs* args, const float* qc, const float* kc, int32_t* idx, int32_t* cnt,
                     mh3_stream_t stream);
 
+/* ---- heads_partial ------------------------------------------------------------------------------------------------
+ * Reference kernel `heads_partial` (mako-common; docs/architecture.md:35-38,61-63,123-125; docs/performance.md:44):
+ * the step between the QKV GEMM and attention. qkv holds one model row a row, [q (heads x 128) | k (heads x 128) |
+ * v (heads x 128)] bf16, the order the reference stacks the fused QKV weight in (docs/architecture.md:61-62). For
+ * output row r, its model row src = map[r] (r when map is NULL), and head h:
+ *   q: y = x * rsqrt(mean(x^2) + eps) * q_w over the head's 128 values, in float; then the rotary positions on the
+ *      first `rot` values: value i < rot / 2 pairs with value i + rot / 2,
+ *      (a, b) -> (a cos - b sin, b cos + a sin), cos = cos_t[src][i], sin = sin_t[src][i];
+ *      values rot .. 127 pass unrotated; one rounding to bf16;
+ *   k: the same with k_w;
+ *   v: copied (skipped when v is NULL).
+ * A map entry outside [0, model_rows) (-1: a cube's padding slot at the grid's edge) writes zeros to every output of
+ * its row and reads nothing. The outputs put element (h, r, d) at h * out_head_stride + r * out_row_stride + d: the head tiles
+ * [heads][rows][128], or the model's own [rows][heads * 128] order. With a cube map the rows come out in the order
+ * cube_pool, cube_select and flash_attn_sparse_128 take as MH3_CUBES_GATHERED (cube c's 64 slots at rows 64 c ..,
+ * then the dense rows). cos_t and sin_t are float [model_rows][rot / 2] (NULL when rot is 0); q_w and k_w are
+ * float [128] shared by the heads (NULL: all 1). The outputs may overwrite their own inputs in place (map NULL, each
+ * output at its input's position); otherwise they may not overlap qkv. */
+typedef struct MH3HeadsArgs {
+    uint32_t rows;       /* output rows */
+    uint32_t model_rows; /* rows of qkv, cos_t and sin_t */
+    uint32_t heads;
+    uint32_t head_dim;   /* 128 */
+    uint32_t rot;        /* rotating values a head: a multiple of 16, <= head_dim (H3: 96) */
+    float eps;           /* > 0 */
+    uint64_t qkv_stride; /* elements between model rows of qkv: >= 3 heads head_dim, a multiple of 8 */
+    uint64_t out_head_stride, out_row_stride; /* elements, multiples of 8 */
+} MH3HeadsArgs;
+int mh3_heads_partial(const MH3HeadsArgs* args, const uint16_t* qkv, const float* q_w, const float* k_w,
+                      const float* cos_t, const float* sin_t, const int32_t* map, uint16_t* q, uint16_t* k,
+                      uint16_t* v, mh3_stream_t stream);
+
 /* ---- flash_attn_sparse_128 ---------------------------------------------------------------------------------------
  * Reference kernel `flash_attn_sparse_128` (mako-common; docs/architecture.md:123-130, docs/performance.md:162-181):
  * flash attention, head_dim 128, over the pass lists of cube_topk / cube_select. Per head h:

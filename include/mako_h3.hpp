@@ -123,6 +123,28 @@ struct Cubes {
     }
 };
 
+// The shape of a heads_partial call: qkv rows [q heads | k heads | v heads] in, head tiles out. Zero strides take
+// the defaults: qkv_stride 3 heads 128, outputs [heads][rows][128].
+struct Heads {
+    uint32_t rows = 0, model_rows = 0, heads = 0;
+    uint32_t rot = 96;
+    float eps = 1e-6f;
+    uint64_t qkv_stride = 0, out_head_stride = 0, out_row_stride = 0;
+
+    MH3HeadsArgs args() const
+    {
+        return MH3HeadsArgs{rows,
+                            model_rows ? model_rows : rows,
+                            heads,
+                            128,
+                            rot,
+                            eps,
+                            qkv_stride ? qkv_stride : 3ull * heads * 128,
+                            out_head_stride ? out_head_stride : uint64_t(rows) * 128,
+                            out_row_stride ? out_row_stride : 128};
+    }
+};
+
 inline std::optional<uint32_t> parse_int8(const std::string& text)
 {
     uint32_t mask = 0;
@@ -195,6 +217,25 @@ public:
     {
         const MH3CubeArgs a = c.args();
         check(mh3_cube_select(&a, qc, kc, idx, cnt, s_), "cube_scores+cube_topk");
+    }
+
+    // After the QKV GEMM: the per-head RMS norm and rotary positions of q and k, v copied, written as head tiles;
+    // with a cube map (map[r] = model row, -1 padding) in the cube order cube_pool, cube_select and
+    // flash_attn_sparse_128 read as MH3_CUBES_GATHERED. v == nullptr skips v.
+    void heads_partial(const Heads& hd, const uint16_t* qkv, const float* q_w, const float* k_w, const float* cos_t,
+                       const float* sin_t, const int32_t* map, uint16_t* q, uint16_t* k, uint16_t* v) const
+    {
+        const MH3HeadsArgs a = hd.args();
+        check(mh3_heads_partial(&a, qkv, q_w, k_w, cos_t, sin_t, map, q, k, v, s_), "heads_partial");
+    }
+    // Flash attention over the pass lists idx / cnt of cube_select (or cube_topk) and the dense rows
+    // [dense_row0, dense_row0 + n_dense); q, k, v and out in c's cube geometry. scale 0: 1 / sqrt(128).
+    void flash_attn_sparse_128(const Cubes& c, const uint16_t* q, const uint16_t* k, const uint16_t* v,
+                               const int32_t* idx, const int32_t* cnt, uint64_t dense_row0, uint32_t n_dense,
+                               uint16_t* out, float scale = 0.0f) const
+    {
+        const MH3AttnArgs a{c.args(), dense_row0, n_dense, scale};
+        check(mh3_flash_attn_sparse_128(&a, q, k, v, idx, cnt, out, s_), "flash_attn_sparse_128");
     }
 
     // Weight rows to int8 with one scale each (at load)

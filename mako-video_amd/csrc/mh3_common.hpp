@@ -103,6 +103,27 @@ __device__ __forceinline__ uint32_t wave_sum_u32(uint32_t v)
 // Lanes below this one in a 64-bit ballot.
 __device__ __forceinline__ uint64_t lanes_below(int lane) { return (uint64_t(1) << lane) - 1; }
 
+// n / d for any 32-bit n by a multiply-high and shifts (Granlund & Montgomery 1994, fig. 4.1).
+struct FastDiv {
+    uint32_t m, s1, s2;
+    __host__ static FastDiv make(uint32_t d)
+    {
+        uint32_t l = 0;
+        while ((uint64_t(1) << l) < d)
+            ++l;
+        FastDiv f;
+        f.m = uint32_t(((uint64_t(1) << 32) * ((uint64_t(1) << l) - d)) / d + 1);
+        f.s1 = l < 1 ? l : 1;
+        f.s2 = l > 1 ? l - 1 : 0;
+        return f;
+    }
+    __device__ __forceinline__ uint32_t div(uint32_t n) const
+    {
+        const uint32_t t = __umulhi(n, m);
+        return (t + ((n - t) >> s1)) >> s2;
+    }
+};
+
 // ---- streaming memory access -----------------------------------------------------------------------------------------
 typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
 

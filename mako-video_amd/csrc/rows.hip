@@ -445,27 +445,6 @@ __global__ __launch_bounds__(MH3_WAVE_BLOCK) void rows_wave_kernel(RowsParams p)
 
 // ---- swiglu ---------------------------------------------------------------------------------------------------------
 
-// n / d for any 32-bit n by a multiply-high and shifts (Granlund & Montgomery 1994, fig. 4.1).
-struct FastDiv {
-    uint32_t m, s1, s2;
-    __host__ static FastDiv make(uint32_t d)
-    {
-        uint32_t l = 0;
-        while ((uint64_t(1) << l) < d)
-            ++l;
-        FastDiv f;
-        f.m = uint32_t(((uint64_t(1) << 32) * ((uint64_t(1) << l) - d)) / d + 1);
-        f.s1 = l < 1 ? l : 1;
-        f.s2 = l > 1 ? l - 1 : 0;
-        return f;
-    }
-    __device__ __forceinline__ uint32_t div(uint32_t n) const
-    {
-        const uint32_t t = __umulhi(n, m);
-        return (t + ((n - t) >> s1)) >> s2;
-    }
-};
-
 // silu(g) * u = g / (1 + exp(-g)) * u, with exp from v_exp_f32 and one reciprocal.
 __device__ __forceinline__ float silu_mul(float g, float u)
 {

@@ -47,6 +47,12 @@ class AttnArgs(C.Structure):
     _fields_ = [("cubes", CubeArgs), ("dense_row0", C.c_uint64), ("n_dense", C.c_uint32), ("scale", C.c_float)]
 
 
+class HeadsArgs(C.Structure):
+    _fields_ = [("rows", C.c_uint32), ("model_rows", C.c_uint32), ("heads", C.c_uint32), ("head_dim", C.c_uint32),
+                ("rot", C.c_uint32), ("eps", C.c_float), ("qkv_stride", C.c_uint64), ("out_head_stride", C.c_uint64),
+                ("out_row_stride", C.c_uint64)]
+
+
 class QuantArgs(C.Structure):
     _fields_ = [("rows", C.c_uint32), ("cols", C.c_uint32), ("dtype", C.c_uint32), ("reserved", C.c_uint32)]
 
@@ -77,6 +83,7 @@ def _load() -> C.CDLL:
         "mh3_cube_scores": (I32, [C.POINTER(CubeArgs), P, P, P, P]),
         "mh3_cube_topk": (I32, [C.POINTER(CubeArgs), P, P, P, P]),
         "mh3_cube_select": (I32, [C.POINTER(CubeArgs), P, P, P, P, P]),
+        "mh3_heads_partial": (I32, [C.POINTER(HeadsArgs), P, P, P, P, P, P, P, P, P, P]),
         "mh3_flash_attn_sparse_128": (I32, [C.POINTER(AttnArgs), P, P, P, P, P, P, P]),
         "mh3_quant_rows_i8": (I32, [C.POINTER(QuantArgs), P, P, P, P]),
         "mh3_gemm_w8a16_swiglu": (I32, [C.POINTER(GemmArgs), P, P, P, P, P]),
@@ -347,6 +354,49 @@ def cube_select(a: CubeArgs, qc, kc, *, idx=None, cnt=None):
     idx, cnt = _topk_out(a, qc.device, idx, cnt)
     _check(lib.mh3_cube_select(C.byref(a), _ptr(qc), _ptr(kc), _ptr(idx), _ptr(cnt), _stream()), "cube_select")
     return idx, cnt
+
+
+# ---- heads_partial ---------------------------------------------------------------------------------------------------
+
+def heads_partial(qkv, heads, q_w=None, k_w=None, cos_t=None, sin_t=None, *, rot=96, eps=1e-6, map=None,
+                  with_v=True, layout="heads", q=None, k=None, v=None):
+    """After the QKV GEMM: qkv bf16 [model_rows][>= 3 heads 128] ([q heads | k heads | v heads] a row) -> q and k
+    with the per-head RMS norm (weights q_w, k_w f32 [128]; None: 1) and the rotary positions on the first `rot`
+    values (cos_t, sin_t f32 [model_rows][rot / 2]), v copied (not written when with_v is False). Output row r is model
+    row map[r] (int32 [rows]; entries outside [0, model_rows) give zeros), or row r without a map. layout "heads"
+    gives [heads][rows][128] tensors, "rows" gives [rows][heads * 128]. Returns (q, k, v)."""
+    if qkv.dim() != 2:
+        raise ValueError("qkv must be [rows][3 heads 128]")
+    model_rows, stride = qkv.shape
+    _need(qkv, "qkv", torch.bfloat16, qkv.numel())
+    rows = model_rows if map is None else map.numel()
+    if map is not None:
+        _need(map, "map", torch.int32, rows)
+    a = HeadsArgs()
+    a.rows, a.model_rows, a.heads, a.head_dim, a.rot, a.eps, a.qkv_stride = rows, model_rows, heads, 128, rot, eps, stride
+    if layout == "heads":
+        shape, a.out_head_stride, a.out_row_stride = (heads, rows, 128), rows * 128, 128
+    elif layout == "rows":
+        shape, a.out_head_stride, a.out_row_stride = (rows, heads * 128), 128, heads * 128
+    else:
+        raise ValueError("layout is 'heads' or 'rows'")
+    for name, t in (("q_w", q_w), ("k_w", k_w)):
+        if t is not None:
+            _need(t, name, torch.float32, 128)
+    if rot:
+        for name, t in (("cos_t", cos_t), ("sin_t", sin_t)):
+            _need(t, name, torch.float32, model_rows * (rot // 2))
+    outs = []
+    for name, t, want in (("q", q, True), ("k", k, True), ("v", v, with_v)):
+        if not want:
+            outs.append(None)
+            continue
+        t = torch.empty(shape, dtype=torch.bfloat16, device=qkv.device) if t is None else t
+        _need(t, name, torch.bfloat16, heads * rows * 128)
+        outs.append(t)
+    _check(lib.mh3_heads_partial(C.byref(a), _ptr(qkv), _ptr(q_w), _ptr(k_w), _ptr(cos_t if rot else None),
+                                 _ptr(sin_t if rot else None), _ptr(map), *(_ptr(t) for t in outs), _stream()), "heads_partial")
+    return tuple(outs)
 
 
 # ---- flash_attn_sparse_128 -------------------------------------------------------------------------------------------

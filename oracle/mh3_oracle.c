@@ -347,6 +347,61 @@ void mh3o_cube_topk_sorted(uint32_t heads, uint32_t gt, uint32_t gh, uint32_t gw
     free(row);
 }
 
+/* ---- heads_partial ------------------------------------------------------------------------------------------ */
+
+/* docs/architecture.md:35-38 ("96 of each head's 128 values rotate (the first 48 with the second 48)"), :61-63 ("RMS
+ * norms per head, rotary positions"), :123-125 (the head tiles gathered through the cube map, padding rows zero).
+ * qkv rows are [q heads | k heads | v heads] (:61-62). Per output row r (model row map[r], or r) and head h:
+ * q and k: y = x / sqrt(mean(x^2) + eps) * w, then (y_i, y_{i+half}) -> (y_i c - y_{i+half} s, y_{i+half} c + y_i s)
+ * for i < half = rot / 2 with c, s = cos_t, sin_t [src][i]; one rounding. v: copied. A map entry outside
+ * [0, model_rows) writes zeros. */
+void mh3o_heads_partial(uint32_t rows, uint32_t model_rows, uint32_t heads, uint32_t rot, float eps,
+                        uint64_t qkv_stride, uint64_t out_head_stride, uint64_t out_row_stride, const uint16_t* qkv,
+                        const float* q_w, const float* k_w, const float* cos_t, const float* sin_t,
+                        const int32_t* map, uint16_t* q, uint16_t* k, uint16_t* v)
+{
+    const uint32_t half = rot / 2;
+    uint16_t* outs[3] = {q, k, v};
+    const float* ws[2] = {q_w, k_w};
+    for (uint64_t r = 0; r < rows; ++r) {
+        const int64_t m = map ? (int64_t)map[r] : (int64_t)r;
+        const int valid = m >= 0 && m < (int64_t)model_rows;
+        for (uint32_t kind = 0; kind < 3; ++kind) {
+            if (!outs[kind])
+                continue;
+            for (uint32_t h = 0; h < heads; ++h) {
+                uint16_t* dst = outs[kind] + h * out_head_stride + r * out_row_stride;
+                if (!valid) {
+                    memset(dst, 0, 128 * sizeof(uint16_t));
+                    continue;
+                }
+                const uint16_t* src = qkv + (uint64_t)m * qkv_stride + ((uint64_t)kind * heads + h) * 128;
+                if (kind == 2) {
+                    memcpy(dst, src, 128 * sizeof(uint16_t));
+                    continue;
+                }
+                double y[128], ss = 0.0;
+                for (int d = 0; d < 128; ++d) {
+                    y[d] = (double)mh3o_bf16_to_float(src[d]);
+                    ss += y[d] * y[d];
+                }
+                const double inv = 1.0 / sqrt(ss / 128.0 + (double)eps);
+                for (int d = 0; d < 128; ++d)
+                    y[d] *= inv * (ws[kind] ? (double)ws[kind][d] : 1.0);
+                double o[128];
+                memcpy(o, y, sizeof o);
+                for (uint32_t i = 0; i < half; ++i) {
+                    const double c = cos_t[(uint64_t)m * half + i], s = sin_t[(uint64_t)m * half + i];
+                    o[i] = y[i] * c - y[i + half] * s;
+                    o[i + half] = y[i + half] * c + y[i] * s;
+                }
+                for (int d = 0; d < 128; ++d)
+                    dst[d] = mh3o_bf16_from_double(o[d]);
+            }
+        }
+    }
+}
+
 /* ---- int8 ------------------------------------------------------------------------------------------------------ */
 
 /* docs/performance.md:122-123: "int8 rows with a float scale each (symmetric, the row's maximum at 127)". The scale

@@ -9,6 +9,7 @@
  *   rms_mod_rows / gate_add_rows   docs/architecture.md:49-52,61,64-66
  *   swiglu_rows                     docs/architecture.md:65,112-114
  *   cube_pool / _scores / _topk     docs/architecture.md:118-133, README.md:81-87, docs/performance.md:175-181
+ *   heads_partial                   docs/architecture.md:35-38,61-63,123-125
  *   quant_rows_i8, W8A16 fc1        docs/performance.md:120-136
  * bf16 results are rounded to nearest even exactly once, from the double value.
  *
@@ -28,6 +29,9 @@
  *                              baseline times: a sort a row instead of the O(C^2) count)
  *   mh3o_attn_sparse(_tile)    torch scaled_dot_product_attention in float64 with a boolean mask built in numpy
  *                              from the pass lists; with every cube selected, the unmasked attention over all rows
+ *   mh3o_heads_partial         torch float64: F.rms_norm per head, then the rotation as a complex product of the
+ *                              (i, i + rot/2) pairs with e^(i angle) (torch.polar); rotation keeps each pair's
+ *                              length; angle 0 is the plain norm, pi/2 maps (a, b) to (-b, a); map -1 gives zeros
  *   mh3o_quant_rows_i8         |q| <= 127, the row maximum maps to +-127, |w - q*s| <= s/2, numpy rint
  *   mh3o_gemm_w8a16_swiglu     torch.matmul in float64; exact integer results for w in {-1,0,1}, s = 1
  *   mh3o_gemm_bf16_swiglu      torch.matmul in float64; exact integer results for w in {-1,0,1}
@@ -88,6 +92,13 @@ void mh3o_attn_sparse(uint32_t heads, uint32_t gt, uint32_t gh, uint32_t gw, int
                       uint64_t head_stride, uint64_t row_stride, uint64_t dense_row0, uint32_t n_dense, double scale,
                       const uint16_t* q, const uint16_t* k, const uint16_t* v, const int32_t* idx, const int32_t* cnt,
                       uint32_t out_stride, uint16_t* out);
+
+/* heads_partial: qkv bf16 rows [q heads | k heads | v heads] -> per-head RMS norm (q, k) and rotary on the first rot
+ * values, v copied; element (h, r, d) of each output at h * out_head_stride + r * out_row_stride + d. v may be NULL. */
+void mh3o_heads_partial(uint32_t rows, uint32_t model_rows, uint32_t heads, uint32_t rot, float eps,
+                        uint64_t qkv_stride, uint64_t out_head_stride, uint64_t out_row_stride, const uint16_t* qkv,
+                        const float* q_w, const float* k_w, const float* cos_t, const float* sin_t,
+                        const int32_t* map, uint16_t* q, uint16_t* k, uint16_t* v);
 
 void mh3o_quant_rows_i8(uint32_t rows, uint32_t cols, int dtype, const void* w, int8_t* q, float* scale);
 

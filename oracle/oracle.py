@@ -53,6 +53,7 @@ _lib.mh3o_cube_topk_sorted.argtypes = [C.c_uint32] * 7 + [_P] * 3
 _ATTN_GEOM = [C.c_uint32] * 3 + [C.c_int, C.c_uint64, C.c_uint64, C.c_uint64, C.c_uint64, C.c_uint32, C.c_double]
 _lib.mh3o_attn_sparse_tile.argtypes = _ATTN_GEOM + [_P] * 5 + [C.c_uint32, C.c_uint32, C.c_uint64, _P]
 _lib.mh3o_attn_sparse.argtypes = [C.c_uint32] + _ATTN_GEOM + [_P] * 5 + [C.c_uint32, _P]
+_lib.mh3o_heads_partial.argtypes = [C.c_uint32] * 4 + [C.c_float] + [C.c_uint64] * 3 + [_P] * 9
 _lib.mh3o_quant_rows_i8.argtypes = [C.c_uint32, C.c_uint32, C.c_int] + [_P] * 3
 _lib.mh3o_gemm_w8a16_swiglu.argtypes = [C.c_uint32] * 3 + [_P] * 4
 _lib.mh3o_gemm_bf16_swiglu.argtypes = [C.c_uint32] * 3 + [_P] * 3
@@ -186,6 +187,23 @@ def cube_topk_row(row_scores, i, grid, k, local, out_stride=None):
     out = np.empty(out_stride, np.int32)
     n = _lib.mh3o_cube_topk_row(*grid, k, local, out_stride, i, _p(row), _p(out))
     return out, int(n)
+
+
+# ---- heads_partial -----------------------------------------------------------------------------------------------------
+
+def heads_partial(qkv, heads, q_w=None, k_w=None, cos_t=None, sin_t=None, rot=96, eps=1e-6, map_=None, with_v=True):
+    """qkv bf16 bits [model_rows][>= 3 heads 128] -> (q, k, v) bf16 bits [heads][rows][128] (v None without with_v):
+    per-head RMS norm and rotary on q and k, v copied, output row r from model row map_[r] (or r)."""
+    model_rows, stride = qkv.shape
+    rows = model_rows if map_ is None else len(map_)
+    qkv = np.ascontiguousarray(qkv, dtype=np.uint16)
+    m = None if map_ is None else np.ascontiguousarray(map_, dtype=np.int32)
+    f = lambda a: None if a is None else np.ascontiguousarray(a, dtype=np.float32)  # noqa: E731
+    q_w, k_w, cos_t, sin_t = f(q_w), f(k_w), f(cos_t), f(sin_t)
+    outs = [np.empty((heads, rows, 128), np.uint16) for _ in range(3 if with_v else 2)] + ([] if with_v else [None])
+    _lib.mh3o_heads_partial(rows, model_rows, heads, rot, eps, stride, rows * 128, 128, _p(qkv), _p(q_w), _p(k_w),
+                            _p(cos_t), _p(sin_t), _p(m), *(_p(a) for a in outs))
+    return tuple(outs)
 
 
 # ---- int8 ------------------------------------------------------------------------------------------------------------

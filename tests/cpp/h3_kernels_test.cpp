@@ -2,7 +2,7 @@
 // (oracle/mh3_oracle.h, the checker), reported the way the reference's tests/h3_ref_test.cpp reports: one line per
 // check, "ok" or "FAIL", the relative RMS error and the lowest row cosine of diff() (h3_ref_test.cpp:67-90), and
 // the number of failures as the exit status.
-//   h3_kernels_test [rows | swiglu | cubes | int8 | errors | all]
+//   h3_kernels_test [rows | swiglu | cubes | attn | int8 | errors | all]
 #include "mako_h3.hpp"
 #include "mh3_oracle.h"
 
@@ -224,6 +224,66 @@ void cubes()
     check(idx2.download() == widx && cnt2.download() == wcnt, "cube_select == cube_scores + cube_topk");
 }
 
+// heads_partial from one qkv tensor, gathered through the cube map, then the selector and flash_attn_sparse_128 on the
+// gathered head tiles; each stage against the oracle run on the oracle's own outputs of the stage before.
+void attn()
+{
+    std::printf("attn\n");
+    Rng r(4);
+    Cubes c;
+    c.heads = 2, c.t = 7, c.h = 9, c.w = 10, c.ratio = 0.25f, c.local = 1, c.layout = MH3_CUBES_GATHERED;
+    const uint32_t video = c.t * c.h * c.w, n_dense = 70, model_rows = n_dense + video, C = c.count();
+    const uint32_t rows = 64 * C + n_dense, rot = 96, half = rot / 2;
+    // The cube map: attention row 64 cube + slot -> the model row of that grid position (video after the text), -1
+    // for padding slots; then the text rows.
+    std::vector<int32_t> map(rows, -1);
+    const uint32_t ch = (c.h + 3) / 4, cw = (c.w + 3) / 4;
+    for (uint32_t cube = 0; cube < C; ++cube)
+        for (uint32_t l = 0; l < 64; ++l) {
+            const uint32_t t = 4 * (cube / (ch * cw)) + l / 16, y = 4 * (cube / cw % ch) + l / 4 % 4,
+                           x = 4 * (cube % cw) + l % 4;
+            if (t < c.t && y < c.h && x < c.w)
+                map[64 * cube + l] = int32_t(n_dense + (t * c.h + y) * c.w + x);
+        }
+    for (uint32_t i = 0; i < n_dense; ++i)
+        map[64 * C + i] = int32_t(i);
+    auto qkv = bf16_normals(r, size_t(model_rows) * 3 * c.heads * 128);
+    auto qw = normals(r, 128, 0.1, 1.0), kw = normals(r, 128, 0.1, 1.0);
+    std::vector<float> cs(size_t(model_rows) * half), sn(cs.size());
+    for (size_t i = 0; i < cs.size(); ++i) {
+        const double a = 6.283185307179586 * (r.uniform() - 0.5);
+        cs[i] = float(std::cos(a)), sn[i] = float(std::sin(a));
+    }
+    const size_t tile = size_t(c.heads) * rows * 128;
+    DeviceBuffer<uint16_t> dqkv(qkv), q(tile), k(tile), v(tile), out(tile);
+    DeviceBuffer<float> dqw(qw), dkw(kw), dcs(cs), dsn(sn), qc(size_t(c.heads) * C * 128), kc(qc.size());
+    DeviceBuffer<int32_t> dmap(map), idx(size_t(c.heads) * C * c.out_stride()), cnt(size_t(c.heads) * C);
+    Heads hd;
+    hd.rows = rows, hd.model_rows = model_rows, hd.heads = c.heads, hd.rot = rot;
+    c.head_stride = uint64_t(rows) * 128;
+    Kernels kern;
+    kern.heads_partial(hd, dqkv.get(), dqw.get(), dkw.get(), dcs.get(), dsn.get(), dmap.get(), q.get(), k.get(),
+                       v.get());
+    kern.cube_pool(c, q.get(), k.get(), qc.get(), kc.get());
+    kern.cube_select(c, qc.get(), kc.get(), idx.get(), cnt.get());
+    kern.flash_attn_sparse_128(c, q.get(), k.get(), v.get(), idx.get(), cnt.get(), 64ull * C, n_dense, out.get());
+    kern.finish();
+    std::vector<uint16_t> oq(tile), ok_(tile), ov(tile), oo(tile, 0);
+    mh3o_heads_partial(rows, model_rows, c.heads, rot, 1e-6f, 3ull * c.heads * 128, uint64_t(rows) * 128, 128,
+                       qkv.data(), qw.data(), kw.data(), cs.data(), sn.data(), map.data(), oq.data(), ok_.data(),
+                       ov.data());
+    compare("heads_partial q, gathered through the cube map", of_bf16(q.download()), of_bf16(oq), 128, 1e-2, 1e-3);
+    compare("heads_partial k, gathered through the cube map", of_bf16(k.download()), of_bf16(ok_), 128, 1e-2, 1e-3);
+    check(v.download() == ov, "heads_partial v (a copy) and padding rows (zeros) bit for bit");
+    // Attention over the GPU's own pass lists, from the oracle's head tiles.
+    const auto gi = idx.download(), gc = cnt.download();
+    mh3o_attn_sparse(c.heads, c.t, c.h, c.w, MH3O_CUBES_GATHERED, 0, uint64_t(rows) * 128, 128, 64ull * C, n_dense,
+                     1.0 / std::sqrt(128.0), oq.data(), ok_.data(), ov.data(), gi.data(), gc.data(), c.out_stride(),
+                     oo.data());
+    compare("flash_attn_sparse_128 over the gathered tiles, 2 heads, 7x9x10 grid + 70 text rows",
+            of_bf16(out.download()), of_bf16(oo), 128, 1e-2, 3e-3);
+}
+
 void int8()
 {
     std::printf("int8\n");
@@ -316,6 +376,8 @@ int main(int argc, char** argv)
             swiglu();
         if (mode == "cubes" || mode == "all")
             cubes();
+        if (mode == "attn" || mode == "all")
+            attn();
         if (mode == "int8" || mode == "all")
             int8();
         if (mode == "errors" || mode == "all")
