@@ -1,6 +1,7 @@
 """Benchmark of the H3 per-block hot path on one MI355X.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--only fused,block_order,copy,swiglu,select,heads,attn,fc1,rms_f32]
+    python bench.py [--gpus 1] [--steps K] [--warmup W]
+                    [--only fused,block_order,copy,swiglu,select,heads,attn,proj,fc1,rms_f32]
                     [--no-cpu] [--no-compare]
 
 A step is one pass of the headline kernel -- the fused adaLN-modulated RMS norm + gated residual -- over the
@@ -317,6 +318,39 @@ def bench_heads(mh, dev, steps, warmup):
     return res
 
 
+def bench_proj(mh, dev, steps, warmup):
+    """The block's other projections at the 768p rows (129,536): qkv 5120 -> 3 x 40 x 128 = 15,360 (plain store), the
+    out projection 5120 -> 5120 and fc2 13,824 -> 5120 with gate_add_rows folded into the epilogue (residual += gate *
+    y, in place), each with int8 weights (weight-only, the --int8 path) and qkv also with bf16 weights. 2 flop a MAC."""
+    g = torch.Generator(device=dev).manual_seed(12)
+    res = {}
+    for name, k, n, epi in (("qkv", DIM, 3 * HEADS * 128, "store"), ("out", DIM, DIM, "gate_add"),
+                            ("fc2", FFN, DIM, "gate_add")):
+        x = torch.randn((ROWS, k), generator=g, device=dev).to(torch.bfloat16)
+        w = torch.randint(-127, 128, (n, k), generator=g, device=dev, dtype=torch.int8)
+        s = (torch.rand(n, generator=g, device=dev) * 1.5e-3 + 0.5e-3).float()
+        y = torch.zeros((ROWS, n), dtype=torch.bfloat16, device=dev)
+        gate = (0.1 * torch.randn(n, generator=g, device=dev)).float()
+        if epi == "store":
+            fn = lambda: mh.gemm(x, w, w_scale=s, out=y)  # noqa: E731
+        else:
+            fn = lambda: mh.gemm_gate_add(x, w, y, gate, w_scale=s)  # noqa: E731
+        ms, _ = time_launches(fn, steps, warmup)
+        flops = 2.0 * ROWS * k * n
+        res[name] = {"ms": ms, "tflops": flops / ms / 1e9, "mfma_util": flops / ms / 1e9 / BF16_PEAK_TFLOPS,
+                     "shape": [ROWS, k, n], "weights": "int8 (W8A16)", "epilogue": epi}
+        if name == "qkv":
+            wb = (w.float() * s[:, None]).to(torch.bfloat16)
+            bms, _ = time_launches(lambda: mh.gemm(x, wb, out=y), steps, warmup)
+            res[name]["bf16_ms"] = bms
+            res[name]["bf16_tflops"] = flops / bms / 1e9
+            res[name]["bf16_mfma_util"] = flops / bms / 1e9 / BF16_PEAK_TFLOPS
+            del wb
+        del x, w, y
+        torch.cuda.empty_cache()
+    return res
+
+
 def bench_fc1(mh, dev, steps, warmup, compare):
     g = torch.Generator(device=dev).manual_seed(9)
     x = torch.randn((ROWS, DIM), generator=g, device=dev).to(torch.bfloat16)
@@ -494,7 +528,7 @@ def main() -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--only", default="fused,block_order,copy,swiglu,select,heads,attn,fc1,rms_f32")
+    ap.add_argument("--only", default="fused,block_order,copy,swiglu,select,heads,attn,proj,fc1,rms_f32")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-compare", action="store_true")
     args = ap.parse_args()
@@ -533,6 +567,9 @@ def main() -> int:
         torch.cuda.empty_cache()
     if "attn" in ops:
         report["flash_attn_sparse_128"] = bench_attn(mh, dev, max(3, args.steps // 2), max(1, args.warmup // 2))
+        torch.cuda.empty_cache()
+    if "proj" in ops:
+        report["projections"] = bench_proj(mh, dev, max(3, args.steps // 2), max(1, args.warmup // 2))
         torch.cuda.empty_cache()
     if "fc1" in ops:
         report["fc1_w8a16_swiglu"] = bench_fc1(mh, dev, max(3, args.steps // 2), max(1, args.warmup // 2),

@@ -29,7 +29,7 @@
 extern "C" {
 #endif
 
-#define MH3_ABI_VERSION 1
+#define MH3_ABI_VERSION 2
 
 /* ---- error codes ------------------------------------------------------------------------------------------------ */
 enum {
@@ -245,8 +245,10 @@ int mh3_quant_rows_i8(const MH3QuantArgs* args, const void* w, int8_t* q, float*
  * uses 7.7e7). */
 typedef struct MH3GemmArgs {
     uint32_t m;
-    uint32_t n; /* output columns; w has 2n rows */
+    uint32_t n;           /* output columns; w has 2n rows with a SwiGLU epilogue, n rows otherwise */
     uint32_t k;
+    uint32_t n_sets;      /* mh3_gemm_gate_add: gate sets (0 means 1); unused by the other calls */
+    uint32_t gate_stride; /* mh3_gemm_gate_add: floats between consecutive gate sets (0 means n) */
     uint32_t reserved;
 } MH3GemmArgs;
 int mh3_gemm_w8a16_swiglu(const MH3GemmArgs* args, const uint16_t* x, const int8_t* w, const float* scale,
@@ -264,6 +266,28 @@ int mh3_gemm_bf16_swiglu(const MH3GemmArgs* args, const uint16_t* x, const uint1
  * k % 128 == 0, n % 128 == 0, m >= 1; x, w and out 16-byte aligned; n * k < 2^30. */
 int mh3_gemm_i8_swiglu(const MH3GemmArgs* args, const int8_t* x, const float* x_scale, const int8_t* w,
                        const float* w_scale, uint16_t* out, mh3_stream_t stream);
+
+/* ---- the block's other GEMMs: the qkv, out and fc2 projections -------------------------------------------------
+ * The reference's bf16 `Gemm::encode` for the QKV, output and fc2 projections, and its `gemm_i8` for them under
+ * --int8 qkv,out,fc2 (mako-common; docs/performance.md:40-43,52-69,120-133; docs/architecture.md:61-66), on the fc1
+ * kernel with two other epilogues. w is [n][k], the weight's output-channel rows. `form` picks the operands:
+ *   MH3_GEMM_BF16:  x bf16 [m][k], w bf16, no scales (x_scale and w_scale unused);
+ *   MH3_GEMM_W8A16: x bf16, w int8 with w_scale float [n] (weight-only, the int8 -> bf16 widening exact);
+ *   MH3_GEMM_W8A8:  x int8 with x_scale float [m] (mh3_quant_rows_i8 of the activations), w int8 with w_scale [n],
+ *                   on the int8 MFMA with exact int32 sums.
+ * y = x w^T in float accumulation, times w_scale[col] and x_scale[row] where the form has them.
+ *   mh3_gemm:          out[m][n] = y, bf16 (the qkv projection: n = 3 heads 128, its rows [q | k | v]).
+ *   mh3_gemm_gate_add: residual[row][col] += gate[s][col] * y, bf16 in place with one rounding, s = set_of_row[row]
+ *                      (NULL: set 0), gate float [n_sets][gate_stride]: the out projection and fc2 with the block's
+ *                      `gate_add_rows` folded into the epilogue (docs/architecture.md:64-66).
+ * k % 64 == 0 (k % 128 == 0 for W8A8), n % 256 == 0, m >= 1; x, w and out 16-byte aligned; w below 2^31 bytes and
+ * 256 k below 2^31 bytes of x, else MH3_ERR_UNSUPPORTED. */
+enum { MH3_GEMM_W8A16 = 0, MH3_GEMM_BF16 = 1, MH3_GEMM_W8A8 = 2 };
+int mh3_gemm(const MH3GemmArgs* args, uint32_t form, const void* x, const float* x_scale, const void* w,
+             const float* w_scale, uint16_t* out, mh3_stream_t stream);
+int mh3_gemm_gate_add(const MH3GemmArgs* args, uint32_t form, const void* x, const float* x_scale, const void* w,
+                      const float* w_scale, const float* gate, const uint8_t* set_of_row, uint16_t* residual,
+                      mh3_stream_t stream);
 
 #ifdef __cplusplus
 }

@@ -248,7 +248,7 @@ public:
     void fc1_swiglu_i8(uint32_t m, uint32_t ffn, uint32_t dim, const uint16_t* x, const int8_t* w, const float* scale,
                        uint16_t* out) const
     {
-        const MH3GemmArgs a{m, ffn, dim, 0};
+        const MH3GemmArgs a{m, ffn, dim, 0, 0, 0};
         check(mh3_gemm_w8a16_swiglu(&a, x, w, scale, out, s_), "gemm_i8+swiglu_rows");
     }
 
@@ -256,15 +256,33 @@ public:
     void fc1_swiglu_bf16(uint32_t m, uint32_t ffn, uint32_t dim, const uint16_t* x, const uint16_t* w,
                          uint16_t* out) const
     {
-        const MH3GemmArgs a{m, ffn, dim, 0};
+        const MH3GemmArgs a{m, ffn, dim, 0, 0, 0};
         check(mh3_gemm_bf16_swiglu(&a, x, w, out, s_), "Gemm::encode+swiglu_rows");
     }
     // The reference's own --int8 fc1: x quantized per row (quant_rows_i8), W8A8 gemm_i8 and SwiGLU
     void fc1_swiglu_w8a8(uint32_t m, uint32_t ffn, uint32_t dim, const int8_t* xq, const float* x_scale,
                          const int8_t* w, const float* w_scale, uint16_t* out) const
     {
-        const MH3GemmArgs a{m, ffn, dim, 0};
+        const MH3GemmArgs a{m, ffn, dim, 0, 0, 0};
         check(mh3_gemm_i8_swiglu(&a, xq, x_scale, w, w_scale, out, s_), "gemm_i8+swiglu_rows");
+    }
+
+    // The qkv projection (Gemm::encode, or gemm_i8 under --int8): out[m][n] = x w^T, w [n][k]. form: MH3_GEMM_BF16
+    // (no scales), MH3_GEMM_W8A16 (int8 w with w_scale), MH3_GEMM_W8A8 (int8 x with x_scale, int8 w with w_scale).
+    void gemm(uint32_t m, uint32_t n, uint32_t k, uint32_t form, const void* x, const float* x_scale, const void* w,
+              const float* w_scale, uint16_t* out) const
+    {
+        const MH3GemmArgs a{m, n, k, 0, 0, 0};
+        check(mh3_gemm(&a, form, x, x_scale, w, w_scale, out, s_), form == MH3_GEMM_BF16 ? "Gemm::encode" : "gemm_i8");
+    }
+    // The out projection and fc2 with gate_add_rows folded in: residual += gate[s] * (x w^T), in place; the gate,
+    // its sets and set stride come from m (its norm fields are not used).
+    void gemm_gate_add(uint32_t rows, uint32_t n, uint32_t k, uint32_t form, const void* x, const float* x_scale,
+                       const void* w, const float* w_scale, const Modulation& m, uint16_t* residual) const
+    {
+        const MH3GemmArgs a{rows, n, k, m.n_sets, m.set_stride, 0};
+        check(mh3_gemm_gate_add(&a, form, x, x_scale, w, w_scale, m.gate, m.set_of_row, residual, s_),
+              form == MH3_GEMM_BF16 ? "Gemm::encode+gate_add_rows" : "gemm_i8+gate_add_rows");
     }
 
 private:

@@ -104,6 +104,21 @@ __device__ __forceinline__ void lds_barrier()
 // The three fc1 forms: int8 weights widened to bf16 with bf16 activations (weight-only), bf16 weights, and int8
 // weights with int8 activations (each row of x with its own scale) on the int8 MFMA.
 enum GemmMode { kW8A16 = 0, kBf16 = 1, kW8A8 = 2 };
+// What the epilogue does with y = x w^T (scaled):
+//   kSwiGLU:  out[m][N] = silu(y gate column) * y up column; w holds N gate rows then N up rows (fc1);
+//   kStore:   out[m][N] = y; w holds N rows (the qkv projection);
+//   kGateAdd: out[m][N] += gate[set(row)] * y, in place on the bf16 residual (the out projection and fc2, with the
+//             reference's gate_add_rows folded in).
+// With kSwiGLU a tile's 256 weight rows are 128 gate rows from n0 and the 128 matching up rows from N + n0; otherwise
+// they are 256 consecutive rows, so both halves of the wave's accumulators are output columns.
+enum GemmEpi { kSwiGLU = 0, kStore = 1, kGateAdd = 2 };
+
+// The epilogue's extra operands (kGateAdd): gate vectors [n_sets][gate_stride] floats, a set per row (NULL: set 0).
+struct GemmGate {
+    const float* gate;
+    const uint8_t* set_of_row;
+    uint32_t gate_stride, n_sets;
+};
 
 typedef int int32x4 __attribute__((ext_vector_type(4)));
 typedef int int32x16 __attribute__((ext_vector_type(16)));
@@ -111,11 +126,11 @@ typedef int int32x16 __attribute__((ext_vector_type(16)));
 // WM x WN wavefronts: wave (wm, wn) computes rows wm * (256 / WM) ... of the tile against its TN gate column tiles
 // (32 columns each, from wn * 32 TN) and the TN matching up column tiles. Every LDS row holds 128 bytes of k: 64 k of
 // bf16 or 128 k of int8, so a K-step is 64 or 128 k.
-template <int WM, int WN, int MODE>
-__global__ __launch_bounds__(MH3_GEMM_WM * MH3_GEMM_WN * 64) void gemm_swiglu_kernel(
+template <int WM, int WN, int MODE, int EPI>
+__global__ __launch_bounds__(MH3_GEMM_WM * MH3_GEMM_WN * 64) void gemm_kernel(
     const void* __restrict__ xv, const void* __restrict__ wv, const float* __restrict__ scale,
     const float* __restrict__ xscale, uint16_t* __restrict__ out, uint32_t M, uint32_t N, uint32_t K, uint32_t mt,
-    uint32_t nt)
+    uint32_t nt, GemmGate gg)
 {
     constexpr bool I8 = MODE == kW8A16;                   // B through registers, widened
     constexpr uint32_t kEA = MODE == kW8A8 ? 1u : 2u;     // bytes of an x element
@@ -127,7 +142,11 @@ __global__ __launch_bounds__(MH3_GEMM_WM * MH3_GEMM_WN * 64) void gemm_swiglu_ke
     extern __shared__ u32x4_t smem[];
     uint32_t tm, tn;
     tile_of(mt, nt, tm, tn);
-    const uint32_t m0 = tm * kBM, n0 = tn * kBN;
+    const uint32_t m0 = tm * kBM;
+    // The tile's two 128-row halves of w (and the output columns they give): gate and up rows, or consecutive rows.
+    const uint32_t w_lo = EPI == kSwiGLU ? tn * kBN : tn * 2u * kBN;
+    const uint32_t w_hi = EPI == kSwiGLU ? N + w_lo : w_lo + kBN;
+    const uint32_t w_rows = EPI == kSwiGLU ? 2u * N : N;
     const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6, wm = wave / WN, wn = wave % WN;
     const uint32_t KT = K / kKS;
 
@@ -159,13 +178,13 @@ __global__ __launch_bounds__(MH3_GEMM_WM * MH3_GEMM_WN * 64) void gemm_swiglu_ke
     // Each 8 consecutive lanes thus write two rows whose swizzles differ in parity, i.e. 8 distinct chunk columns.
     constexpr int BI = int(1024 / kThreads);
     // N * K < 2^30 (int8) or 2^29 (bf16) is checked on the host.
-    const __amdgpu_buffer_rsrc_t rw = buffer_rsrc(wv, uint32_t(2u * N * K * kEB));
+    const __amdgpu_buffer_rsrc_t rw = buffer_rsrc(wv, uint32_t(w_rows * K * kEB));
     uint32_t b_src[BI], b_lo[BI], b_hi[BI];
 #pragma unroll
     for (int i = 0; i < BI && I8; ++i) {
         const uint32_t q = tid + kThreads * uint32_t(i), kc = q & 3u, G = q >> 3;
         const uint32_t brow = 4u * (G >> 1) + 2u * ((q >> 2) & 1u) + (G & 1u);
-        const uint32_t wrow = brow < kBN ? n0 + brow : N + n0 + (brow - kBN);
+        const uint32_t wrow = brow < kBN ? w_lo + brow : w_hi + (brow - kBN);
         const uint32_t sx = (brow >> 1) & 7u;
         b_src[i] = wrow * K + kc * 16u;
         b_lo[i] = brow * 128u + ((2u * kc) ^ sx) * 16u;
@@ -196,7 +215,7 @@ __global__ __launch_bounds__(MH3_GEMM_WM * MH3_GEMM_WN * 64) void gemm_swiglu_ke
     for (int i = 0; i < AI && !I8; ++i) {
         const uint32_t row = (wave * AI + uint32_t(i)) * 8u + (lane >> 3);
         const uint32_t c = (lane & 7u) ^ ((row >> 1) & 7u);
-        const uint32_t wrow = row < kBN ? n0 + row : N + n0 + (row - kBN);
+        const uint32_t wrow = row < kBN ? w_lo + row : w_hi + (row - kBN);
         bd_off[i] = wrow * K * kEB + c * 16u;
     }
     auto b_dma = [&](uint32_t kt) {
@@ -286,7 +305,7 @@ __global__ __launch_bounds__(MH3_GEMM_WM * MH3_GEMM_WN * 64) void gemm_swiglu_ke
     }
     // The epilogue's kernel arguments are read here, before the barrier: a scalar load still in flight at the loop
     // would turn every LDS wait in it into a full wait (scalar loads complete out of order).
-    asm volatile("" ::"s"(scale), "s"(xscale), "s"(out));
+    asm volatile("" ::"s"(scale), "s"(xscale), "s"(out), "s"(gg.gate), "s"(gg.set_of_row));
     lds_barrier();
     bf16x8_t fa[2][TM], fb[2][2 * TN];
     frags(0, 0, fa[0], fb[0]);
@@ -348,12 +367,14 @@ __global__ __launch_bounds__(MH3_GEMM_WM * MH3_GEMM_WN * 64) void gemm_swiglu_ke
         kstep(kt, std::false_type{});
     kstep(KT - 1, std::true_type{});
 
-    // Epilogue: acc[a][b][e] is y[row][col] with row = m0 + wm (256 / WM) + a 32 + 8 (e / 4) + 4 (lane / 32) + e % 4
-    // and col = lane % 32 + 32 b within the wave's gate columns (b < TN; acc[a][TN + b] holds the matching up column).
+    // Epilogue: acc[a][b][e] is y[row][c] with row = m0 + wm (256 / WM) + a 32 + 8 (e / 4) + 4 (lane / 32) + e % 4
+    // and c = lane % 32 + 32 b + wn 32 TN within the tile's first half of w rows (b < TN) or, for acc[a][TN + b], the
+    // same position in its second half.
 #pragma unroll
     for (int b = 0; b < TN; ++b) {
-        const uint32_t col = n0 + wn * 32u * TN + uint32_t(b) * 32u + r32;
-        const float sg = MODE != kBf16 ? scale[col] : 1.0f, su = MODE != kBf16 ? scale[N + col] : 1.0f;
+        const uint32_t c = wn * 32u * TN + uint32_t(b) * 32u + r32;
+        const uint32_t c_lo = w_lo + c, c_hi = w_hi + c; // w rows = output columns (kStore, kGateAdd)
+        const float s_lo = MODE != kBf16 ? scale[c_lo] : 1.0f, s_hi = MODE != kBf16 ? scale[c_hi] : 1.0f;
 #pragma unroll
         for (int a = 0; a < TM; ++a) {
 #pragma unroll
@@ -362,9 +383,22 @@ __global__ __launch_bounds__(MH3_GEMM_WM * MH3_GEMM_WN * 64) void gemm_swiglu_ke
                                      (uint32_t(e) & 3u);
                 if (row < M) {
                     const float sx = MODE == kW8A8 ? xscale[row] : 1.0f;
-                    const float g = float(acc[a][b][e]) * sg * sx, u = float(acc[a][TN + b][e]) * su * sx;
-                    const float o = g * __builtin_amdgcn_rcpf(1.0f + __expf(-g)) * u;
-                    out[uint64_t(row) * N + col] = __builtin_bit_cast(uint16_t, __bf16(o));
+                    const float lo = float(acc[a][b][e]) * s_lo * sx, hi = float(acc[a][TN + b][e]) * s_hi * sx;
+                    uint16_t* orow = out + uint64_t(row) * N;
+                    if constexpr (EPI == kSwiGLU) {
+                        const float o = lo * __builtin_amdgcn_rcpf(1.0f + __expf(-lo)) * hi;
+                        orow[c_lo] = __builtin_bit_cast(uint16_t, __bf16(o));
+                    } else if constexpr (EPI == kStore) {
+                        orow[c_lo] = __builtin_bit_cast(uint16_t, __bf16(lo));
+                        orow[c_hi] = __builtin_bit_cast(uint16_t, __bf16(hi));
+                    } else {
+                        const uint32_t set = gg.set_of_row ? min(uint32_t(gg.set_of_row[row]), gg.n_sets - 1u) : 0u;
+                        const float* g = gg.gate + uint64_t(set) * gg.gate_stride;
+                        const float r_lo = __uint_as_float(uint32_t(orow[c_lo]) << 16);
+                        const float r_hi = __uint_as_float(uint32_t(orow[c_hi]) << 16);
+                        orow[c_lo] = __builtin_bit_cast(uint16_t, __bf16(fmaf(g[c_lo], lo, r_lo)));
+                        orow[c_hi] = __builtin_bit_cast(uint16_t, __bf16(fmaf(g[c_hi], hi, r_hi)));
+                    }
                 }
             }
         }
@@ -375,37 +409,68 @@ __global__ __launch_bounds__(MH3_GEMM_WM * MH3_GEMM_WN * 64) void gemm_swiglu_ke
 
 namespace {
 
-// Shared checks and launch of the three forms.
-template <int MODE>
+// Shared checks and launch of the three forms and three epilogues.
+template <int MODE, int EPI>
 int launch_gemm(const MH3GemmArgs* a, const void* x, const void* w, const float* scale, const float* xscale,
-                uint16_t* out, mh3_stream_t stream)
+                uint16_t* out, const mh3::GemmGate& gg, mh3_stream_t stream)
 {
     using namespace mh3;
     constexpr uint32_t kEA = MODE == kW8A8 ? 1u : 2u, kEB = MODE == kBf16 ? 2u : 1u, kKS = 128u / kEA;
+    constexpr uint32_t kCols = EPI == kSwiGLU ? kBN : 2u * kBN; // output columns a tile
     if (!a)
         return MH3_ERR_POINTER;
-    if (a->m == 0 || a->k == 0 || a->n == 0 || a->k % kKS != 0 || a->n % kBN != 0)
+    if (a->m == 0 || a->k == 0 || a->n == 0 || a->k % kKS != 0 || a->n % kCols != 0)
         return MH3_ERR_SHAPE;
-    if (a->m >= (1u << 31) || uint64_t(a->n) * 2u >= (uint64_t(1) << 31))
+    const uint64_t w_rows = EPI == kSwiGLU ? 2ull * a->n : a->n;
+    if (a->m >= (1u << 31) || w_rows >= (uint64_t(1) << 31))
         return MH3_ERR_SHAPE;
-    if (uint64_t(a->k) * kBM * kEA >= (uint64_t(1) << 31) || uint64_t(a->n) * a->k * 2u * kEB >= (uint64_t(1) << 31))
+    if (uint64_t(a->k) * kBM * kEA >= (uint64_t(1) << 31) || w_rows * a->k * kEB >= (uint64_t(1) << 31))
         return MH3_ERR_UNSUPPORTED; // 32-bit buffer offsets: a tile's A rows, and all of w
     if (!x || !w || (MODE != kBf16 && !scale) || (MODE == kW8A8 && !xscale) || !out)
         return MH3_ERR_POINTER;
+    if (EPI == kGateAdd && (!gg.gate || gg.n_sets == 0 || gg.n_sets > 256 || gg.gate_stride < a->n))
+        return gg.gate ? MH3_ERR_PARAM : MH3_ERR_POINTER;
     if (!host::aligned16(x) || !host::aligned16(w) || !host::aligned16(out))
         return MH3_ERR_ALIGN;
     constexpr int WM = MH3_GEMM_WM, WN = MH3_GEMM_WN;
-    const void* kernel = reinterpret_cast<const void*>(&gemm_swiglu_kernel<WM, WN, MODE>);
+    const void* kernel = reinterpret_cast<const void*>(&gemm_kernel<WM, WN, MODE, EPI>);
     static const int lds_ok = hipFuncSetAttribute(kernel, hipFuncAttributeMaxDynamicSharedMemorySize, int(kGemmLds));
     if (lds_ok != hipSuccess)
         return MH3_ERR_HIP;
-    const uint32_t mt = (a->m + kBM - 1) / kBM, nt = a->n / kBN;
+    const uint32_t mt = (a->m + kBM - 1) / kBM, nt = a->n / kCols;
     const uint64_t tiles = uint64_t(mt) * nt;
     if (tiles >= (uint64_t(1) << 31))
         return MH3_ERR_SHAPE;
-    hipLaunchKernelGGL((gemm_swiglu_kernel<WM, WN, MODE>), dim3(uint32_t(tiles)), dim3(WM * WN * 64), kGemmLds,
-                       static_cast<hipStream_t>(stream), x, w, scale, xscale, out, a->m, a->n, a->k, mt, nt);
+    hipLaunchKernelGGL((gemm_kernel<WM, WN, MODE, EPI>), dim3(uint32_t(tiles)), dim3(WM * WN * 64), kGemmLds,
+                       static_cast<hipStream_t>(stream), x, w, scale, xscale, out, a->m, a->n, a->k, mt, nt, gg);
     return host::check_launch();
+}
+
+const mh3::GemmGate kNoGate{nullptr, nullptr, 0, 0};
+
+// The gate-add epilogue's operands from the C-ABI's arguments.
+mh3::GemmGate gate_of(const MH3GemmArgs* a, const float* gate, const uint8_t* set_of_row)
+{
+    const uint32_t n_sets = a && a->n_sets ? a->n_sets : 1u;
+    const uint32_t stride = a && a->gate_stride ? a->gate_stride : (a ? a->n : 0u);
+    return mh3::GemmGate{gate, set_of_row, stride, n_sets};
+}
+
+// The three weight forms of one epilogue, by the C-ABI's weight dtype.
+template <int EPI>
+int launch_by_form(const MH3GemmArgs* a, uint32_t form, const void* x, const float* x_scale, const void* w,
+                   const float* w_scale, uint16_t* out, const mh3::GemmGate& gg, mh3_stream_t stream)
+{
+    switch (form) {
+    case MH3_GEMM_W8A16:
+        return launch_gemm<mh3::kW8A16, EPI>(a, x, w, w_scale, nullptr, out, gg, stream);
+    case MH3_GEMM_BF16:
+        return launch_gemm<mh3::kBf16, EPI>(a, x, w, nullptr, nullptr, out, gg, stream);
+    case MH3_GEMM_W8A8:
+        return launch_gemm<mh3::kW8A8, EPI>(a, x, w, w_scale, x_scale, out, gg, stream);
+    default:
+        return MH3_ERR_PARAM;
+    }
 }
 
 } // namespace
@@ -413,17 +478,31 @@ int launch_gemm(const MH3GemmArgs* a, const void* x, const void* w, const float*
 extern "C" int mh3_gemm_w8a16_swiglu(const MH3GemmArgs* a, const uint16_t* x, const int8_t* w, const float* scale,
                                      uint16_t* out, mh3_stream_t stream)
 {
-    return launch_gemm<mh3::kW8A16>(a, x, w, scale, nullptr, out, stream);
+    return launch_gemm<mh3::kW8A16, mh3::kSwiGLU>(a, x, w, scale, nullptr, out, kNoGate, stream);
 }
 
 extern "C" int mh3_gemm_bf16_swiglu(const MH3GemmArgs* a, const uint16_t* x, const uint16_t* w, uint16_t* out,
                                     mh3_stream_t stream)
 {
-    return launch_gemm<mh3::kBf16>(a, x, w, nullptr, nullptr, out, stream);
+    return launch_gemm<mh3::kBf16, mh3::kSwiGLU>(a, x, w, nullptr, nullptr, out, kNoGate, stream);
 }
 
 extern "C" int mh3_gemm_i8_swiglu(const MH3GemmArgs* a, const int8_t* x, const float* x_scale, const int8_t* w,
                                   const float* w_scale, uint16_t* out, mh3_stream_t stream)
 {
-    return launch_gemm<mh3::kW8A8>(a, x, w, w_scale, x_scale, out, stream);
+    return launch_gemm<mh3::kW8A8, mh3::kSwiGLU>(a, x, w, w_scale, x_scale, out, kNoGate, stream);
+}
+
+extern "C" int mh3_gemm(const MH3GemmArgs* a, uint32_t form, const void* x, const float* x_scale, const void* w,
+                        const float* w_scale, uint16_t* out, mh3_stream_t stream)
+{
+    return launch_by_form<mh3::kStore>(a, form, x, x_scale, w, w_scale, out, kNoGate, stream);
+}
+
+extern "C" int mh3_gemm_gate_add(const MH3GemmArgs* a, uint32_t form, const void* x, const float* x_scale,
+                                 const void* w, const float* w_scale, const float* gate, const uint8_t* set_of_row,
+                                 uint16_t* residual, mh3_stream_t stream)
+{
+    return launch_by_form<mh3::kGateAdd>(a, form, x, x_scale, w, w_scale, residual, gate_of(a, gate, set_of_row),
+                                         stream);
 }

@@ -23,6 +23,7 @@ _LIB_PATH = Path(os.environ.get("MAKO_H3_LIB", Path(__file__).resolve().parent.p
 OK, ERR_SHAPE, ERR_POINTER, ERR_ALIGN, ERR_PARAM, ERR_HIP, ERR_UNSUPPORTED = 0, -1, -2, -3, -4, -5, -6
 F32, BF16 = 0, 1
 SWIGLU_SPLIT, SWIGLU_FUSED = 0, 1
+GEMM_W8A16, GEMM_BF16, GEMM_W8A8 = 0, 1, 2
 CUBES_GRID, CUBES_GATHERED = 0, 1
 INT8_QKV, INT8_OUT, INT8_FC1, INT8_FC2, INT8_ALL = 1, 2, 4, 8, 15
 
@@ -58,7 +59,8 @@ class QuantArgs(C.Structure):
 
 
 class GemmArgs(C.Structure):
-    _fields_ = [("m", C.c_uint32), ("n", C.c_uint32), ("k", C.c_uint32), ("reserved", C.c_uint32)]
+    _fields_ = [("m", C.c_uint32), ("n", C.c_uint32), ("k", C.c_uint32), ("n_sets", C.c_uint32),
+                ("gate_stride", C.c_uint32), ("reserved", C.c_uint32)]
 
 
 def _load() -> C.CDLL:
@@ -89,6 +91,8 @@ def _load() -> C.CDLL:
         "mh3_gemm_w8a16_swiglu": (I32, [C.POINTER(GemmArgs), P, P, P, P, P]),
         "mh3_gemm_bf16_swiglu": (I32, [C.POINTER(GemmArgs), P, P, P, P]),
         "mh3_gemm_i8_swiglu": (I32, [C.POINTER(GemmArgs), P, P, P, P, P, P]),
+        "mh3_gemm": (I32, [C.POINTER(GemmArgs), U32, P, P, P, P, P, P]),
+        "mh3_gemm_gate_add": (I32, [C.POINTER(GemmArgs), U32, P, P, P, P, P, P, P, P]),
     }
     for name, (res, args) in sig.items():
         f = getattr(lib, name)
@@ -495,3 +499,57 @@ def gemm_i8_swiglu(x, x_scale, w, w_scale, *, out=None):
     _check(lib.mh3_gemm_i8_swiglu(C.byref(a), _ptr(x), _ptr(x_scale), _ptr(w), _ptr(w_scale), _ptr(out), _stream()),
            "gemm_i8_swiglu")
     return out
+
+
+# ---- the qkv, out and fc2 projections -------------------------------------------------------------------------------
+
+def _gemm_operands(x, w, x_scale, w_scale):
+    """The form of a projection from its operand dtypes: bf16 x and w, bf16 x with int8 w (weight-only, w_scale), or
+    int8 x (x_scale) with int8 w (w_scale)."""
+    if x.dim() != 2 or w.dim() != 2 or w.shape[1] != x.shape[1]:
+        raise ValueError("x must be [m][k] and w [n][k]")
+    m, k = x.shape
+    n = w.shape[0]
+    if x.dtype == torch.bfloat16 and w.dtype == torch.bfloat16:
+        form = GEMM_BF16
+    elif x.dtype == torch.bfloat16 and w.dtype == torch.int8:
+        form = GEMM_W8A16
+    elif x.dtype == torch.int8 and w.dtype == torch.int8:
+        form = GEMM_W8A8
+    else:
+        raise ValueError(f"unsupported operand dtypes {x.dtype} x {w.dtype}")
+    _need(x, "x", x.dtype, m * k)
+    _need(w, "w", w.dtype, n * k)
+    if form != GEMM_BF16:
+        _need(w_scale, "w_scale", torch.float32, n)
+    if form == GEMM_W8A8:
+        _need(x_scale, "x_scale", torch.float32, m)
+    a = GemmArgs()
+    a.m, a.n, a.k = m, n, k
+    return a, form
+
+
+def gemm(x, w, *, x_scale=None, w_scale=None, out=None):
+    """The qkv projection (the reference's Gemm::encode, or gemm_i8 under --int8): out = x w^T, bf16 [m][n], with w
+    [n][k] output-channel rows; int8 w takes w_scale f32 [n], int8 x (quant_rows_i8) takes x_scale f32 [m]."""
+    a, form = _gemm_operands(x, w, x_scale, w_scale)
+    out = torch.empty((a.m, a.n), dtype=torch.bfloat16, device=x.device) if out is None else out
+    _need(out, "out", torch.bfloat16, a.m * a.n)
+    _check(lib.mh3_gemm(C.byref(a), form, _ptr(x), _ptr(x_scale if form == GEMM_W8A8 else None), _ptr(w),
+                        _ptr(w_scale if form != GEMM_BF16 else None), _ptr(out), _stream()), "gemm")
+    return out
+
+
+def gemm_gate_add(x, w, residual, gate, *, x_scale=None, w_scale=None, set_of_row=None, n_sets=1):
+    """The out projection and fc2 with gate_add_rows folded in: residual += gate[s] * (x w^T), bf16 [m][n] in place,
+    s = set_of_row[row]; gate f32 [n_sets][n] (or a view with a set stride). Returns residual."""
+    a, form = _gemm_operands(x, w, x_scale, w_scale)
+    _need(residual, "residual", torch.bfloat16, a.m * a.n)
+    stride = _set_stride(gate, "gate", a.n, n_sets)
+    a.n_sets, a.gate_stride = n_sets, stride
+    if set_of_row is not None:
+        _need(set_of_row, "set_of_row", torch.uint8, a.m)
+    _check(lib.mh3_gemm_gate_add(C.byref(a), form, _ptr(x), _ptr(x_scale if form == GEMM_W8A8 else None), _ptr(w),
+                                 _ptr(w_scale if form != GEMM_BF16 else None), _ptr(gate), _ptr(set_of_row),
+                                 _ptr(residual), _stream()), "gemm_gate_add")
+    return residual

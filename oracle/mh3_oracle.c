@@ -498,6 +498,44 @@ void mh3o_gemm_i8_swiglu(uint32_t m, uint32_t n, uint32_t k, const int8_t* x, co
     }
 }
 
+/* The qkv, out and fc2 projections (docs/performance.md:40-43,52-69,120-133; docs/architecture.md:61-66): y = x w^T
+ * with w [n][k] in one of three forms (form 0: x bf16, w int8 with w_scale; 1: both bf16; 2: x int8 with x_scale, w
+ * int8 with w_scale), exact products summed in double (int64 for the int8 pair). epi 0: out = y (bf16); epi 1:
+ * out += gate[s][col] * y with s = set_of_row[row] (NULL: 0), out bf16 in place, one rounding. */
+void mh3o_gemm(uint32_t m, uint32_t n, uint32_t k, int form, int epi, const void* x, const float* x_scale,
+               const void* w, const float* w_scale, const float* gate, const uint8_t* set_of_row, uint32_t gate_stride,
+               uint16_t* out)
+{
+    double* xr = (double*)malloc(sizeof(double) * k);
+    for (uint64_t r = 0; r < m; ++r) {
+        for (uint32_t i = 0; i < k; ++i)
+            xr[i] = form == 2 ? (double)((const int8_t*)x)[r * k + i]
+                              : (double)mh3o_bf16_to_float(((const uint16_t*)x)[r * k + i]);
+        const uint64_t set = set_of_row ? set_of_row[r] : 0;
+        for (uint64_t c = 0; c < n; ++c) {
+            double y = 0;
+            if (form == 2) {
+                int64_t acc = 0;
+                for (uint32_t i = 0; i < k; ++i)
+                    acc += (int64_t)xr[i] * ((const int8_t*)w)[c * k + i];
+                y = (double)acc * (double)x_scale[r] * (double)w_scale[c];
+            } else {
+                for (uint32_t i = 0; i < k; ++i)
+                    y += xr[i] * (form == 0 ? (double)((const int8_t*)w)[c * k + i]
+                                            : (double)mh3o_bf16_to_float(((const uint16_t*)w)[c * k + i]));
+                if (form == 0)
+                    y *= (double)w_scale[c];
+            }
+            uint16_t* o = out + r * n + c;
+            if (epi == 0)
+                *o = mh3o_bf16_from_double(y);
+            else
+                *o = mh3o_bf16_from_double((double)mh3o_bf16_to_float(*o) + (double)gate[set * gate_stride + c] * y);
+        }
+    }
+    free(xr);
+}
+
 /* ---- flash_attn_sparse_128 -------------------------------------------------------------------------------------- */
 
 /* Row of slot l (0..63) of attention tile `tile`: tiles 0 .. nd-1 are the dense rows in runs of 64 (row

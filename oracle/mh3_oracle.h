@@ -11,6 +11,7 @@
  *   cube_pool / _scores / _topk     docs/architecture.md:118-133, README.md:81-87, docs/performance.md:175-181
  *   heads_partial                   docs/architecture.md:35-38,61-63,123-125
  *   quant_rows_i8, W8A16 fc1        docs/performance.md:120-136
+ *   qkv / out / fc2 GEMMs           docs/performance.md:40-43,52-69,120-133, docs/architecture.md:61-66
  * bf16 results are rounded to nearest even exactly once, from the double value.
  *
  * How each function is pinned (tests/test_oracle.py): no reference vector exists for any of them (the reference
@@ -36,6 +37,9 @@
  *   mh3o_gemm_w8a16_swiglu     torch.matmul in float64; exact integer results for w in {-1,0,1}, s = 1
  *   mh3o_gemm_bf16_swiglu      torch.matmul in float64; exact integer results for w in {-1,0,1}
  *   mh3o_gemm_i8_swiglu        torch.matmul of the int64 operands; exact integer results with unit scales
+ *   mh3o_gemm                  torch.matmul in float64 for each form; the gate-add epilogue against gate_add_rows of
+ *                              the rounded product (within one bf16 rounding); gate 0 leaves the residual bit-exact;
+ *                              exact integer results for w in {-1,0,1}
  *   (the order in which gemm_i8's epilogue applies the two scales is not documented: parity unpinned for it)
  */
 #ifndef MH3_ORACLE_H
@@ -110,6 +114,11 @@ void mh3o_gemm_bf16_swiglu(uint32_t m, uint32_t n, uint32_t k, const uint16_t* x
  * with a scale per row; exact integer sums, then y = sum * x_scale[r] * w_scale[c] in double. */
 void mh3o_gemm_i8_swiglu(uint32_t m, uint32_t n, uint32_t k, const int8_t* x, const float* x_scale, const int8_t* w,
                          const float* w_scale, uint16_t* out);
+/* The qkv / out / fc2 projections: y = x w^T, w [n][k]; form 0 W8A16 (w int8 + w_scale), 1 bf16, 2 W8A8 (x int8 +
+ * x_scale, w int8 + w_scale). epi 0: out = y; epi 1: out += gate[set][col] * y in place (the gate_add_rows epilogue). */
+void mh3o_gemm(uint32_t m, uint32_t n, uint32_t k, int form, int epi, const void* x, const float* x_scale,
+               const void* w, const float* w_scale, const float* gate, const uint8_t* set_of_row, uint32_t gate_stride,
+               uint16_t* out);
 
 #ifdef __cplusplus
 }

@@ -58,6 +58,7 @@ _lib.mh3o_quant_rows_i8.argtypes = [C.c_uint32, C.c_uint32, C.c_int] + [_P] * 3
 _lib.mh3o_gemm_w8a16_swiglu.argtypes = [C.c_uint32] * 3 + [_P] * 4
 _lib.mh3o_gemm_bf16_swiglu.argtypes = [C.c_uint32] * 3 + [_P] * 3
 _lib.mh3o_gemm_i8_swiglu.argtypes = [C.c_uint32] * 3 + [_P] * 5
+_lib.mh3o_gemm.argtypes = [C.c_uint32] * 3 + [C.c_int] * 2 + [_P] * 6 + [C.c_uint32, _P]
 _lib.mh3o_bf16_to_float_n.argtypes = [_P, _P, C.c_uint64]
 _lib.mh3o_bf16_from_double_n.argtypes = [_P, _P, C.c_uint64]
 
@@ -241,6 +242,34 @@ def gemm_w8a16_swiglu(x, w, scale):
     out = np.empty((m, n), np.uint16)
     _lib.mh3o_gemm_w8a16_swiglu(m, n, k, _p(np.ascontiguousarray(x)), _p(np.ascontiguousarray(w)),
                                 _p(np.ascontiguousarray(scale)), _p(out))
+    return out
+
+
+GEMM_W8A16, GEMM_BF16, GEMM_W8A8 = 0, 1, 2
+
+
+def gemm(x, w, form, x_scale=None, w_scale=None):
+    """y = x w^T rounded to bf16 bits [m][n]: form GEMM_W8A16 (x bf16 bits, w int8, w_scale), GEMM_BF16 (both bf16
+    bits) or GEMM_W8A8 (x int8 with x_scale, w int8 with w_scale)."""
+    m, k = x.shape
+    n = w.shape[0]
+    out = np.empty((m, n), np.uint16)
+    c = np.ascontiguousarray
+    _lib.mh3o_gemm(m, n, k, form, 0, _p(c(x)), _p(None if x_scale is None else c(x_scale, dtype=np.float32)),
+                   _p(c(w)), _p(None if w_scale is None else c(w_scale, dtype=np.float32)), None, None, 0, _p(out))
+    return out
+
+
+def gemm_gate_add(x, w, form, residual, gate, x_scale=None, w_scale=None, set_of_row=None):
+    """residual + gate[set(row)] * (x w^T), one rounding to bf16 bits; gate f32 [n_sets][n] (or [n])."""
+    m, k = x.shape
+    n = w.shape[0]
+    out = np.array(residual, dtype=np.uint16, copy=True, order="C")
+    c = np.ascontiguousarray
+    g = c(gate, dtype=np.float32).reshape(-1, n)
+    _lib.mh3o_gemm(m, n, k, form, 1, _p(c(x)), _p(None if x_scale is None else c(x_scale, dtype=np.float32)),
+                   _p(c(w)), _p(None if w_scale is None else c(w_scale, dtype=np.float32)), _p(g),
+                   _p(None if set_of_row is None else c(set_of_row, dtype=np.uint8)), n, _p(out))
     return out
 
 

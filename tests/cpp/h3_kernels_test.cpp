@@ -2,7 +2,7 @@
 // (oracle/mh3_oracle.h, the checker), reported the way the reference's tests/h3_ref_test.cpp reports: one line per
 // check, "ok" or "FAIL", the relative RMS error and the lowest row cosine of diff() (h3_ref_test.cpp:67-90), and
 // the number of failures as the exit status.
-//   h3_kernels_test [rows | swiglu | cubes | attn | int8 | errors | all]
+//   h3_kernels_test [rows | swiglu | cubes | attn | int8 | proj | errors | all]
 #include "mako_h3.hpp"
 #include "mh3_oracle.h"
 
@@ -335,6 +335,53 @@ void int8()
     compare("fc1 W8A8 gemm_i8 + swiglu 300x384 -> 384", of_bf16(out.download()), of_bf16(want), n, 1e-2, 1e-4);
 }
 
+// The qkv projection (plain store) and the out / fc2 projections with the gate-add epilogue, one operand form each.
+void proj()
+{
+    std::printf("proj\n");
+    Rng r(5);
+    const uint32_t m = 300, n = 512, k = 384, sets = 3;
+    auto x = bf16_normals(r, size_t(m) * k);
+    std::vector<uint16_t> wb(size_t(n) * k);
+    for (auto& v : wb)
+        v = mh3o_bf16_from_double(0.02 * r.normal());
+    std::vector<int8_t> w8(size_t(n) * k), x8(size_t(m) * k);
+    for (auto& v : w8)
+        v = int8_t(int(r.next() % 255) - 127);
+    for (auto& v : x8)
+        v = int8_t(int(r.next() % 255) - 127);
+    std::vector<float> ws(n), xs(m);
+    for (auto& v : ws)
+        v = float(0.5e-3 + 1.5e-3 * r.uniform());
+    for (auto& v : xs)
+        v = float(0.5e-2 + 1.5e-2 * r.uniform());
+    auto gate = normals(r, sets * n, 0.5);
+    std::vector<uint8_t> set(m);
+    for (auto& v : set)
+        v = uint8_t(r.next() % sets);
+    auto res = bf16_normals(r, size_t(m) * n);
+    DeviceBuffer<uint16_t> dx(x), dwb(wb), out(size_t(m) * n), dres1(res), dres2(res);
+    DeviceBuffer<int8_t> dw8(w8), dx8(x8);
+    DeviceBuffer<float> dws(ws), dxs(xs), dgate(gate);
+    DeviceBuffer<uint8_t> dset(set);
+    Kernels kern;
+    Modulation mod;
+    mod.gate = dgate.get(), mod.set_of_row = dset.get(), mod.n_sets = sets;
+    kern.gemm(m, n, k, MH3_GEMM_BF16, dx.get(), nullptr, dwb.get(), nullptr, out.get());
+    kern.gemm_gate_add(m, n, k, MH3_GEMM_W8A16, dx.get(), nullptr, dw8.get(), dws.get(), mod, dres1.get());
+    kern.gemm_gate_add(m, n, k, MH3_GEMM_W8A8, dx8.get(), dxs.get(), dw8.get(), dws.get(), mod, dres2.get());
+    kern.finish();
+    std::vector<uint16_t> want(size_t(m) * n), w1 = res, w2 = res;
+    mh3o_gemm(m, n, k, 1, 0, x.data(), nullptr, wb.data(), nullptr, nullptr, nullptr, 0, want.data());
+    mh3o_gemm(m, n, k, 0, 1, x.data(), nullptr, w8.data(), ws.data(), gate.data(), set.data(), n, w1.data());
+    mh3o_gemm(m, n, k, 2, 1, x8.data(), xs.data(), w8.data(), ws.data(), gate.data(), set.data(), n, w2.data());
+    compare("qkv projection bf16 300x384 -> 512", of_bf16(out.download()), of_bf16(want), n, 1e-2, 1e-3);
+    compare("out / fc2 projection W8A16 + gate_add_rows, 3 sets", of_bf16(dres1.download()), of_bf16(w1), n, 1e-2,
+            2e-2);
+    compare("out / fc2 projection W8A8 + gate_add_rows, 3 sets", of_bf16(dres2.download()), of_bf16(w2), n, 1e-2,
+            2e-2);
+}
+
 void errors()
 {
     std::printf("errors\n");
@@ -380,6 +427,8 @@ int main(int argc, char** argv)
             attn();
         if (mode == "int8" || mode == "all")
             int8();
+        if (mode == "proj" || mode == "all")
+            proj();
         if (mode == "errors" || mode == "all")
             errors();
     } catch (const std::exception& e) {

@@ -41,7 +41,7 @@ def test_stream_probe_library_loads_and_refuses_bad_calls():
 
 
 def test_abi_version_and_strings():
-    assert mh.lib.mh3_abi_version() == 1
+    assert mh.lib.mh3_abi_version() == 2
     assert mh.strerror(mh.ERR_SHAPE) == "bad shape"
     assert mh.strerror(123) == "unknown error"
 
