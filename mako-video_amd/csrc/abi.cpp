@@ -3,6 +3,7 @@
 
 #include <cmath>
 #include <cstring>
+#include <map>
 #include <mutex>
 #include <string>
 
@@ -39,6 +40,23 @@ int cu_count()
         g_cu_count[dev] = n;
     });
     return g_cu_count[dev];
+}
+
+hipError_t allow_dynamic_lds(const void* kernel, size_t bytes)
+{
+    static std::mutex mu;
+    static std::map<std::pair<int, const void*>, size_t> allowed;
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess)
+        dev = -1;
+    std::lock_guard<std::mutex> lock(mu);
+    auto it = allowed.find({dev, kernel});
+    if (it != allowed.end() && it->second >= bytes)
+        return hipSuccess;
+    const hipError_t e = hipFuncSetAttribute(kernel, hipFuncAttributeMaxDynamicSharedMemorySize, int(bytes));
+    if (e == hipSuccess)
+        allowed[{dev, kernel}] = bytes;
+    return e;
 }
 
 int blocks_per_cu(const void* kernel, int block, size_t lds)

@@ -24,6 +24,9 @@ constexpr uint32_t kHeadsThreads = 512;
 constexpr uint32_t kGroups = kHeadsThreads / 16u; // one head vector a 16-lane group
 constexpr int kHeadsU = 4;                        // head vectors a group has in flight
 constexpr uint32_t kSlots = kGroups * kHeadsU;    // head vectors a workgroup pass
+// Dynamic LDS of at least this much, so three workgroups (24 waves, three rows of qkv at 40 heads) share a CU: that
+// streamed 1-3% faster than the 4 to 6 the registers allow, and two or one were slower (at 768p, alternating runs).
+constexpr size_t kHeadsLdsFloor = 41 * 1024;
 
 struct HeadsParams {
     const uint16_t* qkv;
@@ -204,7 +207,11 @@ extern "C" int mh3_heads_partial(const MH3HeadsArgs* args, const uint16_t* qkv, 
     p.div_row = FastDiv::make(p.per_row);
     p.div_heads = FastDiv::make(a.heads);
     const uint64_t blocks = (uint64_t(a.rows) + p.rows_per_block - 1) / p.rows_per_block;
-    const size_t lds = (256u + p.rows_per_block + 2u * size_t(p.rows_per_block) * p.half) * sizeof(float);
+    size_t lds = (256u + p.rows_per_block + 2u * size_t(p.rows_per_block) * p.half) * sizeof(float);
+    if (lds < kHeadsLdsFloor)
+        lds = kHeadsLdsFloor;
+    if (host::allow_dynamic_lds(reinterpret_cast<const void*>(&heads_kernel), lds) != hipSuccess)
+        return MH3_ERR_HIP;
     hipLaunchKernelGGL(heads_kernel, dim3(uint32_t(blocks)), dim3(kHeadsThreads), lds,
                        static_cast<hipStream_t>(stream), p);
     return host::check_launch();

@@ -162,5 +162,7 @@ int cu_count();
 int blocks_per_cu(const void* kernel, int block, size_t lds);
 
 inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+// Lets `kernel` take `bytes` of dynamic LDS on the current device (hipFuncSetAttribute, once per kernel and device).
+hipError_t allow_dynamic_lds(const void* kernel, size_t bytes);
 
 } // namespace mh3::host

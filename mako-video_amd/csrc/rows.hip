@@ -492,6 +492,7 @@ namespace {
 using namespace mh3;
 
 constexpr size_t kCoefLdsMax = 64 * 1024;
+constexpr size_t kWaveLdsFloor = 81 * 1024; // above half of gfx950's 160 KiB: one wave-kernel workgroup a CU
 #ifndef MH3_ROWS_PER_BLOCK
 #define MH3_ROWS_PER_BLOCK 0 // rows a workgroup streams through; 0: as many as keep every CU's slots busy once
 #endif
@@ -547,7 +548,13 @@ int launch_rows_wave(const RowsParams& p, hipStream_t stream)
     else
         k = pick_wave_kernel<DT, 12, OP>(src);
     const uint32_t threads = MH3_WAVE_BLOCK, waves = threads / 64u;
-    const size_t lds = src == kCoefLds ? size_t(p.n_sets) * p.dim * kPlanes<OP> * sizeof(float) : 0;
+    // The dynamic LDS is at least kWaveLdsFloor, so one workgroup (8 waves, 8 rows in flight) holds a CU: fewer rows in
+    // flight streamed faster than the 2 to 4 workgroups the registers would allow (5.96 to 6.04 TB/s against 5.79 to
+    // 5.91 for the fused op at 768p, alternating runs on one GPU), as fewer open streams contend for the DRAM banks.
+    const size_t table = src == kCoefLds ? size_t(p.n_sets) * p.dim * kPlanes<OP> * sizeof(float) : 0;
+    const size_t lds = table > kWaveLdsFloor ? table : kWaveLdsFloor;
+    if (host::allow_dynamic_lds(k, lds) != hipSuccess)
+        return MH3_ERR_HIP;
     RowsParams arg = p;
     uint64_t blocks;
     constexpr uint32_t kWaveRows = MH3_WAVE_ROWS;
