@@ -272,9 +272,13 @@ def bench_attn(mh, dev, steps, warmup):
     flops = 4.0 * 128 * pairs
     kv_tile_rows = sel * 64 + HEADS * cubes * n_dense + HEADS * (n_dense // 64) * rows
     dense_flops = 4.0 * 128 * HEADS * rows * rows
+    # Each 64-key tile a query tile attends brings 32 KB of K and V for 64 x 64 x 128 x 4 flops: 64 flop a byte, far
+    # below the ridge point (2.5 PFLOP/s / 8 TB/s = 312), so the K/V stream bounds the kernel: kv_frac is it against
+    # HBM (tiles that hit L2 or the MALL let it pass 1).
     return {"ms": ms, "tflops": flops / ms / 1e9, "mfma_util": flops / ms / 1e9 / BF16_PEAK_TFLOPS,
             "flops": flops, "mean_cubes_selected": sel / (HEADS * cubes), "kv_bytes": kv_tile_rows * 512,
-            "kv_GBs": kv_tile_rows * 512 / ms / 1e6, "dense_equivalent_flops": dense_flops,
+            "kv_GBs": kv_tile_rows * 512 / ms / 1e6, "kv_frac": kv_tile_rows * 512 / ms / 1e6 / HBM_PEAK_GBS,
+            "flop_per_kv_byte": flops / (kv_tile_rows * 512), "dense_equivalent_flops": dense_flops,
             "shape": {"heads": HEADS, "grid": list(GRID), "cubes": cubes, "dense_rows": n_dense, "k": kk}}
 
 
