@@ -367,40 +367,67 @@ __global__ __launch_bounds__(MH3_GEMM_WM * MH3_GEMM_WN * 64) void gemm_kernel(
         kstep(kt, std::false_type{});
     kstep(KT - 1, std::true_type{});
 
-    // Epilogue: acc[a][b][e] is y[row][c] with row = m0 + wm (256 / WM) + a 32 + 8 (e / 4) + 4 (lane / 32) + e % 4
-    // and c = lane % 32 + 32 b + wn 32 TN within the tile's first half of w rows (b < TN) or, for acc[a][TN + b], the
-    // same position in its second half.
+    // Epilogue through LDS, idle after the last K-step. acc[a][b][e] is y[r][c] with tile row
+    // r = wm (256 / WM) + a 32 + 8 (e / 4) + 4 (lane / 32) + e % 4 and c = lane % 32 + 32 b + wn 32 TN within the tile's
+    // first 128 w rows (b < TN) or, for acc[a][TN + b], the same position in its second 128. A 128-column half of the
+    // tile at a time, each wave writes its scaled results as floats into a [256][kEpiStride] LDS tile (the two
+    // half-waves' rows, 4 apart, fall on disjoint banks); then each thread takes 8 consecutive columns of a row, so
+    // the output, and with kGateAdd the residual, moves in 16-byte accesses, 16 threads to a row's 256 bytes. The
+    // results round to bf16 once, at the end, as they would written straight from the registers.
+    constexpr uint32_t kEpiStride = kBN + 8u; // floats a staged row: 4 rows apart = 32 banks apart
+    static_assert(kBM * kEpiStride * sizeof(float) <= kGemmLds, "the staged half-tile fits in the LDS");
+    constexpr int kHalves = EPI == kSwiGLU ? 1 : 2;
+    float* const stage = reinterpret_cast<float*>(smem);
+    lds_barrier(); // every wave is done with the last K-step's fragments
 #pragma unroll
-    for (int b = 0; b < TN; ++b) {
-        const uint32_t c = wn * 32u * TN + uint32_t(b) * 32u + r32;
-        const uint32_t c_lo = w_lo + c, c_hi = w_hi + c; // w rows = output columns (kStore, kGateAdd)
-        const float s_lo = MODE != kBf16 ? scale[c_lo] : 1.0f, s_hi = MODE != kBf16 ? scale[c_hi] : 1.0f;
+    for (int hv = 0; hv < kHalves; ++hv) {
+        if (hv)
+            lds_barrier(); // the first half is read out
 #pragma unroll
-        for (int a = 0; a < TM; ++a) {
+        for (int b = 0; b < TN; ++b) {
+            const uint32_t c = wn * 32u * TN + uint32_t(b) * 32u + r32;
+            const float s_lo = MODE != kBf16 ? scale[w_lo + c] : 1.0f, s_hi = MODE != kBf16 ? scale[w_hi + c] : 1.0f;
 #pragma unroll
-            for (int e = 0; e < 16; ++e) {
-                const uint32_t row = m0 + wm * (kBM / WM) + uint32_t(a) * 32u + 8u * (uint32_t(e) >> 2) + 4u * half +
-                                     (uint32_t(e) & 3u);
-                if (row < M) {
-                    const float sx = MODE == kW8A8 ? xscale[row] : 1.0f;
-                    const float lo = float(acc[a][b][e]) * s_lo * sx, hi = float(acc[a][TN + b][e]) * s_hi * sx;
-                    uint16_t* orow = out + uint64_t(row) * N;
+            for (int a = 0; a < TM; ++a) {
+#pragma unroll
+                for (int e = 0; e < 16; ++e) {
+                    const uint32_t r = wm * (kBM / WM) + uint32_t(a) * 32u + 8u * (uint32_t(e) >> 2) + 4u * half +
+                                       (uint32_t(e) & 3u);
+                    const float sx = MODE == kW8A8 ? xscale[min(m0 + r, M - 1u)] : 1.0f;
+                    float v;
                     if constexpr (EPI == kSwiGLU) {
-                        const float o = lo * __builtin_amdgcn_rcpf(1.0f + __expf(-lo)) * hi;
-                        orow[c_lo] = __builtin_bit_cast(uint16_t, __bf16(o));
-                    } else if constexpr (EPI == kStore) {
-                        orow[c_lo] = __builtin_bit_cast(uint16_t, __bf16(lo));
-                        orow[c_hi] = __builtin_bit_cast(uint16_t, __bf16(hi));
+                        const float lo = float(acc[a][b][e]) * s_lo * sx, hi = float(acc[a][TN + b][e]) * s_hi * sx;
+                        v = lo * __builtin_amdgcn_rcpf(1.0f + __expf(-lo)) * hi;
                     } else {
-                        const uint32_t set = gg.set_of_row ? min(uint32_t(gg.set_of_row[row]), gg.n_sets - 1u) : 0u;
-                        const float* g = gg.gate + uint64_t(set) * gg.gate_stride;
-                        const float r_lo = __uint_as_float(uint32_t(orow[c_lo]) << 16);
-                        const float r_hi = __uint_as_float(uint32_t(orow[c_hi]) << 16);
-                        orow[c_lo] = __builtin_bit_cast(uint16_t, __bf16(fmaf(g[c_lo], lo, r_lo)));
-                        orow[c_hi] = __builtin_bit_cast(uint16_t, __bf16(fmaf(g[c_hi], hi, r_hi)));
+                        v = hv == 0 ? float(acc[a][b][e]) * s_lo * sx : float(acc[a][TN + b][e]) * s_hi * sx;
                     }
+                    stage[r * kEpiStride + c] = v;
                 }
             }
+        }
+        lds_barrier();
+        // Output column of staged column 0: the tile's gate columns (SwiGLU), else its first or second 128 columns.
+        const uint32_t col0 = hv == 0 ? w_lo : w_hi;
+        for (uint32_t q = tid; q < kBM * 16u; q += kThreads) {
+            const uint32_t r = q >> 4, c8 = (q & 15u) * 8u, row = m0 + r;
+            if (row >= M)
+                break; // rows grow with q
+            const float4 v0 = *reinterpret_cast<const float4*>(stage + r * kEpiStride + c8);
+            const float4 v1 = *reinterpret_cast<const float4*>(stage + r * kEpiStride + c8 + 4u);
+            float o[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
+            uint4* dst = reinterpret_cast<uint4*>(out + uint64_t(row) * N + col0 + c8);
+            if constexpr (EPI == kGateAdd) {
+                const uint32_t set = gg.set_of_row ? min(uint32_t(gg.set_of_row[row]), gg.n_sets - 1u) : 0u;
+                const float* g = gg.gate + uint64_t(set) * gg.gate_stride + col0 + c8;
+                const uint4 res = *dst;
+                const uint32_t rw[4] = {res.x, res.y, res.z, res.w};
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    o[2 * i] = fmaf(g[2 * i], o[2 * i], bf16_lo(rw[i]));
+                    o[2 * i + 1] = fmaf(g[2 * i + 1], o[2 * i + 1], bf16_hi(rw[i]));
+                }
+            }
+            *dst = uint4{pack_bf16(o[0], o[1]), pack_bf16(o[2], o[3]), pack_bf16(o[4], o[5]), pack_bf16(o[6], o[7])};
         }
     }
 }
