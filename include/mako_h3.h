@@ -64,8 +64,9 @@ enum { MH3_INT8_QKV = 1u, MH3_INT8_OUT = 2u, MH3_INT8_FC1 = 4u, MH3_INT8_FC2 = 8
 int mh3_parse_int8(const char* text, uint32_t* mask);
 /* H3::set_sparse's domain (reference: src/server/video_models.cpp:117-126): ratio in [0, 1], local in {0, 1, 3}. */
 int mh3_check_sparse(float ratio, uint32_t local);
-/* The cubes a query cube keeps by score: ceil(ratio * cubes), clamped to [0, cubes]; -MH3_ERR_PARAM-style negative
- * code for a ratio outside [0, 1]. */
+/* The cubes a query cube keeps by score: ceil(ratio * cubes), clamped to [0, cubes], with the float ratio read as the
+ * decimal it stands for (a product within 2^-22 cubes above an integer counts as that integer: 0.1 of 660 cubes is
+ * 66); a negative code (MH3_ERR_PARAM) for a ratio outside [0, 1]. */
 int64_t mh3_topk_k(float ratio, uint32_t cubes);
 
 /* ---- rows: rms_mod_rows, gate_add_rows, fused rms_mod_gate_add_rows ----------------------------------------------

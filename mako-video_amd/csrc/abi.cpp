@@ -143,7 +143,11 @@ int64_t mh3_topk_k(float ratio, uint32_t cubes)
 {
     if (!(ratio >= 0.0f && ratio <= 1.0f))
         return MH3_ERR_PARAM;
-    const double k = std::ceil(double(ratio) * double(cubes));
+    // The ratio arrives as a float (the reference's Options::sparse, src/video/engine.hpp:35), so 0.1 is 0.1 + 1.5e-9:
+    // a product that exceeds an integer by no more than the float's representation error of the ratio (at most
+    // 2^-24 of it, times the cubes; 2^-22 cubes allows for it with margin) counts as that integer, so 0.1 of 660 cubes
+    // is 66, not 67.
+    const double k = std::ceil(double(ratio) * double(cubes) - std::ldexp(double(cubes), -22));
     return k < 0 ? 0 : (k > cubes ? int64_t(cubes) : int64_t(k));
 }
 

@@ -70,6 +70,10 @@ def test_topk_k_and_cube_count():
     assert mh.topk_k(0.1, 2016) == 202
     assert mh.topk_k(1.0, 2016) == 2016 and mh.topk_k(0.0, 2016) == 0
     assert mh.topk_k(0.5, 2016) == 1008
+    # The float ratio stands for its decimal: 0.1f * 660 = 66.000001 keeps 66 cubes, 0.3f * 10 keeps 3; a genuine
+    # fraction still rounds up.
+    assert mh.topk_k(0.1, 660) == 66 and mh.topk_k(0.3, 10) == 3 and mh.topk_k(0.7, 10) == 7
+    assert mh.topk_k(0.1001, 660) == 67 and mh.topk_k(0.25, 7) == 2
     with pytest.raises(ValueError):
         mh.topk_k(1.5, 10)
 
