@@ -139,8 +139,9 @@ constexpr uint32_t kPaddedRow = 64u * (KPL + 4);
 
 // Scores of query block [i0, i0 + 16) of head h against every key cube; the wave takes key blocks wave, wave + waves...
 // Writes s[r][j] for r < 16, j < cubes into `dst` at r * ld + j, or at r * ld + pad_word<32>(j) when PAD (rows past
-// the last query cube skipped).
-template <bool PAD>
+// the last query cube skipped). The key blocks stream through a DEPTH-deep register ring: block b + DEPTH waves loads
+// while block b's MFMAs run.
+template <bool PAD, int DEPTH>
 __device__ __forceinline__ void score_rows(const CubeGeo& g, const float* __restrict__ qh, const float* __restrict__ kh,
                                            uint32_t i0, float* dst, uint64_t ld, uint32_t wave, uint32_t waves)
 {
@@ -157,34 +158,35 @@ __device__ __forceinline__ void score_rows(const CubeGeo& g, const float* __rest
                 dst[r * ld + (PAD ? pad_word<32>(j) : j)] = acc[v] * kScoreScale;
         }
     };
-    // Key blocks wave, wave + waves, ... through a two-block register ring: block b + 2 waves loads while block b's
-    // MFMAs run.
-    float k0[32], k1[32];
-    uint32_t b = wave;
-    if (b < kblocks)
-        load_operand(kh, b * 16u, g.cubes, k0);
-    if (b + waves < kblocks)
-        load_operand(kh, (b + waves) * 16u, g.cubes, k1);
-    for (; b < kblocks; b += 2u * waves) {
-        const floatx4 a0 = score_block(qa, k0);
-        if (b + 2u * waves < kblocks)
-            load_operand(kh, (b + 2u * waves) * 16u, g.cubes, k0);
-        emit(b, a0);
-        if (b + waves >= kblocks)
-            break;
-        const floatx4 a1 = score_block(qa, k1);
-        if (b + 3u * waves < kblocks)
-            load_operand(kh, (b + 3u * waves) * 16u, g.cubes, k1);
-        emit(b + waves, a1);
+    float kr[DEPTH][32];
+#pragma unroll
+    for (int d = 0; d < DEPTH; ++d)
+        if (wave + uint32_t(d) * waves < kblocks)
+            load_operand(kh, (wave + uint32_t(d) * waves) * 16u, g.cubes, kr[d]);
+    for (uint32_t b0 = wave; b0 < kblocks; b0 += DEPTH * waves) {
+#pragma unroll
+        for (int d = 0; d < DEPTH; ++d) {
+            const uint32_t b = b0 + uint32_t(d) * waves;
+            if (b >= kblocks)
+                break;
+            const floatx4 acc = score_block(qa, kr[d]);
+            if (b + DEPTH * waves < kblocks)
+                load_operand(kh, (b + DEPTH * waves) * 16u, g.cubes, kr[d]);
+            emit(b, acc);
+        }
     }
 }
+
+// Key blocks in flight a wave. Deeper rings measured slower in cube_select at 768p (3: +0.5%, 4: +2%, 6: +13%): the
+// fp32 MFMAs, not the operand loads, set the pace once two are in flight.
+constexpr int kScoreDepth = 2;
 
 __global__ __launch_bounds__(256) void cube_scores_kernel(CubeGeo g, const float* __restrict__ qc,
                                                           const float* __restrict__ kc, float* __restrict__ s)
 {
     const uint32_t h = blockIdx.y, i0 = blockIdx.x * 16u;
     const uint64_t plane = uint64_t(g.cubes) * 128u;
-    score_rows<false>(g, qc + h * plane, kc + h * plane, i0, s + (uint64_t(h) * g.cubes + i0) * g.cubes, g.cubes,
+    score_rows<false, kScoreDepth>(g, qc + h * plane, kc + h * plane, i0, s + (uint64_t(h) * g.cubes + i0) * g.cubes, g.cubes,
                       threadIdx.x >> 6, blockDim.x >> 6);
 }
 
@@ -353,7 +355,7 @@ __global__ __launch_bounds__(kSelectThreads) void cube_select_kernel(CubeGeo g, 
     const uint32_t wave = threadIdx.x >> 6, waves = blockDim.x >> 6;
     uint32_t* cand = reinterpret_cast<uint32_t*>(tile + kSelectRows * kPaddedRow<32>) + wave * 64u;
     const uint64_t plane = uint64_t(g.cubes) * 128u;
-    score_rows<true>(g, qc + h * plane, kc + h * plane, i0, tile, kPaddedRow<32>, wave, waves);
+    score_rows<true, kScoreDepth>(g, qc + h * plane, kc + h * plane, i0, tile, kPaddedRow<32>, wave, waves);
     __syncthreads();
     for (uint32_t r = wave; r < kSelectRows; r += waves) {
         const uint32_t i = i0 + r;
