@@ -186,8 +186,8 @@ __global__ __launch_bounds__(256) void cube_scores_kernel(CubeGeo g, const float
 {
     const uint32_t h = blockIdx.y, i0 = blockIdx.x * 16u;
     const uint64_t plane = uint64_t(g.cubes) * 128u;
-    score_rows<false, kScoreDepth>(g, qc + h * plane, kc + h * plane, i0, s + (uint64_t(h) * g.cubes + i0) * g.cubes, g.cubes,
-                      threadIdx.x >> 6, blockDim.x >> 6);
+    score_rows<false, kScoreDepth>(g, qc + h * plane, kc + h * plane, i0, s + (uint64_t(h) * g.cubes + i0) * g.cubes,
+                                   g.cubes, threadIdx.x >> 6, blockDim.x >> 6);
 }
 
 // Order-preserving key of a float score (larger score, larger key); -0 ranks as +0; key 0 is below every score.

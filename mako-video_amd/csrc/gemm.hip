@@ -368,8 +368,8 @@ __global__ __launch_bounds__(MH3_GEMM_WM * MH3_GEMM_WN * 64) void gemm_kernel(
     kstep(KT - 1, std::true_type{});
 
     // Epilogue through LDS, idle after the last K-step. acc[a][b][e] is y[r][c] with tile row
-    // r = wm (256 / WM) + a 32 + 8 (e / 4) + 4 (lane / 32) + e % 4 and c = lane % 32 + 32 b + wn 32 TN within the tile's
-    // first 128 w rows (b < TN) or, for acc[a][TN + b], the same position in its second 128. A 128-column half of the
+    // r = wm (256 / WM) + a 32 + 8 (e / 4) + 4 (lane / 32) + e % 4 and c = lane % 32 + 32 b + wn 32 TN within the
+    // tile's first 128 w rows (b < TN) or, for acc[a][TN + b], the same position in its second 128. A 128-column half of the
     // tile at a time, each wave writes its scaled results as floats into a [256][kEpiStride] LDS tile (the two
     // half-waves' rows, 4 apart, fall on disjoint banks); then each thread takes 8 consecutive columns of a row, so
     // the output, and with kGateAdd the residual, moves in 16-byte accesses, 16 threads to a row's 256 bytes. The

@@ -186,8 +186,8 @@ extern "C" int mh3_heads_partial(const MH3HeadsArgs* args, const uint16_t* qkv, 
         return MH3_ERR_ALIGN;
     // Outputs over qkv only in place: each output at its own input's position.
     const uint64_t qkv_bytes = ((uint64_t(a.model_rows) - 1) * a.qkv_stride + 3ull * a.heads * 128u) * 2u;
-    const uint64_t out_bytes = ((uint64_t(a.heads) - 1) * a.out_head_stride + (uint64_t(a.rows) - 1) * a.out_row_stride +
-                                128u) * 2u;
+    const uint64_t out_bytes =
+        ((uint64_t(a.heads) - 1) * a.out_head_stride + (uint64_t(a.rows) - 1) * a.out_row_stride + 128u) * 2u;
     uint16_t* outs[3] = {q, k, v};
     for (int t = 0; t < 3; ++t) {
         if (!outs[t] || !overlaps(outs[t], out_bytes, qkv, qkv_bytes))

@@ -311,7 +311,7 @@ __global__ __launch_bounds__(1024) void rows_kernel(RowsParams p)
 // registers, reduces it with DPP and three cross-row reads, and streams the outputs one vector at a time, reading
 // that vector's coefficients from LDS just before use.
 #ifndef MH3_WAVE_BLOCK
-#define MH3_WAVE_BLOCK 640 // threads of a wave-kernel workgroup: 10 waves, measured best of 6 to 16 at one workgroup a CU
+#define MH3_WAVE_BLOCK 640 // wave-kernel workgroup threads: 10 waves, measured best of 6 to 16 at one workgroup a CU
 #endif
 
 template <int DT, int NV, int OP, int SRC>
