@@ -182,10 +182,12 @@ def bench_swiglu(mh, dev, steps, warmup):
     return res
 
 
-def selector_qk(dev, extra_rows=0):
+def selector_qk(dev, extra_rows=0, shared=False):
     """q and k [40][rows + extra_rows][128] bf16: N(0,1) plus, on the video rows, four low-frequency waves over
     (t, y, x) along random unit directions (amplitude 0.5), so cube means separate above the pooled noise; the
-    extra (dense) rows are N(0,1)."""
+    extra (dense) rows are N(0,1). q and k draw their own waves, unless `shared`: then a head's waves are the same in
+    q and k (only the noise differs), so cubes of similar phase score high, as similar content does in a video, and
+    neighbouring query cubes select overlapping key cubes."""
     T, Y, X = GRID
     rows = T * Y * X
     g = torch.Generator(device=dev).manual_seed(7)
@@ -193,16 +195,19 @@ def selector_qk(dev, extra_rows=0):
     tt = torch.arange(T, device=dev, dtype=torch.float32).view(T, 1, 1) / T
     yy = torch.arange(Y, device=dev, dtype=torch.float32).view(1, Y, 1) / Y
     xx = torch.arange(X, device=dev, dtype=torch.float32).view(1, 1, X) / X
+    waves = {}
     qk = []
-    for _ in range(2):
+    for which in range(2):
         t = torch.empty((HEADS, rows + extra_rows, 128), dtype=torch.bfloat16, device=dev)
         for h in range(HEADS):
             acc = torch.randn((rows, 128), generator=g, device=dev)
-            for _j in range(4):
-                f = rng.integers(0, 3, 3)
-                u = rng.standard_normal(128)
-                u = torch.from_numpy(u / np.linalg.norm(u)).float().to(dev)
-                wave = torch.cos(2 * math.pi * (f[0] * tt + f[1] * yy + f[2] * xx) + rng.uniform(0, 6.283))
+            for j in range(4):
+                if not shared or which == 0:
+                    f = rng.integers(0, 3, 3)
+                    u = rng.standard_normal(128)
+                    waves[h, j] = (f, torch.from_numpy(u / np.linalg.norm(u)).float().to(dev), rng.uniform(0, 6.283))
+                f, u, phase = waves[h, j]
+                wave = torch.cos(2 * math.pi * (f[0] * tt + f[1] * yy + f[2] * xx) + phase)
                 acc += 0.5 * wave.reshape(-1, 1) * u
             t[h, :rows] = acc.to(torch.bfloat16)
             if extra_rows:
@@ -248,15 +253,27 @@ def bench_select(mh, dev, steps, warmup):
             "select_bytes": sel_bytes, "unfused_scores_ms": scores_ms, "unfused_topk_ms": topk_ms}
 
 
-def bench_attn(mh, dev, steps, warmup):
+def pass_list_overlap(idx, cnt, cubes):
+    """Mean share of a query cube's selected cubes that the next query cube (same head, next in raster order) also
+    selected: how much K/V a neighbouring tile could find in L2."""
+    heads = idx.shape[0]
+    sel = torch.zeros((heads, cubes, cubes + 1), dtype=torch.bool, device=idx.device)
+    sel.scatter_(2, torch.where(idx >= 0, idx, cubes).long(), True)
+    sel = sel[..., :cubes]
+    both = (sel[:, :-1] & sel[:, 1:]).sum(-1).float()
+    return float((both / cnt[:, :-1].float()).mean())
+
+
+def bench_attn(mh, dev, steps, warmup, shared=False):
     """flash_attn_sparse_128 at the 768p shape: 40 heads, grid 32 x 48 x 84 (2016 cubes) in the model's row order,
     512 text rows after the video rows; the pass lists from cube_pool + cube_select at ratio 0.1 (k = 202), local 1.
     Algorithmic work: 4 x 128 flops (q.k and p.v) per (query, attended key) pair; K/V bytes: 512 per attended key
-    a query tile (one K and one V row per tile that attends it)."""
+    a query tile (one K and one V row per tile that attends it). `shared`: the q/k data whose smooth waves q and k
+    share (selector_qk), so neighbouring query cubes' pass lists overlap."""
     T, Y, X = GRID
     video, n_dense = T * Y * X, 512
     rows = video + n_dense
-    q, k = selector_qk(dev, n_dense)
+    q, k = selector_qk(dev, n_dense, shared=shared)
     v = torch.randn((HEADS, rows, 128), generator=torch.Generator(device=dev).manual_seed(8),
                     device=dev).to(torch.bfloat16)
     cubes = mh.cube_count(*GRID)
@@ -275,11 +292,17 @@ def bench_attn(mh, dev, steps, warmup):
     # Each 64-key tile a query tile attends brings 32 KB of K and V for 64 x 64 x 128 x 4 flops: 64 flop a byte, far
     # below the ridge point (2.5 PFLOP/s / 8 TB/s = 312), so the K/V stream bounds the kernel: kv_frac is it against
     # HBM (tiles that hit L2 or the MALL let it pass 1).
-    return {"ms": ms, "tflops": flops / ms / 1e9, "mfma_util": flops / ms / 1e9 / BF16_PEAK_TFLOPS,
-            "flops": flops, "mean_cubes_selected": sel / (HEADS * cubes), "kv_bytes": kv_tile_rows * 512,
-            "kv_GBs": kv_tile_rows * 512 / ms / 1e6, "kv_frac": kv_tile_rows * 512 / ms / 1e6 / HBM_PEAK_GBS,
-            "flop_per_kv_byte": flops / (kv_tile_rows * 512), "dense_equivalent_flops": dense_flops,
-            "shape": {"heads": HEADS, "grid": list(GRID), "cubes": cubes, "dense_rows": n_dense, "k": kk}}
+    res = {"ms": ms, "tflops": flops / ms / 1e9, "mfma_util": flops / ms / 1e9 / BF16_PEAK_TFLOPS,
+           "flops": flops, "mean_cubes_selected": sel / (HEADS * cubes), "kv_bytes": kv_tile_rows * 512,
+           "kv_GBs": kv_tile_rows * 512 / ms / 1e6, "kv_frac": kv_tile_rows * 512 / ms / 1e6 / HBM_PEAK_GBS,
+           "flop_per_kv_byte": flops / (kv_tile_rows * 512), "dense_equivalent_flops": dense_flops,
+           "pass_list_overlap": pass_list_overlap(idx, cnt, cubes),
+           "shape": {"heads": HEADS, "grid": list(GRID), "cubes": cubes, "dense_rows": n_dense, "k": kk}}
+    del q, k, v, out, qc, kc
+    torch.cuda.empty_cache()
+    if not shared:
+        res["shared_waves"] = bench_attn(mh, dev, steps, warmup, shared=True)
+    return res
 
 
 def bench_heads(mh, dev, steps, warmup):
