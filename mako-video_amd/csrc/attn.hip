@@ -60,6 +60,8 @@ struct AttnParams {
     uint32_t cubes, heads, n_dense, nd; // nd: dense tiles of 64 rows
     uint32_t layout, out_stride;
     uint32_t xcd_slices; // cube tiles mapped to XCDs in eighths of each head (needs 8 | cubes and 8 | nd heads)
+    FastDiv div_plane, div_cw; // c / plane and c / cw by multiply-high: a key tile's cube coordinates cost a few
+                               // scalar instructions instead of integer divisions
     float scale_log2;    // score scale times log2(e): softmax in base 2
 };
 
@@ -83,7 +85,7 @@ __device__ __forceinline__ Tile make_tile(const AttnParams& p, uint32_t t)
         return r;
     }
     const uint32_t c = t - p.nd;
-    const uint32_t ct = c / p.plane, cy = c / p.cw % p.ch, cx = c % p.cw;
+    const uint32_t ct = p.div_plane.div(c), rem = c - ct * p.plane, cy = p.div_cw.div(rem), cx = rem - cy * p.cw;
     r.lim_t = min(4u, p.gt - 4u * ct);
     r.lim_y = min(4u, p.gh - 4u * cy);
     r.lim_x = min(4u, p.gw - 4u * cx);
@@ -427,6 +429,8 @@ extern "C" int mh3_flash_attn_sparse_128(const MH3AttnArgs* args, const uint16_t
     p.q = q, p.k = k, p.v = v, p.out = out, p.idx = idx, p.cnt = cnt;
     p.row0 = c.row0, p.dense_row0 = args->dense_row0, p.head_stride = c.head_stride, p.row_stride = c.row_stride;
     p.plane = uint32_t(plane), p.cubes = uint32_t(cubes), p.heads = c.heads, p.n_dense = args->n_dense;
+    p.div_plane = FastDiv::make(p.plane);
+    p.div_cw = FastDiv::make(p.cw);
     p.nd = uint32_t(nd), p.layout = c.layout, p.out_stride = c.out_stride;
     p.xcd_slices = MH3_ATTN_XCD && cubes % 8u == 0 && (nd * c.heads) % 8u == 0 ? 1u : 0u;
     const float scale = args->scale > 0.0f ? args->scale : 0.08838834764831845f; // 1 / sqrt(128)
