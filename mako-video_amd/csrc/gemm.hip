@@ -1,10 +1,12 @@
-// fc1 as an int8 weight-only GEMM with the SwiGLU epilogue: out = silu(x Wg sg) * (x Wu su).
-// Replaces the reference's `gemm_i8` + `swiglu_rows` pair for fc1 (mako-common; docs/performance.md:120-136,
-// docs/architecture.md:65: fc1's [gate; value] rows, then SwiGLU). The same kernel with bf16 weights (I8 false) is
-// the dense fc1 of the `--int8 none` path (the reference's bf16 `Gemm::encode`, docs/performance.md:52-69): its B
-// tiles then stream into LDS like A's, one K-step ahead, and there is no scale. With int8 x as well (W8A8, the
-// reference's own `gemm_i8`: activations quantized per row) both operands stream into LDS and the int8 MFMA
-// (v_mfma_i32_32x32x32_i8, exact int32 sums) takes 128 k a K-step; the epilogue applies both scales.
+// The block's GEMMs on one kernel. fc1 as an int8 weight-only GEMM with the SwiGLU epilogue:
+// out = silu(x Wg sg) * (x Wu su), replacing the reference's `gemm_i8` + `swiglu_rows` pair for fc1 (mako-common;
+// docs/performance.md:120-136, docs/architecture.md:65: fc1's [gate; value] rows, then SwiGLU). The same kernel with
+// bf16 weights is the dense fc1 of the `--int8 none` path (the reference's bf16 `Gemm::encode`,
+// docs/performance.md:52-69): its B tiles then stream into LDS like A's, one K-step ahead, and there is no scale.
+// With int8 x as well (W8A8, the reference's own `gemm_i8`: activations quantized per row) both operands stream
+// into LDS and the int8 MFMA (v_mfma_i32_32x32x32_i8, exact int32 sums) takes 128 k a K-step; the epilogue applies
+// both scales. Two more epilogues make the same kernel the qkv projection (a plain store) and the out and fc2
+// projections (gate_add_rows folded in: the residual += gate * y, in place).
 //
 // Design (gfx950, v_mfma_f32_32x32x16_bf16):
 // - A workgroup of 8 wavefronts (2 along rows x 4 along columns) computes a 256-row x 128-column output tile, i.e.
@@ -20,6 +22,10 @@
 //   columns per 8 lanes by the chunk-to-thread mapping.
 // - Workgroups are mapped XCD-aware: the hardware deals workgroup b to XCD b % 8, so consecutive tiles are renumbered
 //   onto one XCD, and grouped 4 row-tiles a band so the tiles running together on an XCD share x and w in its L2.
+// - The epilogue goes through the LDS, idle by then: results staged as floats, then written (and the gate-add
+//   residual read) in coalesced 16-byte accesses.
+// - 4 wavefronts of 128 x 128 (fewer LDS bytes a MFMA) measured 10-15% slower than these 8: with one wave a SIMD
+//   nothing hides the fragment reads and the barrier.
 #include "mh3_common.hpp"
 
 #include <type_traits>
