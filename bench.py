@@ -560,8 +560,9 @@ def main() -> int:
     ap.add_argument("--no-compare", action="store_true")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
-        print("bench.py measures one GPU: this build's kernels run on a single MI355X and have no multi-GPU path "
-              "(see DESIGN.md for how they would shard). Run with --gpus 1.", file=sys.stderr)
+        print("bench.py measures one GPU: these kernels run on a single MI355X and have no multi-GPU path (the row "
+              "ops and fc1 would shard by rows, the selector and attention by heads, each GPU running the same "
+              "kernel on its share). Run with --gpus 1.", file=sys.stderr)
         return 2
     import mako_h3 as mh
 
