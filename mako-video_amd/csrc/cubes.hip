@@ -9,8 +9,10 @@
 // - scores: v_mfma_f32_16x16x4_f32 on 16 x 16 blocks; the 128-long contraction is split over the MFMA's 4 k-lanes so
 //   that each operand load of the wave reads 64 contiguous bytes of each of the block's 16 rows.
 // - top-k: one wavefront per (head, query cube) holds the row's scores as order-preserving 32-bit keys in VGPRs, lane l
-//   owning cubes 32 l ... 32 l + 31. It finds the k-th largest key by a binary search over the key range with
-//   per-lane counts and a DPP wave sum, switching to a one-key-per-lane search once at most 64 keys remain in range.
+//   owning cubes 32 l ... 32 l + 31. A 128-bin histogram of the scores, linear in value between the row's minimum and
+//   maximum (LDS atomics, one pass), brackets the k-th largest key to one bin's keys; where that bin holds more than
+//   64 keys a binary search over the key range (per-lane counts, a DPP wave sum) narrows it further, and at most 64
+//   candidates, one to a lane, finish the search.
 //   The selection is a per-lane bit mask; wave prefix sums over lanes rank the ties (lowest index first) and place
 //   each lane's indices, so the output is ascending with no per-element ballots.
 // - cube_select keeps a 16 x C score tile in LDS between the two phases, so the scores never reach HBM.
@@ -209,27 +211,45 @@ __device__ __forceinline__ uint32_t count_ge(const uint32_t (&key)[KPL], uint32_
     return wave_sum_u32((c[0] + c[1]) + (c[2] + c[3]));
 }
 
+// Float value of a key (the inverse of score_key; key 0x80000000 is +0).
+__device__ __forceinline__ float key_value(uint32_t key)
+{
+    return __uint_as_float((key & 0x80000000u) ? (key & 0x7fffffffu) : ~key);
+}
+
+constexpr uint32_t kHistBins = 128; // lanes 0 .. 31 hold four bins each
+
 // Top-k plus local cubes of one (head, query cube i) row of `cubes` scores, by one wavefront. Lane l holds cubes
 // j = l KPL + m (m < KPL), read from `row` in the padded layout of pad_word; entries with j >= cubes are ignored.
-// `cand` is 64 words of LDS private to the wave.
-// The k-th largest key t is the largest t with #{key >= t} >= k. A binary search over the key range keeps
-// lo (#{key >= lo} = n_lo >= k) and hi (#{key > hi} = n_hi < k); once at most 64 keys lie in [lo, hi] they are
-// compacted one to a lane and the search finishes over them alone (#{key >= m} = n_hi + #{candidates >= m}).
+// `cand` (64 words) and `hist` (kHistBins words) are LDS private to the wave.
+// The k-th largest key t is the largest t with #{key >= t} >= k. The search keeps lo (#{key >= lo} = n_lo >= k) and
+// hi (#{key > hi} = n_hi < k), t in [lo, hi]. When the row's scores are finite and not all equal, a histogram sets
+// the first bracket: bin(v) = min(127, (v - vmin) * 128 / (vmax - vmin)) is non-decreasing in v (rounded
+// subtraction, multiplication, minimum and truncation all are), so every key of a higher bin exceeds every key of a
+// lower one. With b the bin where the count from the top first reaches k, lo and hi are the smallest and largest keys
+// of bin b, n_hi the keys above it and n_lo that plus its own. A binary search over the key range then narrows
+// [lo, hi] while more than 64 keys lie in it; the rest are compacted one to a lane and the search finishes over them
+// alone (#{key >= m} = n_hi + #{candidates >= m}).
 // The selection is then a per-lane bit mask: keys above t, the first k - #{key > t} keys equal to t in cube order
 // (ranked by a wave prefix sum of per-lane tie counts) and the local cubes; a prefix sum of the per-lane counts gives
 // each lane its output position, so the indices come out ascending.
+// A row's scores as lane l holds them: keys of cubes j = l KPL + m (m < KPL); bit m of `valid` set when j < cubes
+// (other keys 0).
 template <int KPL>
-__device__ __forceinline__ void topk_row(const float* row, const CubeGeo& g, uint32_t i, uint32_t k, uint32_t local,
-                                         int32_t* __restrict__ out, uint32_t out_stride, int32_t* __restrict__ cnt,
-                                         uint32_t* cand)
-{
+struct RowKeys {
     typedef typename std::conditional<KPL == 32, uint32_t, uint64_t>::type Mask;
-    const uint32_t lane = threadIdx.x & 63u;
-    const uint32_t C = g.cubes, j0 = lane * KPL;
-    const float4* mine = reinterpret_cast<const float4*>(row + lane * (KPL + 4));
     uint32_t key[KPL];
-    Mask valid = 0;
-    uint32_t mn = 0xffffffffu, mx = 0u;
+    Mask valid;
+};
+
+// Lane l's KPL scores of a row in the padded layout of pad_word, as keys.
+template <int KPL>
+__device__ __forceinline__ void load_keys(const float* row, uint32_t C, RowKeys<KPL>& r)
+{
+    typedef typename RowKeys<KPL>::Mask Mask;
+    const uint32_t lane = threadIdx.x & 63u, j0 = lane * KPL;
+    const float4* mine = reinterpret_cast<const float4*>(row + lane * (KPL + 4));
+    r.valid = 0;
 #pragma unroll
     for (int v = 0; v < KPL / 4; ++v) {
         const float4 f = mine[v];
@@ -238,14 +258,72 @@ __device__ __forceinline__ void topk_row(const float* row, const CubeGeo& g, uin
         for (int c = 0; c < 4; ++c) {
             const int m = 4 * v + c;
             const bool ok = j0 + uint32_t(m) < C;
-            key[m] = ok ? score_key(fv[c]) : 0u;
-            valid |= ok ? Mask(1) << m : Mask(0);
-            mn = ok && key[m] < mn ? key[m] : mn;
-            mx = ok && key[m] > mx ? key[m] : mx;
+            r.key[m] = ok ? score_key(fv[c]) : 0u;
+            r.valid |= ok ? Mask(1) << m : Mask(0);
         }
+    }
+}
+
+template <int KPL>
+__device__ __forceinline__ void topk_keys(const RowKeys<KPL>& rk, const CubeGeo& g, uint32_t i, uint32_t k,
+                                          uint32_t local, int32_t* __restrict__ out, uint32_t out_stride,
+                                          int32_t* __restrict__ cnt, uint32_t* cand, uint32_t* hist)
+{
+    typedef typename RowKeys<KPL>::Mask Mask;
+    const uint32_t lane = threadIdx.x & 63u;
+    const uint32_t C = g.cubes, j0 = lane * KPL;
+    const uint32_t(&key)[KPL] = rk.key;
+    const Mask valid = rk.valid;
+    uint32_t mn = 0xffffffffu, mx = 0u;
+#pragma unroll
+    for (int m = 0; m < KPL; ++m) {
+        const bool ok = (valid >> m) & 1u;
+        mn = ok && key[m] < mn ? key[m] : mn;
+        mx = ok && key[m] > mx ? key[m] : mx;
     }
     uint32_t lo = wave_min_u32(mn), hi = wave_max_u32(mx);
     uint32_t n_lo = C, n_hi = 0u; // every valid key is >= the minimum; padding keys (0) are never counted (mid > 0)
+    constexpr uint32_t kKeyNegInf = 0x007fffffu, kKeyPosInf = 0xff800000u; // score_key(-inf), score_key(+inf)
+    const float vmin = key_value(lo), vmax = key_value(hi);
+    const float inv = float(kHistBins) / (vmax - vmin);
+    if (lo > kKeyNegInf && hi < kKeyPosInf && lo < hi && inv < __builtin_huge_valf()) {
+        if (lane < kHistBins / 4u)
+            reinterpret_cast<uint4*>(hist)[lane] = uint4{0u, 0u, 0u, 0u};
+        // NaN (padding keys) gives the top bin; padding is never counted or compared.
+        auto bin_of = [&](uint32_t key_m) {
+            return uint32_t(fminf((key_value(key_m) - vmin) * inv, float(kHistBins - 1u)));
+        };
+#pragma unroll
+        for (int m = 0; m < KPL; ++m)
+            if ((valid >> m) & 1u)
+                atomicAdd(hist + bin_of(key[m]), 1u);
+        __builtin_amdgcn_s_waitcnt(0xC07F); // the wave's own LDS atomics are visible to its reads after lgkmcnt(0)
+        const uint4 h4 = lane < kHistBins / 4u ? reinterpret_cast<const uint4*>(hist)[lane] // bins 4 lane ... + 3
+                                               : uint4{0u, 0u, 0u, 0u};
+        const uint32_t hs[4] = {h4.x, h4.y, h4.z, h4.w};
+        const uint32_t s4 = hs[0] + hs[1] + hs[2] + hs[3];
+        uint32_t above = C - (wave_excl_scan_u32(s4) + s4); // keys in bins above this lane's four
+        uint32_t b = kHistBins, n_above = 0u, n_b = 0u;
+#pragma unroll
+        for (int e = 3; e >= 0; --e) {
+            if (above < k && above + hs[e] >= k)
+                b = 4u * lane + uint32_t(e), n_above = above, n_b = hs[e];
+            above += hs[e];
+        }
+        const uint64_t owner = __ballot(b != kHistBins); // exactly one lane: the counts from the top cross k once
+        const int src = int(__builtin_ctzll(owner));
+        b = uint32_t(__builtin_amdgcn_readlane(int(b), src));
+        n_hi = uint32_t(__builtin_amdgcn_readlane(int(n_above), src));
+        n_lo = n_hi + uint32_t(__builtin_amdgcn_readlane(int(n_b), src));
+        uint32_t bmn = 0xffffffffu, bmx = 0u;
+#pragma unroll
+        for (int m = 0; m < KPL; ++m) {
+            const bool in_b = ((valid >> m) & 1u) && bin_of(key[m]) == b; // recomputed: no registers held
+            bmn = in_b && key[m] < bmn ? key[m] : bmn;
+            bmx = in_b && key[m] > bmx ? key[m] : bmx;
+        }
+        lo = wave_min_u32(bmn), hi = wave_max_u32(bmx);
+    }
     while (lo < hi && n_lo - n_hi > 64u) {
         const uint32_t d = hi - lo;
         const uint32_t mid = lo + (d >> 1) + (d & 1u);
@@ -316,6 +394,16 @@ __device__ __forceinline__ void topk_row(const float* row, const CubeGeo& g, uin
         *cnt = int32_t(total);
 }
 
+template <int KPL>
+__device__ __forceinline__ void topk_row(const float* row, const CubeGeo& g, uint32_t i, uint32_t k, uint32_t local,
+                                         int32_t* __restrict__ out, uint32_t out_stride, int32_t* __restrict__ cnt,
+                                         uint32_t* cand, uint32_t* hist)
+{
+    RowKeys<KPL> rk;
+    load_keys<KPL>(row, g.cubes, rk);
+    topk_keys<KPL>(rk, g, i, k, local, out, out_stride, cnt, cand, hist);
+}
+
 // One wavefront per (head, query cube) row of s: the row is staged into LDS in the padded layout (coalesced loads),
 // then ranked.
 template <int KPL>
@@ -323,10 +411,10 @@ __global__ __launch_bounds__(256) void cube_topk_kernel(CubeGeo g, const float* 
                                                         uint32_t local, uint32_t out_stride, int32_t* __restrict__ idx,
                                                         int32_t* __restrict__ cnt)
 {
-    extern __shared__ float rows[]; // 4 padded rows, then 64 candidate words per wave
+    extern __shared__ float rows[]; // 4 padded rows, then 64 candidate words and a histogram per wave
     const uint32_t wave = threadIdx.x >> 6, lane = threadIdx.x & 63u;
     float* row = rows + wave * kPaddedRow<KPL>;
-    uint32_t* cand = reinterpret_cast<uint32_t*>(rows + 4u * kPaddedRow<KPL>) + wave * 64u;
+    uint32_t* cand = reinterpret_cast<uint32_t*>(rows + 4u * kPaddedRow<KPL>) + wave * (64u + kHistBins);
     const uint32_t item = blockIdx.x * 4u + wave;
     if (item >= g.heads * g.cubes)
         return;
@@ -335,13 +423,16 @@ __global__ __launch_bounds__(256) void cube_topk_kernel(CubeGeo g, const float* 
     for (uint32_t j = lane; j < g.cubes; j += 64u)
         row[pad_word<KPL>(j)] = src[j];
     __builtin_amdgcn_s_waitcnt(0xC07F); // the wave reads only what it wrote itself
-    topk_row<KPL>(row, g, item % g.cubes, k, local, idx + uint64_t(item) * out_stride, out_stride, cnt + item, cand);
+    topk_row<KPL>(row, g, item % g.cubes, k, local, idx + uint64_t(item) * out_stride, out_stride, cnt + item, cand,
+                  cand + 64);
 }
 
-constexpr int kSelectThreads = 512;
+constexpr int kSelectThreads = 1024; // one row a wave ranks; 16 waves measured faster than 8
 constexpr uint32_t kSelectRows = 16;
 constexpr uint32_t kSelectMaxCubes = 2048;
-constexpr size_t kSelectLds = (size_t(kSelectRows) * kPaddedRow<32> + (kSelectThreads / 64) * 64u) * sizeof(float);
+constexpr size_t kSelectLds =
+    (size_t(kSelectRows) * kPaddedRow<32> + (kSelectThreads / 64) * (64u + kHistBins)) * sizeof(float);
+static_assert(kSelectLds <= 160 * 1024, "the select tile, candidates and histograms fit gfx950's LDS");
 
 // Scores of 16 query cubes against every key cube into a padded LDS tile, then one wavefront per row ranks it.
 __global__ __launch_bounds__(kSelectThreads) void cube_select_kernel(CubeGeo g, const float* __restrict__ qc,
@@ -350,10 +441,10 @@ __global__ __launch_bounds__(kSelectThreads) void cube_select_kernel(CubeGeo g, 
                                                                      int32_t* __restrict__ idx,
                                                                      int32_t* __restrict__ cnt)
 {
-    extern __shared__ float tile[]; // [16][padded row], then 64 candidate words per wave
+    extern __shared__ float tile[]; // [16][padded row], then 64 candidate words and a histogram per wave
     const uint32_t h = blockIdx.y, i0 = blockIdx.x * kSelectRows;
     const uint32_t wave = threadIdx.x >> 6, waves = blockDim.x >> 6;
-    uint32_t* cand = reinterpret_cast<uint32_t*>(tile + kSelectRows * kPaddedRow<32>) + wave * 64u;
+    uint32_t* cand = reinterpret_cast<uint32_t*>(tile + kSelectRows * kPaddedRow<32>) + wave * (64u + kHistBins);
     const uint64_t plane = uint64_t(g.cubes) * 128u;
     score_rows<true, kScoreDepth>(g, qc + h * plane, kc + h * plane, i0, tile, kPaddedRow<32>, wave, waves);
     __syncthreads();
@@ -363,7 +454,7 @@ __global__ __launch_bounds__(kSelectThreads) void cube_select_kernel(CubeGeo g, 
             break;
         const uint64_t item = uint64_t(h) * g.cubes + i;
         topk_row<32>(tile + r * kPaddedRow<32>, g, i, k, local, idx + item * out_stride, out_stride, cnt + item,
-                     cand);
+                     cand, cand + 64);
     }
 }
 
@@ -408,11 +499,10 @@ int check_topk_args(const MH3CubeArgs* a, const CubeGeo& g)
     return MH3_OK;
 }
 
+// Dynamic LDS above the default limit for `kernel`, once per device.
 int set_lds_limit(const void* kernel, size_t bytes)
 {
-    return hipFuncSetAttribute(kernel, hipFuncAttributeMaxDynamicSharedMemorySize, int(bytes)) == hipSuccess
-               ? MH3_OK
-               : MH3_ERR_HIP;
+    return host::allow_dynamic_lds(kernel, bytes) == hipSuccess ? MH3_OK : MH3_ERR_HIP;
 }
 
 } // namespace
@@ -465,12 +555,12 @@ int mh3_cube_topk(const MH3CubeArgs* args, const float* s, int32_t* idx, int32_t
     const uint32_t items = g.heads * g.cubes;
     hipStream_t st = static_cast<hipStream_t>(stream);
     if (g.cubes <= 2048) {
-        constexpr size_t lds = (4u * kPaddedRow<32> + 4u * 64u) * sizeof(float);
+        constexpr size_t lds = (4u * kPaddedRow<32> + 4u * (64u + kHistBins)) * sizeof(float);
         hipLaunchKernelGGL(cube_topk_kernel<32>, dim3((items + 3u) / 4u), dim3(256), lds, st, g, s, args->k,
                            args->local, args->out_stride, idx, cnt);
     } else {
-        constexpr size_t lds = (4u * kPaddedRow<64> + 4u * 64u) * sizeof(float);
-        static const int lds_ok = set_lds_limit(reinterpret_cast<const void*>(&cube_topk_kernel<64>), lds);
+        constexpr size_t lds = (4u * kPaddedRow<64> + 4u * (64u + kHistBins)) * sizeof(float);
+        const int lds_ok = set_lds_limit(reinterpret_cast<const void*>(&cube_topk_kernel<64>), lds);
         if (lds_ok != MH3_OK)
             return lds_ok;
         hipLaunchKernelGGL(cube_topk_kernel<64>, dim3((items + 3u) / 4u), dim3(256), lds, st, g, s, args->k,
@@ -494,7 +584,7 @@ int mh3_cube_select(const MH3CubeArgs* args, const float* qc, const float* kc, i
         return MH3_ERR_ALIGN;
     if (g.cubes > kSelectMaxCubes)
         return MH3_ERR_UNSUPPORTED; // more cubes than the LDS tile holds: use cube_scores + cube_topk
-    static const int lds_ok = set_lds_limit(reinterpret_cast<const void*>(&cube_select_kernel), kSelectLds);
+    const int lds_ok = set_lds_limit(reinterpret_cast<const void*>(&cube_select_kernel), kSelectLds);
     if (lds_ok != MH3_OK)
         return lds_ok;
     const dim3 grid((g.cubes + kSelectRows - 1) / kSelectRows, g.heads);

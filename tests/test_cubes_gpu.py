@@ -106,6 +106,38 @@ def test_topk_and_select_match_oracle_on_gpu_scores(dev, grid, local, ratio):
         assert (idx.cpu().numpy()[:, :, :cubes] == np.arange(cubes)).all()
 
 
+@pytest.mark.parametrize("k", [1, 202, 1500])
+def test_topk_score_shapes(dev, k):
+    """cube_topk over crafted rows of 2016 scores against the oracle over the same scores, exactly: normal rows, a
+    far outlier above a narrow bulk (the histogram's bracket bin holds nearly every key, so the binary search takes
+    over), quarter-step ties, +-inf (no histogram), a constant row, signed zeros with scores near +-3e38 (a range that
+    overflows float)."""
+    grid = (32, 48, 84)
+    cubes = mh.cube_count(*grid)
+    rng = np.random.default_rng(k)
+    s = rng.standard_normal((1, cubes, cubes))
+    rows = np.arange(cubes)
+    kind = rows % 6
+    pick = rng.integers(0, cubes, (cubes, 4))
+    s[0, kind == 1] *= 1e-3
+    s[0, rows[kind == 1], pick[kind == 1, 0]] = 1e3
+    s[0, kind == 2] = np.round(s[0, kind == 2] * 4) / 4
+    s[0, rows[kind == 3], pick[kind == 3, 0]] = np.inf
+    s[0, rows[kind == 3], pick[kind == 3, 1]] = -np.inf
+    s[0, kind == 4] = 0.5
+    z = s[0, kind == 5]
+    z[:, ::7] = 0.0
+    z[:, 3::7] = -0.0
+    z[:, 0], z[:, 1] = -3e38, 3e38
+    s[0, kind == 5] = z
+    s32 = s.astype(np.float32)
+    a = mh.cube_args(1, grid, k=k, local=1)
+    idx, cnt = mh.cube_topk(a, torch.from_numpy(s32).to(dev))
+    widx, wcnt = orc.cube_topk(s32.astype(np.float64), grid, k, 1, sorted_form=True)
+    assert (cnt.cpu().numpy() == wcnt).all()
+    assert (idx.cpu().numpy() == widx).all()
+
+
 def test_select_constructed_ranking_and_ties(dev):
     """Cube-constant q and k with an analytic answer: every query cube's pooled q is e0 and cube j's pooled k is
     floor(j / 2) e0 / 16 (exact in bf16), so scores rise with j in equal pairs. The top k are the highest indices;
