@@ -287,8 +287,9 @@ __device__ __forceinline__ void topk_keys(const RowKeys<KPL>& rk, const CubeGeo&
     const float vmin = key_value(lo), vmax = key_value(hi);
     const float inv = float(kHistBins) / (vmax - vmin);
     if (lo > kKeyNegInf && hi < kKeyPosInf && lo < hi && inv < __builtin_huge_valf()) {
-        if (lane < kHistBins / 4u)
-            reinterpret_cast<uint4*>(hist)[lane] = uint4{0u, 0u, 0u, 0u};
+#pragma unroll
+        for (uint32_t e = lane; e < kHistBins; e += 64u)
+            hist[e] = 0u; // 32-bit stores: a hoisted 16-byte zero vector was spilled under 1024 threads
         // NaN (padding keys) gives the top bin; padding is never counted or compared.
         auto bin_of = [&](uint32_t key_m) {
             return uint32_t(fminf((key_value(key_m) - vmin) * inv, float(kHistBins - 1u)));
