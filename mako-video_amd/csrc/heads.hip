@@ -8,7 +8,8 @@
 // HBM-bound. A head vector (128 bf16 = 256 bytes) belongs to one 16-lane DPP row, 16 bytes a lane, so the sum of
 // squares is a DPP row reduction with no LDS and no barrier.
 // - A workgroup of 512 threads is 32 such groups. It takes whole rows, enough that their head vectors fill about 128
-//   slots, and each group has up to 4 head vectors in flight (loads first, then the arithmetic and the stores).
+//   slots and at least two rows, and each group has up to 4 head vectors in flight (loads first, then the arithmetic
+//   and the stores).
 //   Consecutive groups take consecutive head vectors of a row, so a wave's load covers 1 KB of contiguous qkv.
 // - The rotary pairs value i with i + rot / 2: lane p (values 8 p .. 8 p + 7) pairs with lane p +- rot / 16 of the
 //   same group; the partner's raw bf16 words come over by ds_bpermute, and each lane normalizes both halves itself
@@ -203,7 +204,9 @@ extern "C" int mh3_heads_partial(const MH3HeadsArgs* args, const uint16_t* qkv, 
     p.qkv_stride = a.qkv_stride, p.ohs = a.out_head_stride, p.ors = a.out_row_stride;
     p.rows = a.rows, p.model_rows = a.model_rows, p.heads = a.heads, p.half = a.rot / 2u, p.eps = a.eps;
     p.per_row = (v ? 3u : 2u) * a.heads;
-    p.rows_per_block = std::max(1u, kSlots / p.per_row);
+    // At least two rows a workgroup: at 40 heads (120 head vectors a row, two passes) that measured 3-4% faster than
+    // one row, and four rows slower again.
+    p.rows_per_block = std::max(2u, kSlots / p.per_row);
     p.div_row = FastDiv::make(p.per_row);
     p.div_heads = FastDiv::make(a.heads);
     const uint64_t blocks = (uint64_t(a.rows) + p.rows_per_block - 1) / p.rows_per_block;
