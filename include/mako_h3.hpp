@@ -156,7 +156,13 @@ inline std::optional<uint32_t> parse_int8(const std::string& text)
 // The block's row, sparse-selector and int8 kernels on one stream, asynchronous until finish().
 class Kernels {
 public:
-    explicit Kernels(hipStream_t stream = nullptr) : s_(stream) {}
+    // Refuses a library built from another version of mako_h3.h (its argument structs would not match).
+    explicit Kernels(hipStream_t stream = nullptr) : s_(stream)
+    {
+        if (mh3_abi_version() != MH3_ABI_VERSION)
+            throw std::runtime_error("libmako_h3: ABI version " + std::to_string(mh3_abi_version()) +
+                                     ", the header is " + std::to_string(MH3_ABI_VERSION));
+    }
     hipStream_t stream() const { return s_; }
     void finish() const { check_hip(hipStreamSynchronize(s_), "finish"); }
 

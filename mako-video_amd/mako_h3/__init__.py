@@ -20,6 +20,7 @@ import torch
 
 _LIB_PATH = Path(os.environ.get("MAKO_H3_LIB", Path(__file__).resolve().parent.parent / "lib" / "libmako_h3.so"))
 
+ABI_VERSION = 2  # MH3_ABI_VERSION of include/mako_h3.h, whose structs this module mirrors
 OK, ERR_SHAPE, ERR_POINTER, ERR_ALIGN, ERR_PARAM, ERR_HIP, ERR_UNSUPPORTED = 0, -1, -2, -3, -4, -5, -6
 F32, BF16 = 0, 1
 SWIGLU_SPLIT, SWIGLU_FUSED = 0, 1
@@ -97,6 +98,8 @@ def _load() -> C.CDLL:
     for name, (res, args) in sig.items():
         f = getattr(lib, name)
         f.restype, f.argtypes = res, args
+    if lib.mh3_abi_version() != ABI_VERSION:
+        raise ImportError(f"{_LIB_PATH} has ABI version {lib.mh3_abi_version()}, this module mirrors {ABI_VERSION}")
     return lib
 
 

@@ -42,6 +42,9 @@ def test_stream_probe_library_loads_and_refuses_bad_calls():
 
 def test_abi_version_and_strings():
     assert mh.lib.mh3_abi_version() == 2
+    # The Python structs mirror the header: its MH3_ABI_VERSION is the module's (import refuses another library's).
+    header = (Path(__file__).resolve().parent.parent / "include" / "mako_h3.h").read_text()
+    assert re.search(r"#define MH3_ABI_VERSION (\d+)", header).group(1) == str(mh.ABI_VERSION) == "2"
     assert mh.strerror(mh.ERR_SHAPE) == "bad shape"
     assert mh.strerror(123) == "unknown error"
 
