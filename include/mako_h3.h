@@ -39,7 +39,7 @@ enum {
     MH3_ERR_ALIGN = -3,       /* a pointer is not aligned as required (16 bytes for vector rows) */
     MH3_ERR_PARAM = -4,       /* a scalar parameter is outside its domain (dtype, layout, ratio, local, k, eps) */
     MH3_ERR_HIP = -5,         /* the HIP runtime reported an error launching the kernel */
-    MH3_ERR_UNSUPPORTED = -6, /* a valid request this build has no kernel for (e.g. head_dim != 128) */
+    MH3_ERR_UNSUPPORTED = -6, /* a valid request the library has no kernel for (e.g. head_dim != 128) */
 };
 
 /* Element types of activations. */

@@ -1,6 +1,6 @@
 /*
  * mh3_oracle.c — TEST INFRASTRUCTURE ONLY: the scalar CPU restatement of the H3 per-block hot path that the tests,
- * the smoke check and bench.py's CPU-baseline leg use as the parity checker. See mh3_oracle.h for what each
+ * the smoke check and bench.py's CPU-baseline leg compare the GPU results with. See mh3_oracle.h for what each
  * function follows in the reference and how it is pinned. Single-threaded, double accumulation, one rounding at the
  * store (the reference's CPU idiom, src/video/audio_vae.cpp:386-416).
  */

@@ -1,6 +1,6 @@
 /*
  * mh3_oracle.h — TEST INFRASTRUCTURE ONLY. A scalar CPU restatement of the H3 per-block hot-path ops, used by
- * tests/, the smoke check and bench.py's CPU-baseline leg as the parity checker. Nothing in the product links,
+ * tests/, the smoke check and bench.py's CPU-baseline leg to test the GPU results. Nothing in the product links,
  * loads or calls it.
  *
  * The reference's implementation of these ops lives in the un-vendored mako-common submodule (.gitmodules:1-3, empty

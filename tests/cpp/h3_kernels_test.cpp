@@ -1,5 +1,5 @@
 // The H3 block's hot-path kernels through the C++ host layer (mako_h3.hpp) on the GPU, against the CPU oracle
-// (oracle/mh3_oracle.h, the checker), reported the way the reference's tests/h3_ref_test.cpp reports: one line per
+// (oracle/mh3_oracle.h), reported the way the reference's tests/h3_ref_test.cpp reports: one line per
 // check, "ok" or "FAIL", the relative RMS error and the lowest row cosine of diff() (h3_ref_test.cpp:67-90), and
 // the number of failures as the exit status.
 //   h3_kernels_test [rows | swiglu | cubes | attn | int8 | proj | errors | all]
