@@ -419,6 +419,68 @@ def bench_fc1(mh, dev, steps, warmup, compare):
     return res
 
 
+def bench_share(mh, dev, steps, warmup, gpus=8):
+    """The hot path at one GPU's share of a `gpus`-way split, on this one GPU: the row ops and fc1 shard by rows
+    (N / gpus rows, fc1's weights whole), the selector and the attention by heads (40 / gpus heads). Each figure is the
+    share's own throughput; `vs_full` is it over the full shape's (1 = no loss from the smaller launch)."""
+    rows = (ROWS + gpus - 1) // gpus
+    heads = HEADS // gpus
+    g = torch.Generator(device=dev).manual_seed(17)
+    res = {"gpus": gpus, "rows": rows, "heads": heads}
+    x = torch.randn((rows, DIM), generator=g, device=dev).to(torch.bfloat16)
+    r = torch.randn((rows, DIM), generator=g, device=dev).to(torch.bfloat16)
+    w, shift, scale, gate = mod_params(dev, DIM, 1)
+    out = torch.empty_like(x)
+    ms, _ = time_launches(lambda: mh.rms_mod_gate_add_rows(x, r, w, shift, scale, gate, out=out), steps, warmup)
+    nb = rows * DIM * 6
+    res["fused_rms_mod_gate_add"] = {"ms": ms, "GBs": nb / ms / 1e6, "frac": nb / ms / 1e6 / HBM_PEAK_GBS}
+    del r, out
+    gt = torch.randn((rows, FFN), generator=g, device=dev).to(torch.bfloat16)
+    up = torch.randn((rows, FFN), generator=g, device=dev).to(torch.bfloat16)
+    so = torch.empty_like(gt)
+    ms, _ = time_launches(lambda: mh.swiglu_rows(gt, up, out=so), steps, warmup)
+    nb = rows * FFN * 6
+    res["swiglu"] = {"ms": ms, "GBs": nb / ms / 1e6, "frac": nb / ms / 1e6 / HBM_PEAK_GBS}
+    del gt, up
+    wq = torch.randint(-127, 128, (2 * FFN, DIM), generator=g, device=dev, dtype=torch.int8)
+    ws = (torch.rand(2 * FFN, generator=g, device=dev) * 1.5e-3 + 0.5e-3).float()
+    ms, _ = time_launches(lambda: mh.gemm_w8a16_swiglu(x, wq, ws, out=so), max(3, steps // 2), max(1, warmup // 2))
+    fl = 2.0 * rows * DIM * 2 * FFN
+    res["fc1_w8a16_swiglu"] = {"ms": ms, "tflops": fl / ms / 1e9, "mfma_util": fl / ms / 1e9 / BF16_PEAK_TFLOPS}
+    del x, so, wq, ws
+    torch.cuda.empty_cache()
+    # Selector and attention on the first `heads` heads of the 768p q / k.
+    T, Y, X = GRID
+    video, n_dense = T * Y * X, 512
+    q, k = (t[:heads].contiguous() for t in selector_qk(dev, n_dense))
+    torch.cuda.empty_cache()
+    v = torch.randn((heads, video + n_dense, 128), generator=g, device=dev).to(torch.bfloat16)
+    cubes = mh.cube_count(*GRID)
+    kk = mh.topk_k(0.1, cubes)
+    a = mh.cube_args(heads, GRID, head_stride=(video + n_dense) * 128, k=kk, local=1)
+    qc = torch.empty((heads, cubes, 128), dtype=torch.float32, device=dev)
+    kc = torch.empty_like(qc)
+    idx = torch.empty((heads, cubes, kk + 1), dtype=torch.int32, device=dev)
+    cnt = torch.empty((heads, cubes), dtype=torch.int32, device=dev)
+
+    def selector():
+        mh.cube_pool(a, q, k, qc=qc, kc=kc)
+        mh.cube_select(a, qc, kc, idx=idx, cnt=cnt)
+    ms, _ = time_launches(selector, steps, warmup)
+    nb = 2 * heads * video * 128 * 2 + heads * cubes * (kk + 1) * 4
+    res["cube_selector"] = {"ms": ms, "GBs": nb / ms / 1e6, "frac": nb / ms / 1e6 / HBM_PEAK_GBS}
+    o = torch.empty_like(q)
+    ms, _ = time_launches(lambda: mh.flash_attn_sparse_128(a, q, k, v, idx, cnt, dense_row0=video, n_dense=n_dense,
+                                                           out=o), max(3, steps // 2), max(1, warmup // 2))
+    sel = int(cnt.to(torch.int64).sum())
+    rows_all = video + n_dense
+    fl = 4.0 * 128 * (64 * (sel * 64 + heads * cubes * n_dense) + heads * n_dense * rows_all)
+    res["flash_attn_sparse_128"] = {"ms": ms, "tflops": fl / ms / 1e9, "mfma_util": fl / ms / 1e9 / BF16_PEAK_TFLOPS}
+    del q, k, v, o, qc, kc, idx, cnt
+    torch.cuda.empty_cache()
+    return res
+
+
 def cpu_baseline(seconds: float = 10.0) -> dict:
     """The scalar C oracle of the fused op on one host core, on a sample of the 768p rows sized to ~`seconds`."""
     sys.path.insert(0, str(REPO / "oracle"))
@@ -555,7 +617,7 @@ def main() -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--only", default="fused,block_order,copy,swiglu,select,heads,attn,proj,fc1,rms_f32")
+    ap.add_argument("--only", default="fused,block_order,copy,swiglu,select,heads,attn,proj,fc1,rms_f32,share")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-compare", action="store_true")
     args = ap.parse_args()
@@ -602,6 +664,19 @@ def main() -> int:
     if "fc1" in ops:
         report["fc1_w8a16_swiglu"] = bench_fc1(mh, dev, max(3, args.steps // 2), max(1, args.warmup // 2),
                                                not args.no_compare)
+        torch.cuda.empty_cache()
+
+    if "share" in ops:
+        share = bench_share(mh, dev, args.steps, args.warmup)
+        full = {"fused_rms_mod_gate_add": (report.get("fused_rms_mod_gate_add") or {}).get("GBs"),
+                "swiglu": ((report.get("swiglu") or {}).get("split") or {}).get("GBs"),
+                "fc1_w8a16_swiglu": (report.get("fc1_w8a16_swiglu") or {}).get("tflops"),
+                "cube_selector": (report.get("cube_selector") or {}).get("GBs"),
+                "flash_attn_sparse_128": (report.get("flash_attn_sparse_128") or {}).get("tflops")}
+        for name, ref in full.items():
+            mine = share[name].get("GBs", share[name].get("tflops"))
+            share[name]["vs_full"] = mine / ref if ref else None
+        report["per_gpu_share"] = share
         torch.cuda.empty_cache()
 
     head = report.get("fused_rms_mod_gate_add")
