@@ -106,13 +106,13 @@ def test_topk_and_select_match_oracle_on_gpu_scores(dev, grid, local, ratio):
         assert (idx.cpu().numpy()[:, :, :cubes] == np.arange(cubes)).all()
 
 
+@pytest.mark.parametrize("grid", [(32, 48, 84), (52, 52, 52)])
 @pytest.mark.parametrize("k", [1, 202, 1500])
-def test_topk_score_shapes(dev, k):
-    """cube_topk over crafted rows of 2016 scores against the oracle over the same scores, exactly: normal rows, a
-    far outlier above a narrow bulk (the histogram's bracket bin holds nearly every key, so the binary search takes
-    over), quarter-step ties, +-inf (no histogram), a constant row, signed zeros with scores near +-3e38 (a range that
-    overflows float)."""
-    grid = (32, 48, 84)
+def test_topk_score_shapes(dev, grid, k):
+    """cube_topk over crafted rows of scores against the oracle over the same scores, exactly: normal rows, a far
+    outlier above a narrow bulk (the histogram's bracket bin holds nearly every key, so the binary search takes over),
+    quarter-step ties, +-inf (no histogram), a constant row, signed zeros with scores near +-3e38 (a range that
+    overflows float). 2016 cubes (32 a lane) and 2197 (64 a lane)."""
     cubes = mh.cube_count(*grid)
     rng = np.random.default_rng(k)
     s = rng.standard_normal((1, cubes, cubes))
