@@ -18,6 +18,7 @@
 // - cube_select keeps a 16 x C score tile in LDS between the two phases, so the scores never reach HBM.
 #include "mh3_common.hpp"
 
+#include <algorithm>
 #include <type_traits>
 
 namespace mh3 {
@@ -428,14 +429,20 @@ __global__ __launch_bounds__(256) void cube_topk_kernel(CubeGeo g, const float* 
                   cand + 64);
 }
 
-constexpr int kSelectThreads = 1024; // one row a wave ranks; 16 waves measured faster than 8
+// cube_select: a persistent workgroup of 16 waves loops over tiles (16 query cubes of a head, dealt round robin).
+// Iteration j: each wave ranks its own row of tile t_(j-1) from registers (VALU work), then scores its share of the
+// key blocks of tile t_j into the LDS tile (fp32 MFMAs); barrier; each wave copies its row of t_j into registers as
+// keys; barrier (the tile is free again). Waves finish ranking at different times, so on each SIMD some waves
+// already run MFMAs while others still rank. Staggering the order on purpose (half the waves scoring first) needs a
+// row of keys live across the scoring, which spills at 1024 threads' 128 registers and measured slower.
+constexpr int kSelectThreads = 1024;
 constexpr uint32_t kSelectRows = 16;
 constexpr uint32_t kSelectMaxCubes = 2048;
+static_assert(kSelectRows * 64 == kSelectThreads, "one row of a tile a wave");
 constexpr size_t kSelectLds =
     (size_t(kSelectRows) * kPaddedRow<32> + (kSelectThreads / 64) * (64u + kHistBins)) * sizeof(float);
 static_assert(kSelectLds <= 160 * 1024, "the select tile, candidates and histograms fit gfx950's LDS");
 
-// Scores of 16 query cubes against every key cube into a padded LDS tile, then one wavefront per row ranks it.
 __global__ __launch_bounds__(kSelectThreads) void cube_select_kernel(CubeGeo g, const float* __restrict__ qc,
                                                                      const float* __restrict__ kc, uint32_t k,
                                                                      uint32_t local, uint32_t out_stride,
@@ -443,19 +450,33 @@ __global__ __launch_bounds__(kSelectThreads) void cube_select_kernel(CubeGeo g, 
                                                                      int32_t* __restrict__ cnt)
 {
     extern __shared__ float tile[]; // [16][padded row], then 64 candidate words and a histogram per wave
-    const uint32_t h = blockIdx.y, i0 = blockIdx.x * kSelectRows;
-    const uint32_t wave = threadIdx.x >> 6, waves = blockDim.x >> 6;
+    const uint32_t wave = threadIdx.x >> 6, waves = kSelectThreads / 64;
     uint32_t* cand = reinterpret_cast<uint32_t*>(tile + kSelectRows * kPaddedRow<32>) + wave * (64u + kHistBins);
     const uint64_t plane = uint64_t(g.cubes) * 128u;
-    score_rows<true, kScoreDepth>(g, qc + h * plane, kc + h * plane, i0, tile, kPaddedRow<32>, wave, waves);
-    __syncthreads();
-    for (uint32_t r = wave; r < kSelectRows; r += waves) {
-        const uint32_t i = i0 + r;
-        if (i >= g.cubes)
+    const uint32_t row_tiles = (g.cubes + kSelectRows - 1u) / kSelectRows, tiles = row_tiles * g.heads;
+    auto score = [&](uint32_t t) {
+        const uint32_t h = t / row_tiles, i0 = (t - h * row_tiles) * kSelectRows;
+        // One key block in flight a wave: with 16 waves that measured as fast as two, with fewer registers.
+        score_rows<true, 1>(g, qc + h * plane, kc + h * plane, i0, tile, kPaddedRow<32>, wave, waves);
+    };
+    RowKeys<32> rk;
+    auto rank = [&](uint32_t t) {
+        const uint32_t h = t / row_tiles, i = (t - h * row_tiles) * kSelectRows + wave;
+        if (i < g.cubes) {
+            const uint64_t item = uint64_t(h) * g.cubes + i;
+            topk_keys<32>(rk, g, i, k, local, idx + item * out_stride, out_stride, cnt + item, cand, cand + 64);
+        }
+    };
+    for (uint32_t j = 0;; ++j) {
+        const uint32_t t = blockIdx.x + j * gridDim.x;
+        if (j > 0u)
+            rank(t - gridDim.x);
+        if (t >= tiles)
             break;
-        const uint64_t item = uint64_t(h) * g.cubes + i;
-        topk_row<32>(tile + r * kPaddedRow<32>, g, i, k, local, idx + item * out_stride, out_stride, cnt + item,
-                     cand, cand + 64);
+        score(t);
+        __syncthreads(); // tile t scored
+        load_keys<32>(tile + wave * kPaddedRow<32>, g.cubes, rk);
+        __syncthreads(); // every row of t in registers: the tile is free
     }
 }
 
@@ -588,7 +609,9 @@ int mh3_cube_select(const MH3CubeArgs* args, const float* qc, const float* kc, i
     const int lds_ok = set_lds_limit(reinterpret_cast<const void*>(&cube_select_kernel), kSelectLds);
     if (lds_ok != MH3_OK)
         return lds_ok;
-    const dim3 grid((g.cubes + kSelectRows - 1) / kSelectRows, g.heads);
+    // Persistent: one workgroup a CU (the tile takes the LDS), at most one a tile.
+    const uint32_t tiles = (g.cubes + kSelectRows - 1) / kSelectRows * g.heads;
+    const dim3 grid(std::min<uint32_t>(tiles, uint32_t(host::cu_count())));
     hipLaunchKernelGGL(cube_select_kernel, grid, dim3(kSelectThreads), kSelectLds, static_cast<hipStream_t>(stream), g,
                        qc, kc, args->k, args->local, args->out_stride, idx, cnt);
     return host::check_launch();
