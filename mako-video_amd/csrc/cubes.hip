@@ -180,6 +180,44 @@ __device__ __forceinline__ void score_rows(const CubeGeo& g, const float* __rest
     }
 }
 
+// score_rows' products two key blocks at a time, blocks b and b + waves, their two MFMA chains interleaved so that
+// each wave always has an independent MFMA to issue (3-4% faster in cube_select than one chain with the next block
+// prefetched). Same scores, bit for bit: each score is the same 32-MFMA chain.
+template <bool PAD>
+__device__ __forceinline__ void score_rows_pair(const CubeGeo& g, const float* __restrict__ qh,
+                                                const float* __restrict__ kh, uint32_t i0, float* dst, uint64_t ld,
+                                                uint32_t wave, uint32_t waves)
+{
+    const uint32_t lane = threadIdx.x & 63u;
+    float qa[32];
+    load_operand(qh, i0, g.cubes, qa);
+    const uint32_t kblocks = (g.cubes + 15u) / 16u;
+    auto emit = [&](uint32_t kb_i, const floatx4& acc) {
+        const uint32_t j = kb_i * 16u + (lane & 15u);
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+            const uint32_t r = (lane >> 4) * 4u + uint32_t(v);
+            if (j < g.cubes && i0 + r < g.cubes)
+                dst[r * ld + (PAD ? pad_word<32>(j) : j)] = acc[v] * kScoreScale;
+        }
+    };
+    for (uint32_t b0 = wave; b0 < kblocks; b0 += 2u * waves) {
+        const uint32_t b1 = b0 + waves; // past the last block: b0's operands again, not emitted
+        float k0[32], k1[32];
+        load_operand(kh, b0 * 16u, g.cubes, k0);
+        load_operand(kh, (b1 < kblocks ? b1 : b0) * 16u, g.cubes, k1);
+        floatx4 a0 = {0.0f, 0.0f, 0.0f, 0.0f}, a1 = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int s = 0; s < 32; ++s) {
+            a0 = __builtin_amdgcn_mfma_f32_16x16x4f32(qa[s], k0[s], a0, 0, 0, 0);
+            a1 = __builtin_amdgcn_mfma_f32_16x16x4f32(qa[s], k1[s], a1, 0, 0, 0);
+        }
+        emit(b0, a0);
+        if (b1 < kblocks)
+            emit(b1, a1);
+    }
+}
+
 // Key blocks in flight a wave. Deeper rings measured slower in cube_select at 768p (3: +0.5%, 4: +2%, 6: +13%): the
 // fp32 MFMAs, not the operand loads, set the pace once two are in flight.
 constexpr int kScoreDepth = 2;
@@ -456,8 +494,7 @@ __global__ __launch_bounds__(kSelectThreads) void cube_select_kernel(CubeGeo g, 
     const uint32_t row_tiles = (g.cubes + kSelectRows - 1u) / kSelectRows, tiles = row_tiles * g.heads;
     auto score = [&](uint32_t t) {
         const uint32_t h = t / row_tiles, i0 = (t - h * row_tiles) * kSelectRows;
-        // One key block in flight a wave: with 16 waves that measured as fast as two, with fewer registers.
-        score_rows<true, 1>(g, qc + h * plane, kc + h * plane, i0, tile, kPaddedRow<32>, wave, waves);
+        score_rows_pair<true>(g, qc + h * plane, kc + h * plane, i0, tile, kPaddedRow<32>, wave, waves);
     };
     RowKeys<32> rk;
     auto rank = [&](uint32_t t) {
