@@ -15,7 +15,8 @@
 //   candidates, one to a lane, finish the search.
 //   The selection is a per-lane bit mask; wave prefix sums over lanes rank the ties (lowest index first) and place
 //   each lane's indices, so the output is ascending with no per-element ballots.
-// - cube_select keeps a 16 x C score tile in LDS between the two phases, so the scores never reach HBM.
+// - cube_select keeps a 16 x C score tile in LDS between the two phases, so the scores never reach HBM. Its
+//   workgroups are persistent (one a CU) and overlap one tile's ranking with the next tile's scoring across waves.
 #include "mh3_common.hpp"
 
 #include <algorithm>
@@ -218,7 +219,7 @@ __device__ __forceinline__ void score_rows_pair(const CubeGeo& g, const float* _
     }
 }
 
-// Key blocks in flight a wave. Deeper rings measured slower in cube_select at 768p (3: +0.5%, 4: +2%, 6: +13%): the
+// Key blocks in flight a wave in cube_scores. Deeper rings measured slower at 768p (3: +0.5%, 4: +2%, 6: +13%): the
 // fp32 MFMAs, not the operand loads, set the pace once two are in flight.
 constexpr int kScoreDepth = 2;
 
