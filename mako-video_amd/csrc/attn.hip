@@ -26,6 +26,11 @@
 //   lanes (i >> 2) + 4 j, j = 0..3: with lane L naming key (L >> 2)'s columns d0 + 4 (L & 3) .. + 3, lane i receives
 //   column d0 + i of four keys, a V^T fragment, with no transpose in registers. Every fragment address is a lane
 //   constant plus an immediate. Padding slots are fetched from past the buffer's end, which reads zeros.
+// - Each cube tile walks its pass list from a rotated start (position rank mod S of S, S the cube workgroups an XCD
+//   holds at once, rank the tile's place in its XCD's sequence), wrapping round. The XCD's resident tiles then sweep
+//   the key cubes together, so a K/V tile one of them fetches is still in L2 when the others that selected it reach
+//   it: the L2 hit rate at 768p went from 11-15% to 29-35% and the L2 misses fell by a fifth, for 2.4% less time
+//   (the DMA latency of each tile also bounds the kernel).
 // - Softmax in base 2 with the scale folded into the exponent. A query's running maximum moves only when a tile
 //   raises it by more than 8 (in log2 units): P stays below 2^8, and most tiles skip the rescale of O.
 #include "mh3_common.hpp"
@@ -41,6 +46,9 @@ typedef float floatx16 __attribute__((ext_vector_type(16)));
 constexpr uint32_t kAttnThreads = 128;
 #ifndef MH3_ATTN_XCD
 #define MH3_ATTN_XCD 1 // map each XCD to a contiguous eighth of every head's query cubes
+#endif
+#ifndef MH3_ATTN_SWEEP
+#define MH3_ATTN_SWEEP 1 // rotate each cube tile's pass list so an XCD's resident tiles sweep the keys together
 #endif
 #ifndef MH3_ATTN_STAGES
 #define MH3_ATTN_STAGES 1 // K/V stages in LDS (2 overlaps a tile's loads with the previous tile's MFMAs but halves
@@ -60,6 +68,7 @@ struct AttnParams {
     uint32_t cubes, heads, n_dense, nd; // nd: dense tiles of 64 rows
     uint32_t layout, out_stride;
     uint32_t xcd_slices; // cube tiles mapped to XCDs in eighths of each head (needs 8 | cubes and 8 | nd heads)
+    uint32_t sweep;      // with xcd_slices: cube workgroups an XCD runs at once (0: pass lists in plain order)
     FastDiv div_plane, div_cw; // c / plane and c / cw by multiply-high: a key tile's cube coordinates cost a few
                                // scalar instructions instead of integer divisions
     float scale_log2;    // score scale times log2(e): softmax in base 2
@@ -164,7 +173,7 @@ __global__ __launch_bounds__(kAttnThreads, STAGES == 2 ? 1 : 2) void attn_sparse
     // go to the 8 XCDs round-robin (block b to XCD b % 8); when the counts allow, XCD x takes the x-th eighth of each
     // head's cubes in raster order, so the workgroups resident on one XCD are neighbouring query cubes, whose pass
     // lists overlap and meet in that XCD's L2, while all XCDs stay on the same head.
-    uint32_t h, qt;
+    uint32_t h, qt, rank = 0; // rank: the workgroup's place in its XCD's sequence of cube tiles
     {
         const uint32_t b = blockIdx.x, dense_blocks = p.nd * p.heads;
         if (b < dense_blocks) {
@@ -176,6 +185,7 @@ __global__ __launch_bounds__(kAttnThreads, STAGES == 2 ? 1 : 2) void attn_sparse
                 const uint32_t per = p.cubes / 8u, k = r / 8u;
                 h = k / per;
                 qt = p.nd + (r % 8u) * per + (k - h * per);
+                rank = k;
             } else {
                 h = r / p.cubes;
                 qt = p.nd + (r - h * p.cubes);
@@ -197,12 +207,18 @@ __global__ __launch_bounds__(kAttnThreads, STAGES == 2 ? 1 : 2) void attn_sparse
         n_sel = uint32_t(min(max(p.cnt[item], 0), int32_t(p.out_stride)));
     }
     const uint32_t n_tiles = n_sel + p.nd;
+    // The pass list is walked from position rot, wrapping round: a workgroup that starts when the XCD's resident ones
+    // are a fraction f into their lists starts a fraction f into its own, so the resident tiles sweep the key cubes
+    // together and a K/V tile fetched for one is still in that XCD's L2 when the others that selected it reach it.
+    // The order only changes the softmax's summation order.
+    const uint32_t rot = (!dense_q && p.sweep) ? uint32_t(uint64_t(rank % p.sweep) * n_sel / p.sweep) : 0u;
     auto key_tile = [&](uint32_t e) -> uint32_t {
         if (e >= n_sel)
             return e - n_sel;
         if (dense_q)
             return p.nd + e;
-        const int32_t j = list[e];
+        const uint32_t ee = e + rot < n_sel ? e + rot : e + rot - n_sel;
+        const int32_t j = list[ee];
         return j >= 0 && uint32_t(j) < p.cubes ? p.nd + uint32_t(j) : kNoTile;
     };
 
@@ -441,6 +457,13 @@ extern "C" int mh3_flash_attn_sparse_128(const MH3AttnArgs* args, const uint16_t
     const size_t lds = size_t(kStages) * kStageBytes;
     if (hipFuncSetAttribute(kern, hipFuncAttributeMaxDynamicSharedMemorySize, int(lds)) != hipSuccess)
         return MH3_ERR_HIP;
+    if (MH3_ATTN_SWEEP && p.xcd_slices) {
+        int per_cu = 0;
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kern, int(kAttnThreads), lds) != hipSuccess)
+            return MH3_ERR_HIP;
+        // The sweep period: the cube workgroups an XCD holds at once (half or twice that measured slower).
+        p.sweep = uint32_t(uint64_t(std::max(per_cu, 1)) * uint32_t(host::cu_count()) / 8u);
+    }
     hipLaunchKernelGGL(attn_sparse_kernel<kStages>, dim3(uint32_t(blocks)), dim3(kAttnThreads), lds,
                        static_cast<hipStream_t>(stream), p);
     return host::check_launch();
