@@ -39,6 +39,9 @@ CASES = [
     ((8, 8, 12), orc.CUBES_GRID, 5, 0, 0, 3, 0),
     ((4, 5, 4), orc.CUBES_GRID, 64, 0, 64, 1, 1),
     ((13, 10, 9), orc.CUBES_GRID, 0, 1170, 130, 6, 1),
+    # 64 cubes and 4 dense tiles x 2 heads, both multiples of 8: the XCD-sliced order with rotated pass lists
+    ((16, 16, 16), orc.CUBES_GRID, 0, 4096, 256, 6, 1),
+    ((15, 16, 16), orc.CUBES_GATHERED, 256, 0, 200, 9, 3),
 ]
 
 
