@@ -1,15 +1,17 @@
 """Benchmark of the H3 per-block hot path on one MI355X.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W]
-                    [--only fused,block_order,copy,swiglu,select,heads,attn,proj,fc1,rms_f32]
+                    [--only fused,block_order,copy,swiglu,select,heads,attn,proj,fc1,rms_f32,share]
                     [--no-cpu] [--no-compare]
 
 A step is one pass of the headline kernel -- the fused adaLN-modulated RMS norm + gated residual -- over the
 768p-shaped batch (129,536 rows = 32x48x84 video + 512 text, x 5120, bf16), inputs resident in HBM. value is its
 achieved algorithmic HBM bandwidth (6 bytes an element: read x and residual, write out). The same run also times the
 other ops of the path at their shapes (SwiGLU split and fused-row, the cube selector, the int8 fc1 + SwiGLU GEMM, the
-fp32 modulated RMS norm) and reports each as ms, GB/s or TFLOP/s and a fraction of the MI355X roofline. Kernel times
-come from HIP events recorded on the stream the kernels run on (torch's current stream). The CPU baseline is the
+fp32 modulated RMS norm, heads_partial, the sparse attention, the other projections) and reports each as ms, GB/s or
+TFLOP/s and a fraction of the MI355X roofline; `share` repeats the main ones at one GPU's share of an 8-way split. Kernel times
+come from HIP events recorded on the stream the kernels run on (torch's current stream): the mean over the timed
+launches, with the median beside it for the row and selector workloads. The CPU baseline is the
 scalar C oracle on one host core, on a bounded sample of the same workload.
 
 Prints one JSON line.
@@ -41,8 +43,12 @@ ROWS, DIM, FFN = 32 * 48 * 84 + 512, 5120, 13824
 GRID, HEADS = (32, 48, 84), 40
 
 
+LAST_MEDIAN_MS = [0.0]  # the median of the last time_launches call's per-launch event times
+
+
 def time_launches(fn, steps: int, warmup: int) -> tuple[float, float]:
-    """(mean ms per launch from HIP events on the current stream, wall ms per launch) over `steps` launches."""
+    """(mean ms per launch from HIP events on the current stream, wall ms per launch) over `steps` launches; the
+    median of the per-launch times is left in LAST_MEDIAN_MS[0]."""
     for _ in range(warmup):
         fn()
     torch.cuda.synchronize()
@@ -56,6 +62,7 @@ def time_launches(fn, steps: int, warmup: int) -> tuple[float, float]:
     torch.cuda.synchronize()
     wall = (time.perf_counter() - t0) * 1e3 / steps
     ev = [s.elapsed_time(e) for s, e in zip(starts, ends)]
+    LAST_MEDIAN_MS[0] = float(np.median(ev))
     return float(np.mean(ev)), wall
 
 
@@ -75,9 +82,10 @@ def bench_fused(mh, dev, steps, warmup):
     w, shift, scale, gate = mod_params(dev, DIM, 1)
     out = torch.empty_like(x)
     ms, wall = time_launches(lambda: mh.rms_mod_gate_add_rows(x, res, w, shift, scale, gate, out=out), steps, warmup)
+    med = LAST_MEDIAN_MS[0]
     nbytes = ROWS * DIM * 6
-    return {"ms": ms, "wall_ms": wall, "bytes": nbytes, "GBs": nbytes / ms / 1e6, "frac": nbytes / ms / 1e6 /
-            HBM_PEAK_GBS, "shape": [ROWS, DIM]}
+    return {"ms": ms, "median_ms": med, "median_GBs": nbytes / med / 1e6, "wall_ms": wall, "bytes": nbytes,
+            "GBs": nbytes / ms / 1e6, "frac": nbytes / ms / 1e6 / HBM_PEAK_GBS, "shape": [ROWS, DIM]}
 
 
 def bench_block_order(mh, dev, steps, warmup):
@@ -172,11 +180,13 @@ def bench_swiglu(mh, dev, steps, warmup):
     up = torch.randn((ROWS, FFN), generator=g, device=dev).to(torch.bfloat16)
     out = torch.empty_like(gate)
     ms, _ = time_launches(lambda: mh.swiglu_rows(gate, up, out=out), steps, warmup)
-    res["split"] = {"ms": ms, "GBs": nbytes / ms / 1e6, "frac": nbytes / ms / 1e6 / HBM_PEAK_GBS}
+    res["split"] = {"ms": ms, "median_ms": LAST_MEDIAN_MS[0], "GBs": nbytes / ms / 1e6,
+                    "frac": nbytes / ms / 1e6 / HBM_PEAK_GBS}
     del gate, up
     gu = torch.randn((ROWS, 2 * FFN), generator=g, device=dev).to(torch.bfloat16)
     ms, _ = time_launches(lambda: mh.swiglu_rows(gu, out=out), steps, warmup)
-    res["fused_row"] = {"ms": ms, "GBs": nbytes / ms / 1e6, "frac": nbytes / ms / 1e6 / HBM_PEAK_GBS}
+    res["fused_row"] = {"ms": ms, "median_ms": LAST_MEDIAN_MS[0], "GBs": nbytes / ms / 1e6,
+                        "frac": nbytes / ms / 1e6 / HBM_PEAK_GBS}
     res["bytes"] = nbytes
     res["shape"] = [ROWS, FFN]
     return res
@@ -234,6 +244,7 @@ def bench_select(mh, dev, steps, warmup):
         mh.cube_pool(a, q, k, qc=qc, kc=kc)
         mh.cube_select(a, qc, kc, idx=idx, cnt=cnt)
     total_ms, _ = time_launches(both, steps, warmup)
+    total_median = LAST_MEDIAN_MS[0]
     # The unfused pair, scores through HBM: for comparison with the fused select.
     del q, k
     s = torch.empty((HEADS, cubes, cubes), dtype=torch.float32, device=dev)
@@ -244,7 +255,8 @@ def bench_select(mh, dev, steps, warmup):
     sel_bytes = 2 * HEADS * cubes * 128 * 4 + HEADS * cubes * (kk + 2) * 4
     alg_bytes = 2 * HEADS * rows * 128 * 2 + HEADS * cubes * (kk + 1) * 4
     flops = 2.0 * HEADS * cubes * cubes * 128
-    return {"pool_ms": pool_ms, "select_ms": sel_ms, "ms": total_ms, "k": kk, "cubes": cubes,
+    return {"pool_ms": pool_ms, "select_ms": sel_ms, "ms": total_ms, "median_ms": total_median, "k": kk,
+            "cubes": cubes,
             "pool_GBs": pool_bytes / pool_ms / 1e6, "pool_frac": pool_bytes / pool_ms / 1e6 / HBM_PEAK_GBS,
             "alg_bytes": alg_bytes, "GBs": alg_bytes / total_ms / 1e6,
             "frac": alg_bytes / total_ms / 1e6 / HBM_PEAK_GBS,
@@ -692,6 +704,7 @@ def main() -> int:
         "steps": args.steps,
         "warmup": args.warmup,
         "ms_per_step": round(head["ms"], 4) if head else None,
+        "median_ms": round(head["median_ms"], 4) if head else None,
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
