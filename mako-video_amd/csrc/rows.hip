@@ -311,7 +311,7 @@ __global__ __launch_bounds__(1024) void rows_kernel(RowsParams p)
 // registers, reduces it with DPP and three cross-row reads, and streams the outputs one vector at a time, reading
 // that vector's coefficients from LDS just before use.
 #ifndef MH3_WAVE_BLOCK
-#define MH3_WAVE_BLOCK 640 // wave-kernel workgroup threads: 10 waves, measured best of 6 to 16 at one workgroup a CU
+#define MH3_WAVE_BLOCK 704 // wave-kernel workgroup threads: 11 waves, measured best of 6 to 16 at one workgroup a CU
 #endif
 
 template <int DT, int NV, int OP, int SRC>
@@ -549,10 +549,11 @@ int launch_rows_wave(const RowsParams& p, hipStream_t stream)
     else
         k = pick_wave_kernel<DT, 12, OP>(src);
     const uint32_t threads = MH3_WAVE_BLOCK, waves = threads / 64u;
-    // The dynamic LDS is at least kWaveLdsFloor, so one workgroup (10 waves, 10 rows in flight) holds a CU: fewer rows
+    // The dynamic LDS is at least kWaveLdsFloor, so one workgroup (11 waves, 11 rows in flight) holds a CU: fewer rows
     // in flight streamed faster than the 2 to 4 workgroups the registers would allow (at 8 waves a workgroup: 5.96 to
     // 6.04 TB/s against 5.79 to 5.91 for the fused op at 768p, alternating runs on one GPU; 10 waves: 6.05), as fewer
-    // open streams contend for the DRAM banks.
+    // open streams contend for the DRAM banks. 11 waves beat 10 by 0.4-0.5% (and by 1.5-3% at 16,192 rows); 12 equalled
+    // 10 and 13 were 8% slower.
     const size_t table = src == kCoefLds ? size_t(p.n_sets) * p.dim * kPlanes<OP> * sizeof(float) : 0;
     const size_t lds = table > kWaveLdsFloor ? table : kWaveLdsFloor;
     if (host::allow_dynamic_lds(k, lds) != hipSuccess)
