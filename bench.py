@@ -11,8 +11,10 @@ other ops of the path at their shapes (SwiGLU split and fused-row, the cube sele
 fp32 modulated RMS norm, heads_partial, the sparse attention, the other projections) and reports each as ms, GB/s or
 TFLOP/s and a fraction of the MI355X roofline; `share` repeats the main ones at one GPU's share of an 8-way split. Kernel times
 come from HIP events recorded on the stream the kernels run on (torch's current stream): the mean over the timed
-launches, with the median beside it for the row and selector workloads. The CPU baseline is the
-scalar C oracle on one host core, on a bounded sample of the same workload.
+launches, with the median beside it for the row and selector workloads. Launches run back to back with warm caches;
+`cold_ms` beside the fused op, SwiGLU, the select kernel, fc1 and the fp32 norm times each launch after a 512 MiB
+overwrite of L2 and the MALL instead. The CPU baseline is the scalar C oracle on one host core, on a bounded sample of
+the same workload.
 
 Prints one JSON line.
 """
@@ -46,9 +48,21 @@ GRID, HEADS = (32, 48, 84), 40
 LAST_MEDIAN_MS = [0.0]  # the median of the last time_launches call's per-launch event times
 
 
-def time_launches(fn, steps: int, warmup: int) -> tuple[float, float]:
+_FLUSH: list = []
+
+
+def flush_caches() -> None:
+    """Overwrite 512 MiB on the current stream: twice the 256 MB MALL and far more than the 8 x 4 MB of L2, so the
+    launch after it starts with cold caches."""
+    if not _FLUSH:
+        _FLUSH.append(torch.empty(512 << 20, dtype=torch.uint8, device="cuda"))
+    _FLUSH[0].zero_()
+
+
+def time_launches(fn, steps: int, warmup: int, cold: bool = False) -> tuple[float, float]:
     """(mean ms per launch from HIP events on the current stream, wall ms per launch) over `steps` launches; the
-    median of the per-launch times is left in LAST_MEDIAN_MS[0]."""
+    median of the per-launch times is left in LAST_MEDIAN_MS[0]. With `cold`, `flush_caches` runs before each timed
+    launch, outside its events (the wall time then includes the flushes)."""
     for _ in range(warmup):
         fn()
     torch.cuda.synchronize()
@@ -56,6 +70,8 @@ def time_launches(fn, steps: int, warmup: int) -> tuple[float, float]:
     ends = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
     t0 = time.perf_counter()
     for i in range(steps):
+        if cold:
+            flush_caches()
         starts[i].record()
         fn()
         ends[i].record()
@@ -83,9 +99,12 @@ def bench_fused(mh, dev, steps, warmup):
     out = torch.empty_like(x)
     ms, wall = time_launches(lambda: mh.rms_mod_gate_add_rows(x, res, w, shift, scale, gate, out=out), steps, warmup)
     med = LAST_MEDIAN_MS[0]
+    cold_ms, _ = time_launches(lambda: mh.rms_mod_gate_add_rows(x, res, w, shift, scale, gate, out=out), steps,
+                               warmup, cold=True)
     nbytes = ROWS * DIM * 6
     return {"ms": ms, "median_ms": med, "median_GBs": nbytes / med / 1e6, "wall_ms": wall, "bytes": nbytes,
-            "GBs": nbytes / ms / 1e6, "frac": nbytes / ms / 1e6 / HBM_PEAK_GBS, "shape": [ROWS, DIM]}
+            "GBs": nbytes / ms / 1e6, "frac": nbytes / ms / 1e6 / HBM_PEAK_GBS, "shape": [ROWS, DIM],
+            "cold_ms": cold_ms, "cold_GBs": nbytes / cold_ms / 1e6}
 
 
 def bench_block_order(mh, dev, steps, warmup):
@@ -167,8 +186,10 @@ def bench_rms_f32(mh, dev, steps, warmup):
     w, shift, scale, _ = mod_params(dev, 1024, 4)
     out = torch.empty_like(x)
     ms, _ = time_launches(lambda: mh.rms_mod_rows(x, w, shift, scale, out=out), steps, warmup)
+    cold_ms, _ = time_launches(lambda: mh.rms_mod_rows(x, w, shift, scale, out=out), steps, warmup, cold=True)
     nbytes = 4096 * 1024 * 8
     return {"ms": ms, "bytes": nbytes, "GBs": nbytes / ms / 1e6, "shape": [4096, 1024],
+            "cold_ms": cold_ms, "cold_GBs": nbytes / cold_ms / 1e6,
             "note": "33.6 MB: launch- and L2-bound, not an HBM measurement"}
 
 
@@ -182,6 +203,7 @@ def bench_swiglu(mh, dev, steps, warmup):
     ms, _ = time_launches(lambda: mh.swiglu_rows(gate, up, out=out), steps, warmup)
     res["split"] = {"ms": ms, "median_ms": LAST_MEDIAN_MS[0], "GBs": nbytes / ms / 1e6,
                     "frac": nbytes / ms / 1e6 / HBM_PEAK_GBS}
+    res["split"]["cold_ms"], _ = time_launches(lambda: mh.swiglu_rows(gate, up, out=out), steps, warmup, cold=True)
     del gate, up
     gu = torch.randn((ROWS, 2 * FFN), generator=g, device=dev).to(torch.bfloat16)
     ms, _ = time_launches(lambda: mh.swiglu_rows(gu, out=out), steps, warmup)
@@ -239,6 +261,8 @@ def bench_select(mh, dev, steps, warmup):
     cnt = torch.empty((HEADS, cubes), dtype=torch.int32, device=dev)
     pool_ms, _ = time_launches(lambda: mh.cube_pool(a, q, k, qc=qc, kc=kc), steps, warmup)
     sel_ms, _ = time_launches(lambda: mh.cube_select(a, qc, kc, idx=idx, cnt=cnt), steps, warmup)
+    # The pooled inputs (83 MB) fit in the MALL, so back-to-back launches start warm; this timing starts each cold.
+    sel_cold_ms, _ = time_launches(lambda: mh.cube_select(a, qc, kc, idx=idx, cnt=cnt), steps, warmup, cold=True)
 
     def both():
         mh.cube_pool(a, q, k, qc=qc, kc=kc)
@@ -255,7 +279,7 @@ def bench_select(mh, dev, steps, warmup):
     sel_bytes = 2 * HEADS * cubes * 128 * 4 + HEADS * cubes * (kk + 2) * 4
     alg_bytes = 2 * HEADS * rows * 128 * 2 + HEADS * cubes * (kk + 1) * 4
     flops = 2.0 * HEADS * cubes * cubes * 128
-    return {"pool_ms": pool_ms, "select_ms": sel_ms, "ms": total_ms, "median_ms": total_median, "k": kk,
+    return {"pool_ms": pool_ms, "select_ms": sel_ms, "select_cold_ms": sel_cold_ms, "ms": total_ms, "median_ms": total_median, "k": kk,
             "cubes": cubes,
             "pool_GBs": pool_bytes / pool_ms / 1e6, "pool_frac": pool_bytes / pool_ms / 1e6 / HBM_PEAK_GBS,
             "alg_bytes": alg_bytes, "GBs": alg_bytes / total_ms / 1e6,
@@ -398,8 +422,10 @@ def bench_fc1(mh, dev, steps, warmup, compare):
     out = torch.empty((ROWS, FFN), dtype=torch.bfloat16, device=dev)
     ms, _ = time_launches(lambda: mh.gemm_w8a16_swiglu(x, w, s, out=out), steps, warmup)
     flops = 2.0 * ROWS * DIM * 2 * FFN
+    # The int8 weights (141 MB) fit in the MALL; each launch reads them once per row band anyway. Timed cold too.
+    cold_ms, _ = time_launches(lambda: mh.gemm_w8a16_swiglu(x, w, s, out=out), max(3, steps // 2), 1, cold=True)
     res = {"ms": ms, "tflops": flops / ms / 1e9, "mfma_util": flops / ms / 1e9 / BF16_PEAK_TFLOPS,
-           "flops": flops, "shape": [ROWS, DIM, 2 * FFN]}
+           "flops": flops, "shape": [ROWS, DIM, 2 * FFN], "cold_ms": cold_ms}
     # The dense bf16 fc1 the int8 path replaces: this library's bf16 kernel (GEMM + SwiGLU epilogue) and, with
     # compare, hipBLASLt through torch.matmul (GEMM only, no epilogue).
     wb = (w.float() * s[:, None]).to(torch.bfloat16)
