@@ -334,12 +334,15 @@ __global__ __launch_bounds__(MH3_WAVE_BLOCK) void rows_wave_kernel(RowsParams p)
         const uint32_t rr = min(row, p.rows - 1u);
         const __amdgpu_buffer_rsrc_t sx = buffer_rsrc(p.x + uint64_t(rr) * p.nvec, bytes);
         const __amdgpu_buffer_rsrc_t sr = buffer_rsrc(p.res + uint64_t(rr) * p.nvec, bytes);
+        // All of x first, then the residual: loads complete in order, so the sum of squares waits for x alone and
+        // runs while the residual is still in flight (2-3% faster than interleaving the two at 129,536 x 5120).
 #pragma unroll
-        for (int j = 0; j < NV; ++j) {
+        for (int j = 0; j < NV; ++j)
             xv[j] = __builtin_amdgcn_raw_buffer_load_b128(sx, (lane + 64u * j) * 16u, 0, kNonTemporal);
+#pragma unroll
+        for (int j = 0; j < NV; ++j)
             if constexpr (OP != kRmsMod)
                 rv[j] = __builtin_amdgcn_raw_buffer_load_b128(sr, (lane + 64u * j) * 16u, 0, kNonTemporal);
-        }
     };
     const uint32_t coef_total = p.n_sets * p.dim;
     for (uint32_t i = tid; SRC == kCoefLds && i < p.n_sets * p.nvec; i += blockDim.x) {
