@@ -1,7 +1,7 @@
 """Benchmark of the H3 per-block hot path on one MI355X.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W]
-                    [--only fused,block_order,copy,swiglu,select,heads,attn,proj,fc1,rms_f32,share]
+                    [--only fused,block_order,copy,swiglu,select,cond,heads,attn,proj,fc1,rms_f32,share]
                     [--no-cpu] [--no-compare]
 
 A step is one pass of the headline kernel -- the fused adaLN-modulated RMS norm + gated residual -- over the
@@ -138,8 +138,8 @@ def bench_copy(dev, steps, warmup):
 def bench_stream(dev, steps, warmup):
     """The streaming ceiling: a plain HIP kernel reading, copying, and reading two streams into a third (the fused
     row op's and SwiGLU's mix), 16-byte non-temporal accesses over 768p-sized bf16 buffers (1.33 GB each), swept
-    over unroll (2, 4, 8 vectors a thread) and grid (flat; 4, 8, 16 workgroups a CU, grid-stride); the best of each
-    mix is reported. Also the MFMA peaks from the device's CU count and peak clock (flops a clock a CU: bf16 4096,
+    over the access form (global or buffer instructions), unroll (2, 4, 8 vectors a thread) and grid (flat; 4, 8, 16
+    workgroups a CU, grid-stride, for the global form); the best of each mix is reported. Also the MFMA peaks from the device's CU count and peak clock (flops a clock a CU: bf16 4096,
     int8 8192)."""
     import ctypes as C
 
@@ -156,23 +156,27 @@ def bench_stream(dev, steps, warmup):
     c = torch.empty_like(a)
     stream = torch.cuda.current_stream().cuda_stream
     res = {"bytes_per_stream": nbytes}
-    for kind, name, moved in ((0, "read", 1), (1, "copy", 2), (2, "r2w1", 3)):
+    # Each mix in both access forms: global loads and stores (kinds 0-2, flat or grid-stride) and buffer loads and
+    # stores (kinds 3-5, flat), the best of all reported as the mix's ceiling.
+    for kinds, name, moved in (((0, 3), "read", 1), ((1, 4), "copy", 2), ((2, 5), "r2w1", 3)):
         best = None
-        for unroll in (2, 4, 8):
-            for per_cu in (0, 4, 8, 16):
-                blocks = per_cu * cus.value
+        for kind in kinds:
+            for unroll in (2, 4, 8):
+                for per_cu in ((0, 4, 8, 16) if kind < 3 else (0,)):
+                    blocks = per_cu * cus.value
 
-                def run():
-                    rc = lib.mh3_probe_stream(kind, a.data_ptr(), b.data_ptr(), c.data_ptr(), nbytes // 16, unroll,
-                                              blocks, stream)
-                    if rc != 0:
-                        raise RuntimeError(f"mh3_probe_stream({name}) returned {rc}")
-                ms, _ = time_launches(run, max(5, steps // 2), 2)
-                if best is None or ms < best[0]:
-                    best = (ms, unroll, per_cu)
-        ms, unroll, per_cu = best
+                    def run():
+                        rc = lib.mh3_probe_stream(kind, a.data_ptr(), b.data_ptr(), c.data_ptr(), nbytes // 16,
+                                                  unroll, blocks, stream)
+                        if rc != 0:
+                            raise RuntimeError(f"mh3_probe_stream({name}) returned {rc}")
+                    ms, _ = time_launches(run, max(5, steps // 2), 2)
+                    if best is None or ms < best[0]:
+                        best = (ms, unroll, per_cu, kind)
+        ms, unroll, per_cu, kind = best
         res[name] = {"ms": ms, "GBs": moved * nbytes / ms / 1e6, "frac": moved * nbytes / ms / 1e6 / HBM_PEAK_GBS,
-                     "unroll": unroll, "grid": "flat" if per_cu == 0 else f"{per_cu} workgroups a CU"}
+                     "unroll": unroll, "grid": "flat" if per_cu == 0 else f"{per_cu} workgroups a CU",
+                     "access": "buffer" if kind >= 3 else "global"}
     clk = khz.value * 1e3
     res["device"] = {"cus": cus.value, "peak_clock_mhz": khz.value / 1e3,
                      "bf16_mfma_peak_tflops": cus.value * clk * 4096 / 1e12,
@@ -326,11 +330,13 @@ def bench_attn(mh, dev, steps, warmup, shared=False):
     kv_tile_rows = sel * 64 + HEADS * cubes * n_dense + HEADS * (n_dense // 64) * rows
     dense_flops = 4.0 * 128 * HEADS * rows * rows
     # Each 64-key tile a query tile attends brings 32 KB of K and V for 64 x 64 x 128 x 4 flops: 64 flop a byte, far
-    # below the ridge point (2.5 PFLOP/s / 8 TB/s = 312), so the K/V stream bounds the kernel: kv_frac is it against
-    # HBM (tiles that hit L2 or the MALL let it pass 1).
+    # below the ridge point (2.5 PFLOP/s / 8 TB/s = 312), so the K/V stream bounds the kernel. kv_tile_GBs is the rate
+    # at which the CUs' loads receive K/V tile bytes: most of them come from L2 and the MALL (a tile serves several
+    # query tiles), so it is not an HBM figure and is not compared with the HBM peak; the HBM-side rate comes from the
+    # counters (bytes past L2, FETCH_SIZE) in the profile summaries.
     res = {"ms": ms, "tflops": flops / ms / 1e9, "mfma_util": flops / ms / 1e9 / BF16_PEAK_TFLOPS,
-           "flops": flops, "mean_cubes_selected": sel / (HEADS * cubes), "kv_bytes": kv_tile_rows * 512,
-           "kv_GBs": kv_tile_rows * 512 / ms / 1e6, "kv_frac": kv_tile_rows * 512 / ms / 1e6 / HBM_PEAK_GBS,
+           "flops": flops, "mean_cubes_selected": sel / (HEADS * cubes), "kv_tile_bytes": kv_tile_rows * 512,
+           "kv_tile_GBs": kv_tile_rows * 512 / ms / 1e6,
            "flop_per_kv_byte": flops / (kv_tile_rows * 512), "dense_equivalent_flops": dense_flops,
            "pass_list_overlap": pass_list_overlap(idx, cnt, cubes),
            "shape": {"heads": HEADS, "grid": list(GRID), "cubes": cubes, "dense_rows": n_dense, "k": kk}}
@@ -338,6 +344,41 @@ def bench_attn(mh, dev, steps, warmup, shared=False):
     torch.cuda.empty_cache()
     if not shared:
         res["shared_waves"] = bench_attn(mh, dev, steps, warmup, shared=True)
+    return res
+
+
+def bench_cond(mh, dev, steps, warmup):
+    """The modulation table's producer at H3's shapes (docs/architecture.md:49-52): the time MLP (256 -> 5376 -> 2688,
+    float weights, 63 MB) for three levels, and one block's AdaLN projection (bf16 [96,768][2688], 520 MB) for one
+    and three levels, each against HBM: their bytes are the weights read once (plus the small vectors)."""
+    g = torch.Generator(device=dev).manual_seed(11)
+    res = {}
+    w_in = torch.randn((5376, 256), generator=g, device=dev) / 16
+    b_in = torch.randn(5376, generator=g, device=dev) * 0.1
+    w_out = torch.randn((2688, 5376), generator=g, device=dev) / 73
+    b_out = torch.randn(2688, generator=g, device=dev) * 0.1
+    t = torch.tensor([0.9230769, 0.5, 0.999], device=dev)
+    ws = torch.empty(mh.time_embed_workspace_bytes(3, 256, 5376, 2688), dtype=torch.uint8, device=dev)
+    temb = torch.empty((3, 2688), device=dev)
+    cond = torch.empty((3, 2688), dtype=torch.bfloat16, device=dev)
+    ms, _ = time_launches(lambda: mh.time_embed(t, w_in, b_in, w_out, b_out, workspace=ws, temb=temb, cond=cond),
+                          steps, warmup)
+    nb = (5376 * 256 + 5376 + 2688 * 5376 + 2688) * 4
+    res["time_embed"] = {"ms": ms, "bytes": nb, "GBs": nb / ms / 1e6, "frac": nb / ms / 1e6 / HBM_PEAK_GBS,
+                         "shape": {"levels": 3, "freq_dim": 256, "hidden": 5376, "out_dim": 2688}}
+    n, k = 18 * 5376, 2688
+    w = (0.02 * torch.randn((n, k), generator=g, device=dev)).to(torch.bfloat16)
+    bias = torch.randn(n, generator=g, device=dev) * 0.01
+    for levels in (1, 3):
+        c = cond[:levels].contiguous()
+        out = torch.empty((levels, n), device=dev)
+        ms, _ = time_launches(lambda: mh.adaln_mod(c, w, bias, out=out), steps, warmup)
+        cold, _ = time_launches(lambda: mh.adaln_mod(c, w, bias, out=out), steps, warmup, cold=True)
+        nb = n * k * 2 + n * 4 + levels * n * 4
+        res[f"adaln_mod_{levels}_levels"] = {"ms": ms, "cold_ms": cold, "bytes": nb, "GBs": nb / ms / 1e6,
+                                             "frac": nb / ms / 1e6 / HBM_PEAK_GBS,
+                                             "cold_frac": nb / cold / 1e6 / HBM_PEAK_GBS,
+                                             "shape": {"levels": levels, "n": n, "k": k}}
     return res
 
 
@@ -361,16 +402,8 @@ def bench_heads(mh, dev, steps, warmup):
     nbytes = rows * 3 * HEADS * 128 * 4 + rows * 48 * 8
     res = {"ms": ms, "bytes": nbytes, "GBs": nbytes / ms / 1e6, "frac": nbytes / ms / 1e6 / HBM_PEAK_GBS,
            "shape": {"rows": rows, "heads": HEADS, "rot": 96}}
-    # Gathered through the cube map: text rows first in the model (rows 0..511), the video grid after them.
-    cubes = mh.cube_count(*GRID)
-    l = torch.arange(64, device=dev)
-    c = torch.arange(cubes, device=dev)[:, None]
-    ch, cw = Y // 4, X // 4
-    t = 4 * (c // (ch * cw)) + l // 16
-    y = 4 * (c // cw % ch) + l // 4 % 4
-    xx = 4 * (c % cw) + l % 4
-    cube_rows = (n_dense + (t * Y + y) * X + xx).reshape(-1)
-    cmap = torch.cat([cube_rows, torch.arange(n_dense, device=dev)]).to(torch.int32)
+    # Gathered through the cube map (mh3_cube_map): text rows first in the model (rows 0..511), the video grid after them.
+    cmap, _ = mh.cube_map(GRID, n_dense=n_dense, video_row0=n_dense, dense_row0=0, device=dev)
     del outs
     gout = [torch.empty((HEADS, cmap.numel(), 128), dtype=torch.bfloat16, device=dev) for _ in range(3)]
     gms, _ = time_launches(lambda: mh.heads_partial(x, HEADS, qw, kw, ct, st, map=cmap, q=gout[0], k=gout[1],
@@ -519,6 +552,17 @@ def bench_share(mh, dev, steps, warmup, gpus=8):
     return res
 
 
+def cpu_model() -> str:
+    """The host CPU's model name from /proc/cpuinfo (the machine type where the file has none)."""
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return platform.processor() or platform.machine()
+
+
 def cpu_baseline(seconds: float = 10.0) -> dict:
     """The scalar C oracle of the fused op on one host core, on a sample of the 768p rows sized to ~`seconds`."""
     sys.path.insert(0, str(REPO / "oracle"))
@@ -552,9 +596,9 @@ def cpu_baseline(seconds: float = 10.0) -> dict:
         list(ex.map(lambda c: orc.rms_mod_gate_add_rows(x[c[0]:c[-1] + 1], r[c[0]:c[-1] + 1], w, sh, sc, ga),
                     [c for c in chunks if len(c)]))
         tp = time.perf_counter() - t0
-    return {"value": gbs, "unit": "GB/s", "cores": 1, "kind": "port",
+    return {"value": gbs, "unit": "GB/s", "cores": 1, "kind": "port", "cpu": cpu_model(),
             "sample": f"fused modulated RMS norm + gated residual over {n} of the {ROWS} rows x {DIM} bf16 "
-                      f"({t:.1f} s), scalar C oracle, one thread on {platform.processor() or platform.machine()}",
+                      f"({t:.1f} s), scalar C oracle, one thread on {cpu_model()}",
             "row_parallel": {"value": n * DIM * 6 / tp / 1e9, "unit": "GB/s", "cores": cores,
                              "sample": f"the same {n} rows split over {cores} threads ({tp:.2f} s)"}}
 
@@ -646,7 +690,7 @@ def cpu_baseline_configs(gpu: dict) -> dict:
                                "sample": f"4 rows on one thread, {cores} x 4 rows on {cores} threads",
                                "gpu": fc.get("tflops")}
     out["cores"] = cores
-    out["cpu"] = platform.processor() or platform.machine()
+    out["cpu"] = cpu_model()
     return out
 
 
@@ -655,7 +699,7 @@ def main() -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--only", default="fused,block_order,copy,swiglu,select,heads,attn,proj,fc1,rms_f32,share")
+    ap.add_argument("--only", default="fused,block_order,copy,swiglu,select,cond,heads,attn,proj,fc1,rms_f32,share")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-compare", action="store_true")
     args = ap.parse_args()
@@ -689,6 +733,9 @@ def main() -> int:
         torch.cuda.empty_cache()
     if "select" in ops:
         report["cube_selector"] = bench_select(mh, dev, args.steps, args.warmup)
+        torch.cuda.empty_cache()
+    if "cond" in ops:
+        report["modulation"] = bench_cond(mh, dev, args.steps, args.warmup)
         torch.cuda.empty_cache()
     if "heads" in ops:
         report["heads_partial"] = bench_heads(mh, dev, args.steps, args.warmup)

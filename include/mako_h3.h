@@ -29,7 +29,7 @@
 extern "C" {
 #endif
 
-#define MH3_ABI_VERSION 2
+#define MH3_ABI_VERSION 3
 
 /* ---- error codes ------------------------------------------------------------------------------------------------ */
 enum {
@@ -168,6 +168,23 @@ int mh3_cube_topk(const MH3CubeArgs* args, const float* s, int32_t* idx, int32_t
 int mh3_cube_select(const MH3CubeArgs* args, const float* qc, const float* kc, int32_t* idx, int32_t* cnt,
                     mh3_stream_t stream);
 
+/* H3::Cubes' map (docs/architecture.md:120-125), built in the reference's begin(): the attention's row order, the
+ * generated video rows in 4x4x4 cubes of (latent frame, patch row, patch column), the grid padded to multiples of 4
+ * with rows that are no token, then the dense rows (text, keyframe and audio), which every query attends. For
+ * attention row r < cubes * 64 (cube c = r / 64, slot l = r % 64 = (dt * 4 + dy) * 4 + dx, token
+ * (t, y, x) = (4 ct + dt, 4 cy + dy, 4 cx + dx)): map[r] = video_row0 + (t * grid_h + y) * grid_w + x, the token's
+ * model row, or -1 where (t, y, x) lies in the padding (the row's validity is map[r] >= 0). For r = cubes * 64 + j,
+ * j < n_dense: map[r] = dense_row0 + j. counts[c] = cube c's token count (int32 [cubes], may be NULL). map is int32
+ * [cubes * 64 + n_dense], the map mh3_heads_partial gathers through (its rows then come out in the MH3_CUBES_GATHERED
+ * order). Model rows must fit int32, and the dense rows may not overlap the video rows (MH3_ERR_PARAM). */
+typedef struct MH3CubeMapArgs {
+    uint32_t grid_t, grid_h, grid_w;
+    uint32_t n_dense;    /* dense rows after the cubes; 0 allowed */
+    uint64_t video_row0; /* model row of video token (0, 0, 0); the grid follows frame-major, then row-major */
+    uint64_t dense_row0; /* model row of the first dense row; the dense rows are consecutive model rows */
+} MH3CubeMapArgs;
+int mh3_cube_map(const MH3CubeMapArgs* args, int32_t* map, int32_t* counts, mh3_stream_t stream);
+
 /* ---- heads_partial ------------------------------------------------------------------------------------------------
  * Reference kernel `heads_partial` (mako-common; docs/architecture.md:35-38,61-63,123-125; docs/performance.md:44):
  * the step between the QKV GEMM and attention. qkv holds one model row a row, [q (heads x 128) | k (heads x 128) |
@@ -289,6 +306,55 @@ int mh3_gemm(const MH3GemmArgs* args, uint32_t form, const void* x, const float*
 int mh3_gemm_gate_add(const MH3GemmArgs* args, uint32_t form, const void* x, const float* x_scale, const void* w,
                       const float* w_scale, const float* gate, const uint8_t* set_of_row, uint16_t* residual,
                       mh3_stream_t stream);
+
+/* ---- time conditioning: the producer of the modulation table ---------------------------------------------------
+ * What turns a step's distinct noise levels t = 1 - sigma (one to three in H3) into the [U][3][6][D] modulation
+ * table that the row kernels read through set_stride (docs/architecture.md:49-58; written out in torch in
+ * tools/check_pruned_curve.py:57-73; compared in tests/h3_ref_test.cpp:226-241).
+ *
+ * mh3_time_embed: for each level u,
+ *   emb = [cos(t[u] f_0) .. cos(t[u] f_{h-1}), sin(t[u] f_0) .. sin(t[u] f_{h-1})], h = freq_dim / 2,
+ *         f_i = exp(-ln(max_period) i / h)  (the sinusoidal embedding, cos half first);
+ *   hid = silu(w_in emb + b_in)              (w_in float [hidden][freq_dim], b_in [hidden]);
+ *   temb[u] = w_out hid + b_out              (w_out float [out_dim][hidden], b_out [out_dim]): the F32 time MLP;
+ *   cond[u] = bf16(silu(temb[u]))            (rounded once, to nearest even): the AdaLN projections' input.
+ * t is float [levels] in device memory; temb is float [levels][out_dim]; cond is bf16 [levels][out_dim] (may be
+ * NULL); b_in and b_out may be NULL (zero). The embedding is computed in double, the MLP in float. `workspace` holds
+ * the hidden layer: at least mh3_time_embed_workspace_bytes(args) bytes of device memory, 16-byte aligned, which the
+ * call overwrites (a negative code from the query for invalid args). */
+typedef struct MH3TimeArgs {
+    uint32_t levels;   /* 1 .. 64 */
+    uint32_t freq_dim; /* a multiple of 8, <= 1024 (H3: 256) */
+    uint32_t hidden;   /* a multiple of 4, <= 8192 (H3: 5376) */
+    uint32_t out_dim;  /* >= 1 (H3: 2688) */
+    float max_period;  /* > 1 (H3: 10000) */
+    uint32_t reserved[3];
+} MH3TimeArgs;
+int64_t mh3_time_embed_workspace_bytes(const MH3TimeArgs* args);
+int mh3_time_embed(const MH3TimeArgs* args, const float* t, const float* w_in, const float* b_in, const float* w_out,
+                   const float* b_out, void* workspace, uint64_t workspace_bytes, float* temb, uint16_t* cond,
+                   mh3_stream_t stream);
+/* A block's AdaLN projection (and the final layer's, n = 2 D): mod[u][r] = w[r] . cond[u] + bias[r] in float
+ * accumulation, u < args->m levels, r < args->n. cond is bf16 [m][k] (mh3_time_embed's output), w bf16 [n][k] (the
+ * weight's output rows), bias float [n] (may be NULL), mod float [m][n]. With n = 3 * 6 * D the rows of a level are
+ * its [3 tags][6 vectors][D], so mod is the [U][3][6][D] table whose set (u, tag) the row kernels take at
+ * set_stride = 6 D. k % 8 == 0 and k <= 4096, else MH3_ERR_SHAPE / MH3_ERR_UNSUPPORTED; m <= 64; cond and w 16-byte
+ * aligned. args->n_sets and gate_stride are not used. */
+int mh3_adaln_mod(const MH3GemmArgs* args, const uint16_t* cond, const uint16_t* w, const float* bias, float* mod,
+                  mh3_stream_t stream);
+/* The pruned checkpoints' path (docs/architecture.md:53-58, tools/check_pruned_curve.py:69-73): no time MLP; a curve
+ * c(t) is tabulated at `points` values of t over [0, 1] (table float [points][width], H3: [1025][8]) and read with
+ * linear interpolation at pos = t (points - 1), clamped to [0, points - 1]: i0 = min(floor(pos), points - 2),
+ * f = pos - i0, c = (1 - f) table[i0] + f table[i0 + 1]; then mod[u][r] = w[r] . c(t[u]) + bias[r] in float, with w
+ * float [n][width] and no silu. t is float [levels] in device memory; bias may be NULL. */
+typedef struct MH3CurveArgs {
+    uint32_t levels; /* 1 .. 64 */
+    uint32_t n;      /* outputs a level */
+    uint32_t points; /* >= 2 */
+    uint32_t width;  /* 1 .. 32 (H3: 8) */
+} MH3CurveArgs;
+int mh3_curve_mods(const MH3CurveArgs* args, const float* t, const float* table, const float* w, const float* bias,
+                   float* mod, mh3_stream_t stream);
 
 #ifdef __cplusplus
 }

@@ -225,6 +225,45 @@ public:
         check(mh3_cube_select(&a, qc, kc, idx, cnt, s_), "cube_scores+cube_topk");
     }
 
+    // H3::Cubes' map of begin(): attention row -> model row (-1 for a cube's padding slot), the cubes' 64 rows each
+    // and then the n_dense dense rows; counts (may be null) the cubes' token counts.
+    void cube_map(uint32_t grid_t, uint32_t grid_h, uint32_t grid_w, uint32_t n_dense, uint64_t video_row0,
+                  uint64_t dense_row0, int32_t* map, int32_t* counts = nullptr) const
+    {
+        const MH3CubeMapArgs a{grid_t, grid_h, grid_w, n_dense, video_row0, dense_row0};
+        check(mh3_cube_map(&a, map, counts, s_), "H3::Cubes");
+    }
+
+    // A step's conditioning: the sinusoidal embedding of each level t[u] through the F32 time MLP (temb) and
+    // bf16(silu(temb)) (cond), with `workspace` of at least time_embed_workspace_bytes() bytes for its hidden layer.
+    static uint64_t time_embed_workspace_bytes(const MH3TimeArgs& a)
+    {
+        const int64_t n = mh3_time_embed_workspace_bytes(&a);
+        check(n < 0 ? int(n) : MH3_OK, "time_embed");
+        return uint64_t(n);
+    }
+    void time_embed(const MH3TimeArgs& a, const float* t, const float* w_in, const float* b_in, const float* w_out,
+                    const float* b_out, void* workspace, uint64_t workspace_bytes, float* temb, uint16_t* cond) const
+    {
+        check(mh3_time_embed(&a, t, w_in, b_in, w_out, b_out, workspace, workspace_bytes, temb, cond, s_),
+              "time_embed");
+    }
+    // A block's AdaLN projection: mod[levels][n] = w cond^T + bias, n = 3 x 6 x dim (the [U][3][6][D] table whose
+    // (level, tag) sets the row kernels read at set_stride = 6 dim).
+    void adaln_mod(uint32_t levels, uint32_t n, uint32_t k, const uint16_t* cond, const uint16_t* w, const float* bias,
+                   float* mod) const
+    {
+        const MH3GemmArgs a{levels, n, k, 0, 0, 0};
+        check(mh3_adaln_mod(&a, cond, w, bias, mod, s_), "adaln_proj");
+    }
+    // The pruned checkpoints' modulation: the curve table interpolated at each t, through w [n][width] plus bias.
+    void curve_mods(uint32_t levels, uint32_t n, uint32_t points, uint32_t width, const float* t, const float* table,
+                    const float* w, const float* bias, float* mod) const
+    {
+        const MH3CurveArgs a{levels, n, points, width};
+        check(mh3_curve_mods(&a, t, table, w, bias, mod, s_), "curve_mods");
+    }
+
     // After the QKV GEMM: the per-head RMS norm and rotary positions of q and k, v copied, written as head tiles;
     // with a cube map (map[r] = model row, -1 padding) in the cube order cube_pool, cube_select and
     // flash_attn_sparse_128 read as MH3_CUBES_GATHERED. v == nullptr skips v.

@@ -36,7 +36,7 @@ COMMON = [
     f"-I{REPO / 'include'}",
     f"-I{CSRC}",
 ]
-SOURCES = ["rows.hip", "heads.hip", "cubes.hip", "quant.hip", "gemm.hip", "attn.hip", "abi.cpp"]
+SOURCES = ["rows.hip", "cond.hip", "heads.hip", "cubes.hip", "quant.hip", "gemm.hip", "attn.hip", "abi.cpp"]
 # The streaming-bandwidth probe bench.py reports beside the kernels: its own library, not part of the C-ABI.
 PROBE_SOURCE = "probe/stream_probe.hip"
 PROBE_LIB = PKG / "lib" / "libmh3_stream_probe.so"

@@ -44,16 +44,10 @@ typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef float floatx16 __attribute__((ext_vector_type(16)));
 
 constexpr uint32_t kAttnThreads = 128;
-#ifndef MH3_ATTN_XCD
-#define MH3_ATTN_XCD 1 // map each XCD to a contiguous eighth of every head's query cubes
-#endif
-#ifndef MH3_ATTN_SWEEP
-#define MH3_ATTN_SWEEP 1 // rotate each cube tile's pass list so an XCD's resident tiles sweep the keys together
-#endif
-#ifndef MH3_ATTN_STAGES
-#define MH3_ATTN_STAGES 1 // K/V stages in LDS (2 overlaps a tile's loads with the previous tile's MFMAs but halves
-                          // the workgroups a CU holds; one stage and two waves a SIMD measured faster)
-#endif
+constexpr bool kAttnXcd = true;   // map each XCD to a contiguous eighth of every head's query cubes
+constexpr bool kAttnSweep = true; // rotate each cube tile's pass list so an XCD's resident tiles sweep the keys together
+constexpr int kAttnStages = 1;    // K/V stages in LDS (2 overlaps a tile's loads with the previous tile's MFMAs but
+                                  // halves the workgroups a CU holds; one stage and two waves a SIMD measured faster)
 constexpr uint32_t kNoTile = 0xffffffffu;
 
 struct AttnParams {
@@ -448,16 +442,16 @@ extern "C" int mh3_flash_attn_sparse_128(const MH3AttnArgs* args, const uint16_t
     p.div_plane = FastDiv::make(p.plane);
     p.div_cw = FastDiv::make(p.cw);
     p.nd = uint32_t(nd), p.layout = c.layout, p.out_stride = c.out_stride;
-    p.xcd_slices = MH3_ATTN_XCD && cubes % 8u == 0 && (nd * c.heads) % 8u == 0 ? 1u : 0u;
+    p.xcd_slices = kAttnXcd && cubes % 8u == 0 && (nd * c.heads) % 8u == 0 ? 1u : 0u;
     const float scale = args->scale > 0.0f ? args->scale : 0.08838834764831845f; // 1 / sqrt(128)
     p.scale_log2 = scale * 1.4426950408889634f;
     const uint64_t blocks = (cubes + nd) * c.heads;
-    constexpr int kStages = MH3_ATTN_STAGES;
+    constexpr int kStages = kAttnStages;
     const void* kern = reinterpret_cast<const void*>(&attn_sparse_kernel<kStages>);
     const size_t lds = size_t(kStages) * kStageBytes;
     if (hipFuncSetAttribute(kern, hipFuncAttributeMaxDynamicSharedMemorySize, int(lds)) != hipSuccess)
         return MH3_ERR_HIP;
-    if (MH3_ATTN_SWEEP && p.xcd_slices) {
+    if (kAttnSweep && p.xcd_slices) {
         int per_cu = 0;
         if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kern, int(kAttnThreads), lds) != hipSuccess)
             return MH3_ERR_HIP;

@@ -518,6 +518,35 @@ __global__ __launch_bounds__(kSelectThreads) void cube_select_kernel(CubeGeo g, 
     }
 }
 
+// H3::Cubes' map (docs/architecture.md:120-125): attention row 64 c + l is cube c's slot l = (dt * 4 + dy) * 4 + dx,
+// i.e. video token (4 ct + dt, 4 cy + dy, 4 cx + dx), whose model row is video_row0 + (t * grid_h + y) * grid_w + x,
+// or -1 where the slot lies in the grid's padding; attention rows cubes * 64 + j are the dense rows
+// dense_row0 + j. counts[c] is cube c's token count. A thread an attention row.
+struct CubeMapParams {
+    uint32_t gt, gh, gw, ch, cw, plane, cubes, n_dense;
+    uint64_t video_row0, dense_row0;
+};
+
+__global__ __launch_bounds__(256) void cube_map_kernel(CubeMapParams p, int32_t* __restrict__ map,
+                                                       int32_t* __restrict__ counts)
+{
+    const uint64_t r = uint64_t(blockIdx.x) * 256u + threadIdx.x;
+    const uint64_t video = uint64_t(p.cubes) * 64u;
+    if (r < video) {
+        const uint32_t c = uint32_t(r >> 6), l = uint32_t(r & 63u);
+        const uint32_t ct = c / p.plane, rem = c - ct * p.plane, cy = rem / p.cw, cx = rem - cy * p.cw;
+        const uint32_t t = 4u * ct + (l >> 4), y = 4u * cy + ((l >> 2) & 3u), x = 4u * cx + (l & 3u);
+        const bool ok = t < p.gt && y < p.gh && x < p.gw;
+        map[r] = ok ? int32_t(p.video_row0 + (uint64_t(t) * p.gh + y) * p.gw + x) : -1;
+        if (counts && l == 0) {
+            const uint32_t nt = min(4u, p.gt - 4u * ct), ny = min(4u, p.gh - 4u * cy), nx = min(4u, p.gw - 4u * cx);
+            counts[c] = int32_t(nt * ny * nx);
+        }
+    } else if (r < video + p.n_dense) {
+        map[r] = int32_t(p.dense_row0 + (r - video));
+    }
+}
+
 } // namespace mh3
 
 // ---- C-ABI ----------------------------------------------------------------------------------------------------------
@@ -568,6 +597,33 @@ int set_lds_limit(const void* kernel, size_t bytes)
 } // namespace
 
 extern "C" {
+
+int mh3_cube_map(const MH3CubeMapArgs* args, int32_t* map, int32_t* counts, mh3_stream_t stream)
+{
+    if (!args)
+        return MH3_ERR_POINTER;
+    if (args->grid_t == 0 || args->grid_h == 0 || args->grid_w == 0)
+        return MH3_ERR_SHAPE;
+    const uint64_t cubes = uint64_t((args->grid_t + 3u) / 4u) * ((args->grid_h + 3u) / 4u) * ((args->grid_w + 3u) / 4u);
+    const uint64_t tokens = uint64_t(args->grid_t) * args->grid_h * args->grid_w;
+    const uint64_t rows = cubes * 64u + args->n_dense;
+    const uint64_t lim = uint64_t(INT32_MAX);
+    // Model rows are int32 in the map; the dense rows may not be video rows.
+    if (rows > lim || args->video_row0 + tokens > lim + 1u || args->dense_row0 + args->n_dense > lim + 1u)
+        return MH3_ERR_SHAPE;
+    if (args->n_dense && args->dense_row0 < args->video_row0 + tokens &&
+        args->video_row0 < args->dense_row0 + args->n_dense)
+        return MH3_ERR_PARAM;
+    if (!map)
+        return MH3_ERR_POINTER;
+    CubeMapParams p;
+    p.gt = args->grid_t, p.gh = args->grid_h, p.gw = args->grid_w;
+    p.ch = (p.gh + 3u) / 4u, p.cw = (p.gw + 3u) / 4u, p.plane = p.ch * p.cw, p.cubes = uint32_t(cubes);
+    p.n_dense = args->n_dense, p.video_row0 = args->video_row0, p.dense_row0 = args->dense_row0;
+    hipLaunchKernelGGL(cube_map_kernel, dim3(uint32_t((rows + 255u) / 256u)), dim3(256), 0,
+                       static_cast<hipStream_t>(stream), p, map, counts);
+    return host::check_launch();
+}
 
 int mh3_cube_pool(const MH3CubeArgs* args, const uint16_t* q, const uint16_t* k, float* qc, float* kc,
                   int32_t* counts, mh3_stream_t stream)

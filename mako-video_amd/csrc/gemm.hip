@@ -41,10 +41,7 @@ constexpr uint32_t kBM = 256, kBN = 128, kBK = 64;
 constexpr uint32_t kStageChunks = 2048, kAStages = 3, kBStages = 2;
 constexpr uint32_t kBBase = kAStages * kStageChunks;
 constexpr size_t kGemmLds = size_t(kAStages + kBStages) * kStageChunks * 16;
-#ifndef MH3_GEMM_BAND
-#define MH3_GEMM_BAND 4 // row tiles an XCD sweeps across all column tiles before moving on
-#endif
-constexpr uint32_t kBandM = MH3_GEMM_BAND;
+constexpr uint32_t kBandM = 4; // row tiles an XCD sweeps across all column tiles before moving on
 
 typedef __attribute__((address_space(3))) void* lds_ptr_t;
 
@@ -100,12 +97,8 @@ __device__ __forceinline__ void lds_barrier()
     asm volatile("" ::: "memory");
 }
 
-#ifndef MH3_GEMM_WM
-#define MH3_GEMM_WM 2 // wavefronts along the tile's rows
-#endif
-#ifndef MH3_GEMM_WN
-#define MH3_GEMM_WN 4 // wavefronts along its columns
-#endif
+constexpr int kGemmWM = 2; // wavefronts along the tile's rows
+constexpr int kGemmWN = 4; // wavefronts along its columns
 
 // The three fc1 forms: int8 weights widened to bf16 with bf16 activations (weight-only), bf16 weights, and int8
 // weights with int8 activations (each row of x with its own scale) on the int8 MFMA.
@@ -133,7 +126,7 @@ typedef int int32x16 __attribute__((ext_vector_type(16)));
 // (32 columns each, from wn * 32 TN) and the TN matching up column tiles. Every LDS row holds 128 bytes of k: 64 k of
 // bf16 or 128 k of int8, so a K-step is 64 or 128 k.
 template <int WM, int WN, int MODE, int EPI>
-__global__ __launch_bounds__(MH3_GEMM_WM * MH3_GEMM_WN * 64) void gemm_kernel(
+__global__ __launch_bounds__(kGemmWM * kGemmWN * 64) void gemm_kernel(
     const void* __restrict__ xv, const void* __restrict__ wv, const float* __restrict__ scale,
     const float* __restrict__ xscale, uint16_t* __restrict__ out, uint32_t M, uint32_t N, uint32_t K, uint32_t mt,
     uint32_t nt, GemmGate gg)
@@ -465,7 +458,13 @@ int launch_gemm(const MH3GemmArgs* a, const void* x, const void* w, const float*
         return gg.gate ? MH3_ERR_PARAM : MH3_ERR_POINTER;
     if (!host::aligned16(x) || !host::aligned16(w) || !host::aligned16(out))
         return MH3_ERR_ALIGN;
-    constexpr int WM = MH3_GEMM_WM, WN = MH3_GEMM_WN;
+    // The output (for the gate-add epilogue, the residual updated in place) may not overlap an operand: while one
+    // tile writes its columns, the other tiles of its row band still read the same rows of x.
+    const uint64_t out_bytes = uint64_t(a->m) * a->n * 2u;
+    if (host::overlaps(out, out_bytes, x, uint64_t(a->m) * a->k * kEA) ||
+        host::overlaps(out, out_bytes, w, w_rows * a->k * kEB))
+        return MH3_ERR_PARAM;
+    constexpr int WM = kGemmWM, WN = kGemmWN;
     const void* kernel = reinterpret_cast<const void*>(&gemm_kernel<WM, WN, MODE, EPI>);
     static const int lds_ok = hipFuncSetAttribute(kernel, hipFuncAttributeMaxDynamicSharedMemorySize, int(kGemmLds));
     if (lds_ok != hipSuccess)

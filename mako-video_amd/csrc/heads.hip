@@ -149,13 +149,6 @@ __global__ __launch_bounds__(kHeadsThreads) void heads_kernel(HeadsParams p)
     }
 }
 
-// Whether [a, a + an) and [b, b + bn) (bytes) overlap.
-bool overlaps(const void* a, uint64_t an, const void* b, uint64_t bn)
-{
-    const uintptr_t x = reinterpret_cast<uintptr_t>(a), y = reinterpret_cast<uintptr_t>(b);
-    return x < y + bn && y < x + an;
-}
-
 } // namespace
 } // namespace mh3
 
@@ -191,7 +184,7 @@ extern "C" int mh3_heads_partial(const MH3HeadsArgs* args, const uint16_t* qkv, 
         ((uint64_t(a.heads) - 1) * a.out_head_stride + (uint64_t(a.rows) - 1) * a.out_row_stride + 128u) * 2u;
     uint16_t* outs[3] = {q, k, v};
     for (int t = 0; t < 3; ++t) {
-        if (!outs[t] || !overlaps(outs[t], out_bytes, qkv, qkv_bytes))
+        if (!outs[t] || !host::overlaps(outs[t], out_bytes, qkv, qkv_bytes))
             continue;
         const bool in_place = !map && outs[t] == qkv + uint64_t(t) * a.heads * 128u && a.out_head_stride == 128u &&
                               a.out_row_stride == a.qkv_stride;

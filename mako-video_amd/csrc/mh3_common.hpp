@@ -162,6 +162,12 @@ int cu_count();
 int blocks_per_cu(const void* kernel, int block, size_t lds);
 
 inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+// Whether the byte ranges [a, a + an) and [b, b + bn) share a byte.
+inline bool overlaps(const void* a, uint64_t an, const void* b, uint64_t bn)
+{
+    const uintptr_t x = reinterpret_cast<uintptr_t>(a), y = reinterpret_cast<uintptr_t>(b);
+    return an && bn && x < y + bn && y < x + an;
+}
 // Lets `kernel` take `bytes` of dynamic LDS on the current device (hipFuncSetAttribute, once per kernel and device).
 hipError_t allow_dynamic_lds(const void* kernel, size_t bytes);
 

@@ -4,6 +4,8 @@
 //   kind 1 (copy):  c = a;                                 one read stream, one write stream;
 //   kind 2 (r2w1):  c = a + b (as 32-bit lanes);            two read streams, one write: the fused row op's and
 //                                                           SwiGLU's mix.
+// Kinds 3, 4 and 5 are the same three mixes through buffer loads and stores (a descriptor over each whole buffer,
+// 32-bit byte offsets, so n * 16 < 2^32), the access form the row kernels use, with a flat grid only.
 // 256 threads a workgroup; each thread moves U vectors 256 apart per step, non-temporal loads and stores; a flat grid
 // (blocks = 0: one step a thread) or a grid-stride loop over `blocks` workgroups. Every access is i < n. bench.py
 // sweeps U and the grid and reports the best of each mix as the ceiling.
@@ -55,6 +57,40 @@ __global__ __launch_bounds__(kThreads) void stream_kernel(const u32x4* __restric
         c[0] = u32x4{acc, 0u, 0u, 0u};
 }
 
+constexpr int kRsrcFlags = 0x00020000; // raw buffer, 32-bit byte offsets; out-of-range reads return 0
+constexpr int kNonTemporal = 2;
+
+// The buffer-op form, flat grid: workgroup g's thread t takes vectors g * 256 U + t + 256 j, j < U.
+template <int KIND, int U>
+__global__ __launch_bounds__(kThreads) void stream_buffer_kernel(const u32x4* a, const u32x4* b, u32x4* c, uint32_t n)
+{
+    const uint32_t bytes = n * 16u;
+    const auto ra = __builtin_amdgcn_make_buffer_rsrc(const_cast<u32x4*>(a), 0, int(bytes), kRsrcFlags);
+    const auto rb = __builtin_amdgcn_make_buffer_rsrc(const_cast<u32x4*>(b ? b : a), 0, int(bytes), kRsrcFlags);
+    const auto rc = __builtin_amdgcn_make_buffer_rsrc(c, 0, int(bytes), kRsrcFlags);
+    const uint32_t base = (blockIdx.x * kThreads * U + threadIdx.x) * 16u;
+    u32x4 va[U], vb[U];
+#pragma unroll
+    for (int j = 0; j < U; ++j) {
+        va[j] = __builtin_amdgcn_raw_buffer_load_b128(ra, base + uint32_t(j) * kThreads * 16u, 0, kNonTemporal);
+        if constexpr (KIND == 5)
+            vb[j] = __builtin_amdgcn_raw_buffer_load_b128(rb, base + uint32_t(j) * kThreads * 16u, 0, kNonTemporal);
+    }
+    if constexpr (KIND == 3) {
+        uint32_t acc = 0;
+#pragma unroll
+        for (int j = 0; j < U; ++j)
+            acc ^= va[j][0] ^ va[j][1] ^ va[j][2] ^ va[j][3];
+        if (acc == 0x9E3779B9u)
+            __builtin_amdgcn_raw_buffer_store_b128(u32x4{acc, 0u, 0u, 0u}, rc, 0, 0, 0);
+    } else {
+#pragma unroll
+        for (int j = 0; j < U; ++j)
+            __builtin_amdgcn_raw_buffer_store_b128(KIND == 5 ? va[j] + vb[j] : va[j], rc,
+                                                   base + uint32_t(j) * kThreads * 16u, 0, kNonTemporal);
+    }
+}
+
 template <int KIND>
 void launch(int unroll, dim3 grid, hipStream_t s, const u32x4* a, const u32x4* b, u32x4* c, uint64_t n)
 {
@@ -66,17 +102,46 @@ void launch(int unroll, dim3 grid, hipStream_t s, const u32x4* a, const u32x4* b
         hipLaunchKernelGGL((stream_kernel<KIND, 8>), grid, dim3(kThreads), 0, s, a, b, c, n);
 }
 
+template <int KIND>
+void launch_buffer(int unroll, hipStream_t s, const u32x4* a, const u32x4* b, u32x4* c, uint32_t n)
+{
+    const dim3 grid{(n + kThreads * unroll - 1) / (kThreads * unroll)};
+    if (unroll == 2)
+        hipLaunchKernelGGL((stream_buffer_kernel<KIND, 2>), grid, dim3(kThreads), 0, s, a, b, c, n);
+    else if (unroll == 4)
+        hipLaunchKernelGGL((stream_buffer_kernel<KIND, 4>), grid, dim3(kThreads), 0, s, a, b, c, n);
+    else
+        hipLaunchKernelGGL((stream_buffer_kernel<KIND, 8>), grid, dim3(kThreads), 0, s, a, b, c, n);
+}
+
 } // namespace
 
 extern "C" int mh3_probe_stream(int kind, const void* a, const void* b, void* c, uint64_t n, int unroll,
                                 uint32_t blocks, void* stream)
 {
-    if (kind < 0 || kind > 2 || !a || !c || (kind == 2 && !b) || (unroll != 2 && unroll != 4 && unroll != 8))
+    if (kind < 0 || kind > 5 || !a || !c || ((kind == 2 || kind == 5) && !b) ||
+        (unroll != 2 && unroll != 4 && unroll != 8))
         return -1;
     if ((reinterpret_cast<uintptr_t>(a) | reinterpret_cast<uintptr_t>(b) | reinterpret_cast<uintptr_t>(c)) & 15u)
         return -2;
     if (n == 0)
         return 0;
+    if (kind >= 3) {
+        // Buffer offsets are 32-bit bytes: the vectors' byte extent, rounded up to the grid, must stay below 2^32.
+        if (blocks != 0 || n >= (uint64_t(1) << 28) - uint64_t(kThreads) * unroll)
+            return -1;
+        hipStream_t s = static_cast<hipStream_t>(stream);
+        const auto* pa = static_cast<const u32x4*>(a);
+        const auto* pb = static_cast<const u32x4*>(b);
+        auto* pc = static_cast<u32x4*>(c);
+        if (kind == 3)
+            launch_buffer<3>(unroll, s, pa, pb, pc, uint32_t(n));
+        else if (kind == 4)
+            launch_buffer<4>(unroll, s, pa, pb, pc, uint32_t(n));
+        else
+            launch_buffer<5>(unroll, s, pa, pb, pc, uint32_t(n));
+        return hipGetLastError() == hipSuccess ? 0 : -3;
+    }
     const uint64_t flat = (n + kThreads * unroll - 1) / (kThreads * unroll);
     const uint64_t grid_blocks = blocks ? (blocks < flat ? blocks : flat) : flat;
     if (grid_blocks >= (1ull << 31))

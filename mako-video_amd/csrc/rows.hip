@@ -310,12 +310,11 @@ __global__ __launch_bounds__(1024) void rows_kernel(RowsParams p)
 // of every set into LDS once; each wave holds a whole row (NV 16-byte vectors a lane of x, and of the residual) in
 // registers, reduces it with DPP and three cross-row reads, and streams the outputs one vector at a time, reading
 // that vector's coefficients from LDS just before use.
-#ifndef MH3_WAVE_BLOCK
-#define MH3_WAVE_BLOCK 704 // wave-kernel workgroup threads: 11 waves, measured best of 6 to 16 at one workgroup a CU
-#endif
+constexpr uint32_t kWaveBlock = 704; // wave-kernel workgroup threads: 11 waves, measured best of 6 to 16 at one
+                                     // workgroup a CU
 
 template <int DT, int NV, int OP, int SRC>
-__global__ __launch_bounds__(MH3_WAVE_BLOCK) void rows_wave_kernel(RowsParams p)
+__global__ __launch_bounds__(kWaveBlock) void rows_wave_kernel(RowsParams p)
 {
     using V = RowVec<DT>;
     constexpr int E = V::N;
@@ -497,12 +496,7 @@ using namespace mh3;
 constexpr size_t kCoefLdsMax = 64 * 1024;
 constexpr size_t kWaveLdsFloor = 81 * 1024; // above half of gfx950's 160 KiB: one wave-kernel workgroup a CU
 constexpr size_t kSwigluFusedLds = 40 * 1024; // four SwiGLU workgroups a CU (fused-row layout)
-#ifndef MH3_ROWS_PER_BLOCK
-#define MH3_ROWS_PER_BLOCK 0 // rows a workgroup streams through; 0: as many as keep every CU's slots busy once
-#endif
-#ifndef MH3_SWIGLU_U
-#define MH3_SWIGLU_U 1 // 16-byte vectors of gate (and of up) a thread has in flight
-#endif
+constexpr int kSwigluVecs = 1; // 16-byte vectors of gate (and of up) a thread has in flight
 
 template <int DT, int VPT, int OP>
 const void* pick_rows_kernel(int src)
@@ -513,17 +507,6 @@ const void* pick_rows_kernel(int src)
         return reinterpret_cast<const void*>(&rows_kernel<DT, VPT, OP, kCoefLds>);
     return reinterpret_cast<const void*>(&rows_kernel<DT, VPT, OP, kCoefGlobal>);
 }
-
-#ifndef MH3_WAVE_ROWS
-#define MH3_WAVE_ROWS 1 // rows each wavefront of the wave kernel takes; 0: a persistent grid
-#endif
-#ifndef MH3_ROWS_WAVE
-#define MH3_ROWS_WAVE 1 // one wavefront a row when the row fits 12 vectors a lane and the coefficients fit in LDS
-#endif
-
-#ifndef MH3_WAVE_SRC
-#define MH3_WAVE_SRC 1 // the wave kernel's coefficients: 1 an LDS table a workgroup builds, 2 the parameter vectors
-#endif
 
 template <int DT, int NV, int OP>
 const void* pick_wave_kernel(int src)
@@ -537,9 +520,8 @@ template <int DT, int OP>
 int launch_rows_wave(const RowsParams& p, hipStream_t stream)
 {
     const uint32_t need = (p.nvec + 63u) / 64u;
-    const int src = MH3_WAVE_SRC == kCoefLds && size_t(p.n_sets) * p.dim * kPlanes<OP> * sizeof(float) <= kCoefLdsMax
-                        ? kCoefLds
-                        : kCoefGlobal;
+    // The coefficients come from an LDS table the workgroup builds when it fits, else from the parameter vectors.
+    const int src = size_t(p.n_sets) * p.dim * kPlanes<OP> * sizeof(float) <= kCoefLdsMax ? kCoefLds : kCoefGlobal;
     const void* k = nullptr;
     if (need <= 2)
         k = pick_wave_kernel<DT, 2, OP>(src);
@@ -551,7 +533,7 @@ int launch_rows_wave(const RowsParams& p, hipStream_t stream)
         k = pick_wave_kernel<DT, 10, OP>(src);
     else
         k = pick_wave_kernel<DT, 12, OP>(src);
-    const uint32_t threads = MH3_WAVE_BLOCK, waves = threads / 64u;
+    const uint32_t threads = kWaveBlock, waves = threads / 64u;
     // The dynamic LDS is at least kWaveLdsFloor, so one workgroup (11 waves, 11 rows in flight) holds a CU: fewer rows
     // in flight streamed faster than the 2 to 4 workgroups the registers would allow (at 8 waves a workgroup: 5.96 to
     // 6.04 TB/s against 5.79 to 5.91 for the fused op at 768p, alternating runs on one GPU; 10 waves: 6.05), as fewer
@@ -561,20 +543,10 @@ int launch_rows_wave(const RowsParams& p, hipStream_t stream)
     const size_t lds = table > kWaveLdsFloor ? table : kWaveLdsFloor;
     if (host::allow_dynamic_lds(k, lds) != hipSuccess)
         return MH3_ERR_HIP;
+    // A row a wave; a persistent grid (rows_per_wave 0) measured slower.
     RowsParams arg = p;
-    uint64_t blocks;
-    constexpr uint32_t kWaveRows = MH3_WAVE_ROWS;
-    if constexpr (kWaveRows > 0) {
-        arg.rows_per_wave = kWaveRows;
-        blocks = (uint64_t(p.rows) + waves * kWaveRows - 1) / (waves * (kWaveRows > 0 ? kWaveRows : 1));
-    } else {
-        arg.rows_per_wave = 0;
-        const int per_cu = host::blocks_per_cu(k, int(threads), lds);
-        blocks = (p.rows + waves - 1) / waves;
-        const uint64_t cap = uint64_t(host::cu_count()) * per_cu;
-        if (blocks > cap)
-            blocks = cap;
-    }
+    arg.rows_per_wave = 1;
+    const uint64_t blocks = (uint64_t(p.rows) + waves - 1) / waves;
     void* args[] = {&arg};
     if (hipLaunchKernel(k, dim3(uint32_t(blocks)), dim3(threads), args, lds, stream) != hipSuccess)
         return host::check_launch() == MH3_OK ? MH3_ERR_HIP : MH3_ERR_HIP;
@@ -584,7 +556,8 @@ int launch_rows_wave(const RowsParams& p, hipStream_t stream)
 template <int DT, int OP>
 int launch_rows_dt(const RowsParams& p, hipStream_t stream)
 {
-    if (MH3_ROWS_WAVE && p.nvec <= 12u * 64u && size_t(p.n_sets) * p.dim * 2 * sizeof(float) <= kCoefLdsMax)
+    // One wavefront a row when the row fits 12 vectors a lane and the two-plane coefficient table fits in LDS.
+    if (p.nvec <= 12u * 64u && size_t(p.n_sets) * p.dim * 2 * sizeof(float) <= kCoefLdsMax)
         return launch_rows_wave<DT, OP>(p, stream);
     // (The choice between the two kernels depends on the two-plane table size for every op, so gate_add_mod reduces
     // in the same order as rms_mod and their norms agree bit for bit.)
@@ -604,15 +577,11 @@ int launch_rows_dt(const RowsParams& p, hipStream_t stream)
     }
     const size_t lds = 128 * sizeof(float) + (src == kCoefLds ? table : 0);
     const int per_cu = host::blocks_per_cu(k, int(threads), lds);
+    // As many workgroups as keep every CU's slots busy once; each streams through its share of the rows.
     uint64_t blocks = p.rows;
-    constexpr uint32_t kRowsPerBlock = MH3_ROWS_PER_BLOCK;
-    if constexpr (kRowsPerBlock > 0) {
-        blocks = (p.rows + kRowsPerBlock - 1) / (kRowsPerBlock > 0 ? kRowsPerBlock : 1);
-    } else {
-        const uint64_t cap = uint64_t(host::cu_count()) * per_cu;
-        if (blocks > cap)
-            blocks = cap;
-    }
+    const uint64_t cap = uint64_t(host::cu_count()) * per_cu;
+    if (blocks > cap)
+        blocks = cap;
     RowsParams arg = p;
     void* args[] = {&arg};
     if (hipLaunchKernel(k, dim3(uint32_t(blocks)), dim3(threads), args, lds, stream) != hipSuccess)
@@ -784,7 +753,7 @@ int mh3_swiglu_rows(const MH3SwigluArgs* a, const void* gate, const void* up, vo
     const uint4* u = a->layout == MH3_SWIGLU_FUSED ? g + vpr : static_cast<const uint4*>(up);
     const uint32_t stride = a->layout == MH3_SWIGLU_FUSED ? 2u * vpr : vpr;
     const uint32_t total = a->rows * vpr;
-    constexpr int U = MH3_SWIGLU_U;
+    constexpr int U = kSwigluVecs;
     const uint32_t blocks = (total + 256u * U - 1) / (256u * U);
     const FastDiv div = FastDiv::make(vpr);
     hipStream_t s = static_cast<hipStream_t>(stream);

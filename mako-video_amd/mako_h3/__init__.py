@@ -20,7 +20,7 @@ import torch
 
 _LIB_PATH = Path(os.environ.get("MAKO_H3_LIB", Path(__file__).resolve().parent.parent / "lib" / "libmako_h3.so"))
 
-ABI_VERSION = 2  # MH3_ABI_VERSION of include/mako_h3.h, whose structs this module mirrors
+ABI_VERSION = 3  # MH3_ABI_VERSION of include/mako_h3.h, whose structs this module mirrors
 OK, ERR_SHAPE, ERR_POINTER, ERR_ALIGN, ERR_PARAM, ERR_HIP, ERR_UNSUPPORTED = 0, -1, -2, -3, -4, -5, -6
 F32, BF16 = 0, 1
 SWIGLU_SPLIT, SWIGLU_FUSED = 0, 1
@@ -55,6 +55,20 @@ class HeadsArgs(C.Structure):
                 ("out_row_stride", C.c_uint64)]
 
 
+class CubeMapArgs(C.Structure):
+    _fields_ = [("grid_t", C.c_uint32), ("grid_h", C.c_uint32), ("grid_w", C.c_uint32), ("n_dense", C.c_uint32),
+                ("video_row0", C.c_uint64), ("dense_row0", C.c_uint64)]
+
+
+class TimeArgs(C.Structure):
+    _fields_ = [("levels", C.c_uint32), ("freq_dim", C.c_uint32), ("hidden", C.c_uint32), ("out_dim", C.c_uint32),
+                ("max_period", C.c_float), ("reserved", C.c_uint32 * 3)]
+
+
+class CurveArgs(C.Structure):
+    _fields_ = [("levels", C.c_uint32), ("n", C.c_uint32), ("points", C.c_uint32), ("width", C.c_uint32)]
+
+
 class QuantArgs(C.Structure):
     _fields_ = [("rows", C.c_uint32), ("cols", C.c_uint32), ("dtype", C.c_uint32), ("reserved", C.c_uint32)]
 
@@ -86,6 +100,11 @@ def _load() -> C.CDLL:
         "mh3_cube_scores": (I32, [C.POINTER(CubeArgs), P, P, P, P]),
         "mh3_cube_topk": (I32, [C.POINTER(CubeArgs), P, P, P, P]),
         "mh3_cube_select": (I32, [C.POINTER(CubeArgs), P, P, P, P, P]),
+        "mh3_cube_map": (I32, [C.POINTER(CubeMapArgs), P, P, P]),
+        "mh3_time_embed_workspace_bytes": (I64, [C.POINTER(TimeArgs)]),
+        "mh3_time_embed": (I32, [C.POINTER(TimeArgs), P, P, P, P, P, P, C.c_uint64, P, P, P]),
+        "mh3_adaln_mod": (I32, [C.POINTER(GemmArgs), P, P, P, P, P]),
+        "mh3_curve_mods": (I32, [C.POINTER(CurveArgs), P, P, P, P, P, P]),
         "mh3_heads_partial": (I32, [C.POINTER(HeadsArgs), P, P, P, P, P, P, P, P, P, P]),
         "mh3_flash_attn_sparse_128": (I32, [C.POINTER(AttnArgs), P, P, P, P, P, P, P]),
         "mh3_quant_rows_i8": (I32, [C.POINTER(QuantArgs), P, P, P, P]),
@@ -361,6 +380,115 @@ def cube_select(a: CubeArgs, qc, kc, *, idx=None, cnt=None):
     idx, cnt = _topk_out(a, qc.device, idx, cnt)
     _check(lib.mh3_cube_select(C.byref(a), _ptr(qc), _ptr(kc), _ptr(idx), _ptr(cnt), _stream()), "cube_select")
     return idx, cnt
+
+
+def cube_map(grid, *, n_dense=0, video_row0=None, dense_row0=0, device=None, map=None, counts=None):
+    """H3::Cubes' map: int32 [cubes * 64 + n_dense], attention row -> model row (-1 for a cube's padding slot), the
+    video grid's tokens at model rows video_row0 + (t * H + y) * W + x (default: right after the dense rows) and the
+    dense rows at dense_row0 ... Returns (map, counts), counts int32 [cubes] the cubes' token counts."""
+    gt, gh, gw = grid
+    a = CubeMapArgs()
+    a.grid_t, a.grid_h, a.grid_w, a.n_dense = gt, gh, gw, n_dense
+    a.video_row0 = dense_row0 + n_dense if video_row0 is None else video_row0
+    a.dense_row0 = dense_row0
+    cubes = cube_count(gt, gh, gw)
+    device = device or torch.device("cuda", torch.cuda.current_device())
+    map = torch.empty(cubes * 64 + n_dense, dtype=torch.int32, device=device) if map is None else map
+    counts = torch.empty(cubes, dtype=torch.int32, device=device) if counts is None else counts
+    _need(map, "map", torch.int32, cubes * 64 + n_dense)
+    _need(counts, "counts", torch.int32, cubes)
+    _check(lib.mh3_cube_map(C.byref(a), _ptr(map), _ptr(counts), _stream()), "cube_map")
+    return map, counts
+
+
+# ---- time conditioning -------------------------------------------------------------------------------------------------
+
+def _time_args(levels, freq_dim, hidden, out_dim, max_period) -> TimeArgs:
+    a = TimeArgs()
+    a.levels, a.freq_dim, a.hidden, a.out_dim, a.max_period = levels, freq_dim, hidden, out_dim, max_period
+    return a
+
+
+def time_embed_workspace_bytes(levels, freq_dim, hidden, out_dim, max_period=10000.0) -> int:
+    n = int(lib.mh3_time_embed_workspace_bytes(C.byref(_time_args(levels, freq_dim, hidden, out_dim, max_period))))
+    _check(min(n, 0), "time_embed_workspace_bytes")
+    return n
+
+
+def time_embed(t, w_in, b_in, w_out, b_out, *, max_period=10000.0, workspace=None, temb=None, cond=None,
+               with_cond=True):
+    """The sinusoidal embedding of each level t[u] (freq_dim = w_in's width, cos half first) through the F32 time MLP
+    (w_in [hidden][freq_dim], w_out [out_dim][hidden], biases may be None) -> (temb float [levels][out_dim],
+    cond bf16 [levels][out_dim] = bf16(silu(temb)), or None without with_cond)."""
+    levels = t.numel()
+    hidden, freq_dim = w_in.shape
+    out_dim = w_out.shape[0]
+    if w_out.shape[1] != hidden:
+        raise ValueError("w_out must be [out_dim][hidden]")
+    _need(t, "t", torch.float32, levels)
+    _need(w_in, "w_in", torch.float32, hidden * freq_dim)
+    _need(w_out, "w_out", torch.float32, out_dim * hidden)
+    if b_in is not None:
+        _need(b_in, "b_in", torch.float32, hidden)
+    if b_out is not None:
+        _need(b_out, "b_out", torch.float32, out_dim)
+    a = _time_args(levels, freq_dim, hidden, out_dim, max_period)
+    nbytes = int(lib.mh3_time_embed_workspace_bytes(C.byref(a)))
+    _check(min(nbytes, 0), "time_embed")
+    if workspace is None:
+        workspace = torch.empty(nbytes, dtype=torch.uint8, device=t.device)
+    _need(workspace, "workspace", torch.uint8, nbytes)
+    temb = torch.empty((levels, out_dim), dtype=torch.float32, device=t.device) if temb is None else temb
+    _need(temb, "temb", torch.float32, levels * out_dim)
+    if with_cond:
+        cond = torch.empty((levels, out_dim), dtype=torch.bfloat16, device=t.device) if cond is None else cond
+        _need(cond, "cond", torch.bfloat16, levels * out_dim)
+    else:
+        cond = None
+    _check(lib.mh3_time_embed(C.byref(a), _ptr(t), _ptr(w_in), _ptr(b_in), _ptr(w_out), _ptr(b_out),
+                              _ptr(workspace), workspace.numel(), _ptr(temb), _ptr(cond), _stream()), "time_embed")
+    return temb, cond
+
+
+def adaln_mod(cond, w, bias=None, *, out=None):
+    """A block's AdaLN projection: mod[u][r] = w[r] . cond[u] + bias[r] (cond bf16 [levels][k], w bf16 [n][k], bias
+    float [n] or None) -> float [levels][n]; with n = 18 D, view it as the [levels][3][6][D] table."""
+    levels, k = cond.shape
+    n = w.shape[0]
+    if w.dim() != 2 or w.shape[1] != k:
+        raise ValueError("w must be [n][k]")
+    _need(cond, "cond", torch.bfloat16, levels * k)
+    _need(w, "w", torch.bfloat16, n * k)
+    if bias is not None:
+        _need(bias, "bias", torch.float32, n)
+    out = torch.empty((levels, n), dtype=torch.float32, device=cond.device) if out is None else out
+    _need(out, "mod", torch.float32, levels * n)
+    a = GemmArgs()
+    a.m, a.n, a.k = levels, n, k
+    _check(lib.mh3_adaln_mod(C.byref(a), _ptr(cond), _ptr(w), _ptr(bias), _ptr(out), _stream()), "adaln_mod")
+    return out
+
+
+def curve_mods(t, table, w, bias=None, *, out=None):
+    """The pruned checkpoints' modulation: the curve table [points][width] interpolated at t[u] (points - 1), through
+    w float [n][width] plus bias, no silu -> float [levels][n]."""
+    levels = t.numel()
+    points, width = table.shape
+    n = w.shape[0]
+    if w.dim() != 2 or w.shape[1] != width:
+        raise ValueError("w must be [n][width]")
+    _need(t, "t", torch.float32, levels)
+    _need(table, "table", torch.float32, points * width)
+    _need(w, "w", torch.float32, n * width)
+    if bias is not None:
+        _need(bias, "bias", torch.float32, n)
+    out = torch.empty((levels, n), dtype=torch.float32, device=t.device) if out is None else out
+    _need(out, "mod", torch.float32, levels * n)
+    a = CurveArgs()
+    a.levels, a.n, a.points, a.width = levels, n, points, width
+    _check(lib.mh3_curve_mods(C.byref(a), _ptr(t), _ptr(table), _ptr(w), _ptr(bias), _ptr(out), _stream()),
+           "curve_mods")
+    return out
 
 
 # ---- heads_partial ---------------------------------------------------------------------------------------------------

@@ -643,3 +643,103 @@ void mh3o_attn_sparse(uint32_t heads, uint32_t gt, uint32_t gh, uint32_t gw, int
             mh3o_attn_sparse_tile(gt, gh, gw, layout, row0, head_stride, row_stride, dense_row0, n_dense, scale, q,
                                   k, v, idx, cnt, out_stride, h, t, out);
 }
+
+/* ---- H3::Cubes' map (docs/architecture.md:120-125) -------------------------------------------------------------- */
+
+/* Written as a scatter: every slot starts as padding (-1), then each video token (t, y, x) of the grid is placed at
+ * its cube's slot ((t % 4) * 4 + y % 4) * 4 + x % 4 and counted; the dense rows follow the cubes. */
+int64_t mh3o_cube_map(uint32_t gt, uint32_t gh, uint32_t gw, uint32_t n_dense, uint64_t video_row0,
+                      uint64_t dense_row0, int32_t* map, int32_t* counts)
+{
+    const uint32_t ch = (gh + 3u) / 4u, cw = (gw + 3u) / 4u;
+    const int64_t cubes = mh3o_cube_count(gt, gh, gw);
+    for (int64_t r = 0; r < cubes * 64; ++r)
+        map[r] = -1;
+    if (counts)
+        for (int64_t c = 0; c < cubes; ++c)
+            counts[c] = 0;
+    for (uint32_t t = 0; t < gt; ++t)
+        for (uint32_t y = 0; y < gh; ++y)
+            for (uint32_t x = 0; x < gw; ++x) {
+                const uint64_t c = ((uint64_t)(t / 4u) * ch + y / 4u) * cw + x / 4u;
+                const uint32_t slot = ((t % 4u) * 4u + y % 4u) * 4u + x % 4u;
+                map[c * 64u + slot] = (int32_t)(video_row0 + ((uint64_t)t * gh + y) * gw + x);
+                if (counts)
+                    counts[c] += 1;
+            }
+    for (uint32_t j = 0; j < n_dense; ++j)
+        map[cubes * 64 + j] = (int32_t)(dense_row0 + j);
+    return cubes * 64 + n_dense;
+}
+
+/* ---- time conditioning (docs/architecture.md:49-58, tools/check_pruned_curve.py:57-73) ------------------------- */
+
+static double silu_d(double v) { return v / (1.0 + exp(-v)); }
+
+void mh3o_time_embed(uint32_t levels, uint32_t freq_dim, uint32_t hidden, uint32_t out_dim, double max_period,
+                     const float* t, const float* w_in, const float* b_in, const float* w_out, const float* b_out,
+                     float* temb, uint16_t* cond)
+{
+    const uint32_t half = freq_dim / 2;
+    double* emb = malloc(sizeof(double) * freq_dim);
+    double* hid = malloc(sizeof(double) * hidden);
+    for (uint32_t u = 0; u < levels; ++u) {
+        for (uint32_t i = 0; i < half; ++i) {
+            const double arg = (double)t[u] * exp(-log(max_period) * (double)i / (double)half);
+            emb[i] = cos(arg);
+            emb[half + i] = sin(arg);
+        }
+        for (uint32_t r = 0; r < hidden; ++r) {
+            double s = b_in ? b_in[r] : 0.0;
+            for (uint32_t i = 0; i < freq_dim; ++i)
+                s += (double)w_in[(uint64_t)r * freq_dim + i] * emb[i];
+            hid[r] = silu_d(s);
+        }
+        for (uint32_t j = 0; j < out_dim; ++j) {
+            double s = b_out ? b_out[j] : 0.0;
+            for (uint32_t i = 0; i < hidden; ++i)
+                s += (double)w_out[(uint64_t)j * hidden + i] * hid[i];
+            temb[(uint64_t)u * out_dim + j] = (float)s;
+            if (cond)
+                cond[(uint64_t)u * out_dim + j] = mh3o_bf16_from_double(silu_d(s));
+        }
+    }
+    free(emb);
+    free(hid);
+}
+
+void mh3o_adaln_mod(uint32_t levels, uint32_t n, uint32_t k, const uint16_t* cond, const uint16_t* w,
+                    const float* bias, float* mod)
+{
+    for (uint32_t u = 0; u < levels; ++u)
+        for (uint32_t r = 0; r < n; ++r) {
+            double s = bias ? bias[r] : 0.0;
+            for (uint32_t i = 0; i < k; ++i)
+                s += (double)mh3o_bf16_to_float(w[(uint64_t)r * k + i]) *
+                     (double)mh3o_bf16_to_float(cond[(uint64_t)u * k + i]);
+            mod[(uint64_t)u * n + r] = (float)s;
+        }
+}
+
+void mh3o_curve_mods(uint32_t levels, uint32_t n, uint32_t points, uint32_t width, const float* t, const float* table,
+                     const float* w, const float* bias, float* mod)
+{
+    double* c = malloc(sizeof(double) * width);
+    for (uint32_t u = 0; u < levels; ++u) {
+        double pos = (double)t[u] * (double)(points - 1);
+        pos = pos < 0 ? 0 : (pos > (double)(points - 1) ? (double)(points - 1) : pos);
+        uint32_t i0 = (uint32_t)floor(pos);
+        if (i0 > points - 2)
+            i0 = points - 2;
+        const double f = pos - (double)i0;
+        for (uint32_t j = 0; j < width; ++j)
+            c[j] = (1.0 - f) * table[(uint64_t)i0 * width + j] + f * table[(uint64_t)(i0 + 1) * width + j];
+        for (uint32_t r = 0; r < n; ++r) {
+            double s = bias ? bias[r] : 0.0;
+            for (uint32_t j = 0; j < width; ++j)
+                s += (double)w[(uint64_t)r * width + j] * c[j];
+            mod[(uint64_t)u * n + r] = (float)s;
+        }
+    }
+    free(c);
+}

@@ -12,6 +12,9 @@
  *   heads_partial                   docs/architecture.md:35-38,61-63,123-125
  *   quant_rows_i8, W8A16 fc1        docs/performance.md:120-136
  *   qkv / out / fc2 GEMMs           docs/performance.md:40-43,52-69,120-133, docs/architecture.md:61-66
+ *   cube map (H3::Cubes)            docs/architecture.md:120-125
+ *   time_embed / adaln_mod          docs/architecture.md:49-58, tools/check_pruned_curve.py:57-67
+ *   curve_mods                      docs/architecture.md:53-58, tools/check_pruned_curve.py:69-73
  * bf16 results are rounded to nearest even exactly once, from the double value.
  *
  * How each function is pinned (tests/test_oracle.py): no reference vector exists for any of them (the reference
@@ -40,6 +43,13 @@
  *   mh3o_gemm                  torch.matmul in float64 for each form; the gate-add epilogue against gate_add_rows of
  *                              the rounded product (within one bf16 rounding); gate 0 leaves the residual bit-exact;
  *                              exact integer results for w in {-1,0,1}
+ *   mh3o_cube_map              brute force in Python over padded grids (a gather per attention row, where the oracle
+ *                              scatters per token); its map feeds mh3o_heads_partial to the same means as the grid
+ *                              layout of mh3o_cube_pool; counts equal the per-axis product
+ *   mh3o_time_embed            torch float64 restatement of tools/check_pruned_curve.py:57-67 (temb()): the
+ *                              reference's own statement of the embedding and the MLP; t = 0 gives cos = 1, sin = 0
+ *   mh3o_adaln_mod             torch.matmul in float64; exact integer results for small-integer inputs
+ *   mh3o_curve_mods            numpy interp per coordinate, then matmul; t at a table point gives that row exactly
  *   (the order in which gemm_i8's epilogue applies the two scales is not documented: parity unpinned for it)
  */
 #ifndef MH3_ORACLE_H
@@ -119,6 +129,21 @@ void mh3o_gemm_i8_swiglu(uint32_t m, uint32_t n, uint32_t k, const int8_t* x, co
 void mh3o_gemm(uint32_t m, uint32_t n, uint32_t k, int form, int epi, const void* x, const float* x_scale,
                const void* w, const float* w_scale, const float* gate, const uint8_t* set_of_row, uint32_t gate_stride,
                uint16_t* out);
+
+/* H3::Cubes' map: attention row -> model row (-1 for padding), then the dense rows; counts per cube (may be NULL).
+ * Returns the number of map entries. */
+int64_t mh3o_cube_map(uint32_t gt, uint32_t gh, uint32_t gw, uint32_t n_dense, uint64_t video_row0,
+                      uint64_t dense_row0, int32_t* map, int32_t* counts);
+/* The sinusoidal embedding (cos half first) through the time MLP; temb float, cond = bf16(silu(temb)) (may be NULL). */
+void mh3o_time_embed(uint32_t levels, uint32_t freq_dim, uint32_t hidden, uint32_t out_dim, double max_period,
+                     const float* t, const float* w_in, const float* b_in, const float* w_out, const float* b_out,
+                     float* temb, uint16_t* cond);
+/* mod[u][r] = w[r] . cond[u] + bias[r], bf16 operands, double accumulation. */
+void mh3o_adaln_mod(uint32_t levels, uint32_t n, uint32_t k, const uint16_t* cond, const uint16_t* w,
+                    const float* bias, float* mod);
+/* The pruned checkpoints' curve: table interpolated at t (points - 1), through w [n][width] plus bias. */
+void mh3o_curve_mods(uint32_t levels, uint32_t n, uint32_t points, uint32_t width, const float* t, const float* table,
+                     const float* w, const float* bias, float* mod);
 
 #ifdef __cplusplus
 }

@@ -59,6 +59,11 @@ _lib.mh3o_gemm_w8a16_swiglu.argtypes = [C.c_uint32] * 3 + [_P] * 4
 _lib.mh3o_gemm_bf16_swiglu.argtypes = [C.c_uint32] * 3 + [_P] * 3
 _lib.mh3o_gemm_i8_swiglu.argtypes = [C.c_uint32] * 3 + [_P] * 5
 _lib.mh3o_gemm.argtypes = [C.c_uint32] * 3 + [C.c_int] * 2 + [_P] * 6 + [C.c_uint32, _P]
+_lib.mh3o_cube_map.restype = C.c_int64
+_lib.mh3o_cube_map.argtypes = [C.c_uint32] * 4 + [C.c_uint64, C.c_uint64, _P, _P]
+_lib.mh3o_time_embed.argtypes = [C.c_uint32] * 4 + [C.c_double] + [_P] * 7
+_lib.mh3o_adaln_mod.argtypes = [C.c_uint32] * 3 + [_P] * 4
+_lib.mh3o_curve_mods.argtypes = [C.c_uint32] * 4 + [_P] * 5
 _lib.mh3o_bf16_to_float_n.argtypes = [_P, _P, C.c_uint64]
 _lib.mh3o_bf16_from_double_n.argtypes = [_P, _P, C.c_uint64]
 
@@ -312,3 +317,47 @@ def attn_tile_rows(grid, layout, row0, dense_row0, n_dense, tile):
         if t < gt and y < gh and x < gw:
             rows.append(row0 + 64 * c + l if layout == CUBES_GATHERED else row0 + (t * gh + y) * gw + x)
     return np.array(rows, dtype=np.int64)
+
+
+def cube_map(grid, n_dense=0, video_row0=None, dense_row0=0):
+    """H3::Cubes' map -> (map int32 [cubes * 64 + n_dense], counts int32 [cubes]); the video grid's tokens at model
+    rows video_row0 + (t * H + y) * W + x (default: right after the dense rows)."""
+    gt, gh, gw = grid
+    cubes = cube_count(gt, gh, gw)
+    video_row0 = dense_row0 + n_dense if video_row0 is None else video_row0
+    m = np.empty(cubes * 64 + n_dense, np.int32)
+    counts = np.empty(cubes, np.int32)
+    _lib.mh3o_cube_map(gt, gh, gw, n_dense, video_row0, dense_row0, _p(m), _p(counts))
+    return m, counts
+
+
+def time_embed(t, w_in, b_in, w_out, b_out, max_period=10000.0):
+    """The sinusoidal embedding of each t (cos half first) through the time MLP -> (temb float32 [levels][out_dim],
+    cond bf16 bits [levels][out_dim] = bf16(silu(temb)))."""
+    t = np.ascontiguousarray(t, np.float32)
+    hidden, freq_dim = w_in.shape
+    out_dim = w_out.shape[0]
+    temb = np.empty((t.size, out_dim), np.float32)
+    cond = np.empty((t.size, out_dim), np.uint16)
+    _lib.mh3o_time_embed(t.size, freq_dim, hidden, out_dim, max_period, _p(t), _p(w_in), _p(b_in), _p(w_out),
+                         _p(b_out), _p(temb), _p(cond))
+    return temb, cond
+
+
+def adaln_mod(cond, w, bias=None):
+    """mod[u][r] = w[r] . cond[u] + bias[r]: cond and w bf16 bits, double accumulation -> float32 [levels][n]."""
+    levels, k = cond.shape
+    n = w.shape[0]
+    mod = np.empty((levels, n), np.float32)
+    _lib.mh3o_adaln_mod(levels, n, k, _p(cond), _p(w), _p(bias), _p(mod))
+    return mod
+
+
+def curve_mods(t, table, w, bias=None):
+    """The pruned checkpoints' curve: table [points][width] interpolated at t (points - 1), through w [n][width]."""
+    t = np.ascontiguousarray(t, np.float32)
+    points, width = table.shape
+    n = w.shape[0]
+    mod = np.empty((t.size, n), np.float32)
+    _lib.mh3o_curve_mods(t.size, n, points, width, _p(t), _p(table), _p(w), _p(bias), _p(mod))
+    return mod

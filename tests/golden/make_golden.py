@@ -1,7 +1,8 @@
 """Writes the small committed fixtures under tests/golden/: seeded inputs and the CPU oracle's outputs for each
 hot-path op, plus manifest.json. The reference holds no vectors for these ops, so these are the build's own, made
-by the oracle (which tests/test_oracle.py pins against library routines, brute force and invariants). The GPU tests
-compare the kernels against them; tests/test_oracle.py checks the oracle still reproduces them.
+by the oracle (which tests/test_oracle*.py pin against library routines, brute force and invariants).
+tests/test_golden_gpu.py runs each fixture's inputs through the HIP kernels and compares them with the stored
+outputs; tests/test_oracle.py checks the oracle still reproduces them.
 
     python tests/golden/make_golden.py
 """
@@ -57,6 +58,23 @@ def make_inputs(case: dict) -> dict:
         m, n, k = case["m"], case["n"], case["k"]
         return {"x": _bf16(rng, (m, k)), "w": rng.integers(-127, 128, (2 * n, k), dtype=np.int8),
                 "scale": rng.uniform(0.5e-3, 2e-3, 2 * n).astype(np.float32)}
+    if op == "cube_map":
+        return {}
+    if op == "time_embed":
+        f, h, o = case["freq_dim"], case["hidden"], case["out_dim"]
+        return {"t": np.array(case["t"], np.float32),
+                "w_in": (rng.standard_normal((h, f)) / np.sqrt(f)).astype(np.float32),
+                "b_in": (0.1 * rng.standard_normal(h)).astype(np.float32),
+                "w_out": (rng.standard_normal((o, h)) / np.sqrt(h)).astype(np.float32),
+                "b_out": (0.1 * rng.standard_normal(o)).astype(np.float32)}
+    if op == "adaln_mod":
+        return {"cond": _bf16(rng, (case["levels"], case["k"])), "w": _bf16(rng, (case["n"], case["k"]), 0.05),
+                "bias": (0.1 * rng.standard_normal(case["n"])).astype(np.float32)}
+    if op == "curve_mods":
+        return {"t": np.array(case["t"], np.float32),
+                "table": rng.standard_normal((case["points"], case["width"])).astype(np.float32),
+                "w": rng.standard_normal((case["n"], case["width"])).astype(np.float32),
+                "bias": rng.standard_normal(case["n"]).astype(np.float32)}
     raise ValueError(op)
 
 
@@ -81,6 +99,16 @@ def run_case(case: dict, data) -> dict:
         return {"q": q, "s": s}
     if op == "gemm_w8a16_swiglu":
         return {"out": orc.gemm_w8a16_swiglu(data["x"], data["w"], data["scale"])}
+    if op == "cube_map":
+        m, c = orc.cube_map(tuple(case["grid"]), case["n_dense"], case["video_row0"], case["dense_row0"])
+        return {"map": m, "counts": c}
+    if op == "time_embed":
+        temb, cond = orc.time_embed(data["t"], data["w_in"], data["b_in"], data["w_out"], data["b_out"])
+        return {"temb": temb, "cond": cond}
+    if op == "adaln_mod":
+        return {"mod": orc.adaln_mod(data["cond"], data["w"], data["bias"])}
+    if op == "curve_mods":
+        return {"mod": orc.curve_mods(data["t"], data["table"], data["w"], data["bias"])}
     raise ValueError(op)
 
 
@@ -93,6 +121,13 @@ CASES = [
     {"name": "cube_topk_ties", "op": "cube_topk", "seed": 104, "heads": 2, "grid": [12, 8, 8], "k": 5, "local": 3},
     {"name": "quant_rows", "op": "quant_rows_i8", "seed": 105, "rows": 8, "cols": 512},
     {"name": "fc1_small", "op": "gemm_w8a16_swiglu", "seed": 106, "m": 5, "n": 128, "k": 256},
+    {"name": "cube_map_padded", "op": "cube_map", "seed": 107, "grid": [5, 6, 9], "n_dense": 7, "video_row0": 7,
+     "dense_row0": 0},
+    {"name": "time_embed_small", "op": "time_embed", "seed": 108, "t": [0.0, 0.4, 0.9230769], "freq_dim": 256,
+     "hidden": 96, "out_dim": 40},
+    {"name": "adaln_mod_small", "op": "adaln_mod", "seed": 109, "levels": 3, "n": 54, "k": 264},
+    {"name": "curve_mods_small", "op": "curve_mods", "seed": 110, "t": [0.0, 0.0769230769, 0.5, 1.0], "points": 1025,
+     "width": 8, "n": 36},
 ]
 
 

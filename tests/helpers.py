@@ -82,3 +82,66 @@ def check_selection(gpu_idx, gpu_cnt, scores64, oracle_idx, oracle_cnt, k, rel_t
         assert (np.abs(s[r][swapped] - kth) <= tol).all(), \
             f"row {r}: cubes {swapped} differ beyond the tie band (k-th score {kth}, theirs {s[r][swapped]})"
     return differ
+
+
+BF16_NAN = -1  # 0xffff as int16: a bf16 NaN, the fill that shows any output element a kernel leaves unwritten
+
+
+def nan_filled(shape, device):
+    """A bf16 output buffer every element of which is NaN until written."""
+    return torch.full(shape, BF16_NAN, dtype=torch.int16, device=device).view(torch.bfloat16)
+
+
+def check_rows_f64(got: torch.Tensor, want: torch.Tensor, what: str, rtol=1e-2, row_frac=1e-4):
+    """Every element of a bf16 (or float) result against a float64 restatement on the GPU: finite, and
+    |got - want| <= rtol |want| + row_frac rms(want's row). The row term covers results that cancel to near zero (a dot
+    product of 5120 terms whose float32 accumulation error is a fixed fraction of its row's scale); rtol is the bf16
+    bar. Returns the reference's diff() pair over the block."""
+    g = got.double()
+    assert bool(torch.isfinite(g).all()), f"{what}: non-finite outputs (an unwritten or corrupted element)"
+    rms = want.pow(2).mean(1, keepdim=True).sqrt()
+    err = (g - want).abs()
+    bound = rtol * want.abs() + row_frac * rms
+    bad = err > bound
+    if bool(bad.any()):
+        i = int(torch.argmax((err - bound).flatten()))
+        r, c = divmod(i, want.shape[1])
+        raise AssertionError(f"{what}: {int(bad.sum())} elements beyond tolerance; worst at ({r}, {c}) got "
+                             f"{float(g[r, c])!r} want {float(want[r, c])!r}")
+    e2, w2 = float(((g - want) ** 2).sum()), float((want ** 2).sum())
+    gw = (g * want).sum(1)
+    cos = gw / (g.pow(2).sum(1).sqrt() * want.pow(2).sum(1).sqrt()).clamp_min(1e-300)
+    return (e2 / max(w2, 1e-300)) ** 0.5, float(cos.min())
+
+
+def check_gemm_full(out: torch.Tensor, x: torch.Tensor, w: torch.Tensor, what: str, *, x_scale=None, w_scale=None,
+                    epi: str = "store", residual0=None, gate=None, set_of_row=None, chunk: int = 4096):
+    """Every element of a GEMM's output against float64 products on the GPU over the same operands, row chunk by row
+    chunk: y = (x * x_scale[row]) (w * w_scale[col])^T, then epi "store" (out = y), "swiglu" (out = silu(y[:, :n]) *
+    y[:, n:], n = out's width) or "gate_add" (out = residual0 + gate[set_of_row[row]] * y)."""
+    m, n = out.shape
+    wd = w.double()
+    if w_scale is not None:
+        wd = wd * w_scale.double()[:, None]
+    wt = wd.t().contiguous()
+    del wd
+    if gate is not None:
+        gate2 = gate.double().reshape(-1, gate.shape[-1])[:, :n]
+    worst_rel, worst_cos = 0.0, 1.0
+    for r0 in range(0, m, chunk):
+        r1 = min(m, r0 + chunk)
+        xs = x[r0:r1].double()
+        if x_scale is not None:
+            xs = xs * x_scale[r0:r1].double()[:, None]
+        y = xs @ wt
+        if epi == "swiglu":
+            g, u = y[:, :n], y[:, n:]
+            want = g * torch.sigmoid(g) * u
+        elif epi == "gate_add":
+            gr = gate2[set_of_row[r0:r1].long()] if set_of_row is not None else gate2[:1]
+            want = residual0[r0:r1].double() + gr * y
+        else:
+            want = y
+        rel, cos = check_rows_f64(out[r0:r1], want, f"{what} rows {r0}..{r1 - 1}")
+        worst_rel, worst_cos = max(worst_rel, rel), min(worst_cos, cos)
+    return worst_rel, worst_cos

@@ -41,10 +41,10 @@ def test_stream_probe_library_loads_and_refuses_bad_calls():
 
 
 def test_abi_version_and_strings():
-    assert mh.lib.mh3_abi_version() == 2
+    assert mh.lib.mh3_abi_version() == 3
     # The Python structs mirror the header: its MH3_ABI_VERSION is the module's (import refuses another library's).
     header = (Path(__file__).resolve().parent.parent / "include" / "mako_h3.h").read_text()
-    assert re.search(r"#define MH3_ABI_VERSION (\d+)", header).group(1) == str(mh.ABI_VERSION) == "2"
+    assert re.search(r"#define MH3_ABI_VERSION (\d+)", header).group(1) == str(mh.ABI_VERSION) == "3"
     assert mh.strerror(mh.ERR_SHAPE) == "bad shape"
     assert mh.strerror(123) == "unknown error"
 
@@ -208,3 +208,85 @@ def test_flash_attn_sparse_pointer_checks():
     out = C.c_void_p(0x2000)
     assert mh.lib.mh3_flash_attn_sparse_128(C.byref(a), ODD, FAKE, FAKE, FAKE, FAKE, out, None) == mh.ERR_ALIGN
     assert mh.lib.mh3_flash_attn_sparse_128(C.byref(a), FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, None) == mh.ERR_PARAM
+
+
+def test_gemm_refuses_an_output_that_overlaps_an_operand():
+    """An out (or gate-add residual) range that overlaps x or w races with the tiles still reading them: refused."""
+    g = mh.GemmArgs()
+    g.m, g.n, g.k = 256, 256, 256
+    x = C.c_void_p(0x100000)
+    w = C.c_void_p(0x200000)
+    gate = C.c_void_p(0x300000)
+    inside_x = C.c_void_p(0x100000 + 256 * 256)             # out starts in the middle of x
+    assert mh.lib.mh3_gemm_gate_add(C.byref(g), mh.GEMM_BF16, x, None, w, None, gate, None, inside_x, None) == \
+        mh.ERR_PARAM
+    assert mh.lib.mh3_gemm(C.byref(g), mh.GEMM_BF16, x, None, w, None, w, None) == mh.ERR_PARAM
+    before_x = C.c_void_p(0x100000 - 256 * 256 * 2 + 16)    # out's last bytes reach into x
+    assert mh.lib.mh3_gemm_gate_add(C.byref(g), mh.GEMM_W8A16, x, None, w, FAKE, gate, None, before_x, None) == \
+        mh.ERR_PARAM
+    assert mh.lib.mh3_gemm_w8a16_swiglu(C.byref(g), x, w, FAKE, x, None) == mh.ERR_PARAM
+
+
+def test_cube_map_validation():
+    a = mh.CubeMapArgs()
+    a.grid_t, a.grid_h, a.grid_w, a.n_dense, a.video_row0, a.dense_row0 = 32, 48, 84, 512, 512, 0
+    assert mh.lib.mh3_cube_map(None, FAKE, None, None) == mh.ERR_POINTER
+    assert mh.lib.mh3_cube_map(C.byref(a), None, None, None) == mh.ERR_POINTER
+    a.dense_row0 = 600                                      # dense rows inside the video rows
+    assert mh.lib.mh3_cube_map(C.byref(a), FAKE, None, None) == mh.ERR_PARAM
+    a.dense_row0, a.grid_w = 0, 0
+    assert mh.lib.mh3_cube_map(C.byref(a), FAKE, None, None) == mh.ERR_SHAPE
+    a.grid_w, a.video_row0 = 84, 2**31 - 100                # model rows beyond int32
+    assert mh.lib.mh3_cube_map(C.byref(a), FAKE, None, None) == mh.ERR_SHAPE
+
+
+def time_args(**kw):
+    a = mh.TimeArgs()
+    a.levels, a.freq_dim, a.hidden, a.out_dim, a.max_period = 3, 256, 5376, 2688, 10000.0
+    for k, v in kw.items():
+        setattr(a, k, v)
+    return a
+
+
+@pytest.mark.parametrize("kw,code", [({"levels": 0}, mh.ERR_SHAPE), ({"levels": 65}, mh.ERR_SHAPE),
+                                     ({"freq_dim": 100}, mh.ERR_SHAPE), ({"freq_dim": 2048}, mh.ERR_SHAPE),
+                                     ({"hidden": 5378}, mh.ERR_SHAPE), ({"hidden": 8196}, mh.ERR_SHAPE),
+                                     ({"out_dim": 0}, mh.ERR_SHAPE), ({"max_period": 1.0}, mh.ERR_PARAM)])
+def test_time_embed_validation(kw, code):
+    a = time_args(**kw)
+    assert mh.lib.mh3_time_embed_workspace_bytes(C.byref(a)) == code
+    assert mh.lib.mh3_time_embed(C.byref(a), FAKE, FAKE, None, FAKE, None, FAKE, 1 << 30, FAKE, None, None) == code
+
+
+def test_time_embed_workspace_checks():
+    a = time_args()
+    need = mh.lib.mh3_time_embed_workspace_bytes(C.byref(a))
+    assert need >= 3 * 5376 * 4 and need % 256 == 0
+    assert mh.lib.mh3_time_embed(C.byref(a), FAKE, FAKE, None, FAKE, None, FAKE, need - 1, FAKE, None, None) == \
+        mh.ERR_SHAPE
+    assert mh.lib.mh3_time_embed(C.byref(a), FAKE, FAKE, None, FAKE, None, None, need, FAKE, None, None) == \
+        mh.ERR_POINTER
+    assert mh.lib.mh3_time_embed(C.byref(a), FAKE, FAKE, None, FAKE, None, ODD, need, FAKE, None, None) == \
+        mh.ERR_ALIGN
+    assert mh.lib.mh3_time_embed(C.byref(a), None, FAKE, None, FAKE, None, FAKE, need, FAKE, None, None) == \
+        mh.ERR_POINTER
+
+
+def test_adaln_and_curve_validation():
+    g = mh.GemmArgs()
+    g.m, g.n, g.k = 3, 96768, 2688
+    assert mh.lib.mh3_adaln_mod(C.byref(g), FAKE, None, None, FAKE, None) == mh.ERR_POINTER
+    assert mh.lib.mh3_adaln_mod(C.byref(g), FAKE, ODD, None, FAKE, None) == mh.ERR_ALIGN
+    g.k = 2690
+    assert mh.lib.mh3_adaln_mod(C.byref(g), FAKE, FAKE, None, FAKE, None) == mh.ERR_SHAPE
+    g.k = 4104
+    assert mh.lib.mh3_adaln_mod(C.byref(g), FAKE, FAKE, None, FAKE, None) == mh.ERR_UNSUPPORTED
+    g.k, g.m = 2688, 65
+    assert mh.lib.mh3_adaln_mod(C.byref(g), FAKE, FAKE, None, FAKE, None) == mh.ERR_SHAPE
+    c = mh.CurveArgs()
+    c.levels, c.n, c.points, c.width = 2, 96768, 1025, 8
+    assert mh.lib.mh3_curve_mods(C.byref(c), FAKE, FAKE, None, None, FAKE, None) == mh.ERR_POINTER
+    c.points = 1
+    assert mh.lib.mh3_curve_mods(C.byref(c), FAKE, FAKE, FAKE, None, FAKE, None) == mh.ERR_SHAPE
+    c.points, c.width = 1025, 33
+    assert mh.lib.mh3_curve_mods(C.byref(c), FAKE, FAKE, FAKE, None, FAKE, None) == mh.ERR_SHAPE

@@ -129,3 +129,44 @@ def test_flash_attn_sparse_768p_sampled(dev):
     for h, tile in tiles:
         r = orc.attn_tile_rows(grid, orc.CUBES_GRID, 0, video, n_dense, tile)
         check(ob[h, r], want[h, r], f"768p head {h} tile {tile}")
+
+
+def test_flash_attn_sparse_768p_40_heads(dev):
+    """The launch bench.py times: 40 heads of the 768p shape (2016 cubes, 512 text rows after the video rows), whose
+    tile count lets each XCD take a contiguous eighth of every head's query cubes with rotated pass lists, the pass
+    lists from cube_select at ratio 0.1 (k = 202), local 1. Every output is finite, and tiles of every head --
+    one dense tile of each fifth head, cube tiles spread over all XCD slices -- against the oracle."""
+    grid, heads, n_dense = (32, 48, 84), 40, 512
+    video = 32 * 48 * 84
+    rows = video + n_dense
+    g = torch.Generator(device=dev).manual_seed(15)
+    q, k, v = [torch.randn((heads, rows, 128), generator=g, device=dev).to(torch.bfloat16) for _ in range(3)]
+    t = torch.arange(video, device=dev)
+    tt, yy, xx = (t // (48 * 84)).float() / 32, (t // 84 % 48).float() / 48, (t % 84).float() / 84
+    for h in range(heads):
+        u = torch.randn(128, generator=g, device=dev)
+        wave = torch.cos(2 * math.pi * ((h % 3) * tt + (h % 2 + 1) * yy + (h % 4) * xx))
+        q[h, :video] += (0.5 * wave[:, None] * u[None, :]).to(torch.bfloat16)
+        k[h, :video] += (0.5 * wave[:, None] * u[None, :]).to(torch.bfloat16)
+    C = orc.cube_count(*grid)
+    kk = mh.topk_k(0.1, C)
+    a = mh.cube_args(heads, grid, head_stride=rows * 128, k=kk, local=1)
+    qc, kc = mh.cube_pool(a, q, k)
+    idx, cnt = mh.cube_select(a, qc, kc)
+    out = mh.flash_attn_sparse_128(a, q, k, v, idx, cnt, dense_row0=video, n_dense=n_dense)
+    torch.cuda.synchronize()
+    assert bool(torch.isfinite(out).all())
+    nd = n_dense // 64
+    rng = np.random.default_rng(16)
+    # cube c of head h lands in XCD slice c * 8 // C; cover every slice across the heads
+    tiles = [(h, int(rng.integers(0, nd))) for h in range(0, heads, 5)]
+    tiles += [(h, nd + int(c)) for h in range(heads) for c in [((h % 8) * C) // 8 + int(rng.integers(0, C // 8))]]
+    hs = sorted({h for h, _ in tiles})
+    sub = lambda x: to_bits(x[hs])  # noqa: E731
+    qb, kb, vb, ob = sub(q), sub(k), sub(v), sub(out)
+    idx_n, cnt_n = idx[hs].cpu().numpy(), cnt[hs].cpu().numpy()
+    local = [(hs.index(h), tile) for h, tile in tiles]
+    want = orc.attn_sparse(qb, kb, vb, idx_n, cnt_n, grid, video, n_dense, tiles=local)
+    for (h, tile), (lh, _) in zip(tiles, local):
+        r = orc.attn_tile_rows(grid, orc.CUBES_GRID, 0, video, n_dense, tile)
+        check(ob[lh, r], want[lh, r], f"768p 40 heads: head {h} tile {tile}")

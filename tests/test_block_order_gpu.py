@@ -41,9 +41,12 @@ def bits(t):
 
 
 # dim 5120 with 9 sets and f32 at 5120 (1280 vectors a row) take the workgroup-per-row kernel; the rest one wave a row.
+# bf16 (23, 6144, 1) and (21, 4096, 2): the wave kernel whose three-plane coefficient table (gate too) exceeds 64 KiB
+# while rms_mod's two planes fit, so the block order reads its coefficients from the parameter vectors while
+# rms_mod_rows reads them from LDS; the results must still agree bit for bit.
 @pytest.mark.parametrize("dtype", ["bf16", "f32"])
 @pytest.mark.parametrize("rows,dim,n_sets", [(1, 8, 1), (67, 520, 1), (33, 5120, 1), (20, 5376, 1), (45, 5376, 3),
-                                             (19, 5120, 9)])
+                                             (19, 5120, 9), (23, 6144, 1), (21, 4096, 2)])
 def test_equals_gate_add_then_rms_mod(dev, dtype, rows, dim, n_sets):
     rng = np.random.default_rng(rows * 7 + dim + n_sets)
     x, y, tx, ty, gate, shift, scale, w, sets = inputs(rng, dev, rows, dim, dtype, n_sets)

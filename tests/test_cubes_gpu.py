@@ -192,9 +192,14 @@ def smooth_qk(dev, heads, grid, alpha, seed):
     return out
 
 
-def test_select_768p_sampled_heads(dev):
+def test_select_768p_every_head(dev):
     """Q, K bf16 [40, 129,024, 128] on the 32x48x84 grid with the smooth component (alpha 0.5), 2016 cubes, ratio 0.1
-    (k = 202), local 1. The oracle pools two whole heads (compared for every cube) and ranks 48 query cubes of each."""
+    (k = 202), local 1.
+    - Every head's pooled means against a float64 reshape-mean on the GPU.
+    - Every (head, query cube)'s selection against torch's stable descending sort of the GPU's own scores (higher
+      score first, equal scores lower index first), united with the local cube: all 80,640 rows.
+    - The oracle pools two whole heads (compared for every cube) and ranks 48 query cubes of each from its float64
+      scores (ties within 1e-3 may differ)."""
     heads, grid = 40, (32, 48, 84)
     q, k = smooth_qk(dev, heads, grid, 0.5, seed=0)
     cubes = mh.cube_count(*grid)
@@ -206,6 +211,27 @@ def test_select_768p_sampled_heads(dev):
     torch.cuda.synchronize()
     c = cnt.cpu().numpy()
     assert ((c == kk) | (c == kk + 1)).all()
+    T, Y, X = grid
+    for h in range(heads):
+        for got, src in ((qc[h], q[h]), (kc[h], k[h])):
+            want = src.double().reshape(T // 4, 4, Y // 4, 4, X // 4, 4, 128).mean((1, 3, 5)).reshape(cubes, 128)
+            assert bool(((got.double() - want).abs() <= 1e-5 * want.abs() + 1e-6).all()), f"pool head {h}"
+    s = mh.cube_scores(a, qc, kc)
+    order = torch.sort(s, dim=-1, descending=True, stable=True).indices[..., :kk]
+    want_sel = torch.zeros((heads, cubes, cubes), dtype=torch.bool, device=dev)
+    want_sel.scatter_(2, order, True)
+    ar = torch.arange(cubes, device=dev)
+    want_sel[:, ar, ar] = True
+    del order, s
+    got_sel = torch.zeros((heads, cubes, cubes + 1), dtype=torch.bool, device=dev)
+    got_sel.scatter_(2, torch.where(idx >= 0, idx, cubes).long(), True)
+    assert torch.equal(got_sel[..., :cubes], want_sel), "selection differs from the sorted scores"
+    assert torch.equal(cnt.long(), want_sel.sum(-1))
+    pos = torch.arange(idx.shape[2], device=dev)
+    valid = pos[None, None, :] < cnt[..., None]
+    assert bool((idx[~valid] == -1).all())
+    assert bool((idx[..., 1:] > idx[..., :-1])[valid[..., 1:]].all()), "indices not ascending"
+    del want_sel, got_sel
     rng = np.random.default_rng(0)
     for h in (0, heads - 1):
         qh, kh = to_bits(q[h]).reshape(1, -1, 128), to_bits(k[h]).reshape(1, -1, 128)

@@ -98,17 +98,13 @@ def test_h3_sparse_path(dev):
     ct, st = torch.cos(ang), torch.sin(ang)
     qw = 1 + 0.1 * torch.randn(128, generator=g, device=dev)
     kw = 1 + 0.1 * torch.randn(128, generator=g, device=dev)
-    # The cube map: attention row 64 c + l is cube c's slot l (-1 where the padded grid has no token), then the dense
-    # rows.
-    ch, cw = (gh + 3) // 4, (gw + 3) // 4
-    c = np.arange(C)[:, None]
-    l = np.arange(64)[None, :]
-    t, y, x = 4 * (c // (ch * cw)) + l // 16, 4 * (c // cw % ch) + l // 4 % 4, 4 * (c % cw) + l % 4
-    ok = (t < gt) & (y < gh) & (x < gw)
-    cube_rows = np.where(ok, N_DENSE + (t * gh + y) * gw + x, -1).reshape(-1)
-    cmap = np.concatenate([cube_rows, np.arange(N_DENSE)]).astype(np.int32)
+    # The cube map (the library's mh3_cube_map, checked against the oracle's): attention row 64 c + l is cube c's slot l
+    # (-1 where the padded grid has no token), then the dense rows.
+    dmap, dcounts = mh.cube_map((gt, gh, gw), n_dense=N_DENSE, video_row0=N_DENSE, dense_row0=0, device=dev)
+    cmap, counts = orc.cube_map((gt, gh, gw), N_DENSE, N_DENSE, 0)
+    assert np.array_equal(dmap.cpu().numpy(), cmap) and np.array_equal(dcounts.cpu().numpy(), counts)
     att_rows = cmap.size
-    q, k, v = mh.heads_partial(qkv, HEADS, qw, kw, ct, st, map=torch.from_numpy(cmap).to(dev))
+    q, k, v = mh.heads_partial(qkv, HEADS, qw, kw, ct, st, map=dmap)
     rows = np.unique(np.concatenate([np.flatnonzero(cmap < 0)[:3], np.random.default_rng(1).integers(0, att_rows, 40),
                                      [att_rows - 1]]))
     ri = torch.from_numpy(rows).to(dev)

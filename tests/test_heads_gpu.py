@@ -85,23 +85,6 @@ def test_heads_partial_rows_layout_and_in_place(dev):
     assert torch.equal(y[:, 2 * third:].view(torch.int16), x[:, 2 * third:].view(torch.int16))
 
 
-def gather_map(grid, row0, n_dense, dense_row0):
-    """The cube map of a grid: attention row 64 c + l is the model row of cube c's slot l (-1 for padding), then the
-    dense rows."""
-    gt, gh, gw = grid
-    ch, cw = (gh + 3) // 4, (gw + 3) // 4
-    C = orc.cube_count(*grid)
-    m = np.full(64 * C + n_dense, -1, np.int32)
-    for c in range(C):
-        ct_, cy, cx = c // (ch * cw), c // cw % ch, c % cw
-        for l in range(64):
-            t, y, x = 4 * ct_ + l // 16, 4 * cy + l // 4 % 4, 4 * cx + l % 4
-            if t < gt and y < gh and x < gw:
-                m[64 * c + l] = row0 + (t * gh + y) * gw + x
-    m[64 * C:] = np.arange(dense_row0, dense_row0 + n_dense)
-    return m
-
-
 @pytest.mark.parametrize("grid", [(8, 8, 12), (7, 9, 10)])
 def test_heads_partial_cube_map_feeds_pool_and_attention(dev, grid):
     rng = np.random.default_rng(sum(grid))
@@ -110,8 +93,10 @@ def test_heads_partial_cube_map_feeds_pool_and_attention(dev, grid):
     rows = n_dense + video  # text rows first, then the video rows (row0 = n_dense)
     qkv, q_w, k_w, cos_t, sin_t = make(rng, rows, heads, rot)
     x, qw, kw, ct, st = dev_args(dev, qkv, q_w, k_w, cos_t, sin_t)
-    m = gather_map(grid, n_dense, n_dense, 0)
-    gq, gk, gv = mh.heads_partial(x, heads, qw, kw, ct, st, rot=rot, map=torch.from_numpy(m).to(dev))
+    dm, _ = mh.cube_map(grid, n_dense=n_dense, video_row0=n_dense, dense_row0=0, device=dev)
+    m = dm.cpu().numpy()
+    assert np.array_equal(m, orc.cube_map(grid, n_dense, n_dense, 0)[0])
+    gq, gk, gv = mh.heads_partial(x, heads, qw, kw, ct, st, rot=rot, map=dm)
     fq, fk, fv = mh.heads_partial(x, heads, qw, kw, ct, st, rot=rot)
     C = orc.cube_count(*grid)
     for g, f in ((gq, fq), (gk, fk), (gv, fv)):

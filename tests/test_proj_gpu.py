@@ -1,13 +1,13 @@
 """Parity of the qkv / out / fc2 projections (mh3_gemm, mh3_gemm_gate_add) with the oracle, in each operand form:
-bf16 outputs within 1e-2 relative (plus the row scale for the gate-add, whose result can cancel), the reference's
-diff() pair, the gate-add in place on the residual with per-row gate sets, and the error paths."""
+bf16 outputs within 1e-2 relative plus 1e-4 of the row's RMS (products of a few thousand terms can cancel to near
+zero, where the float32 accumulation error is a fixed fraction of the row's scale), the reference's diff() pair, the gate-add in place on the residual with per-row gate sets, and the error paths."""
 import numpy as np
 import pytest
 import torch
 
 import mako_h3 as mh
 import oracle as orc
-from helpers import bits_to_f64, diff, from_bits, randn_bf16_bits, to_bits
+from helpers import bits_to_f64, check_gemm_full, diff, from_bits, nan_filled, randn_bf16_bits, to_bits
 
 pytestmark = pytest.mark.gpu
 
@@ -39,7 +39,7 @@ def check(got_bits, want_bits, width, what):
     g, w = bits_to_f64(got_bits).reshape(-1, width), bits_to_f64(want_bits).reshape(-1, width)
     scale = np.sqrt((w ** 2).mean(1, keepdims=True)) + 1e-30
     err = np.abs(g - w)
-    assert np.all(err <= 1e-2 * np.abs(w) + 1e-3 * scale), f"{what}: worst {(err / (np.abs(w) + scale)).max():.3g}"
+    assert np.all(err <= 1e-2 * np.abs(w) + 1e-4 * scale), f"{what}: worst {(err / (np.abs(w) + scale)).max():.3g}"
     rel, cos = diff(g, w, width)
     assert rel < 5e-3 and cos > 0.9999, f"{what}: rel {rel:.3g} cos {cos:.6f}"
 
@@ -100,36 +100,53 @@ def test_gemm_store_equals_fc1_halves(dev):
     assert np.allclose(fused, sw, rtol=2e-2, atol=2e-2 * np.abs(sw).mean())
 
 
-@pytest.mark.parametrize("which", ["qkv", "fc2"])
-def test_gemm_768p_sampled_rows(dev, which):
-    """The 768p projections at full size (129,536 rows): qkv 5120 -> 15,360 (bf16) and fc2 13,824 -> 5120 with the
-    gate-add (int8 weight-only); sampled rows against the oracle, every output finite."""
+@pytest.mark.parametrize("which,form", [("qkv", "bf16"), ("qkv", "w8a8"), ("out", "w8a16"), ("fc2", "w8a16"),
+                                        ("fc2", "bf16")])
+def test_gemm_768p_every_row(dev, which, form):
+    """The 768p projections at full size (129,536 rows): qkv 5120 -> 15,360, the out projection 5120 -> 5120 and fc2
+    13,824 -> 5120 with the gate-add (three gate sets, a set a row), in the weight forms the reference runs them in.
+    qkv writes into a NaN-filled output; every element of every projection is checked against float64 products on
+    the GPU over the same operands, and 16 sampled rows against the oracle."""
     m = 129536
-    k, n = (5120, 15360) if which == "qkv" else (13824, 5120)
-    g = torch.Generator(device=dev).manual_seed(5)
-    x = torch.randn((m, k), generator=g, device=dev).to(torch.bfloat16)
-    if which == "qkv":
+    k, n = {"qkv": (5120, 15360), "out": (5120, 5120), "fc2": (13824, 5120)}[which]
+    f = FORMS[form]
+    g = torch.Generator(device=dev).manual_seed(5 + f)
+    if f == orc.GEMM_W8A8:
+        x = torch.randint(-127, 128, (m, k), generator=g, device=dev, dtype=torch.int8)
+        xs = (torch.rand(m, generator=g, device=dev) * 0.01 + 0.005).float()
+    else:
+        x = torch.randn((m, k), generator=g, device=dev).to(torch.bfloat16)
+        xs = None
+    if f == orc.GEMM_BF16:
         w = (0.02 * torch.randn((n, k), generator=g, device=dev)).to(torch.bfloat16)
-        out = mh.gemm(x, w)
         ws = None
     else:
         w = torch.randint(-127, 128, (n, k), generator=g, device=dev, dtype=torch.int8)
         ws = (torch.rand(n, generator=g, device=dev) * 1.5e-3 + 0.5e-3).float()
+    if which == "qkv":
+        out = mh.gemm(x, w, x_scale=xs, w_scale=ws, out=nan_filled((m, n), dev))
+        rel, cos = check_gemm_full(out, x, w, f"{which} {form} 768p", x_scale=xs, w_scale=ws)
+    else:
         res = torch.randn((m, n), generator=g, device=dev).to(torch.bfloat16)
         res0 = res.clone()
-        gate = (0.1 * torch.randn(n, generator=g, device=dev)).float()
-        out = mh.gemm_gate_add(x, w, res, gate, w_scale=ws)
-    torch.cuda.synchronize()
-    assert bool(torch.isfinite(out).all())
+        gate = (0.1 * torch.randn((3, n), generator=g, device=dev)).float()
+        sets = torch.randint(0, 3, (m,), generator=g, device=dev, dtype=torch.uint8)
+        out = mh.gemm_gate_add(x, w, res, gate, x_scale=xs, w_scale=ws, set_of_row=sets, n_sets=3)
+        rel, cos = check_gemm_full(out, x, w, f"{which} {form} 768p", x_scale=xs, w_scale=ws, epi="gate_add",
+                                   residual0=res0, gate=gate, set_of_row=sets)
+    assert rel < 5e-3 and cos > 0.9999, (rel, cos)
     rows = np.unique(np.concatenate([[0, 1, 255, 256, m - 1], np.random.default_rng(0).integers(0, m, 11)]))
     ri = torch.from_numpy(rows).to(dev)
-    xs = to_bits(x[ri])
+    xb = to_bits(x[ri]) if f != orc.GEMM_W8A8 else x[ri].cpu().numpy()
+    wb = to_bits(w) if f == orc.GEMM_BF16 else w.cpu().numpy()
+    xsb = None if xs is None else xs[ri].cpu().numpy()
+    wsb = None if ws is None else ws.cpu().numpy()
     if which == "qkv":
-        want = orc.gemm(xs, to_bits(w), orc.GEMM_BF16)
+        want = orc.gemm(xb, wb, f, xsb, wsb)
     else:
-        want = orc.gemm_gate_add(xs, w.cpu().numpy(), orc.GEMM_W8A16, to_bits(res0[ri]), gate.cpu().numpy(), None,
-                                 ws.cpu().numpy())
-    check(to_bits(out[ri]), want, n, f"{which} 768p")
+        want = orc.gemm_gate_add(xb, wb, f, to_bits(res0[ri]), gate.cpu().numpy(), xsb, wsb,
+                                 sets[ri].cpu().numpy())
+    check(to_bits(out[ri]), want, n, f"{which} {form} 768p oracle rows")
 
 
 def test_gemm_rejects_bad_calls(dev):
