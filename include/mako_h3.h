@@ -334,6 +334,16 @@ int64_t mh3_time_embed_workspace_bytes(const MH3TimeArgs* args);
 int mh3_time_embed(const MH3TimeArgs* args, const float* t, const float* w_in, const float* b_in, const float* w_out,
                    const float* b_out, void* workspace, uint64_t workspace_bytes, float* temb, uint16_t* cond,
                    mh3_stream_t stream);
+/* mh3_time_embed without a workspace: it calls no allocator of any kind, so callers that cannot allocate device
+ * memory (code under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc) can produce the
+ * conditioning. This entry point has no counterpart in the reference. The hidden layer lives in a 256 KiB array of
+ * the library's own, one per GPU, held until the process ends: levels * hidden must be at most 65,536 floats (H3's
+ * 3 levels of 5376 use 16,128), else MH3_ERR_UNSUPPORTED. Every call on a GPU shares that GPU's array, so calls that
+ * overlap in time on one GPU (on different streams, or from several host threads) race; calls on one stream, or
+ * ordered by events, do not. Each call writes the part of the array it reads before reading it. Same results as
+ * mh3_time_embed, bit for bit. MH3_ERR_HIP if the array's address on the current device cannot be obtained. */
+int mh3_time_embed_noalloc(const MH3TimeArgs* args, const float* t, const float* w_in, const float* b_in,
+                           const float* w_out, const float* b_out, float* temb, uint16_t* cond, mh3_stream_t stream);
 /* A block's AdaLN projection (and the final layer's, n = 2 D): mod[u][r] = w[r] . cond[u] + bias[r] in float
  * accumulation, u < args->m levels, r < args->n. cond is bf16 [m][k] (mh3_time_embed's output), w bf16 [n][k] (the
  * weight's output rows), bias float [n] (may be NULL), mod float [m][n]. With n = 3 * 6 * D the rows of a level are

@@ -19,6 +19,7 @@
 #include "mh3_common.hpp"
 
 #include <cmath>
+#include <mutex>
 
 namespace mh3 {
 
@@ -335,6 +336,35 @@ int time_embed_check(const MH3TimeArgs* args, const float* t, const float* w_in,
     return MH3_OK;
 }
 
+// ---- the variant that allocates nothing ------------------------------------------------------------------------------
+// mh3_time_embed_noalloc keeps the hidden layer in this file-scope array instead of a caller's workspace: each GPU the
+// library runs on holds its own copy (256 KiB) until the process ends. Its address on the current device comes from
+// hipGetSymbolAddress, once per device; host code passes that address to the kernels, never the array's name (which
+// in host code is only a stand-in for the symbol).
+constexpr uint32_t kScratchFloats = 65536; // levels x hidden at most: e.g. 12 levels of H3's 5376
+static __device__ __align__(256) float scratch[kScratchFloats];
+
+namespace {
+constexpr int kMaxScratchDevices = 64;
+std::once_flag g_scratch_once[kMaxScratchDevices];
+float* g_scratch_ptr[kMaxScratchDevices];
+hipError_t g_scratch_rc[kMaxScratchDevices];
+} // namespace
+
+// The current device's copy of `scratch`, or null (with the HIP error recorded) if its address is not available.
+float* scratch_on_current_device()
+{
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxScratchDevices)
+        return nullptr;
+    std::call_once(g_scratch_once[dev], [dev] {
+        void* ptr = nullptr;
+        g_scratch_rc[dev] = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+        g_scratch_ptr[dev] = g_scratch_rc[dev] == hipSuccess ? static_cast<float*>(ptr) : nullptr;
+    });
+    return g_scratch_ptr[dev];
+}
+
 } // namespace mh3
 
 using namespace mh3;
@@ -362,6 +392,20 @@ int mh3_time_embed(const MH3TimeArgs* args, const float* t, const float* w_in, c
         return MH3_ERR_SHAPE;
     return time_embed_launch(args, t, w_in, b_in, w_out, b_out, static_cast<float*>(workspace), temb, cond,
                              static_cast<hipStream_t>(stream));
+}
+
+int mh3_time_embed_noalloc(const MH3TimeArgs* args, const float* t, const float* w_in, const float* b_in,
+                           const float* w_out, const float* b_out, float* temb, uint16_t* cond, mh3_stream_t stream)
+{
+    int rc = time_embed_check(args, t, w_in, w_out, temb);
+    if (rc != MH3_OK)
+        return rc;
+    if (uint64_t(args->levels) * args->hidden > kScratchFloats)
+        return MH3_ERR_UNSUPPORTED;
+    float* hid = scratch_on_current_device();
+    if (!hid)
+        return MH3_ERR_HIP;
+    return time_embed_launch(args, t, w_in, b_in, w_out, b_out, hid, temb, cond, static_cast<hipStream_t>(stream));
 }
 
 int mh3_adaln_mod(const MH3GemmArgs* args, const uint16_t* cond, const uint16_t* w, const float* bias, float* mod,

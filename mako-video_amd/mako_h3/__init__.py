@@ -103,6 +103,7 @@ def _load() -> C.CDLL:
         "mh3_cube_map": (I32, [C.POINTER(CubeMapArgs), P, P, P]),
         "mh3_time_embed_workspace_bytes": (I64, [C.POINTER(TimeArgs)]),
         "mh3_time_embed": (I32, [C.POINTER(TimeArgs), P, P, P, P, P, P, C.c_uint64, P, P, P]),
+        "mh3_time_embed_noalloc": (I32, [C.POINTER(TimeArgs), P, P, P, P, P, P, P, P]),
         "mh3_adaln_mod": (I32, [C.POINTER(GemmArgs), P, P, P, P, P]),
         "mh3_curve_mods": (I32, [C.POINTER(CurveArgs), P, P, P, P, P, P]),
         "mh3_heads_partial": (I32, [C.POINTER(HeadsArgs), P, P, P, P, P, P, P, P, P, P]),
