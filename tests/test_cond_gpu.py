@@ -53,8 +53,9 @@ def check_temb(temb, cond, want_temb, want_cond):
     rel, cos = diff(got, want, want.shape[1])
     assert rel < 1e-4 and cos > 0.999999, (rel, cos)
     g, w = bits_to_f64(to_bits(cond)), bits_to_f64(want_cond)
-    # one bf16 rounding of silu(temb) each: the two roundings may fall either side of a tie point
-    assert (np.abs(g - w) <= 2.0 ** -8 * np.abs(w) + 1e-30).all()
+    # one bf16 rounding each of silu(temb), from temb values 1e-5 of the level's scale apart: the two may round to
+    # neighbouring bf16 values (one step, up to 2^-7 of the value), plus that 1e-5 where silu(temb) is near zero
+    assert (np.abs(g - w) <= 2.0 ** -7 * np.abs(w) + 1e-5 * np.abs(w).max(1, keepdims=True)).all()
 
 
 @pytest.mark.parametrize("t", [[0.9230769], [0.5, 0.999], [0.0, 0.25, 1.0], [0.1, 0.3, 0.5, 0.7, 0.9]])

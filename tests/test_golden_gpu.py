@@ -66,7 +66,7 @@ def test_golden_fixture_on_gpu(dev, case):
         temb, cond = mh.time_embed(t(d["t"]), t(d["w_in"]), t(d["b_in"]), t(d["w_out"]), t(d["b_out"]))
         close_rows(temb.cpu().numpy(), d["temb"], 1e-5, case["out_dim"])
         g, w = bits_to_f64(to_bits(cond)), bits_to_f64(d["cond"])
-        assert (np.abs(g - w) <= 2.0 ** -8 * np.abs(w) + 1e-30).all()
+        assert (np.abs(g - w) <= 2.0 ** -7 * np.abs(w) + 1e-5 * np.abs(w).max(1, keepdims=True)).all()
     elif op == "adaln_mod":
         got = mh.adaln_mod(from_bits(d["cond"], dev), from_bits(d["w"], dev), t(d["bias"]))
         close_rows(got.cpu().numpy(), d["mod"], 1e-5, case["n"])
