@@ -122,6 +122,80 @@ struct GemmGate {
 typedef int int32x4 __attribute__((ext_vector_type(4)));
 typedef int int32x16 __attribute__((ext_vector_type(16)));
 
+// The epilogue shared by the GEMM kernels, through the LDS (idle after the last K-step). acc[a][b][e] is y[r][c]
+// with tile row r = wm (256 / WM) + a 32 + 8 (e / 4) + 4 (lane / 32) + e % 4 and c = lane % 32 + 32 b + wn 32 TN
+// within the tile's first 128 w rows (b < TN) or, for acc[a][TN + b], the same position in its second 128. A
+// 128-column half of the tile at a time, each wave writes its scaled results as floats into a [256][kEpiStride] LDS
+// tile (the two half-waves' rows, 4 apart, fall on disjoint banks); then each thread takes 8 consecutive columns of
+// a row, so the output, and with kGateAdd the residual, moves in 16-byte accesses, 16 threads to a row's 256 bytes.
+// The results round to bf16 once, at the end, as they would written straight from the registers.
+template <int WM, int WN, int MODE, int EPI, int TM, int TN, typename Acc>
+__device__ __forceinline__ void gemm_epilogue(Acc (&acc)[TM][2 * TN], u32x4_t* smem, uint32_t M, uint32_t N,
+                                              uint32_t m0, uint32_t w_lo, uint32_t w_hi,
+                                              const float* __restrict__ scale, const float* __restrict__ xscale,
+                                              uint16_t* __restrict__ out, const GemmGate& gg)
+{
+    constexpr uint32_t kThreads = WM * WN * 64;
+    const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6, wm = wave / WN, wn = wave % WN;
+    const uint32_t half = lane >> 5, r32 = lane & 31u;
+    constexpr uint32_t kEpiStride = kBN + 8u; // floats a staged row: 4 rows apart = 32 banks apart
+    static_assert(kBM * kEpiStride * sizeof(float) <= kGemmLds, "the staged half-tile fits in the LDS");
+    constexpr int kHalves = EPI == kSwiGLU ? 1 : 2;
+    float* const stage = reinterpret_cast<float*>(smem);
+    lds_barrier(); // every wave is done with the last K-step's fragments
+#pragma unroll
+    for (int hv = 0; hv < kHalves; ++hv) {
+        if (hv)
+            lds_barrier(); // the first half is read out
+#pragma unroll
+        for (int b = 0; b < TN; ++b) {
+            const uint32_t c = wn * 32u * TN + uint32_t(b) * 32u + r32;
+            const float s_lo = MODE != kBf16 ? scale[w_lo + c] : 1.0f, s_hi = MODE != kBf16 ? scale[w_hi + c] : 1.0f;
+#pragma unroll
+            for (int a = 0; a < TM; ++a) {
+#pragma unroll
+                for (int e = 0; e < 16; ++e) {
+                    const uint32_t r = wm * (kBM / WM) + uint32_t(a) * 32u + 8u * (uint32_t(e) >> 2) + 4u * half +
+                                       (uint32_t(e) & 3u);
+                    const float sx = MODE == kW8A8 ? xscale[min(m0 + r, M - 1u)] : 1.0f;
+                    float v;
+                    if constexpr (EPI == kSwiGLU) {
+                        const float lo = float(acc[a][b][e]) * s_lo * sx, hi = float(acc[a][TN + b][e]) * s_hi * sx;
+                        v = lo * __builtin_amdgcn_rcpf(1.0f + __expf(-lo)) * hi;
+                    } else {
+                        v = hv == 0 ? float(acc[a][b][e]) * s_lo * sx : float(acc[a][TN + b][e]) * s_hi * sx;
+                    }
+                    stage[r * kEpiStride + c] = v;
+                }
+            }
+        }
+        lds_barrier();
+        // Output column of staged column 0: the tile's gate columns (SwiGLU), else its first or second 128 columns.
+        const uint32_t col0 = hv == 0 ? w_lo : w_hi;
+        for (uint32_t q = tid; q < kBM * 16u; q += kThreads) {
+            const uint32_t r = q >> 4, c8 = (q & 15u) * 8u, row = m0 + r;
+            if (row >= M)
+                break; // rows grow with q
+            const float4 v0 = *reinterpret_cast<const float4*>(stage + r * kEpiStride + c8);
+            const float4 v1 = *reinterpret_cast<const float4*>(stage + r * kEpiStride + c8 + 4u);
+            float o[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
+            uint4* dst = reinterpret_cast<uint4*>(out + uint64_t(row) * N + col0 + c8);
+            if constexpr (EPI == kGateAdd) {
+                const uint32_t set = gg.set_of_row ? min(uint32_t(gg.set_of_row[row]), gg.n_sets - 1u) : 0u;
+                const float* g = gg.gate + uint64_t(set) * gg.gate_stride + col0 + c8;
+                const uint4 res = *dst;
+                const uint32_t rw[4] = {res.x, res.y, res.z, res.w};
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    o[2 * i] = fmaf(g[2 * i], o[2 * i], bf16_lo(rw[i]));
+                    o[2 * i + 1] = fmaf(g[2 * i + 1], o[2 * i + 1], bf16_hi(rw[i]));
+                }
+            }
+            *dst = uint4{pack_bf16(o[0], o[1]), pack_bf16(o[2], o[3]), pack_bf16(o[4], o[5]), pack_bf16(o[6], o[7])};
+        }
+    }
+}
+
 // WM x WN wavefronts: wave (wm, wn) computes rows wm * (256 / WM) ... of the tile against its TN gate column tiles
 // (32 columns each, from wn * 32 TN) and the TN matching up column tiles. Every LDS row holds 128 bytes of k: 64 k of
 // bf16 or 128 k of int8, so a K-step is 64 or 128 k.
@@ -366,69 +440,7 @@ __global__ __launch_bounds__(kGemmWM * kGemmWN * 64) void gemm_kernel(
         kstep(kt, std::false_type{});
     kstep(KT - 1, std::true_type{});
 
-    // Epilogue through LDS, idle after the last K-step. acc[a][b][e] is y[r][c] with tile row
-    // r = wm (256 / WM) + a 32 + 8 (e / 4) + 4 (lane / 32) + e % 4 and c = lane % 32 + 32 b + wn 32 TN within the
-    // tile's first 128 w rows (b < TN) or, for acc[a][TN + b], the same position in its second 128. A 128-column half of the
-    // tile at a time, each wave writes its scaled results as floats into a [256][kEpiStride] LDS tile (the two
-    // half-waves' rows, 4 apart, fall on disjoint banks); then each thread takes 8 consecutive columns of a row, so
-    // the output, and with kGateAdd the residual, moves in 16-byte accesses, 16 threads to a row's 256 bytes. The
-    // results round to bf16 once, at the end, as they would written straight from the registers.
-    constexpr uint32_t kEpiStride = kBN + 8u; // floats a staged row: 4 rows apart = 32 banks apart
-    static_assert(kBM * kEpiStride * sizeof(float) <= kGemmLds, "the staged half-tile fits in the LDS");
-    constexpr int kHalves = EPI == kSwiGLU ? 1 : 2;
-    float* const stage = reinterpret_cast<float*>(smem);
-    lds_barrier(); // every wave is done with the last K-step's fragments
-#pragma unroll
-    for (int hv = 0; hv < kHalves; ++hv) {
-        if (hv)
-            lds_barrier(); // the first half is read out
-#pragma unroll
-        for (int b = 0; b < TN; ++b) {
-            const uint32_t c = wn * 32u * TN + uint32_t(b) * 32u + r32;
-            const float s_lo = MODE != kBf16 ? scale[w_lo + c] : 1.0f, s_hi = MODE != kBf16 ? scale[w_hi + c] : 1.0f;
-#pragma unroll
-            for (int a = 0; a < TM; ++a) {
-#pragma unroll
-                for (int e = 0; e < 16; ++e) {
-                    const uint32_t r = wm * (kBM / WM) + uint32_t(a) * 32u + 8u * (uint32_t(e) >> 2) + 4u * half +
-                                       (uint32_t(e) & 3u);
-                    const float sx = MODE == kW8A8 ? xscale[min(m0 + r, M - 1u)] : 1.0f;
-                    float v;
-                    if constexpr (EPI == kSwiGLU) {
-                        const float lo = float(acc[a][b][e]) * s_lo * sx, hi = float(acc[a][TN + b][e]) * s_hi * sx;
-                        v = lo * __builtin_amdgcn_rcpf(1.0f + __expf(-lo)) * hi;
-                    } else {
-                        v = hv == 0 ? float(acc[a][b][e]) * s_lo * sx : float(acc[a][TN + b][e]) * s_hi * sx;
-                    }
-                    stage[r * kEpiStride + c] = v;
-                }
-            }
-        }
-        lds_barrier();
-        // Output column of staged column 0: the tile's gate columns (SwiGLU), else its first or second 128 columns.
-        const uint32_t col0 = hv == 0 ? w_lo : w_hi;
-        for (uint32_t q = tid; q < kBM * 16u; q += kThreads) {
-            const uint32_t r = q >> 4, c8 = (q & 15u) * 8u, row = m0 + r;
-            if (row >= M)
-                break; // rows grow with q
-            const float4 v0 = *reinterpret_cast<const float4*>(stage + r * kEpiStride + c8);
-            const float4 v1 = *reinterpret_cast<const float4*>(stage + r * kEpiStride + c8 + 4u);
-            float o[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
-            uint4* dst = reinterpret_cast<uint4*>(out + uint64_t(row) * N + col0 + c8);
-            if constexpr (EPI == kGateAdd) {
-                const uint32_t set = gg.set_of_row ? min(uint32_t(gg.set_of_row[row]), gg.n_sets - 1u) : 0u;
-                const float* g = gg.gate + uint64_t(set) * gg.gate_stride + col0 + c8;
-                const uint4 res = *dst;
-                const uint32_t rw[4] = {res.x, res.y, res.z, res.w};
-#pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    o[2 * i] = fmaf(g[2 * i], o[2 * i], bf16_lo(rw[i]));
-                    o[2 * i + 1] = fmaf(g[2 * i + 1], o[2 * i + 1], bf16_hi(rw[i]));
-                }
-            }
-            *dst = uint4{pack_bf16(o[0], o[1]), pack_bf16(o[2], o[3]), pack_bf16(o[4], o[5]), pack_bf16(o[6], o[7])};
-        }
-    }
+    gemm_epilogue<WM, WN, MODE, EPI, TM, TN>(acc, smem, M, N, m0, w_lo, w_hi, scale, xscale, out, gg);
 }
 
 } // namespace mh3

@@ -310,8 +310,7 @@ __global__ __launch_bounds__(1024) void rows_kernel(RowsParams p)
 // of every set into LDS once; each wave holds a whole row (NV 16-byte vectors a lane of x, and of the residual) in
 // registers, reduces it with DPP and three cross-row reads, and streams the outputs one vector at a time, reading
 // that vector's coefficients from LDS just before use.
-constexpr uint32_t kWaveBlock = 704; // wave-kernel workgroup threads: 11 waves, measured best of 6 to 16 at one
-                                     // workgroup a CU
+constexpr uint32_t kWaveBlock = 512; // wave-kernel workgroup threads: 8 waves, two workgroups a CU
 
 template <int DT, int NV, int OP, int SRC>
 __global__ __launch_bounds__(kWaveBlock) void rows_wave_kernel(RowsParams p)
@@ -494,7 +493,7 @@ namespace {
 using namespace mh3;
 
 constexpr size_t kCoefLdsMax = 64 * 1024;
-constexpr size_t kWaveLdsFloor = 81 * 1024; // above half of gfx950's 160 KiB: one wave-kernel workgroup a CU
+constexpr size_t kWaveLdsFloor = 54 * 1024; // above a third of gfx950's 160 KiB: two wave-kernel workgroups a CU
 constexpr size_t kSwigluFusedLds = 40 * 1024; // four SwiGLU workgroups a CU (fused-row layout)
 constexpr int kSwigluVecs = 1; // 16-byte vectors of gate (and of up) a thread has in flight
 
@@ -534,11 +533,12 @@ int launch_rows_wave(const RowsParams& p, hipStream_t stream)
     else
         k = pick_wave_kernel<DT, 12, OP>(src);
     const uint32_t threads = kWaveBlock, waves = threads / 64u;
-    // The dynamic LDS is at least kWaveLdsFloor, so one workgroup (11 waves, 11 rows in flight) holds a CU: fewer rows
-    // in flight streamed faster than the 2 to 4 workgroups the registers would allow (at 8 waves a workgroup: 5.96 to
-    // 6.04 TB/s against 5.79 to 5.91 for the fused op at 768p, alternating runs on one GPU; 10 waves: 6.05), as fewer
-    // open streams contend for the DRAM banks. 11 waves beat 10 by 0.4-0.5% (and by 1.5-3% at 16,192 rows); 12 equalled
-    // 10 and 13 were 8% slower.
+    // The dynamic LDS is at least kWaveLdsFloor, so two workgroups (16 waves, 16 rows in flight) share a CU. Fewer
+    // rows in flight streamed faster than the registers would allow (at three or four 8-wave workgroups a CU: 5.79 to
+    // 5.91 TB/s for the fused op at 768p), as fewer open streams contend for the DRAM banks; of one workgroup of 10 to
+    // 16 waves, or two of 5 to 9, two of 7 or 8 were fastest, 0.5-1.6% ahead of one of 11 (alternating runs on one
+    // GPU), since while one workgroup drains its last rows the other keeps the CU's loads going. A grid of persistent
+    // workgroups, whose waves stride through far-apart rows, was 9-15% slower.
     const size_t table = src == kCoefLds ? size_t(p.n_sets) * p.dim * kPlanes<OP> * sizeof(float) : 0;
     const size_t lds = table > kWaveLdsFloor ? table : kWaveLdsFloor;
     if (host::allow_dynamic_lds(k, lds) != hipSuccess)
