@@ -2,7 +2,7 @@
 // (oracle/mh3_oracle.h), reported the way the reference's tests/h3_ref_test.cpp reports: one line per
 // check, "ok" or "FAIL", the relative RMS error and the lowest row cosine of diff() (h3_ref_test.cpp:67-90), and
 // the number of failures as the exit status.
-//   h3_kernels_test [rows | swiglu | cubes | attn | int8 | proj | errors | all]
+//   h3_kernels_test [rows | swiglu | cubes | attn | int8 | proj | cond | errors | all]
 #include "mako_h3.hpp"
 #include "mh3_oracle.h"
 
@@ -382,6 +382,89 @@ void proj()
             2e-2);
 }
 
+// H3::Cubes' map and a step's conditioning (the time MLP, a block's AdaLN projection, the pruned curve) through the
+// C++ layer, against the oracle; the table then feeds the fused row op through set_stride = 6 D.
+void cond()
+{
+    std::printf("cond\n");
+    Kernels k;
+    {
+        const uint32_t T = 37, H = 24, W = 42, nd = 640;
+        const int64_t C = mh3_cube_count(T, H, W);
+        const size_t cubes = size_t(C);
+        DeviceBuffer<int32_t> map(cubes * 64 + nd), counts(cubes);
+        k.cube_map(T, H, W, nd, nd, 0, map.get(), counts.get());
+        std::vector<int32_t> wm(map.size()), wc(counts.size());
+        mh3o_cube_map(T, H, W, nd, nd, 0, wm.data(), wc.data());
+        check(map.download() == wm && counts.download() == wc,
+              "H3::Cubes map of the padded 37 x 24 x 42 grid (660 cubes) + 640 dense rows, bit for bit");
+    }
+    Rng r(7);
+    const uint32_t levels = 3, fd = 256, hid = 1024, D = 1024, od = D / 2, n = 18 * D;
+    auto w_in = normals(r, size_t(hid) * fd, 1.0 / 16), b_in = normals(r, hid, 0.1);
+    auto w_out = normals(r, size_t(od) * hid, 1.0 / 32), b_out = normals(r, od, 0.1);
+    const std::vector<float> t = {0.9230769f, 0.5f, 0.999f};
+    DeviceBuffer<float> dt(t), dwi(w_in), dbi(b_in), dwo(w_out), dbo(b_out), temb(size_t(levels) * od);
+    DeviceBuffer<uint16_t> cond(size_t(levels) * od);
+    const MH3TimeArgs ta{levels, fd, hid, od, 10000.0f, {0, 0, 0}};
+    DeviceBuffer<uint8_t> ws(Kernels::time_embed_workspace_bytes(ta));
+    k.time_embed(ta, dt.get(), dwi.get(), dbi.get(), dwo.get(), dbo.get(), ws.get(), ws.size(), temb.get(),
+                 cond.get());
+    std::vector<float> wt(temb.size());
+    std::vector<uint16_t> wcond(cond.size());
+    mh3o_time_embed(levels, fd, hid, od, 10000.0, t.data(), w_in.data(), b_in.data(), w_out.data(), b_out.data(),
+                    wt.data(), wcond.data());
+    compare("time embedding (256 -> 1024 -> 512, 3 levels)", of_f32(temb.download()), of_f32(wt), od, 1e-4, 1e-5);
+    // The projection over the GPU's own cond, so that it is tested alone.
+    std::vector<uint16_t> wa(size_t(n) * od);
+    for (auto& x : wa)
+        x = mh3o_bf16_from_double(0.02 * r.normal());
+    auto bias = normals(r, n, 0.01);
+    DeviceBuffer<uint16_t> dwa(wa);
+    DeviceBuffer<float> dbias(bias), mod(size_t(levels) * n);
+    k.adaln_mod(levels, n, od, cond.get(), dwa.get(), dbias.get(), mod.get());
+    const auto gcond = cond.download();
+    std::vector<float> wmod(mod.size());
+    mh3o_adaln_mod(levels, n, od, gcond.data(), wa.data(), bias.data(), wmod.data());
+    compare("AdaLN projection (512 -> 18 x 1024, 3 levels)", of_f32(mod.download()), of_f32(wmod), D, 1e-4, 1e-5);
+    // The pruned checkpoints' curve.
+    auto table = normals(r, 1025 * 8), wc8 = normals(r, size_t(n) * 8);
+    DeviceBuffer<float> dtab(table), dwc(wc8), cmod(size_t(levels) * n);
+    k.curve_mods(levels, n, 1025, 8, dt.get(), dtab.get(), dwc.get(), dbias.get(), cmod.get());
+    std::vector<float> wcm(cmod.size());
+    mh3o_curve_mods(levels, n, 1025, 8, t.data(), table.data(), wc8.data(), bias.data(), wcm.data());
+    compare("pruned curve modulation ([1025][8] table, 3 levels)", of_f32(cmod.download()), of_f32(wcm), D, 1e-4,
+            1e-5);
+    // The table's (level, tag) sets into the fused row op: set 3 u + tag at set_stride 6 D.
+    const uint32_t rows = 96;
+    auto x = bf16_normals(r, size_t(rows) * D), res = bf16_normals(r, size_t(rows) * D);
+    std::vector<uint8_t> sets(rows);
+    for (uint32_t i = 0; i < rows; ++i)
+        sets[i] = uint8_t(i % 9);
+    auto nw = normals(r, D, 0.02, 1.0);
+    DeviceBuffer<uint16_t> dx(x), dres(res), dout(size_t(rows) * D);
+    DeviceBuffer<uint8_t> dsets(sets);
+    DeviceBuffer<float> dnw(nw);
+    Modulation m;
+    m.w = dnw.get(), m.shift = mod.get(), m.scale = mod.get() + D, m.gate = mod.get() + 2 * D;
+    m.set_of_row = dsets.get(), m.n_sets = 9, m.set_stride = 6 * D;
+    k.rms_mod_gate_add_rows(rows, D, MH3_BF16, dx.get(), dres.get(), m, dout.get());
+    const auto gmod = mod.download();
+    std::vector<float> sh(9 * D), sc(9 * D), ga(9 * D);
+    for (uint32_t s = 0; s < 9; ++s)
+        for (uint32_t j = 0; j < D; ++j) {
+            sh[s * D + j] = gmod[(size_t(s) * 6 + 0) * D + j];
+            sc[s * D + j] = gmod[(size_t(s) * 6 + 1) * D + j];
+            ga[s * D + j] = gmod[(size_t(s) * 6 + 2) * D + j];
+        }
+    std::vector<uint16_t> want(size_t(rows) * D);
+    mh3o_rms_mod_gate_add_rows(rows, D, 1e-6f, MH3O_BF16, x.data(), res.data(), nw.data(), sh.data(), sc.data(),
+                               ga.data(), sets.data(), want.data());
+    compare("fused rows with 9 (level, tag) sets from the [3][3][6][D] table", of_bf16(dout.download()), of_bf16(want),
+            D, 1e-2, 1e-5);
+    k.finish();
+}
+
 void errors()
 {
     std::printf("errors\n");
@@ -429,6 +512,8 @@ int main(int argc, char** argv)
             int8();
         if (mode == "proj" || mode == "all")
             proj();
+        if (mode == "cond" || mode == "all")
+            cond();
         if (mode == "errors" || mode == "all")
             errors();
     } catch (const std::exception& e) {

@@ -17,7 +17,7 @@ def test_driver_is_built_and_links():
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("mode", ["rows", "swiglu", "cubes", "attn", "int8", "proj", "errors"])
+@pytest.mark.parametrize("mode", ["rows", "swiglu", "cubes", "attn", "int8", "proj", "cond", "errors"])
 def test_host_layer_parity(mode):
     r = subprocess.run([str(EXE), mode], capture_output=True, text=True, timeout=300)
     print(r.stdout)
