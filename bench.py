@@ -411,6 +411,19 @@ def bench_heads(mh, dev, steps, warmup):
     gbytes = cmap.numel() * 3 * HEADS * 128 * 4 + cmap.numel() * (48 * 8 + 4)
     res["gathered"] = {"ms": gms, "bytes": gbytes, "GBs": gbytes / gms / 1e6,
                        "frac": gbytes / gms / 1e6 / HBM_PEAK_GBS, "rows": cmap.numel()}
+    # The same pass with cube_pool fused in (mh3_heads_partial_pool): the selector's cube means from the values as
+    # they are stored, against the gathered heads_partial followed by cube_pool over its output.
+    cubes = mh.cube_count(*GRID)
+    qc = torch.empty((HEADS, cubes, 128), dtype=torch.float32, device=dev)
+    kc = torch.empty_like(qc)
+    pa = mh.cube_args(HEADS, GRID, layout=mh.CUBES_GATHERED, row0=0, head_stride=cmap.numel() * 128)
+    pool_ms, _ = time_launches(lambda: mh.cube_pool(pa, gout[0], gout[1], qc=qc, kc=kc), steps, warmup)
+    fms, _ = time_launches(lambda: mh.heads_partial_pool(x, HEADS, GRID, qw, kw, ct, st, map=cmap, q=gout[0],
+                                                         k=gout[1], v=gout[2], qc=qc, kc=kc), steps, warmup)
+    fbytes = gbytes + 2 * HEADS * cubes * 128 * 4
+    res["gathered_pool"] = {"ms": fms, "bytes": fbytes, "GBs": fbytes / fms / 1e6,
+                            "frac": fbytes / fms / 1e6 / HBM_PEAK_GBS, "two_kernel_ms": gms + pool_ms,
+                            "pool_ms": pool_ms, "pool_cost_in_pass_ms": fms - gms}
     return res
 
 
@@ -740,6 +753,11 @@ def main() -> int:
     if "heads" in ops:
         report["heads_partial"] = bench_heads(mh, dev, args.steps, args.warmup)
         torch.cuda.empty_cache()
+    sel, hp = report.get("cube_selector"), report.get("heads_partial")
+    if sel and hp:
+        # The selector with its pool folded into heads_partial: what the pool still costs there, plus cube_select.
+        extra = hp["gathered_pool"]["pool_cost_in_pass_ms"]
+        sel["pool_in_heads_partial"] = {"pool_ms": extra, "ms": extra + sel["select_ms"]}
     if "attn" in ops:
         report["flash_attn_sparse_128"] = bench_attn(mh, dev, max(3, args.steps // 2), max(1, args.warmup // 2))
         torch.cuda.empty_cache()

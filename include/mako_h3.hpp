@@ -273,6 +273,17 @@ public:
         const MH3HeadsArgs a = hd.args();
         check(mh3_heads_partial(&a, qkv, q_w, k_w, cos_t, sin_t, map, q, k, v, s_), "heads_partial");
     }
+    // heads_partial, then cube_pool over its output, in one pass: c is the gathered geometry of the head tiles this
+    // call writes (its strides those of hd's outputs).
+    void heads_partial_pool(const Heads& hd, const Cubes& c, const uint16_t* qkv, const float* q_w, const float* k_w,
+                            const float* cos_t, const float* sin_t, const int32_t* map, uint16_t* q, uint16_t* k,
+                            uint16_t* v, float* qc, float* kc, int32_t* counts = nullptr) const
+    {
+        const MH3HeadsArgs a = hd.args();
+        const MH3CubeArgs ca = c.args();
+        check(mh3_heads_partial_pool(&a, &ca, qkv, q_w, k_w, cos_t, sin_t, map, q, k, v, qc, kc, counts, s_),
+              "heads_partial_pool");
+    }
     // Flash attention over the pass lists idx / cnt of cube_select (or cube_topk) and the dense rows
     // [dense_row0, dense_row0 + n_dense); q, k, v and out in c's cube geometry. scale 0: 1 / sqrt(128).
     void flash_attn_sparse_128(const Cubes& c, const uint16_t* q, const uint16_t* k, const uint16_t* v,

@@ -107,6 +107,7 @@ def _load() -> C.CDLL:
         "mh3_adaln_mod": (I32, [C.POINTER(GemmArgs), P, P, P, P, P]),
         "mh3_curve_mods": (I32, [C.POINTER(CurveArgs), P, P, P, P, P, P]),
         "mh3_heads_partial": (I32, [C.POINTER(HeadsArgs), P, P, P, P, P, P, P, P, P, P]),
+        "mh3_heads_partial_pool": (I32, [C.POINTER(HeadsArgs), C.POINTER(CubeArgs)] + [P] * 13),
         "mh3_flash_attn_sparse_128": (I32, [C.POINTER(AttnArgs), P, P, P, P, P, P, P]),
         "mh3_quant_rows_i8": (I32, [C.POINTER(QuantArgs), P, P, P, P]),
         "mh3_gemm_w8a16_swiglu": (I32, [C.POINTER(GemmArgs), P, P, P, P, P]),
@@ -494,13 +495,7 @@ def curve_mods(t, table, w, bias=None, *, out=None):
 
 # ---- heads_partial ---------------------------------------------------------------------------------------------------
 
-def heads_partial(qkv, heads, q_w=None, k_w=None, cos_t=None, sin_t=None, *, rot=96, eps=1e-6, map=None,
-                  with_v=True, layout="heads", q=None, k=None, v=None):
-    """After the QKV GEMM: qkv bf16 [model_rows][>= 3 heads 128] ([q heads | k heads | v heads] a row) -> q and k
-    with the per-head RMS norm (weights q_w, k_w f32 [128]; None: 1) and the rotary positions on the first `rot`
-    values (cos_t, sin_t f32 [model_rows][rot / 2]), v copied (not written when with_v is False). Output row r is model
-    row map[r] (int32 [rows]; entries outside [0, model_rows) give zeros), or row r without a map. layout "heads"
-    gives [heads][rows][128] tensors, "rows" gives [rows][heads * 128]. Returns (q, k, v)."""
+def _heads_setup(qkv, heads, q_w, k_w, cos_t, sin_t, rot, eps, map, with_v, layout, q, k, v):
     if qkv.dim() != 2:
         raise ValueError("qkv must be [rows][3 heads 128]")
     model_rows, stride = qkv.shape
@@ -530,9 +525,41 @@ def heads_partial(qkv, heads, q_w=None, k_w=None, cos_t=None, sin_t=None, *, rot
         t = torch.empty(shape, dtype=torch.bfloat16, device=qkv.device) if t is None else t
         _need(t, name, torch.bfloat16, heads * rows * 128)
         outs.append(t)
-    _check(lib.mh3_heads_partial(C.byref(a), _ptr(qkv), _ptr(q_w), _ptr(k_w), _ptr(cos_t if rot else None),
-                                 _ptr(sin_t if rot else None), _ptr(map), *(_ptr(t) for t in outs), _stream()), "heads_partial")
+    ptrs = (_ptr(qkv), _ptr(q_w), _ptr(k_w), _ptr(cos_t if rot else None), _ptr(sin_t if rot else None), _ptr(map))
+    return a, outs, ptrs
+
+
+def heads_partial(qkv, heads, q_w=None, k_w=None, cos_t=None, sin_t=None, *, rot=96, eps=1e-6, map=None,
+                  with_v=True, layout="heads", q=None, k=None, v=None):
+    """After the QKV GEMM: qkv bf16 [model_rows][>= 3 heads 128] ([q heads | k heads | v heads] a row) -> q and k
+    with the per-head RMS norm (weights q_w, k_w f32 [128]; None: 1) and the rotary positions on the first `rot`
+    values (cos_t, sin_t f32 [model_rows][rot / 2]), v copied (not written when with_v is False). Output row r is model
+    row map[r] (int32 [rows]; entries outside [0, model_rows) give zeros), or row r without a map. layout "heads"
+    gives [heads][rows][128] tensors, "rows" gives [rows][heads * 128]. Returns (q, k, v)."""
+    a, outs, ptrs = _heads_setup(qkv, heads, q_w, k_w, cos_t, sin_t, rot, eps, map, with_v, layout, q, k, v)
+    _check(lib.mh3_heads_partial(C.byref(a), *ptrs, *(_ptr(t) for t in outs), _stream()), "heads_partial")
     return tuple(outs)
+
+
+def heads_partial_pool(qkv, heads, grid, q_w=None, k_w=None, cos_t=None, sin_t=None, *, rot=96, eps=1e-6, map=None,
+                       with_v=True, layout="heads", row0=0, q=None, k=None, v=None, qc=None, kc=None, counts=None):
+    """heads_partial followed by cube_pool over its output in the gathered layout, in one pass: cube c of the video
+    grid (T, H, W) = `grid` is output rows row0 + 64 c ... + 63. Returns (q, k, v, qc, kc), the same bits as
+    heads_partial(...) then cube_pool(cube_args(heads, grid, layout=CUBES_GATHERED, row0=row0, ...), q, k)."""
+    a, outs, ptrs = _heads_setup(qkv, heads, q_w, k_w, cos_t, sin_t, rot, eps, map, with_v, layout, q, k, v)
+    ca = cube_args(heads, grid, layout=CUBES_GATHERED, row0=row0, head_stride=a.out_head_stride,
+                   row_stride=a.out_row_stride)
+    cubes = cube_count(*grid)
+    shape = (heads, cubes, 128)
+    qc = torch.empty(shape, dtype=torch.float32, device=qkv.device) if qc is None else qc
+    kc = torch.empty(shape, dtype=torch.float32, device=qkv.device) if kc is None else kc
+    _need(qc, "qc", torch.float32, heads * cubes * 128)
+    _need(kc, "kc", torch.float32, heads * cubes * 128)
+    if counts is not None:
+        _need(counts, "counts", torch.int32, cubes)
+    _check(lib.mh3_heads_partial_pool(C.byref(a), C.byref(ca), *ptrs, *(_ptr(t) for t in outs), _ptr(qc), _ptr(kc),
+                                      _ptr(counts), _stream()), "heads_partial_pool")
+    return (*outs, qc, kc)
 
 
 # ---- flash_attn_sparse_128 -------------------------------------------------------------------------------------------

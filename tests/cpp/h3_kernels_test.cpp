@@ -282,6 +282,22 @@ void attn()
                      oo.data());
     compare("flash_attn_sparse_128 over the gathered tiles, 2 heads, 7x9x10 grid + 70 text rows",
             of_bf16(out.download()), of_bf16(oo), 128, 1e-2, 3e-3);
+    // heads_partial and cube_pool in one pass: the same bits as the two calls above.
+    DeviceBuffer<uint16_t> q2(tile), k2(tile), v2(tile);
+    DeviceBuffer<float> qc2(qc.size()), kc2(kc.size());
+    DeviceBuffer<int32_t> counts2(C);
+    kern.heads_partial_pool(hd, c, dqkv.get(), dqw.get(), dkw.get(), dcs.get(), dsn.get(), dmap.get(), q2.get(),
+                            k2.get(), v2.get(), qc2.get(), kc2.get(), counts2.get());
+    kern.finish();
+    check(q2.download() == q.download() && k2.download() == k.download() && v2.download() == v.download(),
+          "heads_partial_pool head tiles bit for bit as heads_partial's");
+    check(qc2.download() == qc.download() && kc2.download() == kc.download(),
+          "heads_partial_pool cube means bit for bit as cube_pool's over those tiles");
+    std::vector<int32_t> want_counts(C);
+    for (uint32_t cube = 0; cube < C; ++cube)
+        want_counts[cube] = int32_t(std::count_if(map.begin() + 64 * cube, map.begin() + 64 * (cube + 1),
+                                                  [](int32_t m) { return m >= 0; }));
+    check(counts2.download() == want_counts, "heads_partial_pool token counts");
 }
 
 void int8()

@@ -293,3 +293,39 @@ def test_adaln_and_curve_validation():
     assert mh.lib.mh3_curve_mods(C.byref(c), FAKE, FAKE, FAKE, None, FAKE, None) == mh.ERR_SHAPE
     c.points, c.width = 1025, 33
     assert mh.lib.mh3_curve_mods(C.byref(c), FAKE, FAKE, FAKE, None, FAKE, None) == mh.ERR_SHAPE
+
+
+def test_heads_partial_pool_validation():
+    """The fused heads_partial + cube_pool takes only the gathered geometry of the tiles it writes."""
+    grid, heads = (8, 8, 12), 2
+    cubes = 2 * 2 * 3
+    rows = cubes * 64 + 70
+    h = mh.HeadsArgs()
+    h.rows, h.model_rows, h.heads, h.head_dim, h.rot, h.eps = rows, rows, heads, 128, 96, 1e-6
+    h.qkv_stride, h.out_head_stride, h.out_row_stride = 3 * heads * 128, rows * 128, 128
+
+    base = 0x1000  # aligned; never dereferenced
+
+    def call(cube_kw=None, qc=base, hk=None, **ptrs):
+        ca = mh.cube_args(heads, grid, layout=mh.CUBES_GATHERED, head_stride=rows * 128)
+        for key, val in (cube_kw or {}).items():
+            setattr(ca, key, val)
+        a = mh.HeadsArgs.from_buffer_copy(h)
+        for key, val in (hk or {}).items():
+            setattr(a, key, val)
+        p = dict(qkv=base, cos=base, q=base + 2**34, k=base + 2**35, kc=base + 2**36)
+        p.update(ptrs)
+        return mh.lib.mh3_heads_partial_pool(C.byref(a), C.byref(ca), p["qkv"], None, None, p["cos"], p["cos"], None,
+                                             p["q"], p["k"], None, qc, p["kc"], None, None)
+
+    assert mh.lib.mh3_heads_partial_pool(None, None, *([None] * 13)) == mh.ERR_POINTER
+    assert call({"layout": mh.CUBES_GRID}) == mh.ERR_PARAM             # the pool reads what this call writes
+    assert call({"heads": 3}) == mh.ERR_PARAM
+    assert call({"row_stride": 256}) == mh.ERR_PARAM
+    assert call({"head_stride": rows * 128 + 8}) == mh.ERR_PARAM
+    assert call({"row0": 71}) == mh.ERR_SHAPE                            # the cube rows run past the output rows
+    assert call(hk={"rows": cubes * 64 - 1}) == mh.ERR_SHAPE
+    assert call(hk={"rot": 24}) == mh.ERR_PARAM                          # heads_partial's own checks still apply
+    assert call(qc=None) == mh.ERR_POINTER
+    assert call(qc=base + 4) == mh.ERR_ALIGN
+    assert call(kc=base + 2**36 + 8) == mh.ERR_ALIGN
