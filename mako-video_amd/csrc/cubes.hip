@@ -334,10 +334,17 @@ __device__ __forceinline__ void topk_keys(const RowKeys<KPL>& rk, const CubeGeo&
         auto bin_of = [&](uint32_t key_m) {
             return uint32_t(fminf((key_value(key_m) - vmin) * inv, float(kHistBins - 1u)));
         };
+        // Each key's bin, kept four to a register (byte m % 4 of bins[m / 4]; 0xff for a padding key, which no bin
+        // index equals) for the bracket's pass below.
+        uint32_t bins[KPL / 4];
 #pragma unroll
-        for (int m = 0; m < KPL; ++m)
-            if ((valid >> m) & 1u)
-                atomicAdd(hist + bin_of(key[m]), 1u);
+        for (int m = 0; m < KPL; ++m) {
+            const bool ok = (valid >> m) & 1u;
+            const uint32_t b_m = ok ? bin_of(key[m]) : 0xffu;
+            if (ok)
+                atomicAdd(hist + b_m, 1u);
+            bins[m / 4] = (m % 4 == 0 ? 0u : bins[m / 4]) | (b_m << (8 * (m % 4)));
+        }
         __builtin_amdgcn_s_waitcnt(0xC07F); // the wave's own LDS atomics are visible to its reads after lgkmcnt(0)
         const uint4 h4 = lane < kHistBins / 4u ? reinterpret_cast<const uint4*>(hist)[lane] // bins 4 lane ... + 3
                                                : uint4{0u, 0u, 0u, 0u};
@@ -359,7 +366,7 @@ __device__ __forceinline__ void topk_keys(const RowKeys<KPL>& rk, const CubeGeo&
         uint32_t bmn = 0xffffffffu, bmx = 0u;
 #pragma unroll
         for (int m = 0; m < KPL; ++m) {
-            const bool in_b = ((valid >> m) & 1u) && bin_of(key[m]) == b; // recomputed: no registers held
+            const bool in_b = ((bins[m / 4] >> (8 * (m % 4))) & 0xffu) == b;
             bmn = in_b && key[m] < bmn ? key[m] : bmn;
             bmx = in_b && key[m] > bmx ? key[m] : bmx;
         }
