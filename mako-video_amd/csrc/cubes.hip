@@ -289,7 +289,8 @@ __device__ __forceinline__ void load_keys(const float* row, uint32_t C, RowKeys<
     typedef typename RowKeys<KPL>::Mask Mask;
     const uint32_t lane = threadIdx.x & 63u, j0 = lane * KPL;
     const float4* mine = reinterpret_cast<const float4*>(row + lane * (KPL + 4));
-    r.valid = 0;
+    const uint32_t nv = C > j0 ? min(C - j0, uint32_t(KPL)) : 0u; // the lane's cubes: keys 0 .. nv - 1
+    r.valid = nv >= uint32_t(KPL) ? ~Mask(0) : (Mask(1) << nv) - Mask(1);
 #pragma unroll
     for (int v = 0; v < KPL / 4; ++v) {
         const float4 f = mine[v];
@@ -297,9 +298,7 @@ __device__ __forceinline__ void load_keys(const float* row, uint32_t C, RowKeys<
 #pragma unroll
         for (int c = 0; c < 4; ++c) {
             const int m = 4 * v + c;
-            const bool ok = j0 + uint32_t(m) < C;
-            r.key[m] = ok ? score_key(fv[c]) : 0u;
-            r.valid |= ok ? Mask(1) << m : Mask(0);
+            r.key[m] = uint32_t(m) < nv ? score_key(fv[c]) : 0u;
         }
     }
 }
@@ -430,12 +429,18 @@ __device__ __forceinline__ void topk_keys(const RowKeys<KPL>& rk, const CubeGeo&
     for (int e = 0; e < 3; ++e)
         sel |= loc[e] / KPL == lane ? Mask(1) << (loc[e] % KPL) : Mask(0);
     const uint32_t n_sel = uint32_t(__popcll(uint64_t(sel)));
-    uint32_t pos = wave_excl_scan_u32(n_sel);
+    const uint32_t pos = wave_excl_scan_u32(n_sel);
     const uint32_t total = uint32_t(__builtin_amdgcn_readlane(int(pos + n_sel), 63));
-#pragma unroll
-    for (int m = 0; m < KPL; ++m)
-        if ((sel >> m) & 1u)
-            out[pos++] = int32_t(j0 + uint32_t(m));
+    // Store r writes each lane's r-th selected index: as many store instructions as the fullest lane has indices,
+    // not one per key slot.
+    const uint32_t most = wave_max_u32(n_sel);
+    uint64_t rest = uint64_t(sel);
+    for (uint32_t r = 0; r < most; ++r) {
+        if (rest) {
+            out[pos + r] = int32_t(j0 + uint32_t(__builtin_ctzll(rest)));
+            rest &= rest - 1u;
+        }
+    }
     for (uint32_t j = total + lane; j < out_stride; j += 64u)
         out[j] = -1;
     if (lane == 0)
