@@ -7,8 +7,8 @@
 // Design (gfx950): the op reads every element of q, k and v once and writes it once (4 bytes an element), so it is
 // HBM-bound. A head vector (128 bf16 = 256 bytes) belongs to one 16-lane DPP row, 16 bytes a lane, so the sum of
 // squares is a DPP row reduction with no LDS and no barrier.
-// - A workgroup of 512 threads is 32 such groups. It takes whole rows, enough that their head vectors fill about 128
-//   slots and at least two rows, and each group has up to 4 head vectors in flight (loads first, then the arithmetic
+// - A workgroup of 512 threads is 32 such groups. It takes whole rows, enough that their head vectors fill about 96
+//   slots and at least two rows, and each group has up to 3 head vectors in flight (loads first, then the arithmetic
 //   and the stores).
 //   Consecutive groups take consecutive head vectors of a row, so a wave's load covers 1 KB of contiguous qkv.
 // - The rotary pairs value i with i + rot / 2: lane p (values 8 p .. 8 p + 7) pairs with lane p +- rot / 16 of the
@@ -25,7 +25,7 @@ namespace {
 
 constexpr uint32_t kHeadsThreads = 512;
 constexpr uint32_t kGroups = kHeadsThreads / 16u; // one head vector a 16-lane group
-constexpr int kHeadsU = 4;                        // head vectors a group has in flight
+constexpr int kHeadsU = 3;                        // head vectors a group has in flight
 constexpr uint32_t kSlots = kGroups * kHeadsU;    // head vectors a workgroup pass
 // Dynamic LDS of at least this much, so three workgroups (24 waves, three rows of qkv at 40 heads) share a CU: that
 // streamed 1-3% faster than the 4 to 6 the registers allow, and two or one were slower (at 768p, alternating runs).
@@ -67,7 +67,8 @@ __device__ __forceinline__ RotLane rot_lane(uint32_t lane, uint32_t half)
 
 // One head vector of a 16-lane group, 16 bytes a lane: q or k (kind 0 or 1) normalized with its weights wk[128] and
 // rotated with the row's tables c[] and s[] (already offset by the lane's column), or v (kind 2) passed through. Every
-// lane of the wave must call it (the partner exchange is a wave-wide ds_bpermute).
+// lane of the wave must call it (the partner exchange is a wave-wide ds_bpermute). wk, c and s are 16-byte aligned
+// LDS; the tables are read by every lane (a lane that does not rotate reads column 0 and keeps its values).
 __device__ __forceinline__ uint4 head_vector(const uint4 raw, uint32_t kind, const float* wk, const float* c,
                                              const float* s, const RotLane& rl, uint32_t part, float eps)
 {
@@ -90,17 +91,26 @@ __device__ __forceinline__ uint4 head_vector(const uint4 raw, uint32_t kind, con
     ss = row16_sum(ss);
     if (kind >= 2u)
         return raw;
-    const float inv = 1.0f / sqrtf(fmaf(ss, 1.0f / 128.0f, eps));
+    // The hardware reciprocal square root (within 1 ulp; one instruction where 1 / sqrtf is some 25).
+    const float inv = __builtin_amdgcn_rsqf(fmaf(ss, 1.0f / 128.0f, eps));
+    float wm[8], wp[8], cv[8], sv[8];
+    auto ld8 = [](const float* src, float (&dst)[8]) {
+        const float4 lo = reinterpret_cast<const float4*>(src)[0], hi = reinterpret_cast<const float4*>(src)[1];
+        dst[0] = lo.x, dst[1] = lo.y, dst[2] = lo.z, dst[3] = lo.w, dst[4] = hi.x, dst[5] = hi.y, dst[6] = hi.z,
+        dst[7] = hi.w;
+    };
+    ld8(wk + 8u * part, wm);
+    ld8(wk + rl.pd, wp);
+    ld8(c, cv);
+    ld8(s, sv);
+    // (a, b) -> (a cos - b sin, b cos + a sin): the first half's partner term enters negated.
+    const float sg = rl.first_half ? -1.0f : 1.0f;
     float y[8];
 #pragma unroll
-    for (int e = 0; e < 8; ++e)
-        y[e] = x[e] * inv * wk[8u * part + e];
-    if (rl.rotating) {
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-            const float b = xp[e] * inv * wk[rl.pd + e];
-            y[e] = rl.first_half ? fmaf(y[e], c[e], -b * s[e]) : fmaf(y[e], c[e], b * s[e]);
-        }
+    for (int e = 0; e < 8; ++e) {
+        const float a = x[e] * inv * wm[e];
+        const float b = xp[e] * inv * wp[e];
+        y[e] = rl.rotating ? fmaf(a, cv[e], sg * b * sv[e]) : a;
     }
     return uint4{pack_bf16(y[0], y[1]), pack_bf16(y[2], y[3]), pack_bf16(y[4], y[5]), pack_bf16(y[6], y[7])};
 }
@@ -125,7 +135,7 @@ __global__ __launch_bounds__(kHeadsThreads) void heads_kernel(HeadsParams p)
     const uint32_t nr = min(p.rows_per_block, p.rows - r0);
     float* wt = lds;
     int32_t* srcs = reinterpret_cast<int32_t*>(lds + 256);
-    float* ct = lds + 256 + p.rows_per_block;
+    float* ct = lds + 256 + ((p.rows_per_block + 3u) & ~3u); // 16-byte aligned
     float* st = ct + p.rows_per_block * p.half;
     stage_weights(wt, p.qw, p.kw, tid, kHeadsThreads);
     // A map entry outside [0, model_rows) is a padding slot.
@@ -366,7 +376,7 @@ int launch_heads(HeadsParams p, uint32_t row_begin, uint32_t row_end, hipStream_
         return MH3_OK;
     p.row_begin = row_begin, p.rows = row_end;
     const uint64_t blocks = (uint64_t(row_end - row_begin) + p.rows_per_block - 1) / p.rows_per_block;
-    size_t lds = (256u + p.rows_per_block + 2u * size_t(p.rows_per_block) * p.half) * sizeof(float);
+    size_t lds = (256u + ((p.rows_per_block + 3u) & ~3u) + 2u * size_t(p.rows_per_block) * p.half) * sizeof(float);
     if (lds < kHeadsLdsFloor)
         lds = kHeadsLdsFloor;
     if (host::allow_dynamic_lds(reinterpret_cast<const void*>(&heads_kernel), lds) != hipSuccess)
