@@ -1,7 +1,7 @@
 """Benchmark of the H3 per-block hot path on one MI355X.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W]
-                    [--only fused,block_order,copy,swiglu,select,cond,heads,attn,proj,fc1,rms_f32,share]
+                    [--only fused,block_order,copy,swiglu,select,cond,heads,attn,proj,fc1,rms_f32,ref,share]
                     [--no-cpu] [--no-compare]
 
 A step is one pass of the headline kernel -- the fused adaLN-modulated RMS norm + gated residual -- over the
@@ -9,7 +9,9 @@ A step is one pass of the headline kernel -- the fused adaLN-modulated RMS norm 
 achieved algorithmic HBM bandwidth (6 bytes an element: read x and residual, write out). The same run also times the
 other ops of the path at their shapes (SwiGLU split and fused-row, the cube selector, the int8 fc1 + SwiGLU GEMM, the
 fp32 modulated RMS norm, heads_partial, the sparse attention, the other projections) and reports each as ms, GB/s or
-TFLOP/s and a fraction of the MI355X roofline; `share` repeats the main ones at one GPU's share of an 8-way split. Kernel times
+TFLOP/s and a fraction of the MI355X roofline; `share` repeats the main ones at one GPU's share of an 8-way split;
+`ref` times the reference's own published workloads at H3's dimensions beside its published Apple M5 Max times
+(`reference_shapes`). Kernel times
 come from HIP events recorded on the stream the kernels run on (torch's current stream): the mean over the timed
 launches, with the median beside it for the row and selector workloads. Launches run back to back with warm caches;
 `cold_ms` beside the fused op, SwiGLU, the select kernel, fc1 and the fp32 norm times each launch after a 512 MiB
@@ -427,6 +429,116 @@ def bench_heads(mh, dev, steps, warmup):
     return res
 
 
+# The reference's own published timings (docs/performance.md, Apple M5 Max, 40-core GPU): its dense GEMM bench at
+# 19,456 rows (:52-62), the per-forward kernel times of a 960x544, 124-frame forward of 50 blocks at 19,308 rows
+# (:36-46) and the sparse path at that shape (:165-177, 37 x 17 x 30 patch grid -> 400 cubes, 435 dense rows).
+REF_HW = "Apple M5 Max, 40-core GPU (docs/performance.md)"
+H3_D, H3_HEADS, H3_FFN, H3_BLOCKS = 5376, 56, 14336, 50
+
+
+def bench_reference_shapes(mh, dev, steps, warmup):
+    """The reference's own headline workloads at H3's real dimensions (D 5376, 56 heads, fc1 5376 -> 2 x 14,336), timed
+    here beside the reference's published M5 Max times for the same work. Per-forward figures are one block's kernels
+    times the forward's 50 blocks. GEMMs are the bf16 forms (the reference's table is bf16) plus the int8 fc1 it
+    quotes; our fc1 includes the SwiGLU epilogue the reference runs as a separate kernel."""
+    g = torch.Generator(device=dev).manual_seed(31)
+    rnd = lambda *shape: torch.randn(shape, generator=g, device=dev).to(torch.bfloat16)  # noqa: E731
+    out = {"reference_hardware": REF_HW}
+
+    def entry(ms, ref_ms, what):
+        return {"ms": ms, "reference_ms": ref_ms, "speedup": ref_ms / ms, "work": what}
+
+    # Dense GEMMs at 19,456 rows (docs/performance.md:55-58, the 64 x 128-tile column).
+    m = 19456
+    gemms = {}
+    x = rnd(m, H3_D)
+    w = (0.02 * torch.randn((2 * H3_FFN, H3_D), generator=g, device=dev)).to(torch.bfloat16)
+    ms, _ = time_launches(lambda: mh.gemm_bf16_swiglu(x, w), steps, warmup)
+    gemms["fc1_bf16"] = entry(ms, 99.0, "19,456 x 5376 -> 28,672 (+ SwiGLU here)")
+    wq, ws = mh.quant_rows_i8(w)
+
+    def fc1_i8():
+        xq, xs = mh.quant_rows_i8(x)
+        mh.gemm_i8_swiglu(xq, xs, wq, ws)
+    ms, _ = time_launches(fc1_i8, steps, warmup)
+    gemms["fc1_int8"] = entry(ms, 62.0, "the same, W8A8 with the activations quantized each call (+ SwiGLU here)")
+    del w, wq, ws
+    wqkv = (0.02 * torch.randn((3 * H3_HEADS * 128, H3_D), generator=g, device=dev)).to(torch.bfloat16)
+    ms, _ = time_launches(lambda: mh.gemm(x, wqkv), steps, warmup)
+    gemms["qkv_bf16"] = entry(ms, 74.0, "19,456 x 5376 -> 21,504")
+    del wqkv
+    for name, k_in, ref in (("out_bf16", H3_HEADS * 128, 25.0), ("fc2_bf16", H3_FFN, 54.0)):
+        xi = rnd(m, k_in)
+        wi = (0.02 * torch.randn((H3_D, k_in), generator=g, device=dev)).to(torch.bfloat16)
+        ms, _ = time_launches(lambda: mh.gemm(xi, wi), steps, warmup)
+        gemms[name] = entry(ms, ref, f"19,456 x {k_in} -> 5376")
+        del xi, wi
+    del x
+    out["gemm_19456_rows"] = gemms
+
+    # The row kernels of one block at 19,308 rows (docs/performance.md:44: heads_partial, swiglu_rows,
+    # gate_add_rows and rms_mod_rows, 1.3-1.5 s a forward): rms_mod_rows and gate_add_rows twice (attention and MLP
+    # halves), swiglu_rows once over fc1's [gate | up] rows, heads_partial once (56 heads).
+    rows = 19308
+    xr, yr = rnd(rows, H3_D), rnd(rows, H3_D)
+    wv, shv, scv, gav = mod_params(dev, H3_D, 32)
+    hbuf = torch.empty_like(xr)
+    fc1o = rnd(rows, 2 * H3_FFN)
+    sw = torch.empty((rows, H3_FFN), dtype=torch.bfloat16, device=dev)
+    qkv = rnd(rows, 3 * H3_HEADS * 128)
+    ang = torch.rand((rows, 48), generator=g, device=dev) * 6.2831853 - 3.1415927
+    ct, st = torch.cos(ang), torch.sin(ang)
+    heads_out = [torch.empty((H3_HEADS, rows, 128), dtype=torch.bfloat16, device=dev) for _ in range(3)]
+
+    def block_rows():
+        for _ in range(2):
+            mh.rms_mod_rows(xr, wv, shv, scv, out=hbuf)
+            mh.gate_add_rows(xr, yr, gav)
+        mh.swiglu_rows(fc1o, out=sw)
+        mh.heads_partial(qkv, H3_HEADS, None, None, ct, st, q=heads_out[0], k=heads_out[1], v=heads_out[2])
+    ms, _ = time_launches(block_rows, steps, warmup)
+    out["row_kernels_per_forward"] = entry(ms * H3_BLOCKS, 1400.0,
+                                           "a block's rms_mod_rows x2, gate_add_rows x2, swiglu_rows, heads_partial at "
+                                           "19,308 rows, x 50 blocks (reference 1.3-1.5 s; its midpoint)")
+    del xr, yr, hbuf, fc1o, sw, qkv, heads_out
+
+    # The sparse path at 960x544 (docs/performance.md:165-177): 37 x 17 x 30 patch grid (400 cubes), 435 dense rows,
+    # 56 heads, ratio 0.1 (k = 40), local 1; selection 0.3 s and attention 4.7 s a forward.
+    grid = (37, 17, 30)
+    video, n_dense = grid[0] * grid[1] * grid[2], 435
+    arows = video + n_dense
+    cubes = mh.cube_count(*grid)
+    kk = mh.topk_k(0.1, cubes)
+    q, k, v = rnd(H3_HEADS, arows, 128), rnd(H3_HEADS, arows, 128), rnd(H3_HEADS, arows, 128)
+    a = mh.cube_args(H3_HEADS, grid, head_stride=arows * 128, k=kk, local=1)
+    qc = torch.empty((H3_HEADS, cubes, 128), dtype=torch.float32, device=dev)
+    kc = torch.empty_like(qc)
+    idx = torch.empty((H3_HEADS, cubes, kk + 1), dtype=torch.int32, device=dev)
+    cnt = torch.empty((H3_HEADS, cubes), dtype=torch.int32, device=dev)
+
+    def select():
+        mh.cube_pool(a, q, k, qc=qc, kc=kc)
+        mh.cube_select(a, qc, kc, idx=idx, cnt=cnt)
+    ms, _ = time_launches(select, steps, warmup)
+    out["sparse_selection_per_forward"] = entry(ms * H3_BLOCKS, 300.0,
+                                                "cube_pool + cube_select, 56 heads, 400 cubes, k = 40, x 50 blocks")
+    ao = torch.empty_like(q)
+    ms, _ = time_launches(lambda: mh.flash_attn_sparse_128(a, q, k, v, idx, cnt, dense_row0=video, n_dense=n_dense,
+                                                           out=ao), steps, warmup)
+    out["sparse_attention_per_forward"] = entry(ms * H3_BLOCKS, 4700.0,
+                                                "flash_attn_sparse_128 over those pass lists, 19,305 rows, x 50 blocks")
+    del q, k, v, ao
+
+    # The AdaLN projections (docs/performance.md:45: gemm BF16 2688 x 96768, 50 a forward, 70-85 ms).
+    cond = rnd(1, 2688)
+    wa = (0.02 * torch.randn((6 * 3 * H3_D, 2688), generator=g, device=dev)).to(torch.bfloat16)
+    mod = torch.empty((1, 6 * 3 * H3_D), dtype=torch.float32, device=dev)
+    ms, _ = time_launches(lambda: mh.adaln_mod(cond, wa, out=mod), steps, warmup)
+    out["adaln_projections_per_forward"] = entry(ms * H3_BLOCKS, 77.5,
+                                                 "cond [1][2688] -> [96,768] table, x 50 blocks (reference 70-85 ms)")
+    return out
+
+
 def bench_proj(mh, dev, steps, warmup):
     """The block's other projections at the 768p rows (129,536): qkv 5120 -> 3 x 40 x 128 = 15,360 (plain store), the
     out projection 5120 -> 5120 and fc2 13,824 -> 5120 with gate_add_rows folded into the epilogue (residual += gate *
@@ -712,7 +824,7 @@ def main() -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--only", default="fused,block_order,copy,swiglu,select,cond,heads,attn,proj,fc1,rms_f32,share")
+    ap.add_argument("--only", default="fused,block_order,copy,swiglu,select,cond,heads,attn,proj,fc1,rms_f32,ref,share")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-compare", action="store_true")
     args = ap.parse_args()
@@ -767,6 +879,10 @@ def main() -> int:
     if "fc1" in ops:
         report["fc1_w8a16_swiglu"] = bench_fc1(mh, dev, max(3, args.steps // 2), max(1, args.warmup // 2),
                                                not args.no_compare)
+        torch.cuda.empty_cache()
+
+    if "ref" in ops:
+        report["reference_shapes"] = bench_reference_shapes(mh, dev, max(3, args.steps // 2), max(1, args.warmup // 2))
         torch.cuda.empty_cache()
 
     if "share" in ops:
