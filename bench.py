@@ -426,6 +426,18 @@ def bench_heads(mh, dev, steps, warmup):
     res["gathered_pool"] = {"ms": fms, "bytes": fbytes, "GBs": fbytes / fms / 1e6,
                             "frac": fbytes / fms / 1e6 / HBM_PEAK_GBS, "two_kernel_ms": gms + pool_ms,
                             "pool_ms": pool_ms, "pool_cost_in_pass_ms": fms - gms}
+    # The same in the model's order (MH3_CUBES_GRID, no map): the sparse path then needs no gather either way.
+    del gout
+    outs = [torch.empty((HEADS, rows, 128), dtype=torch.bfloat16, device=dev) for _ in range(3)]
+    ga = mh.cube_args(HEADS, GRID, layout=mh.CUBES_GRID, row0=n_dense, head_stride=rows * 128)
+    gpool_ms, _ = time_launches(lambda: mh.cube_pool(ga, outs[0], outs[1], qc=qc, kc=kc), steps, warmup)
+    gfms, _ = time_launches(lambda: mh.heads_partial_pool(x, HEADS, GRID, qw, kw, ct, st, row0=n_dense,
+                                                          cube_layout=mh.CUBES_GRID, q=outs[0], k=outs[1], v=outs[2],
+                                                          qc=qc, kc=kc), steps, warmup)
+    pbytes = nbytes + 2 * HEADS * cubes * 128 * 4
+    res["grid_pool"] = {"ms": gfms, "bytes": pbytes, "GBs": pbytes / gfms / 1e6,
+                        "frac": pbytes / gfms / 1e6 / HBM_PEAK_GBS, "two_kernel_ms": ms + gpool_ms,
+                        "pool_ms": gpool_ms, "pool_cost_in_pass_ms": gfms - ms}
     return res
 
 
@@ -867,9 +879,12 @@ def main() -> int:
         torch.cuda.empty_cache()
     sel, hp = report.get("cube_selector"), report.get("heads_partial")
     if sel and hp:
-        # The selector with its pool folded into heads_partial: what the pool still costs there, plus cube_select.
-        extra = hp["gathered_pool"]["pool_cost_in_pass_ms"]
-        sel["pool_in_heads_partial"] = {"pool_ms": extra, "ms": extra + sel["select_ms"]}
+        # The selector with its pool folded into heads_partial: what the pool still costs in that pass (gathered
+        # through the cube map, or in the model's order), plus cube_select.
+        sel["pool_in_heads_partial"] = {
+            lay: {"pool_ms": hp[key]["pool_cost_in_pass_ms"],
+                  "ms": max(hp[key]["pool_cost_in_pass_ms"], 0.0) + sel["select_ms"]}
+            for lay, key in (("gathered", "gathered_pool"), ("grid", "grid_pool"))}
     if "attn" in ops:
         report["flash_attn_sparse_128"] = bench_attn(mh, dev, max(3, args.steps // 2), max(1, args.warmup // 2))
         torch.cuda.empty_cache()

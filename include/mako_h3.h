@@ -220,10 +220,13 @@ int mh3_heads_partial(const MH3HeadsArgs* args, const uint16_t* qkv, const float
  * q, k, v) followed by mh3_cube_pool(cubes, q, k, qc, kc, counts), bit for bit, without reading q and k back. The
  * reference runs the two kernels one after the other (docs/architecture.md:123-128: the head tiles are gathered
  * through the cube map, then the selector pools them); this entry point has no reference counterpart of its own.
- * cubes must describe the head tiles this call writes: layout MH3_CUBES_GATHERED, the same heads and head_dim,
- * head_stride = out_head_stride and row_stride = out_row_stride (MH3_ERR_PARAM otherwise), and its cube rows
- * row0 .. row0 + 64 cubes - 1 within args->rows (MH3_ERR_SHAPE). Rows outside them (the dense rows) get
- * heads_partial alone. qc and kc are float [heads][cubes][128], 16-byte aligned. */
+ * cubes must describe the head tiles this call writes: the same heads and head_dim, head_stride = out_head_stride
+ * and row_stride = out_row_stride (MH3_ERR_PARAM otherwise), in either layout:
+ *   MH3_CUBES_GATHERED: the cube rows row0 .. row0 + 64 cubes - 1, gathered through map (or not), within args->rows;
+ *   MH3_CUBES_GRID: no map (MH3_ERR_PARAM), output rows in the model's order, the grid's tokens at rows
+ *                   row0 .. row0 + T H W - 1 within args->rows.
+ * (MH3_ERR_SHAPE when the rows do not fit.) Rows outside them (the dense rows) get heads_partial alone. qc and kc are
+ * float [heads][cubes][128], 16-byte aligned. */
 int mh3_heads_partial_pool(const MH3HeadsArgs* args, const MH3CubeArgs* cubes, const uint16_t* qkv, const float* q_w,
                            const float* k_w, const float* cos_t, const float* sin_t, const int32_t* map, uint16_t* q,
                            uint16_t* k, uint16_t* v, float* qc, float* kc, int32_t* counts, mh3_stream_t stream);

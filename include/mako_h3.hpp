@@ -273,8 +273,8 @@ public:
         const MH3HeadsArgs a = hd.args();
         check(mh3_heads_partial(&a, qkv, q_w, k_w, cos_t, sin_t, map, q, k, v, s_), "heads_partial");
     }
-    // heads_partial, then cube_pool over its output, in one pass: c is the gathered geometry of the head tiles this
-    // call writes (its strides those of hd's outputs).
+    // heads_partial, then cube_pool over its output, in one pass: c is the geometry of the head tiles this call writes
+    // (its strides those of hd's outputs), gathered through map, or in the model's order (MH3_CUBES_GRID, no map).
     void heads_partial_pool(const Heads& hd, const Cubes& c, const uint16_t* qkv, const float* q_w, const float* k_w,
                             const float* cos_t, const float* sin_t, const int32_t* map, uint16_t* q, uint16_t* k,
                             uint16_t* v, float* qc, float* kc, int32_t* counts = nullptr) const

@@ -202,8 +202,9 @@ struct HeadsPoolParams {
     float* qc;
     float* kc;
     int32_t* counts;
-    uint64_t row0; // output row of cube 0's slot 0
+    uint64_t row0; // gathered: output row of cube 0's slot 0; grid: the model row of grid position (0, 0, 0)
     uint32_t gt, gh, gw, cw, plane, cubes;
+    uint32_t grid; // nonzero: no map, each token's row read and written at its model row (the grid layout)
 };
 constexpr uint32_t kPoolThreads = 512;
 constexpr int kPoolU = 8;                           // slots a group has in flight
@@ -222,7 +223,16 @@ heads_pool_kernel(HeadsPoolParams pp)
     float* ct = lds + 256 + 64;
     float* st = ct + 64u * p.half;
     stage_weights(wt, p.qw, p.kw, tid, kPoolThreads);
+    const uint32_t cube_t = c / pp.plane, rem = c - cube_t * pp.plane, cube_y = rem / pp.cw, cube_x = rem - cube_y * pp.cw;
+    // Slot l's model row (-1: none). Gathered: through the map (or l's own output row); grid: the token at the slot's
+    // grid position, if it lies in the grid.
     auto src_of = [&](uint32_t l) -> int32_t {
+        if (pp.grid) {
+            const uint32_t tt = cube_t * 4u + (l >> 4), yy = cube_y * 4u + ((l >> 2) & 3u), xx = cube_x * 4u + (l & 3u);
+            return tt < pp.gt && yy < pp.gh && xx < pp.gw
+                       ? int32_t(pp.row0 + (uint64_t(tt) * pp.gh + yy) * pp.gw + xx)
+                       : -1;
+        }
         const int32_t m = p.map ? p.map[orow0 + l] : int32_t(orow0 + l);
         return m >= 0 && uint32_t(m) < p.model_rows ? m : -1;
     };
@@ -234,7 +244,6 @@ heads_pool_kernel(HeadsPoolParams pp)
         ct[i] = src >= 0 ? p.cos_t[uint64_t(src) * p.half + col] : 0.0f;
         st[i] = src >= 0 ? p.sin_t[uint64_t(src) * p.half + col] : 0.0f;
     }
-    const uint32_t cube_t = c / pp.plane, rem = c - cube_t * pp.plane, cube_y = rem / pp.cw, cube_x = rem - cube_y * pp.cw;
     const uint32_t nt = min(4u, pp.gt - cube_t * 4u), ny = min(4u, pp.gh - cube_y * 4u), nx = min(4u, pp.gw - cube_x * 4u);
     if (pp.counts && tid == 0)
         pp.counts[c] = int32_t(nt * ny * nx);
@@ -276,8 +285,10 @@ heads_pool_kernel(HeadsPoolParams pp)
                     uint4 o = head_vector(raw[u], kind, wk, ct + l * p.half + rl.ci, st + l * p.half + rl.ci, rl,
                                           part, p.eps);
                     o = src_r[u] >= 0 ? o : uint4{0u, 0u, 0u, 0u};
-                    if (live)
-                        st_stream(reinterpret_cast<uint4*>(out + (orow0 + l) * p.ors + 8u * part), o);
+                    // Gathered: every slot's row is written (a padding slot's zeros); grid: a token's own row only.
+                    const uint64_t orow = pp.grid ? uint64_t(src_r[u] >= 0 ? src_r[u] : 0) : orow0 + l;
+                    if (live && (!pp.grid || src_r[u] >= 0))
+                        st_stream(reinterpret_cast<uint4*>(out + orow * p.ors + 8u * part), o);
                     const bool ok = x_ok && cube_t * 4u + (s >> 2) < pp.gt && cube_y * 4u + (s & 3u) < pp.gh;
                     const uint32_t w[4] = {o.x, o.y, o.z, o.w};
 #pragma unroll
@@ -406,13 +417,16 @@ extern "C" int mh3_heads_partial_pool(const MH3HeadsArgs* args, const MH3CubeArg
     if (!args || !cubes)
         return MH3_ERR_POINTER;
     const MH3CubeArgs& cb = *cubes;
-    if (cb.layout != MH3_CUBES_GATHERED || cb.heads != args->heads || cb.head_dim != args->head_dim ||
-        cb.head_stride != args->out_head_stride || cb.row_stride != args->out_row_stride)
-        return MH3_ERR_PARAM; // the pool must read the gathered head tiles this call writes
+    const bool grid = cb.layout == MH3_CUBES_GRID;
+    if ((cb.layout != MH3_CUBES_GATHERED && !grid) || cb.heads != args->heads || cb.head_dim != args->head_dim ||
+        cb.head_stride != args->out_head_stride || cb.row_stride != args->out_row_stride || (grid && map))
+        return MH3_ERR_PARAM; // the pool must read the head tiles this call writes
     if (cb.grid_t == 0 || cb.grid_h == 0 || cb.grid_w == 0)
         return MH3_ERR_SHAPE;
     const uint64_t ncubes = uint64_t((cb.grid_t + 3u) / 4u) * ((cb.grid_h + 3u) / 4u) * ((cb.grid_w + 3u) / 4u);
-    if (ncubes * cb.heads >= (uint64_t(1) << 31) || cb.row0 + ncubes * 64u > args->rows)
+    // The rows the cubes cover: 64 a cube in the gathered layout, the grid's tokens in the model's order.
+    const uint64_t span = grid ? uint64_t(cb.grid_t) * cb.grid_h * cb.grid_w : ncubes * 64u;
+    if (ncubes * cb.heads >= (uint64_t(1) << 31) || cb.row0 + span > args->rows)
         return MH3_ERR_SHAPE;
     HeadsParams p;
     const int rc = heads_setup(args, qkv, q_w, k_w, cos_t, sin_t, map, q, k, v, p);
@@ -423,7 +437,7 @@ extern "C" int mh3_heads_partial_pool(const MH3HeadsArgs* args, const MH3CubeArg
     if (!host::aligned16(qc) || !host::aligned16(kc))
         return MH3_ERR_ALIGN;
     hipStream_t st = static_cast<hipStream_t>(stream);
-    const uint32_t video0 = uint32_t(cb.row0), video1 = uint32_t(cb.row0 + ncubes * 64u);
+    const uint32_t video0 = uint32_t(cb.row0), video1 = uint32_t(cb.row0 + span);
     int r = launch_heads(p, 0u, video0, st); // rows before the cubes, and after them (the dense rows)
     if (r == MH3_OK)
         r = launch_heads(p, video1, args->rows, st);
@@ -432,7 +446,7 @@ extern "C" int mh3_heads_partial_pool(const MH3HeadsArgs* args, const MH3CubeArg
     HeadsPoolParams pp{};
     pp.hp = p, pp.qc = qc, pp.kc = kc, pp.counts = counts, pp.row0 = cb.row0;
     pp.gt = cb.grid_t, pp.gh = cb.grid_h, pp.gw = cb.grid_w, pp.cw = (cb.grid_w + 3u) / 4u;
-    pp.plane = ((cb.grid_h + 3u) / 4u) * pp.cw, pp.cubes = uint32_t(ncubes);
+    pp.plane = ((cb.grid_h + 3u) / 4u) * pp.cw, pp.cubes = uint32_t(ncubes), pp.grid = grid ? 1u : 0u;
     const size_t lds = (256u + 64u + 2u * 64u * size_t(p.half)) * sizeof(float); // 26 KB at rot 96
     if (host::allow_dynamic_lds(reinterpret_cast<const void*>(&heads_pool_kernel), lds) != hipSuccess)
         return MH3_ERR_HIP;

@@ -542,12 +542,14 @@ def heads_partial(qkv, heads, q_w=None, k_w=None, cos_t=None, sin_t=None, *, rot
 
 
 def heads_partial_pool(qkv, heads, grid, q_w=None, k_w=None, cos_t=None, sin_t=None, *, rot=96, eps=1e-6, map=None,
-                       with_v=True, layout="heads", row0=0, q=None, k=None, v=None, qc=None, kc=None, counts=None):
-    """heads_partial followed by cube_pool over its output in the gathered layout, in one pass: cube c of the video
-    grid (T, H, W) = `grid` is output rows row0 + 64 c ... + 63. Returns (q, k, v, qc, kc), the same bits as
-    heads_partial(...) then cube_pool(cube_args(heads, grid, layout=CUBES_GATHERED, row0=row0, ...), q, k)."""
+                       with_v=True, layout="heads", row0=0, cube_layout=CUBES_GATHERED, q=None, k=None, v=None,
+                       qc=None, kc=None, counts=None):
+    """heads_partial followed by cube_pool over its output, in one pass. Gathered (the default): cube c of the video
+    grid (T, H, W) = `grid` is output rows row0 + 64 c ... + 63. CUBES_GRID (no map): the outputs stay in the model's
+    order, the grid's tokens at rows row0 + (t H + y) W + x. Returns (q, k, v, qc, kc), the same bits as
+    heads_partial(...) then cube_pool(cube_args(heads, grid, layout=cube_layout, row0=row0, ...), q, k)."""
     a, outs, ptrs = _heads_setup(qkv, heads, q_w, k_w, cos_t, sin_t, rot, eps, map, with_v, layout, q, k, v)
-    ca = cube_args(heads, grid, layout=CUBES_GATHERED, row0=row0, head_stride=a.out_head_stride,
+    ca = cube_args(heads, grid, layout=cube_layout, row0=row0, head_stride=a.out_head_stride,
                    row_stride=a.out_row_stride)
     cubes = cube_count(*grid)
     shape = (heads, cubes, 128)

@@ -315,11 +315,13 @@ def test_heads_partial_pool_validation():
             setattr(a, key, val)
         p = dict(qkv=base, cos=base, q=base + 2**34, k=base + 2**35, kc=base + 2**36)
         p.update(ptrs)
-        return mh.lib.mh3_heads_partial_pool(C.byref(a), C.byref(ca), p["qkv"], None, None, p["cos"], p["cos"], None,
-                                             p["q"], p["k"], None, qc, p["kc"], None, None)
+        return mh.lib.mh3_heads_partial_pool(C.byref(a), C.byref(ca), p["qkv"], None, None, p["cos"], p["cos"],
+                                             p.get("map"), p["q"], p["k"], None, qc, p["kc"], None, None)
 
     assert mh.lib.mh3_heads_partial_pool(None, None, *([None] * 13)) == mh.ERR_POINTER
-    assert call({"layout": mh.CUBES_GRID}) == mh.ERR_PARAM             # the pool reads what this call writes
+    assert call({"layout": 2}) == mh.ERR_PARAM
+    assert call({"layout": mh.CUBES_GRID}, map=base + 2**37) == mh.ERR_PARAM  # the grid layout keeps the model's order
+    assert call({"layout": mh.CUBES_GRID, "row0": rows - 768 + 1}) == mh.ERR_SHAPE  # the grid's tokens past the rows
     assert call({"heads": 3}) == mh.ERR_PARAM
     assert call({"row_stride": 256}) == mh.ERR_PARAM
     assert call({"head_stride": rows * 128 + 8}) == mh.ERR_PARAM

@@ -102,3 +102,50 @@ def test_heads_partial_pool_768p(dev):
     for name, a, b in zip(("q", "k", "v", "qc", "kc"), got, want):
         assert same(a, b), f"{name} differs at 768p"
     assert bool(torch.isfinite(got[3]).all()) and bool(torch.isfinite(got[4]).all())
+
+
+GRID_CASES = [
+    # grid, heads, rot, rows before the video rows, rows after them, layout
+    ((8, 8, 12), 2, 96, 70, 0, "heads"),
+    ((7, 9, 10), 3, 96, 0, 33, "heads"),
+    ((5, 3, 6), 5, 128, 12, 7, "rows"),
+    ((3, 5, 9), 40, 96, 19, 0, "heads"),
+]
+
+
+@pytest.mark.parametrize("grid,heads,rot,n_before,n_after,layout", GRID_CASES)
+def test_heads_partial_pool_grid_layout(dev, grid, heads, rot, n_before, n_after, layout):
+    """The grid layout: no map, the outputs in the model's order; the same bits as heads_partial then cube_pool with
+    MH3_CUBES_GRID at the video rows' first row."""
+    C = orc.cube_count(*grid)
+    video = grid[0] * grid[1] * grid[2]
+    rows = n_before + video + n_after
+    x, qw, kw, ct, st = inputs(dev, rows, heads, rot, seed=7 * sum(grid) + heads)
+    q, k, v = mh.heads_partial(x, heads, qw, kw, ct, st, rot=rot, layout=layout)
+    hs, rs = (rows * 128, 128) if layout == "heads" else (128, heads * 128)
+    counts_a = torch.full((C,), -7, dtype=torch.int32, device=dev)
+    counts_b = torch.full((C,), -9, dtype=torch.int32, device=dev)
+    qc, kc = mh.cube_pool(mh.cube_args(heads, grid, layout=mh.CUBES_GRID, row0=n_before, head_stride=hs,
+                                       row_stride=rs), q, k, counts=counts_a)
+    got = mh.heads_partial_pool(x, heads, grid, qw, kw, ct, st, rot=rot, layout=layout, row0=n_before,
+                                cube_layout=mh.CUBES_GRID, counts=counts_b)
+    torch.cuda.synchronize()
+    for name, g_, w_ in zip(("q", "k", "v", "qc", "kc"), got, (q, k, v, qc, kc)):
+        assert same(g_, w_), f"{name} differs for grid {grid} heads {heads} layout {layout}"
+    assert torch.equal(counts_a, counts_b)
+
+
+def test_heads_partial_pool_grid_layout_768p(dev):
+    """768p in the model's order: 512 text rows, then the 32 x 48 x 84 grid; 40 heads."""
+    grid, heads, rot, n_dense = (32, 48, 84), 40, 96, 512
+    rows = n_dense + grid[0] * grid[1] * grid[2]
+    g = torch.Generator(device=dev).manual_seed(2)
+    x = torch.randn((rows, 3 * heads * 128), generator=g, device=dev).to(torch.bfloat16)
+    ang = torch.rand((rows, rot // 2), generator=g, device=dev) * 6.283 - 3.1416
+    ct, st = torch.cos(ang), torch.sin(ang)
+    q, k, v = mh.heads_partial(x, heads, None, None, ct, st, rot=rot)
+    qc, kc = mh.cube_pool(mh.cube_args(heads, grid, layout=mh.CUBES_GRID, row0=n_dense, head_stride=rows * 128), q, k)
+    got = mh.heads_partial_pool(x, heads, grid, None, None, ct, st, rot=rot, row0=n_dense, cube_layout=mh.CUBES_GRID)
+    torch.cuda.synchronize()
+    for name, a, b in zip(("q", "k", "v", "qc", "kc"), got, (q, k, v, qc, kc)):
+        assert same(a, b), f"{name} differs at 768p (grid layout)"
