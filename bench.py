@@ -850,12 +850,19 @@ def main() -> int:
     dev = torch.device("cuda:0")
     ops = set(args.only.split(","))
     report = {}
+
+    def done(name: str) -> None:
+        # one progress line a leg, on stderr, so the JSON line stays alone on stdout
+        print(f"bench: {name} done", file=sys.stderr, flush=True)
+
     if "fused" in ops:
         report["fused_rms_mod_gate_add"] = bench_fused(mh, dev, args.steps, args.warmup)
         torch.cuda.empty_cache()
+        done("fused")
     if "block_order" in ops:
         report["gate_add_rms_mod"] = bench_block_order(mh, dev, args.steps, args.warmup)
         torch.cuda.empty_cache()
+        done("block_order")
     if "copy" in ops:
         report["hbm_copy"] = bench_copy(dev, args.steps, args.warmup)
         report["stream_ceiling"] = bench_stream(dev, args.steps, args.warmup)
@@ -863,20 +870,26 @@ def main() -> int:
         if head:
             report["stream_ceiling"]["fused_vs_r2w1"] = head["GBs"] / report["stream_ceiling"]["r2w1"]["GBs"]
         torch.cuda.empty_cache()
+        done("copy")
     if "rms_f32" in ops:
         report["rms_mod_f32_4096x1024"] = bench_rms_f32(mh, dev, args.steps, args.warmup)
+        done("rms_f32")
     if "swiglu" in ops:
         report["swiglu"] = bench_swiglu(mh, dev, args.steps, args.warmup)
         torch.cuda.empty_cache()
+        done("swiglu")
     if "select" in ops:
         report["cube_selector"] = bench_select(mh, dev, args.steps, args.warmup)
         torch.cuda.empty_cache()
+        done("select")
     if "cond" in ops:
         report["modulation"] = bench_cond(mh, dev, args.steps, args.warmup)
         torch.cuda.empty_cache()
+        done("cond")
     if "heads" in ops:
         report["heads_partial"] = bench_heads(mh, dev, args.steps, args.warmup)
         torch.cuda.empty_cache()
+        done("heads")
     sel, hp = report.get("cube_selector"), report.get("heads_partial")
     if sel and hp:
         # The selector with its pool folded into heads_partial: what the pool still costs in that pass (gathered
@@ -888,17 +901,21 @@ def main() -> int:
     if "attn" in ops:
         report["flash_attn_sparse_128"] = bench_attn(mh, dev, max(3, args.steps // 2), max(1, args.warmup // 2))
         torch.cuda.empty_cache()
+        done("attn")
     if "proj" in ops:
         report["projections"] = bench_proj(mh, dev, max(3, args.steps // 2), max(1, args.warmup // 2))
         torch.cuda.empty_cache()
+        done("proj")
     if "fc1" in ops:
         report["fc1_w8a16_swiglu"] = bench_fc1(mh, dev, max(3, args.steps // 2), max(1, args.warmup // 2),
                                                not args.no_compare)
         torch.cuda.empty_cache()
+        done("fc1")
 
     if "ref" in ops:
         report["reference_shapes"] = bench_reference_shapes(mh, dev, max(3, args.steps // 2), max(1, args.warmup // 2))
         torch.cuda.empty_cache()
+        done("ref")
 
     if "share" in ops:
         share = bench_share(mh, dev, args.steps, args.warmup)
@@ -912,6 +929,7 @@ def main() -> int:
             share[name]["vs_full"] = mine / ref if ref else None
         report["per_gpu_share"] = share
         torch.cuda.empty_cache()
+        done("share")
 
     head = report.get("fused_rms_mod_gate_add")
     traffic = None

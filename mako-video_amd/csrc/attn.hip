@@ -20,12 +20,14 @@
 //   16-key chunk c is key 32 (c / 2) + 16 (c % 2) + 8 (p % 8 / 4) + 4 (p / 8) + p % 4.
 // - K and V tiles (64 rows each, 32 KB) go from global memory straight into LDS (buffer_load ... lds), one tile
 //   ahead of the MFMAs when two stages fit. Each lane fetches whichever source chunk its LDS slot holds, so the
-//   layouts are free: K in 2 KB blocks of 8 rows interleaved at 16 bytes (8 lanes reading 8 consecutive rows of a
-//   fragment touch 128 contiguous bytes), V in 1 KB blocks of 4 keys interleaved at 16 bytes, read with
-//   ds_read_b64_tr_b16. That instruction hands lane i of a 16-lane group element i & 3 of the 8-byte rows named by
-//   lanes (i >> 2) + 4 j, j = 0..3: with lane L naming key (L >> 2)'s columns d0 + 4 (L & 3) .. + 3, lane i receives
-//   column d0 + i of four keys, a V^T fragment, with no transpose in registers. Every fragment address is a lane
-//   constant plus an immediate. Padding slots are fetched from past the buffer's end, which reads zeros.
+//   layouts are free, with one constraint from the address unit: the four lanes of a quad must fetch one aligned
+//   64-byte piece (a quad spread over four rows is four accesses, and held the K/V stream to about 16 bytes a clock a
+//   CU). K is 256-byte rows whose 16-byte chunks are XOR-swizzled by the row (operand reads of 16 rows hit distinct
+//   banks); V is 1 KB blocks of 4 keys whose 64-byte pieces are interleaved, read with ds_read_b64_tr_b16. That
+//   instruction hands lane i of a 16-lane group element i & 3 of the 8-byte rows named by lanes (i >> 2) + 4 j,
+//   j = 0..3: with lane L naming key (L >> 2)'s columns d0 + 4 (L & 3) .. + 3, lane i receives column d0 + i of four
+//   keys, a V^T fragment, with no transpose in registers. Padding slots are fetched from past the buffer's end, which
+//   reads zeros.
 // - Each cube tile walks its pass list from a rotated start (position rank mod S of S, S the cube workgroups an XCD
 //   holds at once, rank the tile's place in its XCD's sequence), wrapping round. The XCD's resident tiles then sweep
 //   the key cubes together, so a K/V tile one of them fetches is still in L2 when the others that selected it reach
@@ -216,18 +218,21 @@ __global__ __launch_bounds__(kAttnThreads, STAGES == 2 ? 1 : 2) void attn_sparse
         return j >= 0 && uint32_t(j) < p.cubes ? p.nd + uint32_t(j) : kNoTile;
     };
 
-    // DMA source offsets of this wave's 8 K and 8 V instructions (instruction i = 8 wave + u of the workgroup's 16),
-    // for cubes in the grid layout (G) and for consecutive rows (L: gathered cubes, dense runs).
-    //   K: instruction i fills half i % 2 of the 2 KB block of rows 8 (i / 2) .. + 7; lane L's LDS position
-    //      P = 64 (i % 2) + L holds chunk P / 8 of row 8 (i / 2) + P % 8.
-    //   V: instruction i fills the 1 KB block of keys 4 i .. + 3; lane L's position holds chunk L / 4 of key
-    //      4 i + L % 4.
-    // Each offset is a lane constant (voffset) plus a term of i alone (soffset): a slot's grid offset
-    // (dt gh + dy) gw + dx splits that way because i fixes dt and, for K, dy's high bit.
-    const uint32_t rs2 = uint32_t(p.row_stride) * 2u, gw_rs2 = p.gw * rs2, plane_rs2 = p.gh * gw_rs2;
-    const uint32_t kL_lane = (lane & 7u) * rs2 + 16u * (lane >> 3);
-    const uint32_t kG_lane = (((lane >> 2) & 1u) * p.gw + (lane & 3u)) * rs2 + 16u * (lane >> 3);
-    const uint32_t v_lane_off = (lane & 3u) * rs2 + 16u * (lane >> 2);
+    // DMA source offsets of this wave's 8 K and 8 V instructions. Instruction i = 8 wave + u of the workgroup's 16
+    // fills the LDS kilobyte 1024 i with slots 4 i .. 4 i + 3 (K rows, and V's keys); the hardware puts lane L's
+    // 16 bytes at position 16 L of it, and each lane fetches whichever source chunk that position holds:
+    //   K: position L holds chunk (L % 16) ^ (r % 16) of tile row r = 4 i + L / 16 (256-byte rows whose 16-byte
+    //      chunks are XOR-swizzled by the row, so that the MFMA operand reads of 16 rows hit distinct banks);
+    //   V: position L holds chunk 4 (L / 16) + L % 4 of key 4 i + (L / 4) % 4 (the four keys' 64-byte pieces
+    //      interleaved, so that a transposed read of four keys' 8-byte rows hits distinct banks).
+    // Either way every four consecutive lanes fetch one aligned 64-byte piece of one row, which the address unit
+    // takes as one access. (Lanes of a quad on four different rows, the layout this replaced, cost four accesses and
+    // capped the K/V stream at about 16 bytes a clock a CU.) Slots 4 i .. 4 i + 3 are four consecutive rows in both
+    // layouts (in the grid dt = i / 4, dy = i % 4, dx = 0 .. 3), so each offset is a lane constant (voffset) plus a
+    // term of i alone (soffset).
+    const uint32_t rs2 = uint32_t(p.row_stride) * 2u, gw_rs2 = p.gw * rs2;
+    const uint32_t k_row = lane >> 4, k_pos = lane & 15u, v_key = (lane >> 2) & 3u;
+    const uint32_t v_lane_off = v_key * rs2 + 16u * (4u * (lane >> 4) + (lane & 3u));
     // Starts tile t's loads into stage st; returns its key mask (bit l: slot l is a token).
     auto dma_tile = [&](uint32_t t, uint32_t st) -> uint64_t {
         const Tile tl = make_tile(p, t);
@@ -241,22 +246,19 @@ __global__ __launch_bounds__(kAttnThreads, STAGES == 2 ? 1 : 2) void attn_sparse
         char* ks = lds + st * kStageBytes;
         char* vs = ks + 16384;
         const bool full = tile_full(tl), grid = tl.kind == 1;
-        const uint32_t k_lane = grid ? kG_lane : kL_lane;
 #pragma unroll
         for (int u = 0; u < 8; ++u) {
             const uint32_t i = 8u * wave + uint32_t(u);
-            const uint32_t k_i = grid ? (i >> 2) * plane_rs2 + 2u * ((i >> 1) & 1u) * gw_rs2 + 128u * (i & 1u)
-                                      : 8u * (i >> 1) * rs2 + 128u * (i & 1u);
-            const uint32_t v_i = grid ? ((i >> 2) * p.gh + (i & 3u)) * gw_rs2 : 4u * i * rs2;
-            uint32_t ko = k_lane, vo = v_lane_off;
+            const uint32_t s_i = grid ? ((i >> 2) * p.gh + (i & 3u)) * gw_rs2 : 4u * i * rs2; // slot 4 i's row
+            // K chunk (L % 16) ^ (r % 16), r % 16 = 4 (i % 4) + L / 16
+            uint32_t ko = k_row * rs2 + 16u * (k_pos ^ (4u * (i & 3u) + k_row)), vo = v_lane_off;
             if (!full) {
-                ko = slot_token(tl, 8u * (i >> 1) + (lane & 7u)) ? ko : kPastEnd;
-                vo = slot_token(tl, 4u * i + (lane & 3u)) ? vo : kPastEnd;
+                ko = slot_token(tl, 4u * i + k_row) ? ko : kPastEnd;
+                vo = slot_token(tl, 4u * i + v_key) ? vo : kPastEnd;
             }
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(rk, (lds_ptr_t)(ks + 1024u * i), 16, ko,
-                                                     int(__builtin_amdgcn_readfirstlane(k_i)), 0, 0);
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(rv, (lds_ptr_t)(vs + 1024u * i), 16, vo,
-                                                     int(__builtin_amdgcn_readfirstlane(v_i)), 0, 0);
+            const int so = int(__builtin_amdgcn_readfirstlane(s_i));
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rk, (lds_ptr_t)(ks + 1024u * i), 16, ko, so, 0, 0);
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rv, (lds_ptr_t)(vs + 1024u * i), 16, vo, so, 0, 0);
         }
         return full ? ~0ull : __ballot(slot_token(tl, lane));
     };
@@ -280,11 +282,13 @@ __global__ __launch_bounds__(kAttnThreads, STAGES == 2 ? 1 : 2) void attn_sparse
         for (int e = 0; e < 16; ++e)
             o[b][e] = 0.0f;
     float m_run = -__builtin_inff(), l_run = 0.0f;
-    // Fragment addresses: lane constants; the rest is immediates.
-    const uint32_t k_lane = 2048u * (n >> 3) + 128u * hh + 16u * (n & 7u);
+    // Fragment addresses: lane constants, and immediates or (K's swizzle) an XOR with 32 dc.
+    //   K: row 32 b + n, chunk 2 dc + hh at 8192 b + 256 n + 16 ((2 dc + hh) ^ (n % 16)) = 8192 b + (k_lane ^ 32 dc).
+    //   V: key k, column d of a 4-key block at 256 (d / 32) + 64 k + 2 (d % 32); lane L of 16-lane group grp names
+    //      key L / 4's columns d0 + 4 (L % 4) .. + 3, d0 = 32 db + 16 (grp % 2), of the block 2 (8 b + 4 g) + grp / 2.
+    const uint32_t k_lane = 256u * n + 16u * (hh ^ (n & 15u));
     const uint32_t L = lane & 15u, grp = lane >> 4;
-    const uint32_t v_lane = 1024u * (grp >> 1) + 128u * (grp & 1u) + 64u * ((L & 3u) >> 1) + 16u * (L >> 2) +
-                            8u * (L & 1u);
+    const uint32_t v_lane = 1024u * (grp >> 1) + 32u * (grp & 1u) + 64u * (L >> 2) + 8u * (L & 3u);
 
     uint64_t mask = n_tiles ? dma_tile(key_tile(0), 0) : 0ull;
     for (uint32_t e = 0; e < n_tiles; ++e) {
@@ -294,7 +298,7 @@ __global__ __launch_bounds__(kAttnThreads, STAGES == 2 ? 1 : 2) void attn_sparse
         uint64_t mask_next = 0;
         if (STAGES == 2 && e + 1 < n_tiles)
             mask_next = dma_tile(key_tile(e + 1), st ^ 1u);
-        const char* ks = lds + st * kStageBytes + k_lane;
+        const char* ks = lds + st * kStageBytes;
         const char* vs = lds + st * kStageBytes + 16384u + v_lane;
 
         // S^T: lane (n, hh), element i of block b is key 32 b + 8 (i / 4) + 4 hh + i % 4 of query n.
@@ -306,7 +310,7 @@ __global__ __launch_bounds__(kAttnThreads, STAGES == 2 ? 1 : 2) void attn_sparse
                 s[b][i] = 0.0f;
 #pragma unroll
             for (int dc = 0; dc < 8; ++dc) {
-                const bf16x8_t a = *reinterpret_cast<const bf16x8_t*>(ks + 8192u * b + 256u * dc);
+                const bf16x8_t a = *reinterpret_cast<const bf16x8_t*>(ks + 8192u * b + (k_lane ^ (32u * dc)));
                 s[b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, qf[dc], s[b], 0, 0, 0);
             }
         }
