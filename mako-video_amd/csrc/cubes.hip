@@ -3,9 +3,10 @@
 // docs/architecture.md:118-133, README.md:81-87 and docs/performance.md:162-181.
 //
 // Design (gfx950):
-// - cube_pool: one wavefront per (head, cube) pools q and k together. Lane 4 p + x takes dimensions 8 p ... 8 p + 7 of
-//   the cube's x position x, so each load instruction reads four adjacent rows (1 KiB contiguous per head in the grid
-//   layout); all 32 loads of a lane are in flight at once. Lane sums in float, then two DPP quad permutations.
+// - cube_pool: one wavefront per (head, cube) pools q and k together. Lane 16 x + p takes dimensions 8 p ... 8 p + 7
+//   of the cube's x position x, so each load instruction reads four adjacent rows (1 KiB contiguous per head in the
+//   grid layout) and each quad of lanes one aligned 64-byte piece of a row; all 32 loads of a lane are in flight at
+//   once. Lane sums in float, then two lane exchanges across the 16-lane rows.
 // - scores: v_mfma_f32_16x16x4_f32 on 16 x 16 blocks; the 128-long contraction is split over the MFMA's 4 k-lanes so
 //   that each operand load of the wave reads 64 contiguous bytes of each of the block's 16 rows.
 // - top-k: one wavefront per (head, query cube) holds the row's scores as order-preserving 32-bit keys in VGPRs, lane l
@@ -44,7 +45,10 @@ __global__ __launch_bounds__(256) void cube_pool_kernel(CubeGeo g, const uint16_
         return;
     const uint32_t h = item / g.cubes, c = item - h * g.cubes;
     const uint32_t ct = c / g.plane, rem = c - ct * g.plane, cy = rem / g.cw, cx = rem - cy * g.cw;
-    const uint32_t dx = lane & 3u, part = lane >> 2; // x slot of the cube (a quad's 4 lanes); 8 of the 128 dimensions
+    // x slot of the cube (one 16-lane row of the wave each) and 8 of the 128 dimensions: each load of a 16-lane row
+    // reads one token's 256 bytes, so every quad of lanes fetches one aligned 64-byte piece (a quad spread over four
+    // rows would be four accesses for the address unit).
+    const uint32_t dx = lane >> 4, part = lane & 15u;
     const uint32_t x = cx * 4u + dx;
     const uint16_t* qh = q + h * g.head_stride + part * 8u;
     const uint16_t* kh = k + h * g.head_stride + part * 8u;
@@ -81,13 +85,13 @@ __global__ __launch_bounds__(256) void cube_pool_kernel(CubeGeo g, const uint16_
             ak[2 * e + 1] += bf16_hi(kw[e]);
         }
     }
-    // The cube's 4 x positions are a quad's 4 lanes: two DPP quad permutations sum them.
+    // The cube's 4 x positions are the wave's four 16-lane rows: (x0 + x1) + (x2 + x3) by two lane exchanges.
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
-        aq[e] += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, aq[e]), 0xB1, 0xF, 0xF, true));
-        aq[e] += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, aq[e]), 0x4E, 0xF, 0xF, true));
-        ak[e] += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, ak[e]), 0xB1, 0xF, 0xF, true));
-        ak[e] += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, ak[e]), 0x4E, 0xF, 0xF, true));
+        aq[e] += __shfl_xor(aq[e], 16, kWave);
+        aq[e] += __shfl_xor(aq[e], 32, kWave);
+        ak[e] += __shfl_xor(ak[e], 16, kWave);
+        ak[e] += __shfl_xor(ak[e], 32, kWave);
     }
     const uint32_t nt = min(4u, g.gt - ct * 4u), ny = min(4u, g.gh - cy * 4u), nx = min(4u, g.gw - cx * 4u);
     const float n = float(nt * ny * nx);

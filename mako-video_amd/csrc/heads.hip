@@ -298,7 +298,7 @@ heads_pool_kernel(HeadsPoolParams pp)
                     }
                 }
             }
-            // (dx 0 + dx 1) + (dx 2 + dx 3), as cube_pool_kernel's two quad exchanges combine them.
+            // (dx 0 + dx 1) + (dx 2 + dx 3), as cube_pool_kernel's two lane exchanges combine them.
 #pragma unroll
             for (int e = 0; e < 8; ++e) {
                 if (dx == 0u)
