@@ -108,18 +108,28 @@ __global__ __launch_bounds__(256) void cube_pool_kernel(CubeGeo g, const uint16_
 }
 
 // The 32 contraction operands of lane l for a 16-row block starting at r0: row r0 + l % 16 (clamped to the last row);
-// operand 4 v + u is dimension 16 v + 4 (l / 16) + u. Each 16-byte load of the wave thus reads 64 contiguous bytes of
-// each of the 16 rows (16 cache lines, not 64), and the 32 MFMA steps still cover all 128 dimensions once.
+// operand 4 v + u is dimension 16 v + 4 (l / 16) + u, so the 32 MFMA steps cover all 128 dimensions once. The loads
+// take another lane order: lane l reads row r0 + l / 4, dimensions 16 v + 4 (l % 4) .. + 3, so each quad of lanes
+// fetches one aligned 64-byte piece of a row (a quad spread over four rows costs the address unit four accesses and
+// held these loads to about 16 bytes a clock a CU); a lane exchange (ds_bpermute, lane l from lane 4 (l % 16) + l / 16)
+// then gives each lane its MFMA operands.
 __device__ __forceinline__ void load_operand(const float* __restrict__ base, uint32_t r0, uint32_t rows, float (&v)[32])
 {
     const uint32_t lane = threadIdx.x & 63u;
-    uint32_t r = r0 + (lane & 15u);
+    uint32_t r = r0 + (lane >> 2);
     r = r < rows ? r : rows - 1u;
-    const float* p = base + uint64_t(r) * 128u + (lane >> 4) * 4u;
+    const float* p = base + uint64_t(r) * 128u + (lane & 3u) * 4u;
+    const int src = int(4u * (4u * (lane & 15u) + (lane >> 4)));
+    float4 t[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+        t[i] = *reinterpret_cast<const float4*>(p + 16 * i);
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
-        const float4 t = *reinterpret_cast<const float4*>(p + 16 * i);
-        v[4 * i] = t.x, v[4 * i + 1] = t.y, v[4 * i + 2] = t.z, v[4 * i + 3] = t.w;
+        const float c[4] = {t[i].x, t[i].y, t[i].z, t[i].w};
+#pragma unroll
+        for (int u = 0; u < 4; ++u)
+            v[4 * i + u] = __int_as_float(__builtin_amdgcn_ds_bpermute(src, __float_as_int(c[u])));
     }
 }
 
