@@ -195,44 +195,6 @@ __device__ __forceinline__ void score_rows(const CubeGeo& g, const float* __rest
     }
 }
 
-// score_rows' products two key blocks at a time, blocks b and b + waves, their two MFMA chains interleaved so that
-// each wave always has an independent MFMA to issue (3-4% faster in cube_select than one chain with the next block
-// prefetched). Same scores, bit for bit: each score is the same 32-MFMA chain.
-template <bool PAD>
-__device__ __forceinline__ void score_rows_pair(const CubeGeo& g, const float* __restrict__ qh,
-                                                const float* __restrict__ kh, uint32_t i0, float* dst, uint64_t ld,
-                                                uint32_t wave, uint32_t waves)
-{
-    const uint32_t lane = threadIdx.x & 63u;
-    float qa[32];
-    load_operand(qh, i0, g.cubes, qa);
-    const uint32_t kblocks = (g.cubes + 15u) / 16u;
-    auto emit = [&](uint32_t kb_i, const floatx4& acc) {
-        const uint32_t j = kb_i * 16u + (lane & 15u);
-#pragma unroll
-        for (int v = 0; v < 4; ++v) {
-            const uint32_t r = (lane >> 4) * 4u + uint32_t(v);
-            if (j < g.cubes && i0 + r < g.cubes)
-                dst[r * ld + (PAD ? pad_word<32>(j) : j)] = acc[v] * kScoreScale;
-        }
-    };
-    for (uint32_t b0 = wave; b0 < kblocks; b0 += 2u * waves) {
-        const uint32_t b1 = b0 + waves; // past the last block: b0's operands again, not emitted
-        float k0[32], k1[32];
-        load_operand(kh, b0 * 16u, g.cubes, k0);
-        load_operand(kh, (b1 < kblocks ? b1 : b0) * 16u, g.cubes, k1);
-        floatx4 a0 = {0.0f, 0.0f, 0.0f, 0.0f}, a1 = {0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-        for (int s = 0; s < 32; ++s) {
-            a0 = __builtin_amdgcn_mfma_f32_16x16x4f32(qa[s], k0[s], a0, 0, 0, 0);
-            a1 = __builtin_amdgcn_mfma_f32_16x16x4f32(qa[s], k1[s], a1, 0, 0, 0);
-        }
-        emit(b0, a0);
-        if (b1 < kblocks)
-            emit(b1, a1);
-    }
-}
-
 // Key blocks in flight a wave in cube_scores. Deeper rings measured slower at 768p (3: +0.5%, 4: +2%, 6: +13%): the
 // fp32 MFMAs, not the operand loads, set the pace once two are in flight.
 constexpr int kScoreDepth = 2;
@@ -498,8 +460,10 @@ __global__ __launch_bounds__(256) void cube_topk_kernel(CubeGeo g, const float* 
 // Iteration j: each wave ranks its own row of tile t_(j-1) from registers (VALU work), then scores its share of the
 // key blocks of tile t_j into the LDS tile (fp32 MFMAs); barrier; each wave copies its row of t_j into registers as
 // keys; barrier (the tile is free again). Waves finish ranking at different times, so on each SIMD some waves
-// already run MFMAs while others still rank. Staggering the order on purpose (half the waves scoring first) needs a
-// row of keys live across the scoring, which spills at 1024 threads' 128 registers and measured slower.
+// already run MFMAs while others still rank. A wave scores one key block at a time (one 32-MFMA chain, the next
+// block's operands loaded after it): two interleaved chains measured 3% slower once the operand loads were
+// coalesced. Staggering the order on purpose (half the waves scoring first) keeps a row of keys live across the
+// scoring and measured the same (16 registers spilled at 1024 threads' 128).
 constexpr int kSelectThreads = 1024;
 constexpr uint32_t kSelectRows = 16;
 constexpr uint32_t kSelectMaxCubes = 2048;
@@ -521,7 +485,7 @@ __global__ __launch_bounds__(kSelectThreads) void cube_select_kernel(CubeGeo g, 
     const uint32_t row_tiles = (g.cubes + kSelectRows - 1u) / kSelectRows, tiles = row_tiles * g.heads;
     auto score = [&](uint32_t t) {
         const uint32_t h = t / row_tiles, i0 = (t - h * row_tiles) * kSelectRows;
-        score_rows_pair<true>(g, qc + h * plane, kc + h * plane, i0, tile, kPaddedRow<32>, wave, waves);
+        score_rows<true, 1>(g, qc + h * plane, kc + h * plane, i0, tile, kPaddedRow<32>, wave, waves);
     };
     RowKeys<32> rk;
     auto rank = [&](uint32_t t) {
