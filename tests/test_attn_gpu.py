@@ -63,6 +63,30 @@ def test_flash_attn_sparse_matches_oracle(dev, grid, layout, row0, dense_row0, n
         assert len(pad) and (got[:, pad] == 0).all()
 
 
+@pytest.mark.parametrize("grid,layout,row0,dense_row0,n_dense", [((7, 9, 10), orc.CUBES_GRID, 0, 630, 70),
+                                                                   ((7, 9, 10), orc.CUBES_GATHERED, 70, 0, 70)])
+def test_flash_attn_sparse_interleaved_rows(dev, grid, layout, row0, dense_row0, n_dense):
+    """q, k, v (and out) as the model's rows, [rows][heads x 128] (head stride 128, row stride heads x 128): the K/V
+    loads' row offsets then differ from the head tiles' 256 bytes."""
+    heads = 3
+    rng = np.random.default_rng(31 + layout)
+    C = orc.cube_count(*grid)
+    video = C * 64 if layout == orc.CUBES_GATHERED else grid[0] * grid[1] * grid[2]
+    rows = max(row0 + video, dense_row0 + n_dense)
+    q, k, v = [randn_bf16_bits(rng, (heads, rows, 128)) for _ in range(3)]
+    idx, cnt = orc.cube_topk(rng.standard_normal((heads, C, C)), grid, 5, 1, out_stride=8)
+    want = orc.attn_sparse(q, k, v, idx, cnt, grid, dense_row0, n_dense, layout, row0)
+    a = mh.cube_args(heads, grid, layout=layout, row0=row0, head_stride=128, row_stride=heads * 128, out_stride=8)
+    rowwise = lambda x: from_bits(np.ascontiguousarray(x.transpose(1, 0, 2)), dev)  # noqa: E731
+    t = lambda x: torch.from_numpy(np.ascontiguousarray(x)).to(dev)  # noqa: E731
+    got = mh.flash_attn_sparse_128(a, rowwise(q), rowwise(k), rowwise(v), t(idx), t(cnt), dense_row0=dense_row0,
+                                   n_dense=n_dense)
+    got = to_bits(got).reshape(rows, heads, 128).transpose(1, 0, 2)
+    rows_written = np.concatenate([orc.attn_tile_rows(grid, layout, row0, dense_row0, n_dense, t_)
+                                   for t_ in range((n_dense + 63) // 64 + C)])
+    check(got[:, rows_written], want[:, rows_written], f"interleaved rows {grid} layout {layout}")
+
+
 def test_flash_attn_sparse_every_cube_is_dense_attention(dev):
     """Every cube selected: each query attends every token, as torch's attention (float32 on the GPU) does."""
     rng = np.random.default_rng(21)
