@@ -690,11 +690,20 @@ def bench_share(mh, dev, steps, warmup, gpus=8):
 
 
 def cpu_model() -> str:
-    """The host CPU's model name from /proc/cpuinfo (the machine type where the file has none)."""
+    """The host CPU from /proc/cpuinfo: its model name, with the family / model / stepping numbers (a virtualized host
+    may report a bare family name) and the logical CPUs the file lists; the machine type where the file has none."""
     try:
+        fields, cpus = {}, 0
         for line in Path("/proc/cpuinfo").read_text().splitlines():
-            if line.startswith("model name"):
-                return line.split(":", 1)[1].strip()
+            key, _, val = line.partition(":")
+            key = key.strip()
+            if key == "processor":
+                cpus += 1
+            elif key in ("model name", "cpu family", "model", "stepping") and key not in fields:
+                fields[key] = val.strip()
+        if "model name" in fields:
+            ids = ", ".join(f"{k} {fields[k]}" for k in ("cpu family", "model", "stepping") if k in fields)
+            return f"{fields['model name']} ({ids}; {cpus} logical CPUs)" if ids else fields["model name"]
     except OSError:
         pass
     return platform.processor() or platform.machine()
