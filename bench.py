@@ -138,11 +138,12 @@ def bench_copy(dev, steps, warmup):
 
 
 def bench_stream(dev, steps, warmup):
-    """The streaming ceiling: a plain HIP kernel reading, copying, and reading two streams into a third (the fused
-    row op's and SwiGLU's mix), 16-byte non-temporal accesses over 768p-sized bf16 buffers (1.33 GB each), swept
-    over the access form (global or buffer instructions), unroll (2, 4, 8 vectors a thread) and grid (flat; 4, 8, 16
-    workgroups a CU, grid-stride, for the global form); the best of each mix is reported. Also the MFMA peaks from the device's CU count and peak clock (flops a clock a CU: bf16 4096,
-    int8 8192)."""
+    """The streaming ceiling: a plain HIP kernel reading, copying, reading two streams into a third (the fused row
+    op's and SwiGLU's mix) and reading two streams into two (the block's own order: x += gate y and h = norm of x),
+    16-byte non-temporal accesses over 768p-sized bf16 buffers (1.33 GB each), swept over the access form (global or
+    buffer instructions), unroll (2, 4, 8 vectors a thread) and grid (flat; 4, 8, 16 workgroups a CU, grid-stride,
+    for the global form); the best of each mix is reported. Also the MFMA peaks from the device's CU count and peak
+    clock (flops a clock a CU: bf16 4096, int8 8192)."""
     import ctypes as C
 
     lib = C.CDLL(str(REPO / "mako-video_amd" / "lib" / "libmh3_stream_probe.so"))
@@ -155,16 +156,16 @@ def bench_stream(dev, steps, warmup):
     nbytes = ROWS * DIM * 2
     a = torch.empty(nbytes, dtype=torch.uint8, device=dev).fill_(1)
     b = torch.empty_like(a).fill_(2)
-    c = torch.empty_like(a)
+    c = torch.empty(2 * nbytes, dtype=torch.uint8, device=dev)  # two write streams for r2w2
     stream = torch.cuda.current_stream().cuda_stream
     res = {"bytes_per_stream": nbytes}
-    # Each mix in both access forms: global loads and stores (kinds 0-2, flat or grid-stride) and buffer loads and
-    # stores (kinds 3-5, flat), the best of all reported as the mix's ceiling.
-    for kinds, name, moved in (((0, 3), "read", 1), ((1, 4), "copy", 2), ((2, 5), "r2w1", 3)):
+    # Each mix in both access forms: global loads and stores (kinds 0-3, flat or grid-stride) and buffer loads and
+    # stores (kinds 4-7, flat), the best of all reported as the mix's ceiling.
+    for kinds, name, moved in (((0, 4), "read", 1), ((1, 5), "copy", 2), ((2, 6), "r2w1", 3), ((3, 7), "r2w2", 4)):
         best = None
         for kind in kinds:
             for unroll in (2, 4, 8):
-                for per_cu in ((0, 4, 8, 16) if kind < 3 else (0,)):
+                for per_cu in ((0, 4, 8, 16) if kind < 4 else (0,)):
                     blocks = per_cu * cus.value
 
                     def run():
@@ -178,7 +179,7 @@ def bench_stream(dev, steps, warmup):
         ms, unroll, per_cu, kind = best
         res[name] = {"ms": ms, "GBs": moved * nbytes / ms / 1e6, "frac": moved * nbytes / ms / 1e6 / HBM_PEAK_GBS,
                      "unroll": unroll, "grid": "flat" if per_cu == 0 else f"{per_cu} workgroups a CU",
-                     "access": "buffer" if kind >= 3 else "global"}
+                     "access": "buffer" if kind >= 4 else "global"}
     clk = khz.value * 1e3
     res["device"] = {"cus": cus.value, "peak_clock_mhz": khz.value / 1e3,
                      "bf16_mfma_peak_tflops": cus.value * clk * 4096 / 1e12,
@@ -878,6 +879,9 @@ def main() -> int:
         head = report.get("fused_rms_mod_gate_add")
         if head:
             report["stream_ceiling"]["fused_vs_r2w1"] = head["GBs"] / report["stream_ceiling"]["r2w1"]["GBs"]
+        order = report.get("gate_add_rms_mod")
+        if order:
+            report["stream_ceiling"]["block_order_vs_r2w2"] = order["GBs"] / report["stream_ceiling"]["r2w2"]["GBs"]
         torch.cuda.empty_cache()
         done("copy")
     if "rms_f32" in ops:

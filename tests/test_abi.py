@@ -33,11 +33,14 @@ def test_stream_probe_library_loads_and_refuses_bad_calls():
     assert hasattr(probe, "mh3_probe_device")
     buf = C.create_string_buffer(64)
     a = (C.addressof(buf) + 15) // 16 * 16
-    assert probe.mh3_probe_stream(6, a, a, a, 1, 4, 0, None) == -1
-    assert probe.mh3_probe_stream(5, a, None, a, 1, 4, 0, None) == -1     # two read streams need b
-    assert probe.mh3_probe_stream(4, a, None, a, 1, 4, 8, None) == -1     # the buffer form has a flat grid only
-    assert probe.mh3_probe_stream(3, a, None, a, 1 << 28, 4, 0, None) == -1  # beyond 32-bit byte offsets
+    assert probe.mh3_probe_stream(8, a, a, a, 1, 4, 0, None) == -1
+    assert probe.mh3_probe_stream(-1, a, a, a, 1, 4, 0, None) == -1
+    assert probe.mh3_probe_stream(6, a, None, a, 1, 4, 0, None) == -1     # two read streams need b
+    assert probe.mh3_probe_stream(7, a, None, a, 1, 4, 0, None) == -1
+    assert probe.mh3_probe_stream(5, a, None, a, 1, 4, 8, None) == -1     # the buffer form has a flat grid only
+    assert probe.mh3_probe_stream(4, a, None, a, 1 << 28, 4, 0, None) == -1  # beyond 32-bit byte offsets
     assert probe.mh3_probe_stream(2, a, None, a, 1, 4, 0, None) == -1
+    assert probe.mh3_probe_stream(3, a, None, a, 1, 4, 0, None) == -1
     assert probe.mh3_probe_stream(1, a, None, a, 1, 3, 0, None) == -1
     assert probe.mh3_probe_stream(1, a + 4, None, a, 1, 4, 0, None) == -2
     assert probe.mh3_probe_stream(1, a, None, a, 0, 4, 0, None) == 0
