@@ -494,6 +494,7 @@ using namespace mh3;
 
 constexpr size_t kCoefLdsMax = 64 * 1024;
 constexpr size_t kWaveLdsFloor = 54 * 1024; // above a third of gfx950's 160 KiB: two wave-kernel workgroups a CU
+constexpr size_t kOrderLdsFloor = 81 * 1024; // above half of it: one workgroup a CU (the block's own order)
 constexpr size_t kSwigluFusedLds = 40 * 1024; // four SwiGLU workgroups a CU (fused-row layout)
 constexpr int kSwigluVecs = 1; // 16-byte vectors of gate (and of up) a thread has in flight
 
@@ -539,8 +540,12 @@ int launch_rows_wave(const RowsParams& p, hipStream_t stream)
     // 16 waves, or two of 5 to 9, two of 7 or 8 were fastest, 0.5-1.6% ahead of one of 11 (alternating runs on one
     // GPU), since while one workgroup drains its last rows the other keeps the CU's loads going. A grid of persistent
     // workgroups, whose waves stride through far-apart rows, was 9-15% slower.
+    // The block's own order (two read and two write streams) streams faster still with 8 rows in flight a CU: one
+    // workgroup a CU measured 1.3% faster than two at 129,536 x 5120 (0.922-0.926 against 0.934-0.940 ms, alternated
+    // on one GPU), while the fused op (one write stream) was 3% slower that way.
     const size_t table = src == kCoefLds ? size_t(p.n_sets) * p.dim * kPlanes<OP> * sizeof(float) : 0;
-    const size_t lds = table > kWaveLdsFloor ? table : kWaveLdsFloor;
+    const size_t floor = OP == kGateAddMod ? kOrderLdsFloor : kWaveLdsFloor;
+    const size_t lds = table > floor ? table : floor;
     if (host::allow_dynamic_lds(k, lds) != hipSuccess)
         return MH3_ERR_HIP;
     // A row a wave; a persistent grid (rows_per_wave 0) measured slower.
