@@ -163,7 +163,10 @@ __global__ __launch_bounds__(kAttnThreads, STAGES == 2 ? 1 : 2) void attn_sparse
 {
     extern __shared__ __attribute__((aligned(16))) char lds[]; // STAGES x (K stage, V stage)
 
-    const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6, n = lane & 31u, hh = lane >> 5;
+    const uint32_t tid = threadIdx.x, lane = tid & 63u, n = lane & 31u, hh = lane >> 5;
+    // The wave index is uniform: held in a scalar register, the DMA's per-instruction row offsets (soffset) are
+    // scalar arithmetic and take no vector registers (which otherwise spill).
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
 
     // This workgroup's head and query tile: the dense query tiles of every head first, then the cube tiles. Blocks
     // go to the 8 XCDs round-robin (block b to XCD b % 8); when the counts allow, XCD x takes the x-th eighth of each
