@@ -335,7 +335,8 @@ int mh3_gemm_gate_add(const MH3GemmArgs* args, uint32_t form, const void* x, con
  * t is float [levels] in device memory; temb is float [levels][out_dim]; cond is bf16 [levels][out_dim] (may be
  * NULL); b_in and b_out may be NULL (zero). The embedding is computed in double, the MLP in float. `workspace` holds
  * the hidden layer: at least mh3_time_embed_workspace_bytes(args) bytes of device memory, 16-byte aligned, which the
- * call overwrites (a negative code from the query for invalid args). */
+ * call overwrites (a negative code from the query for invalid args). temb, cond and the workspace may not overlap
+ * each other or an input (MH3_ERR_PARAM). */
 typedef struct MH3TimeArgs {
     uint32_t levels;   /* 1 .. 64 */
     uint32_t freq_dim; /* a multiple of 8, <= 1024 (H3: 256) */
@@ -363,14 +364,15 @@ int mh3_time_embed_noalloc(const MH3TimeArgs* args, const float* t, const float*
  * weight's output rows), bias float [n] (may be NULL), mod float [m][n]. With n = 3 * 6 * D the rows of a level are
  * its [3 tags][6 vectors][D], so mod is the [U][3][6][D] table whose set (u, tag) the row kernels take at
  * set_stride = 6 D. k % 8 == 0 and k <= 4096, else MH3_ERR_SHAPE / MH3_ERR_UNSUPPORTED; m <= 64; cond and w 16-byte
- * aligned. args->n_sets and gate_stride are not used. */
+ * aligned; mod may not overlap cond, w or bias (MH3_ERR_PARAM). args->n_sets and gate_stride are not used. */
 int mh3_adaln_mod(const MH3GemmArgs* args, const uint16_t* cond, const uint16_t* w, const float* bias, float* mod,
                   mh3_stream_t stream);
 /* The pruned checkpoints' path (docs/architecture.md:53-58, tools/check_pruned_curve.py:69-73): no time MLP; a curve
  * c(t) is tabulated at `points` values of t over [0, 1] (table float [points][width], H3: [1025][8]) and read with
  * linear interpolation at pos = t (points - 1), clamped to [0, points - 1]: i0 = min(floor(pos), points - 2),
  * f = pos - i0, c = (1 - f) table[i0] + f table[i0 + 1]; then mod[u][r] = w[r] . c(t[u]) + bias[r] in float, with w
- * float [n][width] and no silu. t is float [levels] in device memory; bias may be NULL. */
+ * float [n][width] and no silu. t is float [levels] in device memory; bias may be NULL; mod may not overlap an input
+ * (MH3_ERR_PARAM). */
 typedef struct MH3CurveArgs {
     uint32_t levels; /* 1 .. 64 */
     uint32_t n;      /* outputs a level */

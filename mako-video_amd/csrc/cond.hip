@@ -336,6 +336,32 @@ int time_embed_check(const MH3TimeArgs* args, const float* t, const float* w_in,
     return MH3_OK;
 }
 
+// The time MLP's outputs (temb, cond, and the hidden layer's buffer) may not overlap each other or any input: a
+// kernel would read what another workgroup of the same pass is writing. MH3_ERR_PARAM if they do.
+int time_embed_aliasing(const MH3TimeArgs* a, const float* t, const float* w_in, const float* b_in, const float* w_out,
+                        const float* b_out, const void* hid, uint64_t hid_bytes, const float* temb, const uint16_t* cond)
+{
+    const uint64_t lv = a->levels;
+    const struct {
+        const void* p;
+        uint64_t n;
+    } in[] = {{t, lv * 4u},
+              {w_in, uint64_t(a->hidden) * a->freq_dim * 4u},
+              {b_in, b_in ? uint64_t(a->hidden) * 4u : 0u},
+              {w_out, uint64_t(a->out_dim) * a->hidden * 4u},
+              {b_out, b_out ? uint64_t(a->out_dim) * 4u : 0u}},
+      out[] = {{temb, lv * a->out_dim * 4u}, {cond, cond ? lv * a->out_dim * 2u : 0u}, {hid, hid_bytes}};
+    for (size_t i = 0; i < 3; ++i) {
+        for (const auto& x : in)
+            if (host::overlaps(out[i].p, out[i].n, x.p, x.n))
+                return MH3_ERR_PARAM;
+        for (size_t j = i + 1; j < 3; ++j)
+            if (host::overlaps(out[i].p, out[i].n, out[j].p, out[j].n))
+                return MH3_ERR_PARAM;
+    }
+    return MH3_OK;
+}
+
 // ---- the variant that allocates nothing ------------------------------------------------------------------------------
 // mh3_time_embed_noalloc keeps the hidden layer in this file-scope array instead of a caller's workspace: each GPU the
 // library runs on holds its own copy (256 KiB) until the process ends. Its address on the current device comes from
@@ -390,6 +416,9 @@ int mh3_time_embed(const MH3TimeArgs* args, const float* t, const float* w_in, c
         return MH3_ERR_ALIGN;
     if (workspace_bytes < time_workspace(args))
         return MH3_ERR_SHAPE;
+    rc = time_embed_aliasing(args, t, w_in, b_in, w_out, b_out, workspace, time_workspace(args), temb, cond);
+    if (rc != MH3_OK)
+        return rc;
     return time_embed_launch(args, t, w_in, b_in, w_out, b_out, static_cast<float*>(workspace), temb, cond,
                              static_cast<hipStream_t>(stream));
 }
@@ -402,6 +431,9 @@ int mh3_time_embed_noalloc(const MH3TimeArgs* args, const float* t, const float*
         return rc;
     if (uint64_t(args->levels) * args->hidden > kScratchFloats)
         return MH3_ERR_UNSUPPORTED;
+    rc = time_embed_aliasing(args, t, w_in, b_in, w_out, b_out, nullptr, 0, temb, cond);
+    if (rc != MH3_OK)
+        return rc;
     float* hid = scratch_on_current_device();
     if (!hid)
         return MH3_ERR_HIP;
@@ -422,6 +454,12 @@ int mh3_adaln_mod(const MH3GemmArgs* args, const uint16_t* cond, const uint16_t*
         return MH3_ERR_POINTER;
     if (!host::aligned16(cond) || !host::aligned16(w))
         return MH3_ERR_ALIGN;
+    // mod may not overlap an input: other workgroups of the launch still read them.
+    const uint64_t mod_bytes = uint64_t(levels) * n * 4u;
+    if (host::overlaps(mod, mod_bytes, cond, uint64_t(levels) * k * 2u) ||
+        host::overlaps(mod, mod_bytes, w, uint64_t(n) * k * 2u) ||
+        (bias && host::overlaps(mod, mod_bytes, bias, uint64_t(n) * 4u)))
+        return MH3_ERR_PARAM;
     const AdalnParams p{cond, w, bias, mod, levels, n, k};
     hipStream_t st = static_cast<hipStream_t>(stream);
     switch ((k / 8 + 63) / 64) {
@@ -447,6 +485,13 @@ int mh3_curve_mods(const MH3CurveArgs* args, const float* t, const float* table,
         return MH3_ERR_SHAPE;
     if (!t || !table || !w || !mod)
         return MH3_ERR_POINTER;
+    // mod may not overlap an input: other threads of the launch still read them.
+    const uint64_t mod_bytes = uint64_t(args->levels) * args->n * 4u;
+    if (host::overlaps(mod, mod_bytes, t, uint64_t(args->levels) * 4u) ||
+        host::overlaps(mod, mod_bytes, table, uint64_t(args->points) * args->width * 4u) ||
+        host::overlaps(mod, mod_bytes, w, uint64_t(args->n) * args->width * 4u) ||
+        (bias && host::overlaps(mod, mod_bytes, bias, uint64_t(args->n) * 4u)))
+        return MH3_ERR_PARAM;
     const CurveParams p{t, table, w, bias, mod, args->levels, args->n, args->points, args->width};
     hipLaunchKernelGGL(curve_mods_kernel, dim3((args->n + 255u) / 256u), dim3(256), 0,
                        static_cast<hipStream_t>(stream), p);

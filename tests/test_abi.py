@@ -278,6 +278,36 @@ def test_time_embed_workspace_checks():
         mh.ERR_POINTER
 
 
+def test_time_embed_refuses_overlapping_outputs():
+    """temb, cond and the workspace overlapping each other or an input would race inside the launch: refused."""
+    a = time_args()
+    need = mh.lib.mh3_time_embed_workspace_bytes(C.byref(a))
+    t, w_in, w_out = C.c_void_p(0x1000), C.c_void_p(0x100000), C.c_void_p(0x1000000)
+    ws, temb, cond = C.c_void_p(0x10000000), C.c_void_p(0x20000000), C.c_void_p(0x30000000)
+    call = mh.lib.mh3_time_embed
+    assert call(C.byref(a), t, w_in, None, w_out, None, ws, need, ws, None, None) == mh.ERR_PARAM      # temb = ws
+    assert call(C.byref(a), t, w_in, None, w_out, None, ws, need, temb, temb, None) == mh.ERR_PARAM    # cond = temb
+    inside_w_out = C.c_void_p(0x1000000 + 4096)
+    assert call(C.byref(a), t, w_in, None, w_out, None, ws, need, inside_w_out, None, None) == mh.ERR_PARAM
+    assert call(C.byref(a), t, w_in, None, w_out, None, C.c_void_p(0x1000 - 256), need, temb, cond, None) == \
+        mh.ERR_PARAM                                                                       # ws runs into t
+    assert mh.lib.mh3_time_embed_noalloc(C.byref(a), t, w_in, None, w_out, None, w_in, None, None) == mh.ERR_PARAM
+
+
+def test_adaln_and_curve_refuse_overlapping_outputs():
+    g = mh.GemmArgs()
+    g.m, g.n, g.k = 3, 96768, 2688
+    cond, w, mod = C.c_void_p(0x1000), C.c_void_p(0x100000), C.c_void_p(0x100000 + 2 * 2688 * 10)
+    assert mh.lib.mh3_adaln_mod(C.byref(g), cond, w, None, mod, None) == mh.ERR_PARAM          # mod inside w
+    assert mh.lib.mh3_adaln_mod(C.byref(g), cond, w, None, cond, None) == mh.ERR_PARAM         # mod = cond
+    c = mh.CurveArgs()
+    c.levels, c.n, c.points, c.width = 2, 96768, 1025, 8
+    t, table, cw = C.c_void_p(0x1000), C.c_void_p(0x10000), C.c_void_p(0x100000)
+    assert mh.lib.mh3_curve_mods(C.byref(c), t, table, cw, None, table, None) == mh.ERR_PARAM  # mod = table
+    assert mh.lib.mh3_curve_mods(C.byref(c), t, table, cw, cw, C.c_void_p(0x100000 + 4 * 8 * 96768 - 4), None) == \
+        mh.ERR_PARAM                                                                         # mod on w's last float
+
+
 def test_adaln_and_curve_validation():
     g = mh.GemmArgs()
     g.m, g.n, g.k = 3, 96768, 2688
