@@ -145,6 +145,8 @@ int mh3_swiglu_rows(const MH3SwigluArgs* args, const void* gate, const void* up,
  *             already among the k. out_stride >= k + local.
  * cube_select: cube_scores and cube_topk fused; the scores stay on chip. Up to 2048 cubes (MH3_ERR_UNSUPPORTED
  *             beyond: use cube_scores + cube_topk, which take up to 4096).
+ * Each call's outputs may not overlap its inputs or each other (MH3_ERR_PARAM): for q and k the span from the array's
+ * start to the last head's last row read.
  * mh3_cube_count() gives the number of cubes of a grid; mh3_topk_k() gives k for a ratio. */
 enum { MH3_CUBES_GRID = 0, MH3_CUBES_GATHERED = 1 };
 typedef struct MH3CubeArgs {
@@ -176,7 +178,8 @@ int mh3_cube_select(const MH3CubeArgs* args, const float* qc, const float* kc, i
  * model row, or -1 where (t, y, x) lies in the padding (the row's validity is map[r] >= 0). For r = cubes * 64 + j,
  * j < n_dense: map[r] = dense_row0 + j. counts[c] = cube c's token count (int32 [cubes], may be NULL). map is int32
  * [cubes * 64 + n_dense], the map mh3_heads_partial gathers through (its rows then come out in the MH3_CUBES_GATHERED
- * order). Model rows must fit int32, and the dense rows may not overlap the video rows (MH3_ERR_PARAM). */
+ * order). Model rows must fit int32, and the dense rows may not overlap the video rows (MH3_ERR_PARAM); nor may map
+ * and counts overlap (MH3_ERR_PARAM). */
 typedef struct MH3CubeMapArgs {
     uint32_t grid_t, grid_h, grid_w;
     uint32_t n_dense;    /* dense rows after the cubes; 0 allowed */
@@ -242,7 +245,8 @@ int mh3_heads_partial_pool(const MH3HeadsArgs* args, const MH3CubeArgs* cubes, c
  * Output rows are written where the queries lie: the grid layout writes the token rows and the dense rows (the
  * reference's write-back to the model's rows, with no gather or scatter pass); the gathered layout also writes a
  * cube's padding slots, as zeros. idx entries outside [0, cubes) are skipped; cnt is clamped to [0, out_stride].
- * out may not be q, k or v. cubes.k and cubes.local are not used. */
+ * out may not be q, k or v, nor overlap k or v, each taken as the span from its start to the last head's last row
+ * read (MH3_ERR_PARAM). cubes.k and cubes.local are not used. */
 typedef struct MH3AttnArgs {
     MH3CubeArgs cubes;   /* heads, head_dim (128), grid, layout, row0, head_stride, row_stride; out_stride: idx's
                             int32 entries per (head, query cube) */
@@ -257,7 +261,8 @@ int mh3_flash_attn_sparse_128(const MH3AttnArgs* args, const uint16_t* q, const 
  * Reference kernel `quant_rows_i8` (mako-common; docs/performance.md:122-123, docs/architecture.md:54-56): each row
  * of a [rows][cols] matrix (the weight's [out][in] rows) to symmetric int8 with one float scale:
  * scale = max|row| / 127 (float), q = round-to-nearest-even(w / scale) in [-127, 127]; an all-zero row gets
- * scale 0 and q 0. w is float or bf16 (`dtype`), cols % 16 == 0, 16-byte aligned. */
+ * scale 0 and q 0. w is float or bf16 (`dtype`), cols % 16 == 0, 16-byte aligned. q and scale may not overlap w or
+ * each other (MH3_ERR_PARAM). */
 typedef struct MH3QuantArgs {
     uint32_t rows;
     uint32_t cols;

@@ -584,6 +584,35 @@ int set_lds_limit(const void* kernel, size_t bytes)
     return host::allow_dynamic_lds(kernel, bytes) == hipSuccess ? MH3_OK : MH3_ERR_HIP;
 }
 
+// Bytes from the start of a head-tile array (q or k) to the end of the last row the selector reads: its last head's
+// last cube row (the grid's last token, or the last gathered cube's last slot).
+uint64_t tile_span_bytes(const CubeGeo& g)
+{
+    const uint64_t last_row =
+        g.row0 + (g.layout == MH3_CUBES_GRID ? uint64_t(g.gt) * g.gh * g.gw : uint64_t(g.cubes) * 64u) - 1u;
+    return ((uint64_t(g.heads) - 1u) * g.head_stride + last_row * g.row_stride + 128u) * 2u;
+}
+
+// Whether any of the outputs (pointer, bytes; null pointers skipped) overlaps an input or another output: a launch
+// would read what its other workgroups are writing.
+struct Span {
+    const void* p;
+    uint64_t n;
+};
+template <size_t NI, size_t NO>
+bool any_overlap(const Span (&in)[NI], const Span (&out)[NO])
+{
+    for (size_t i = 0; i < NO; ++i) {
+        for (size_t j = 0; j < NI; ++j)
+            if (out[i].p && in[j].p && host::overlaps(out[i].p, out[i].n, in[j].p, in[j].n))
+                return true;
+        for (size_t j = i + 1; j < NO; ++j)
+            if (out[i].p && out[j].p && host::overlaps(out[i].p, out[i].n, out[j].p, out[j].n))
+                return true;
+    }
+    return false;
+}
+
 } // namespace
 
 extern "C" {
@@ -606,6 +635,8 @@ int mh3_cube_map(const MH3CubeMapArgs* args, int32_t* map, int32_t* counts, mh3_
         return MH3_ERR_PARAM;
     if (!map)
         return MH3_ERR_POINTER;
+    if (counts && host::overlaps(map, rows * 4u, counts, cubes * 4u))
+        return MH3_ERR_PARAM;
     CubeMapParams p;
     p.gt = args->grid_t, p.gh = args->grid_h, p.gw = args->grid_w;
     p.ch = (p.gh + 3u) / 4u, p.cw = (p.gw + 3u) / 4u, p.plane = p.ch * p.cw, p.cubes = uint32_t(cubes);
@@ -627,6 +658,11 @@ int mh3_cube_pool(const MH3CubeArgs* args, const uint16_t* q, const uint16_t* k,
     if (args->row_stride % 8 != 0 || args->head_stride % 8 != 0 || !host::aligned16(q) || !host::aligned16(k) ||
         !host::aligned16(qc) || !host::aligned16(kc))
         return MH3_ERR_ALIGN;
+    const uint64_t pooled = uint64_t(g.heads) * g.cubes * 128u * 4u;
+    const Span in[] = {{q, tile_span_bytes(g)}, {k, tile_span_bytes(g)}};
+    const Span out[] = {{qc, pooled}, {kc, pooled}, {counts, uint64_t(g.cubes) * 4u}};
+    if (any_overlap(in, out))
+        return MH3_ERR_PARAM;
     const uint32_t items = g.heads * g.cubes;
     hipLaunchKernelGGL(cube_pool_kernel, dim3((items + 3u) / 4u), dim3(256), 0, static_cast<hipStream_t>(stream), g,
                        q, k, qc, kc, counts);
@@ -643,6 +679,11 @@ int mh3_cube_scores(const MH3CubeArgs* args, const float* qc, const float* kc, f
         return MH3_ERR_POINTER;
     if (!host::aligned16(qc) || !host::aligned16(kc))
         return MH3_ERR_ALIGN;
+    const uint64_t pooled = uint64_t(g.heads) * g.cubes * 128u * 4u;
+    const Span in[] = {{qc, pooled}, {kc, pooled}};
+    const Span out[] = {{s, uint64_t(g.heads) * g.cubes * g.cubes * 4u}};
+    if (any_overlap(in, out))
+        return MH3_ERR_PARAM;
     hipLaunchKernelGGL(cube_scores_kernel, dim3((g.cubes + 15u) / 16u, g.heads), dim3(256), 0,
                        static_cast<hipStream_t>(stream), g, qc, kc, s);
     return host::check_launch();
@@ -658,6 +699,13 @@ int mh3_cube_topk(const MH3CubeArgs* args, const float* s, int32_t* idx, int32_t
         return rc;
     if (!s || !idx || !cnt)
         return MH3_ERR_POINTER;
+    {
+        const Span in[] = {{s, uint64_t(g.heads) * g.cubes * g.cubes * 4u}};
+        const Span out[] = {{idx, uint64_t(g.heads) * g.cubes * args->out_stride * 4u},
+                            {cnt, uint64_t(g.heads) * g.cubes * 4u}};
+        if (any_overlap(in, out))
+            return MH3_ERR_PARAM;
+    }
     const uint32_t items = g.heads * g.cubes;
     hipStream_t st = static_cast<hipStream_t>(stream);
     if (g.cubes <= 2048) {
@@ -688,6 +736,14 @@ int mh3_cube_select(const MH3CubeArgs* args, const float* qc, const float* kc, i
         return MH3_ERR_POINTER;
     if (!host::aligned16(qc) || !host::aligned16(kc))
         return MH3_ERR_ALIGN;
+    {
+        const uint64_t pooled = uint64_t(g.heads) * g.cubes * 128u * 4u;
+        const Span in[] = {{qc, pooled}, {kc, pooled}};
+        const Span out[] = {{idx, uint64_t(g.heads) * g.cubes * args->out_stride * 4u},
+                            {cnt, uint64_t(g.heads) * g.cubes * 4u}};
+        if (any_overlap(in, out))
+            return MH3_ERR_PARAM;
+    }
     if (g.cubes > kSelectMaxCubes)
         return MH3_ERR_UNSUPPORTED; // more cubes than the LDS tile holds: use cube_scores + cube_topk
     const int lds_ok = set_lds_limit(reinterpret_cast<const void*>(&cube_select_kernel), kSelectLds);

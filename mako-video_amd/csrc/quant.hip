@@ -201,6 +201,12 @@ extern "C" int mh3_quant_rows_i8(const MH3QuantArgs* a, const void* w, int8_t* q
         return MH3_ERR_POINTER;
     if (!host::aligned16(w) || !host::aligned16(q))
         return MH3_ERR_ALIGN;
+    // The outputs may not overlap w (other workgroups still read it) or each other.
+    const uint64_t w_bytes = uint64_t(a->rows) * a->cols * (a->dtype == MH3_BF16 ? 2u : 4u);
+    const uint64_t q_bytes = uint64_t(a->rows) * a->cols, s_bytes = uint64_t(a->rows) * 4u;
+    if (host::overlaps(q, q_bytes, w, w_bytes) || host::overlaps(scale, s_bytes, w, w_bytes) ||
+        host::overlaps(q, q_bytes, scale, s_bytes))
+        return MH3_ERR_PARAM;
     hipStream_t s = static_cast<hipStream_t>(stream);
     const dim3 grid((a->rows + 3u) / 4u);
     if (a->dtype == MH3_BF16)

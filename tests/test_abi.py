@@ -216,6 +216,27 @@ def test_flash_attn_sparse_pointer_checks():
     assert mh.lib.mh3_flash_attn_sparse_128(C.byref(a), FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, None) == mh.ERR_PARAM
 
 
+def test_flash_attn_sparse_refuses_an_output_over_k_or_v():
+    """out overlapping k or v (read by every other workgroup) is refused; separate arrays pass validation."""
+    a = attn_args()                        # 2 heads; video rows 0 .. 767, dense rows 768 .. 807
+    q, k, v = C.c_void_p(0x100000), C.c_void_p(0x200000), C.c_void_p(0x300000)
+    span = (a.cubes.head_stride + 807 * a.cubes.row_stride + 128) * 2   # start to the last head's last row
+    inside_v = C.c_void_p(0x300000 + span - 256)            # out's first row is v's last
+    assert mh.lib.mh3_flash_attn_sparse_128(C.byref(a), q, k, v, FAKE, FAKE, inside_v, None) == mh.ERR_PARAM
+    before_k = C.c_void_p(0x200000 - span + 256)            # out's last row is k's first
+    assert mh.lib.mh3_flash_attn_sparse_128(C.byref(a), q, k, v, FAKE, FAKE, before_k, None) == mh.ERR_PARAM
+
+
+def test_quant_refuses_overlapping_outputs():
+    a = mh.QuantArgs()
+    a.rows, a.cols, a.dtype = 64, 128, mh.BF16             # w 16 KiB, q 8 KiB, scale 256 B
+    w = C.c_void_p(0x100000)
+    assert mh.lib.mh3_quant_rows_i8(C.byref(a), w, C.c_void_p(0x100000 + 8192), FAKE, None) == mh.ERR_PARAM
+    assert mh.lib.mh3_quant_rows_i8(C.byref(a), w, C.c_void_p(0x200000), w, None) == mh.ERR_PARAM
+    assert mh.lib.mh3_quant_rows_i8(C.byref(a), w, C.c_void_p(0x200000), C.c_void_p(0x200000 + 8188), None) == \
+        mh.ERR_PARAM                                                                        # scale on q's last bytes
+
+
 def test_gemm_refuses_an_output_that_overlaps_an_operand():
     """An out (or gate-add residual) range that overlaps x or w races with the tiles still reading them: refused."""
     g = mh.GemmArgs()
@@ -244,6 +265,28 @@ def test_cube_map_validation():
     assert mh.lib.mh3_cube_map(C.byref(a), FAKE, None, None) == mh.ERR_SHAPE
     a.grid_w, a.video_row0 = 84, 2**31 - 100                # model rows beyond int32
     assert mh.lib.mh3_cube_map(C.byref(a), FAKE, None, None) == mh.ERR_SHAPE
+
+
+def test_selector_refuses_overlapping_outputs():
+    """A selector output overlapping its inputs or another output races inside the launch: refused."""
+    a = mh.CubeArgs()
+    a.heads, a.head_dim, a.grid_t, a.grid_h, a.grid_w = 2, 128, 8, 8, 12
+    a.layout, a.row0, a.head_stride, a.row_stride = mh.CUBES_GRID, 0, 768 * 128, 128
+    a.k, a.local, a.out_stride = 4, 1, 5                     # 24 cubes
+    q, k = C.c_void_p(0x100000), C.c_void_p(0x200000)      # each spans 2 * 768 * 256 bytes
+    qc, kc = C.c_void_p(0x1000000), C.c_void_p(0x1010000)
+    lib = mh.lib
+    assert lib.mh3_cube_pool(C.byref(a), q, k, C.c_void_p(0x100000 + 768 * 256), kc, None, None) == mh.ERR_PARAM
+    assert lib.mh3_cube_pool(C.byref(a), q, k, qc, qc, None, None) == mh.ERR_PARAM            # qc = kc
+    assert lib.mh3_cube_pool(C.byref(a), q, k, qc, kc, C.c_void_p(0x1000000 + 16), None) == mh.ERR_PARAM
+    assert lib.mh3_cube_scores(C.byref(a), qc, kc, kc, None) == mh.ERR_PARAM                  # s over kc
+    s, idx, cnt = C.c_void_p(0x2000000), C.c_void_p(0x3000000), C.c_void_p(0x4000000)
+    assert lib.mh3_cube_topk(C.byref(a), s, s, cnt, None) == mh.ERR_PARAM                     # idx = s
+    assert lib.mh3_cube_topk(C.byref(a), s, idx, C.c_void_p(0x3000000 + 4), None) == mh.ERR_PARAM
+    assert lib.mh3_cube_select(C.byref(a), qc, kc, idx, qc, None) == mh.ERR_PARAM             # cnt = qc
+    m = mh.CubeMapArgs()
+    m.grid_t, m.grid_h, m.grid_w, m.n_dense, m.video_row0, m.dense_row0 = 8, 8, 12, 16, 0, 768
+    assert lib.mh3_cube_map(C.byref(m), idx, C.c_void_p(0x3000000 + 64), None) == mh.ERR_PARAM
 
 
 def time_args(**kw):
