@@ -75,7 +75,9 @@ int64_t mh3_topk_k(float ratio, uint32_t cubes);
  * set_of_row is non-NULL, else 0; a value >= n_sets is read as n_sets - 1. shift, scale and gate are [n_sets][dim]
  * float, w is [dim] float (NULL: all 1). x, residual, y and out are [rows][dim] of `dtype`. bf16 rows need
  * dim % 8 == 0, float rows dim % 4 == 0; every pointer, the float vectors included, 16-byte aligned. Math is float,
- * the sum of squares accumulated in float, and bf16 results are rounded to nearest even once, at the store. */
+ * the sum of squares accumulated in float, and bf16 results are rounded to nearest even once, at the store. An output
+ * may equal an input row array where stated below; any other overlap of an output with an input (the float vectors
+ * and set_of_row included) or with another output is refused (MH3_ERR_PARAM). */
 typedef struct MH3RowsArgs {
     uint32_t rows;
     uint32_t dim;
@@ -93,18 +95,18 @@ typedef struct MH3RowsArgs {
 /* y = x * rsqrt(mean(x^2) + eps) * w * (1 + scale[s]) + shift[s]. y may equal x. */
 int mh3_rms_mod_rows(const MH3RowsArgs* args, const void* x, const float* w, const float* shift, const float* scale,
                      const uint8_t* set_of_row, void* y, mh3_stream_t stream);
-/* x += gate[s] * y, in place (the reference's residual update after out-proj and after fc2). */
+/* x += gate[s] * y, in place (the reference's residual update after out-proj and after fc2). y may equal x. */
 int mh3_gate_add_rows(const MH3RowsArgs* args, void* x, const void* y, const float* gate, const uint8_t* set_of_row,
                       mh3_stream_t stream);
 /* out = residual + gate[s] * (x * rsqrt(mean(x^2) + eps) * w * (1 + scale[s]) + shift[s]): the two reference
- * kernels fused into one HBM pass (reads x and residual once, writes out once). out may equal residual. */
+ * kernels fused into one HBM pass (reads x and residual once, writes out once). out may equal residual or x. */
 int mh3_rms_mod_gate_add_rows(const MH3RowsArgs* args, const void* x, const void* residual, const float* w,
                               const float* shift, const float* scale, const float* gate, const uint8_t* set_of_row,
                               void* out, mh3_stream_t stream);
 /* The block's own order after the out projection and after fc2 (docs/architecture.md:61-66): x += gate[s] * y,
  * then h = the modulated RMS norm of the updated x with this half's w, shift[s] and scale[s], as the next GEMM's
  * input. One HBM pass (reads x and y, writes x and h) with the same results, bit for bit, as mh3_gate_add_rows
- * followed by mh3_rms_mod_rows on the updated x. h must not alias x or y. */
+ * followed by mh3_rms_mod_rows on the updated x. h may not overlap x or y; y may equal x. */
 int mh3_gate_add_rms_mod_rows(const MH3RowsArgs* args, void* x, const void* y, const float* gate, const float* w,
                               const float* shift, const float* scale, const uint8_t* set_of_row, void* h,
                               mh3_stream_t stream);
@@ -114,7 +116,8 @@ int mh3_gate_add_rms_mod_rows(const MH3RowsArgs* args, void* x, const void* y, c
  * silu(g) = g / (1 + exp(-g)), float math, out rounded once. fc1's row is [gate (dim) | up (dim)].
  *   MH3_SWIGLU_SPLIT: gate and up are separate [rows][dim] tensors.
  *   MH3_SWIGLU_FUSED: gate points at [rows][2*dim] rows (gate = columns [0, dim), up = [dim, 2*dim)); up is NULL.
- * out is [rows][dim]. dim % 8 == 0 (bf16) or % 4 == 0 (float); 16-byte aligned pointers. */
+ * out is [rows][dim]. dim % 8 == 0 (bf16) or % 4 == 0 (float); 16-byte aligned pointers. In the split layout out may
+ * equal gate or up; otherwise it may not overlap them (MH3_ERR_PARAM). */
 enum { MH3_SWIGLU_SPLIT = 0, MH3_SWIGLU_FUSED = 1 };
 typedef struct MH3SwigluArgs {
     uint32_t rows;

@@ -629,6 +629,27 @@ int check_rows(const MH3RowsArgs* a, bool needs_eps)
     return MH3_OK;
 }
 
+// Aliasing rules of the row entry points. An output is a [rows][dim] array; it may equal an input row array where
+// `same_ok` (each wave or workgroup reads a row whole before it writes that row), but any other overlap with an input
+// row array races across rows.
+bool rows_clash(const MH3RowsArgs* a, const void* out, const void* in, bool same_ok)
+{
+    const uint64_t bytes = uint64_t(a->rows) * a->dim * (a->dtype == MH3_BF16 ? 2u : 4u);
+    return in && host::overlaps(out, bytes, in, bytes) && !(same_ok && out == in);
+}
+
+// Whether an output overlaps the vectors every workgroup reads: w [dim], shift / scale / gate (n_sets sets of dim
+// floats, set_stride apart) and set_of_row [rows].
+bool params_clash(const MH3RowsArgs* a, const void* out, const float* w, const float* shift, const float* scale,
+                  const float* gate, const uint8_t* sets)
+{
+    const uint64_t bytes = uint64_t(a->rows) * a->dim * (a->dtype == MH3_BF16 ? 2u : 4u);
+    const uint64_t vec = (uint64_t(a->n_sets - 1u) * (a->set_stride ? a->set_stride : a->dim) + a->dim) * 4u;
+    return host::overlaps(out, bytes, w, w ? uint64_t(a->dim) * 4u : 0u) ||
+           host::overlaps(out, bytes, shift, shift ? vec : 0u) || host::overlaps(out, bytes, scale, scale ? vec : 0u) ||
+           host::overlaps(out, bytes, gate, gate ? vec : 0u) || host::overlaps(out, bytes, sets, sets ? a->rows : 0u);
+}
+
 } // namespace
 
 extern "C" {
@@ -646,6 +667,8 @@ int mh3_rms_mod_rows(const MH3RowsArgs* args, const void* x, const float* w, con
     if (!host::aligned16(x) || !host::aligned16(y) || !host::aligned16(w) || !host::aligned16(shift) ||
         !host::aligned16(scale))
         return MH3_ERR_ALIGN;
+    if (rows_clash(args, y, x, true) || params_clash(args, y, w, shift, scale, nullptr, set_of_row))
+        return MH3_ERR_PARAM;
     RowsParams p{};
     p.x = static_cast<const u32x4_t*>(x);
     p.out = static_cast<u32x4_t*>(y);
@@ -668,6 +691,8 @@ int mh3_gate_add_rows(const MH3RowsArgs* args, void* x, const void* y, const flo
         return MH3_ERR_POINTER;
     if (!host::aligned16(x) || !host::aligned16(y) || !host::aligned16(gate))
         return MH3_ERR_ALIGN;
+    if (rows_clash(args, x, y, true) || params_clash(args, x, nullptr, nullptr, nullptr, gate, set_of_row))
+        return MH3_ERR_PARAM;
     RowsParams p{};
     p.x = static_cast<const u32x4_t*>(y);
     p.res = static_cast<const u32x4_t*>(x);
@@ -691,6 +716,9 @@ int mh3_rms_mod_gate_add_rows(const MH3RowsArgs* args, const void* x, const void
     if (!host::aligned16(x) || !host::aligned16(residual) || !host::aligned16(out) || !host::aligned16(w) ||
         !host::aligned16(shift) || !host::aligned16(scale) || !host::aligned16(gate))
         return MH3_ERR_ALIGN;
+    if (rows_clash(args, out, x, true) || rows_clash(args, out, residual, true) ||
+        params_clash(args, out, w, shift, scale, gate, set_of_row))
+        return MH3_ERR_PARAM;
     RowsParams p{};
     p.x = static_cast<const u32x4_t*>(x);
     p.res = static_cast<const u32x4_t*>(residual);
@@ -719,6 +747,10 @@ int mh3_gate_add_rms_mod_rows(const MH3RowsArgs* args, void* x, const void* y, c
     if (!host::aligned16(x) || !host::aligned16(y) || !host::aligned16(h) || !host::aligned16(gate) ||
         !host::aligned16(w) || !host::aligned16(shift) || !host::aligned16(scale))
         return MH3_ERR_ALIGN;
+    if (rows_clash(args, h, x, false) || rows_clash(args, h, y, false) || rows_clash(args, x, y, true) ||
+        params_clash(args, h, w, shift, scale, gate, set_of_row) ||
+        params_clash(args, x, w, shift, scale, gate, set_of_row))
+        return MH3_ERR_PARAM;
     RowsParams p{};
     p.x = static_cast<const u32x4_t*>(y);
     p.res = static_cast<const u32x4_t*>(x);
@@ -754,6 +786,15 @@ int mh3_swiglu_rows(const MH3SwigluArgs* a, const void* gate, const void* up, vo
         return MH3_ERR_PARAM;
     if (!host::aligned16(gate) || !host::aligned16(out) || (up && !host::aligned16(up)))
         return MH3_ERR_ALIGN;
+    {
+        // out may equal gate or up in the split layout (elementwise in place); any other overlap races.
+        const uint64_t ob = uint64_t(a->rows) * vpr * 16u;
+        const uint64_t gb = a->layout == MH3_SWIGLU_FUSED ? 2u * ob : ob;
+        const bool split = a->layout == MH3_SWIGLU_SPLIT;
+        if ((host::overlaps(out, ob, gate, gb) && !(split && out == gate)) ||
+            (up && host::overlaps(out, ob, up, ob) && out != up))
+            return MH3_ERR_PARAM;
+    }
     const uint4* g = static_cast<const uint4*>(gate);
     const uint4* u = a->layout == MH3_SWIGLU_FUSED ? g + vpr : static_cast<const uint4*>(up);
     const uint32_t stride = a->layout == MH3_SWIGLU_FUSED ? 2u * vpr : vpr;

@@ -123,6 +123,29 @@ def test_rows_pointer_checks():
     assert mh.lib.mh3_gate_add_rows(C.byref(rows_args(eps=0.0)), FAKE, ODD, FAKE, None, None) == mh.ERR_ALIGN
 
 
+def test_rows_refuse_partial_overlaps():
+    """A row output may equal an input row array where documented; a shifted overlap (rows racing each other) or an
+    overlap with the modulation vectors is refused."""
+    a = rows_args(rows=64, dim=5120)                        # 64 rows x 10 KiB
+    x, r, o = C.c_void_p(0x1000000), C.c_void_p(0x2000000), C.c_void_p(0x3000000)
+    vec = C.c_void_p(0x4000000)
+    lib = mh.lib
+    shifted_x = C.c_void_p(0x1000000 + 10240)              # one row on
+    assert lib.mh3_rms_mod_rows(C.byref(a), x, None, vec, vec, None, shifted_x, None) == mh.ERR_PARAM
+    assert lib.mh3_rms_mod_rows(C.byref(a), x, None, vec, C.c_void_p(0x3000000 + 512), None, o, None) == mh.ERR_PARAM
+    assert lib.mh3_gate_add_rows(C.byref(a), x, shifted_x, vec, None, None) == mh.ERR_PARAM
+    assert lib.mh3_rms_mod_gate_add_rows(C.byref(a), x, r, None, vec, vec, vec, None, C.c_void_p(0x2000000 + 16),
+                                         None) == mh.ERR_PARAM
+    assert lib.mh3_rms_mod_gate_add_rows(C.byref(a), x, r, None, vec, vec, vec, o, o, None) == mh.ERR_PARAM   # sets
+    assert lib.mh3_gate_add_rms_mod_rows(C.byref(a), x, r, vec, None, vec, vec, None, C.c_void_p(0x2000000 - 1024),
+                                         None) == mh.ERR_PARAM                          # h's last row inside y
+    s = mh.SwigluArgs()
+    s.rows, s.dim, s.layout, s.dtype = 64, 5120, mh.SWIGLU_FUSED, mh.BF16
+    assert lib.mh3_swiglu_rows(C.byref(s), x, None, x, None) == mh.ERR_PARAM           # fused rows are 2 dim wide
+    s.layout = mh.SWIGLU_SPLIT
+    assert lib.mh3_swiglu_rows(C.byref(s), x, r, C.c_void_p(0x2000000 + 10240), None) == mh.ERR_PARAM
+
+
 def test_swiglu_validation():
     a = mh.SwigluArgs()
     a.rows, a.dim, a.layout, a.dtype = 4, 13824, mh.SWIGLU_FUSED, mh.BF16
