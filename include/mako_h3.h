@@ -282,7 +282,8 @@ int mh3_quant_rows_i8(const MH3QuantArgs* args, const void* w, int8_t* q, float*
  * The int8 -> bf16 widening is exact (|w| <= 127); the scale is applied to the float accumulator.
  * k % 64 == 0, n % 128 == 0, m >= 1; x, w and out 16-byte aligned. The kernel addresses w and a 256-row block of x
  * with 32-bit offsets: n * k < 2^30 and k < 2^22, else MH3_ERR_UNSUPPORTED (H3's fc1, n = 14,336 and k = 5376,
- * uses 7.7e7). */
+ * uses 7.7e7). For every GEMM entry point, out (the residual for mh3_gemm_gate_add) may not overlap x, w or the
+ * scale, gate and set_of_row vectors (MH3_ERR_PARAM): other tiles are still reading them. */
 typedef struct MH3GemmArgs {
     uint32_t m;
     uint32_t n;           /* output columns; w has 2n rows with a SwiGLU epilogue, n rows otherwise */

@@ -476,6 +476,13 @@ int launch_gemm(const MH3GemmArgs* a, const void* x, const void* w, const float*
     if (host::overlaps(out, out_bytes, x, uint64_t(a->m) * a->k * kEA) ||
         host::overlaps(out, out_bytes, w, w_rows * a->k * kEB))
         return MH3_ERR_PARAM;
+    // Nor the vectors every epilogue reads: the scales, the gate sets and the row-to-set map.
+    if (host::overlaps(out, out_bytes, scale, scale ? w_rows * 4u : 0u) ||
+        host::overlaps(out, out_bytes, xscale, xscale ? uint64_t(a->m) * 4u : 0u) ||
+        (EPI == kGateAdd &&
+         (host::overlaps(out, out_bytes, gg.gate, (uint64_t(gg.n_sets) - 1u) * gg.gate_stride * 4u + a->n * 4ull) ||
+          host::overlaps(out, out_bytes, gg.set_of_row, gg.set_of_row ? uint64_t(a->m) : 0u))))
+        return MH3_ERR_PARAM;
     constexpr int WM = kGemmWM, WN = kGemmWN;
     const void* kernel = reinterpret_cast<const void*>(&gemm_kernel<WM, WN, MODE, EPI>);
     static const int lds_ok = hipFuncSetAttribute(kernel, hipFuncAttributeMaxDynamicSharedMemorySize, int(kGemmLds));

@@ -275,6 +275,12 @@ def test_gemm_refuses_an_output_that_overlaps_an_operand():
     assert mh.lib.mh3_gemm_gate_add(C.byref(g), mh.GEMM_W8A16, x, None, w, FAKE, gate, None, before_x, None) == \
         mh.ERR_PARAM
     assert mh.lib.mh3_gemm_w8a16_swiglu(C.byref(g), x, w, FAKE, x, None) == mh.ERR_PARAM
+    out = C.c_void_p(0x400000)                              # clear of x and w, but not of the vectors below
+    assert mh.lib.mh3_gemm_w8a16_swiglu(C.byref(g), x, w, C.c_void_p(0x400000 + 64), out, None) == mh.ERR_PARAM
+    assert mh.lib.mh3_gemm_gate_add(C.byref(g), mh.GEMM_BF16, x, None, w, None, C.c_void_p(0x400000 + 256), None,
+                                    out, None) == mh.ERR_PARAM                           # gate inside residual
+    assert mh.lib.mh3_gemm_gate_add(C.byref(g), mh.GEMM_BF16, x, None, w, None, gate, C.c_void_p(0x400000), out,
+                                    None) == mh.ERR_PARAM                                # set_of_row inside residual
 
 
 def test_cube_map_validation():
