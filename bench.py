@@ -11,8 +11,8 @@ other ops of the path at their shapes (SwiGLU split and fused-row, the cube sele
 fp32 modulated RMS norm, heads_partial, the sparse attention, the other projections) and reports each as ms, GB/s or
 TFLOP/s and a fraction of the MI355X roofline; `share` repeats the main ones at one GPU's share of an 8-way split;
 `ref` times the reference's own published workloads at H3's dimensions beside its published Apple M5 Max times
-(`reference_shapes`). Kernel times
-come from HIP events recorded on the stream the kernels run on (torch's current stream): the mean over the timed
+(`reference_shapes`), and sums a forward's kernels (dense and sparse) against the reference's GPU time a forward.
+Kernel times come from HIP events recorded on the stream the kernels run on (torch's current stream): the mean over the timed
 launches, with the median beside it for the row and selector workloads. Launches run back to back with warm caches;
 `cold_ms` beside the fused op, SwiGLU, the select kernel, fc1 and the fp32 norm times each launch after a 512 MiB
 overwrite of L2 and the MALL instead. The CPU baseline is the scalar C oracle on one host core, on a bounded sample of
@@ -540,7 +540,17 @@ def bench_reference_shapes(mh, dev, steps, warmup):
                                                            out=ao), steps, warmup)
     out["sparse_attention_per_forward"] = entry(ms * H3_BLOCKS, 4700.0,
                                                 "flash_attn_sparse_128 over those pass lists, 19,305 rows, x 50 blocks")
-    del q, k, v, ao
+    # Dense attention (docs/performance.md:168-169: 17.2 s a forward) is the same kernel with every cube selected
+    # (ratio 1, which the reference's tests treat as dense).
+    ad = mh.cube_args(H3_HEADS, grid, head_stride=arows * 128, k=cubes, local=0)
+    idx_d = torch.arange(cubes, dtype=torch.int32, device=dev).expand(H3_HEADS, cubes, cubes).contiguous()
+    cnt_d = torch.full((H3_HEADS, cubes), cubes, dtype=torch.int32, device=dev)
+    ms_d, _ = time_launches(lambda: mh.flash_attn_sparse_128(ad, q, k, v, idx_d, cnt_d, dense_row0=video,
+                                                             n_dense=n_dense, out=ao), steps, warmup)
+    out["dense_attention_per_forward"] = entry(ms_d * H3_BLOCKS, 17200.0,
+                                               "flash_attn_sparse_128 with every cube selected, 19,305 rows, x 50 "
+                                               "blocks")
+    del q, k, v, ao, idx_d, cnt_d
 
     # The AdaLN projections (docs/performance.md:45: gemm BF16 2688 x 96768, 50 a forward, 70-85 ms).
     cond = rnd(1, 2688)
@@ -549,6 +559,17 @@ def bench_reference_shapes(mh, dev, steps, warmup):
     ms, _ = time_launches(lambda: mh.adaln_mod(cond, wa, out=mod), steps, warmup)
     out["adaln_projections_per_forward"] = entry(ms * H3_BLOCKS, 77.5,
                                                  "cond [1][2688] -> [96,768] table, x 50 blocks (reference 70-85 ms)")
+    # A forward's kernels summed, against the reference's GPU time a forward at 960x544 (docs/performance.md:167-168:
+    # dense 34.4 s, sparse at ratio 0.1 21.3 s, nominal thermal state): the four bf16 GEMMs (at 19,456 rows; fc1
+    # with SwiGLU in its epilogue, which the row kernels time again) x 50, the row kernels, the AdaLN projections, and
+    # the attention (with its selection when sparse).
+    gemm_fwd = sum(gemms[n]["ms"] for n in ("fc1_bf16", "qkv_bf16", "out_bf16", "fc2_bf16")) * H3_BLOCKS
+    common = gemm_fwd + out["row_kernels_per_forward"]["ms"] + out["adaln_projections_per_forward"]["ms"]
+    out["sparse_forward_kernels"] = entry(common + out["sparse_selection_per_forward"]["ms"] +
+                                          out["sparse_attention_per_forward"]["ms"], 21300.0,
+                                          "the entries above summed for a sparse (ratio 0.1) forward")
+    out["dense_forward_kernels"] = entry(common + out["dense_attention_per_forward"]["ms"], 34400.0,
+                                         "the entries above summed for a dense forward")
     return out
 
 
