@@ -52,32 +52,35 @@ struct TimeParams {
 __device__ __forceinline__ float silu(float v) { return v / (1.0f + __expf(-v)); }
 
 // Layer 1: hid[u][r] = silu(w_in[r] . emb(t[u]) + b_in[r]). A wave per weight row (freq_dim floats, a lane's float4
-// pieces at c = lane + 64 i); the lane's embedding values are computed once, in double, for the block's levels.
+// pieces at c = lane + 64 i). The block's threads compute the embedding of its levels once, in double, one value a
+// thread, into LDS (each wave computing all of its lanes' values itself took 16 times the double-precision
+// transcendentals and most of the kernel's time); each lane then holds its pieces in registers.
 __global__ __launch_bounds__(256) void time_mlp_in_kernel(TimeParams p)
 {
+    __shared__ __attribute__((aligned(16))) float emb_s[kLevelGroup][kMaxFreqDim];
     const int lane = threadIdx.x & 63;
     const uint32_t wave = threadIdx.x >> 6;
     const uint32_t u0 = blockIdx.y * kLevelGroup;
     const int nu = min(kLevelGroup, int(p.levels - u0));
     const uint32_t half = p.freq_dim / 2, nchunk = p.freq_dim / 4;
+    for (uint32_t v = threadIdx.x; v < p.freq_dim; v += blockDim.x) {
+        const uint32_t f = v < half ? v : v - half;
+        const double freq = exp(-p.log_period * double(f) / double(half));
+        for (int u = 0; u < nu; ++u) {
+            const double arg = double(p.t[u0 + u]) * freq;
+            emb_s[u][v] = float(v < half ? cos(arg) : sin(arg));
+        }
+    }
+    __syncthreads();
     float emb[kFreqChunks][kLevelGroup][4];
 #pragma unroll
     for (int i = 0; i < kFreqChunks; ++i) {
         const uint32_t c = lane + 64u * i;
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const uint32_t v = 4u * c + j;
-            const uint32_t f = v < half ? v : v - half;
-            const double freq = exp(-p.log_period * double(f) / double(half));
-#pragma unroll
-            for (int u = 0; u < kLevelGroup; ++u) {
-                float e = 0.0f;
-                if (c < nchunk && u < nu) {
-                    const double arg = double(p.t[u0 + u]) * freq;
-                    e = float(v < half ? cos(arg) : sin(arg));
-                }
-                emb[i][u][j] = e;
-            }
+        for (int u = 0; u < kLevelGroup; ++u) {
+            const float4 e = c < nchunk && u < nu ? *reinterpret_cast<const float4*>(&emb_s[u][4u * c])
+                                                  : float4{0.0f, 0.0f, 0.0f, 0.0f};
+            emb[i][u][0] = e.x, emb[i][u][1] = e.y, emb[i][u][2] = e.z, emb[i][u][3] = e.w;
         }
     }
     for (uint32_t r = blockIdx.x * 4u + wave; r < p.hidden; r += gridDim.x * 4u) {
