@@ -105,9 +105,11 @@ __global__ __launch_bounds__(256) void time_mlp_in_kernel(TimeParams p)
     }
 }
 
-// Layer 2: temb[u][j] = w_out[j] . hid[u] + b_out[j], and cond[u][j] = bf16(silu(temb[u][j])). The block stages its
-// levels' hidden vectors in LDS; a wave per weight row (hidden floats, float4 pieces c = lane + 64 i).
-__global__ __launch_bounds__(512) void time_mlp_out_kernel(TimeParams p)
+// Layer 2: temb[u][j] = w_out[j] . hid[u] + b_out[j], and cond[u][j] = bf16(silu(temb[u][j])). One 16-wave block a
+// CU stages its levels' hidden vectors in LDS once; a wave per weight row (hidden floats, float4 pieces
+// c = lane + 64 i), rows dealt round-robin over the blocks so every CU streams the same share of w_out.
+constexpr uint32_t kOutWaves = 16;
+__global__ __launch_bounds__(kOutWaves * 64) void time_mlp_out_kernel(TimeParams p)
 {
     extern __shared__ float4 hs[]; // [nu][hidden / 4]
     const int lane = threadIdx.x & 63;
@@ -119,7 +121,7 @@ __global__ __launch_bounds__(512) void time_mlp_out_kernel(TimeParams p)
     for (uint32_t i = threadIdx.x; i < uint32_t(nu) * hc; i += blockDim.x)
         hs[i] = src[i];
     __syncthreads();
-    for (uint32_t j = blockIdx.x * 8u + wave; j < p.out_dim; j += gridDim.x * 8u) {
+    for (uint32_t j = blockIdx.x + wave * gridDim.x; j < p.out_dim; j += gridDim.x * kOutWaves) {
         float acc[kLevelGroup] = {};
         const float4* row = reinterpret_cast<const float4*>(p.w_out + uint64_t(j) * p.hidden);
 #pragma unroll 4
@@ -322,8 +324,8 @@ int time_embed_launch(const MH3TimeArgs* args, const float* t, const float* w_in
     if (lds > 64u * 1024u && host::allow_dynamic_lds(reinterpret_cast<const void*>(&time_mlp_out_kernel), lds) !=
                                  hipSuccess)
         return MH3_ERR_HIP;
-    const uint32_t out_blocks = (args->out_dim + 7u) / 8u;
-    hipLaunchKernelGGL(time_mlp_out_kernel, dim3(out_blocks, groups), dim3(512), lds, st, p);
+    const uint32_t out_blocks = min(args->out_dim, uint32_t(host::cu_count()));
+    hipLaunchKernelGGL(time_mlp_out_kernel, dim3(out_blocks, groups), dim3(kOutWaves * 64u), lds, st, p);
     return host::check_launch();
 }
 
