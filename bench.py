@@ -1,7 +1,7 @@
 """Benchmark of the H3 per-block hot path on one MI355X.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W]
-                    [--only fused,block_order,copy,swiglu,select,cond,heads,attn,proj,fc1,rms_f32,ref,share]
+                    [--only fused,block_order,copy,swiglu,select,cond,heads,attn,proj,fc1,rms_f32,block,ref,share]
                     [--no-cpu] [--no-compare]
 
 A step is one pass of the headline kernel -- the fused adaLN-modulated RMS norm + gated residual -- over the
@@ -9,7 +9,8 @@ A step is one pass of the headline kernel -- the fused adaLN-modulated RMS norm 
 achieved algorithmic HBM bandwidth (6 bytes an element: read x and residual, write out). The same run also times the
 other ops of the path at their shapes (SwiGLU split and fused-row, the cube selector, the int8 fc1 + SwiGLU GEMM, the
 fp32 modulated RMS norm, heads_partial, the sparse attention, the other projections) and reports each as ms, GB/s or
-TFLOP/s and a fraction of the MI355X roofline; `share` repeats the main ones at one GPU's share of an 8-way split;
+TFLOP/s and a fraction of the MI355X roofline; `block` times one whole H3 block at 768p as one sequence of
+launches; `share` repeats the main ones at one GPU's share of an 8-way split;
 `ref` times the reference's own published workloads at H3's dimensions beside its published Apple M5 Max times
 (`reference_shapes`), and sums a forward's kernels (dense and sparse) against the reference's GPU time a forward.
 Kernel times come from HIP events recorded on the stream the kernels run on (torch's current stream): the mean over the timed
@@ -573,6 +574,61 @@ def bench_reference_shapes(mh, dev, steps, warmup):
     return out
 
 
+def bench_block(mh, dev, steps, warmup):
+    """One whole H3 block at the 768p shape through the library, in the model's row order from end to end (no gather
+    or scatter): rms_mod_rows; the qkv projection (int8 weights, W8A16); heads_partial with cube_pool in its pass,
+    its outputs [rows][heads x 128]; cube_select at ratio 0.1; flash_attn_sparse_128 over those rows; the out
+    projection with gate_add_rows in its epilogue; rms_mod_rows; fc1 W8A16 + SwiGLU; fc2 with gate_add_rows. Weights
+    are random normals quantized per row by quant_rows_i8, rows and modulation synthetic; the residual is updated in
+    place by every timed block. The sequence of launches is timed as one step; `stages_ms` sums the stages' own
+    times from the other legs for comparison."""
+    T, Y, X = GRID
+    video, n_dense = T * Y * X, ROWS - T * Y * X
+    g = torch.Generator(device=dev).manual_seed(51)
+
+    def w8(n, k):
+        w = (0.02 * torch.randn((n, k), generator=g, device=dev)).to(torch.bfloat16)
+        return mh.quant_rows_i8(w)
+    wqkv, sqkv = w8(3 * HEADS * 128, DIM)
+    wo, so = w8(DIM, HEADS * 128)
+    w1, s1 = w8(2 * FFN, DIM)
+    w2, s2 = w8(DIM, FFN)
+    n1, sh_a, sc_a, ga_a = mod_params(dev, DIM, 52)
+    n2, sh_m, sc_m, ga_m = mod_params(dev, DIM, 53)
+    ang = torch.rand((ROWS, 48), generator=g, device=dev) * 6.2831853 - 3.1415927
+    cs, sn = torch.cos(ang), torch.sin(ang)
+    x = torch.randn((ROWS, DIM), generator=g, device=dev).to(torch.bfloat16)
+    h = torch.empty_like(x)
+    qkv = torch.empty((ROWS, 3 * HEADS * 128), dtype=torch.bfloat16, device=dev)
+    q, k, v = (torch.empty((ROWS, HEADS * 128), dtype=torch.bfloat16, device=dev) for _ in range(3))
+    cubes = mh.cube_count(*GRID)
+    kk = mh.topk_k(0.1, cubes)
+    a = mh.cube_args(HEADS, GRID, head_stride=128, row_stride=HEADS * 128, k=kk, local=1)
+    qc = torch.empty((HEADS, cubes, 128), dtype=torch.float32, device=dev)
+    kc = torch.empty_like(qc)
+    idx = torch.empty((HEADS, cubes, kk + 1), dtype=torch.int32, device=dev)
+    cnt = torch.empty((HEADS, cubes), dtype=torch.int32, device=dev)
+    att = torch.empty((ROWS, HEADS * 128), dtype=torch.bfloat16, device=dev)
+    f = torch.empty((ROWS, FFN), dtype=torch.bfloat16, device=dev)
+
+    def block():
+        mh.rms_mod_rows(x, n1, sh_a, sc_a, out=h)
+        mh.gemm(h, wqkv, w_scale=sqkv, out=qkv)
+        mh.heads_partial_pool(qkv, HEADS, GRID, None, None, cs, sn, rot=96, layout="rows", cube_layout=mh.CUBES_GRID,
+                              q=q, k=k, v=v, qc=qc, kc=kc)
+        mh.cube_select(a, qc, kc, idx=idx, cnt=cnt)
+        mh.flash_attn_sparse_128(a, q, k, v, idx, cnt, dense_row0=video, n_dense=n_dense, out=att)
+        mh.gemm_gate_add(att, wo, x, ga_a, w_scale=so)
+        mh.rms_mod_rows(x, n2, sh_m, sc_m, out=h)
+        mh.gemm_w8a16_swiglu(h, w1, s1, out=f)
+        mh.gemm_gate_add(f, w2, x, ga_m, w_scale=s2)
+    ms, wall = time_launches(block, steps, warmup)
+    finite = bool(torch.isfinite(x.float()).all())
+    return {"ms": ms, "median_ms": LAST_MEDIAN_MS[0], "wall_ms": wall, "rows": ROWS, "finite": finite,
+            "shape": {"rows": ROWS, "dim": DIM, "ffn": FFN, "heads": HEADS, "grid": list(GRID), "k": kk},
+            "weights": "int8 (W8A16)"}
+
+
 def bench_proj(mh, dev, steps, warmup):
     """The block's other projections at the 768p rows (129,536): qkv 5120 -> 3 x 40 x 128 = 15,360 (plain store), the
     out projection 5120 -> 5120 and fc2 13,824 -> 5120 with gate_add_rows folded into the epilogue (residual += gate *
@@ -867,7 +923,8 @@ def main() -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--only", default="fused,block_order,copy,swiglu,select,cond,heads,attn,proj,fc1,rms_f32,ref,share")
+    ap.add_argument("--only",
+                    default="fused,block_order,copy,swiglu,select,cond,heads,attn,proj,fc1,rms_f32,block,ref,share")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-compare", action="store_true")
     args = ap.parse_args()
@@ -945,6 +1002,24 @@ def main() -> int:
                                                not args.no_compare)
         torch.cuda.empty_cache()
         done("fc1")
+
+    if "block" in ops:
+        blk = bench_block(mh, dev, 3, 1)
+        # The same stages timed on their own in the legs above (all but the two rms_mod_rows), summed, where those
+        # legs ran: qkv, heads_partial with the pool (grid layout), cube_select, the attention, out, fc1, fc2.
+        proj = report.get("projections") or {}
+        parts = [(proj.get("qkv") or {}).get("ms"),
+                 ((report.get("heads_partial") or {}).get("grid_pool") or {}).get("ms"),
+                 (report.get("cube_selector") or {}).get("select_ms"),
+                 (report.get("flash_attn_sparse_128") or {}).get("ms"),
+                 (proj.get("out") or {}).get("ms"),
+                 (report.get("fc1_w8a16_swiglu") or {}).get("ms"),
+                 (proj.get("fc2") or {}).get("ms")]
+        if all(t is not None for t in parts):
+            blk["stages_ms_without_norms"] = sum(parts)
+        report["block_768p"] = blk
+        torch.cuda.empty_cache()
+        done("block")
 
     if "ref" in ops:
         report["reference_shapes"] = bench_reference_shapes(mh, dev, max(3, args.steps // 2), max(1, args.warmup // 2))
