@@ -580,8 +580,8 @@ def bench_block(mh, dev, steps, warmup):
     its outputs [rows][heads x 128]; cube_select at ratio 0.1; flash_attn_sparse_128 over those rows; the out
     projection with gate_add_rows in its epilogue; rms_mod_rows; fc1 W8A16 + SwiGLU; fc2 with gate_add_rows. Weights
     are random normals quantized per row by quant_rows_i8, rows and modulation synthetic; the residual is updated in
-    place by every timed block. The sequence of launches is timed as one step; `stages_ms` sums the stages' own
-    times from the other legs for comparison."""
+    place by every timed block. The sequence of launches is timed as one step. `w8a8_ms` is the same block with the
+    reference's own --int8 all (each GEMM's activations quantized per row, the int8 MFMA)."""
     T, Y, X = GRID
     video, n_dense = T * Y * X, ROWS - T * Y * X
     g = torch.Generator(device=dev).manual_seed(51)
@@ -623,10 +623,36 @@ def bench_block(mh, dev, steps, warmup):
         mh.gemm_w8a16_swiglu(h, w1, s1, out=f)
         mh.gemm_gate_add(f, w2, x, ga_m, w_scale=s2)
     ms, wall = time_launches(block, steps, warmup)
+    med = LAST_MEDIAN_MS[0]
     finite = bool(torch.isfinite(x.float()).all())
-    return {"ms": ms, "median_ms": LAST_MEDIAN_MS[0], "wall_ms": wall, "rows": ROWS, "finite": finite,
+
+    # The same block under the reference's own --int8 all (W8A8): each GEMM's activations quantized per row by
+    # quant_rows_i8 first, then the int8 MFMA.
+    xq = torch.empty((ROWS, max(DIM, FFN)), dtype=torch.int8, device=dev)
+    xs = torch.empty(ROWS, dtype=torch.float32, device=dev)
+
+    def quant(t):
+        n = t.shape[1]
+        q8 = xq.view(-1)[:ROWS * n].view(ROWS, n)
+        mh.quant_rows_i8(t, q=q8, scale=xs)
+        return q8
+
+    def block_w8a8():
+        mh.rms_mod_rows(x, n1, sh_a, sc_a, out=h)
+        mh.gemm(quant(h), wqkv, x_scale=xs, w_scale=sqkv, out=qkv)
+        mh.heads_partial_pool(qkv, HEADS, GRID, None, None, cs, sn, rot=96, layout="rows", cube_layout=mh.CUBES_GRID,
+                              q=q, k=k, v=v, qc=qc, kc=kc)
+        mh.cube_select(a, qc, kc, idx=idx, cnt=cnt)
+        mh.flash_attn_sparse_128(a, q, k, v, idx, cnt, dense_row0=video, n_dense=n_dense, out=att)
+        mh.gemm_gate_add(quant(att), wo, x, ga_a, x_scale=xs, w_scale=so)
+        mh.rms_mod_rows(x, n2, sh_m, sc_m, out=h)
+        mh.gemm_i8_swiglu(quant(h), xs, w1, s1, out=f)
+        mh.gemm_gate_add(quant(f), w2, x, ga_m, x_scale=xs, w_scale=s2)
+    ms8, _ = time_launches(block_w8a8, steps, warmup)
+    finite = finite and bool(torch.isfinite(x.float()).all())
+    return {"ms": ms, "median_ms": med, "wall_ms": wall, "rows": ROWS, "finite": finite,
             "shape": {"rows": ROWS, "dim": DIM, "ffn": FFN, "heads": HEADS, "grid": list(GRID), "k": kk},
-            "weights": "int8 (W8A16)"}
+            "weights": "int8 (W8A16)", "w8a8_ms": ms8, "w8a8_median_ms": LAST_MEDIAN_MS[0]}
 
 
 def bench_proj(mh, dev, steps, warmup):
