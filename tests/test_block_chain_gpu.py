@@ -134,3 +134,67 @@ def test_one_block_through_the_library(dev):
     rel, cos = diff(bits_to_f64(to_bits(x2)), bits_to_f64(ox2), D)
     print(f"whole block against the oracle's chain: rel {rel:.3g}, min row cos {cos:.7f}")
     assert rel < 2e-3 and cos > 0.99999, f"whole block: rel {rel:.3g} cos {cos:.7f}"
+
+
+def test_one_block_in_the_models_row_order(dev):
+    """The same block with no gather or scatter, as bench.py's `block` leg runs it: heads_partial writes q, k and v as
+    the model's rows ([rows][heads x 128]) with cube_pool in its pass over the grid layout, the selection and the
+    attention read those rows where they lie, and the attention's output rows are the out projection's input. The
+    video grid's rows come first here and the dense rows after them."""
+    rng = np.random.default_rng(43)
+    t = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(dev)  # noqa: E731
+    npv = lambda a: a.cpu().numpy()  # noqa: E731
+    video = GRID[0] * GRID[1] * GRID[2]
+    rows = video + N_DENSE
+
+    def w8(n, k):
+        return mh.quant_rows_i8(t((0.05 * rng.standard_normal((n, k))).astype(np.float32)))
+    wqkv, sqkv = w8(3 * HEADS * 128, D)
+    wo, so = w8(D, HEADS * 128)
+    w1, s1 = w8(2 * FFN, D)
+    w2, s2 = w8(D, FFN)
+    n1, n2 = [(1 + 0.02 * rng.standard_normal(D)).astype(np.float32) for _ in range(2)]
+    sh_a, sc_a, ga_a, sh_m, sc_m, ga_m = [(0.1 * rng.standard_normal((1, D))).astype(np.float32) for _ in range(6)]
+    qw, kw = [(1 + 0.1 * rng.standard_normal(128)).astype(np.float32) for _ in range(2)]
+    ang = rng.uniform(-np.pi, np.pi, (rows, ROT // 2))
+    cs, sn = np.cos(ang).astype(np.float32), np.sin(ang).astype(np.float32)
+    x0 = randn_bf16_bits(rng, (rows, D))
+
+    x = from_bits(x0, dev)
+    h = mh.rms_mod_rows(x, t(n1), t(sh_a[0]), t(sc_a[0]))
+    qkv = mh.gemm(h, wqkv, w_scale=sqkv)
+    q, k, v, qc, kc = mh.heads_partial_pool(qkv, HEADS, GRID, t(qw), t(kw), t(cs), t(sn), rot=ROT, layout="rows",
+                                            cube_layout=mh.CUBES_GRID)
+    kk = mh.topk_k(0.25, mh.cube_count(*GRID))
+    a = mh.cube_args(HEADS, GRID, head_stride=128, row_stride=HEADS * 128, k=kk, local=1)
+    idx, cnt = mh.cube_select(a, qc, kc)
+    att = mh.flash_attn_sparse_128(a, q, k, v, idx, cnt, dense_row0=video, n_dense=N_DENSE)
+    x1 = mh.gemm_gate_add(att, wo, x, t(ga_a[0]), w_scale=so)
+    h2 = mh.rms_mod_rows(x1, t(n2), t(sh_m[0]), t(sc_m[0]))
+    f = mh.gemm_w8a16_swiglu(h2, w1, s1)
+    x2 = mh.gemm_gate_add(f, w2, x1, t(ga_m[0]), w_scale=s2)
+
+    # The pooled means and the selection against the oracle on the GPU's own head rows.
+    heads_of = lambda a_: to_bits(a_).reshape(rows, HEADS, 128).transpose(1, 0, 2)  # noqa: E731
+    oqc, okc, _ = orc.cube_pool(np.ascontiguousarray(heads_of(q)), np.ascontiguousarray(heads_of(k)), HEADS, GRID,
+                                layout=orc.CUBES_GRID, head_stride=rows * 128)
+    assert_close(npv(qc), oqc, 1e-5, 1e-6, "pooled q (model's rows)")
+    assert_close(npv(kc), okc, 1e-5, 1e-6, "pooled k (model's rows)")
+    widx, wcnt = orc.cube_topk(mh.cube_scores(a, qc, kc).cpu().numpy().astype(np.float64), GRID, kk, 1)
+    assert np.array_equal(npv(idx), widx) and np.array_equal(npv(cnt), wcnt), "cube_select (model's rows)"
+
+    # The whole block against the oracle's own chain from x0, on the GPU's selection.
+    row = lambda a_: a_.reshape(1, D)  # noqa: E731
+    oh = orc.rms_mod_rows(x0, n1, row(sh_a), row(sc_a))
+    oqkv = orc.gemm(oh, npv(wqkv), orc.GEMM_W8A16, w_scale=npv(sqkv))
+    oq, ok, ov = orc.heads_partial(oqkv, HEADS, qw, kw, cs, sn, rot=ROT)
+    oatt = orc.attn_sparse(oq, ok, ov, npv(idx), npv(cnt), GRID, video, N_DENSE, layout=orc.CUBES_GRID)
+    oatt_rows = np.ascontiguousarray(oatt.transpose(1, 0, 2)).reshape(rows, HEADS * 128)
+    check_bits(to_bits(att), oatt_rows, 128, "attention in the model's rows", 1e-2, 1e-2)
+    ox1 = orc.gemm_gate_add(oatt_rows, npv(wo), orc.GEMM_W8A16, x0, ga_a, w_scale=npv(so))
+    oh2 = orc.rms_mod_rows(ox1, n2, row(sh_m), row(sc_m))
+    of = orc.gemm_w8a16_swiglu(oh2, npv(w1), npv(s1))
+    ox2 = orc.gemm_gate_add(of, npv(w2), orc.GEMM_W8A16, ox1, ga_m, w_scale=npv(s2))
+    rel, cos = diff(bits_to_f64(to_bits(x2)), bits_to_f64(ox2), D)
+    print(f"whole block in the model's rows against the oracle's chain: rel {rel:.3g}, min row cos {cos:.7f}")
+    assert rel < 2e-3 and cos > 0.99999, f"whole block (model's rows): rel {rel:.3g} cos {cos:.7f}"
