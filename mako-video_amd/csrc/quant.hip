@@ -177,6 +177,9 @@ void launch_quant(dim3 grid, hipStream_t s, const void* w, int8_t* q, float* sca
     else if (cpl <= 8)
         hipLaunchKernelGGL((quant_rows_kernel<DT, 8>), grid, dim3(256), kQuantLdsFloor, s, w, q, scale, rows,
                            cols);
+    else if (cpl <= 14) // fc2's input rows (13,824 or 14,336 bf16) in registers: one HBM read instead of two
+        hipLaunchKernelGGL((quant_rows_kernel<DT, 14>), grid, dim3(256), kQuantLdsFloor, s, w, q, scale, rows,
+                           cols);
     else
         hipLaunchKernelGGL((quant_rows_kernel<DT, 0>), grid, dim3(256), kQuantLdsFloor, s, w, q, scale, rows,
                            cols);

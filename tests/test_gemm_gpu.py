@@ -13,9 +13,9 @@ pytestmark = pytest.mark.gpu
 
 @pytest.mark.parametrize("dtype", ["bf16", "f32"])
 @pytest.mark.parametrize("rows,cols", [(1, 16), (7, 5120), (300, 208), (5, 2048), (6, 4096), (3, 8192), (3, 8208),
-                                       (2, 27648)])
+                                       (4, 13824), (2, 14336), (3, 14352), (2, 27648)])
 def test_quant_rows_i8_bit_exact(dev, dtype, rows, cols):
-    """Widths up to 8192 keep the row in registers (2, 4 or 8 chunks of 16 a lane); wider rows take the two-read
+    """Widths up to 14,336 keep the row in registers (2, 4, 8 or 14 chunks of 16 a lane); wider rows take the two-read
     path. The row's last element carries its maximum in one row, so a dropped tail chunk changes the scale."""
     rng = np.random.default_rng(rows + cols)
     if dtype == "bf16":
@@ -36,7 +36,7 @@ def test_quant_rows_i8_bit_exact(dev, dtype, rows, cols):
     assert (q.cpu().numpy() == wq).all()
 
 
-@pytest.mark.parametrize("cols", [208, 5120, 27648])
+@pytest.mark.parametrize("cols", [208, 5120, 13824, 27648])
 def test_quant_rows_i8_rounding_and_scale_range(dev, cols):
     """Bit-exact at the cases where a quotient computed other than by IEEE division would differ: exact ties
     (k + 0.5 at scale 1 and 0.5, rounding to even), scales on both sides of 2^-100 and 2^100 (the kernel switches its
