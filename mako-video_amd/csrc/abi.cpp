@@ -22,8 +22,11 @@ namespace mh3::host {
 int check_launch()
 {
     const hipError_t e = hipGetLastError();
-    if (e == hipSuccess)
-        return MH3_OK;
+    return e == hipSuccess ? MH3_OK : hip_error(e);
+}
+
+int hip_error(hipError_t e)
+{
     g_last_hip_error = hipGetErrorString(e);
     return MH3_ERR_HIP;
 }

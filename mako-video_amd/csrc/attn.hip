@@ -463,12 +463,13 @@ extern "C" int mh3_flash_attn_sparse_128(const MH3AttnArgs* args, const uint16_t
     constexpr int kStages = kAttnStages;
     const void* kern = reinterpret_cast<const void*>(&attn_sparse_kernel<kStages>);
     const size_t lds = size_t(kStages) * kStageBytes;
-    if (hipFuncSetAttribute(kern, hipFuncAttributeMaxDynamicSharedMemorySize, int(lds)) != hipSuccess)
-        return MH3_ERR_HIP;
+    if (const hipError_t e = host::allow_dynamic_lds(kern, lds); e != hipSuccess)
+        return host::hip_error(e);
     if (kAttnSweep && p.xcd_slices) {
         int per_cu = 0;
-        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kern, int(kAttnThreads), lds) != hipSuccess)
-            return MH3_ERR_HIP;
+        if (const hipError_t e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kern, int(kAttnThreads), lds);
+            e != hipSuccess)
+            return host::hip_error(e);
         // The sweep period: the cube workgroups an XCD holds at once (half or twice that measured slower).
         p.sweep = uint32_t(uint64_t(std::max(per_cu, 1)) * uint32_t(host::cu_count()) / 8u);
     }

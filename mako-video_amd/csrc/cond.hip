@@ -321,9 +321,10 @@ int time_embed_launch(const MH3TimeArgs* args, const float* t, const float* w_in
     if (rc != MH3_OK)
         return rc;
     const size_t lds = size_t(min(args->levels, uint32_t(kLevelGroup))) * args->hidden * 4u;
-    if (lds > 64u * 1024u && host::allow_dynamic_lds(reinterpret_cast<const void*>(&time_mlp_out_kernel), lds) !=
-                                 hipSuccess)
-        return MH3_ERR_HIP;
+    if (lds > 64u * 1024u)
+        if (const hipError_t e = host::allow_dynamic_lds(reinterpret_cast<const void*>(&time_mlp_out_kernel), lds);
+            e != hipSuccess)
+            return host::hip_error(e);
     const uint32_t out_blocks = min(args->out_dim, uint32_t(host::cu_count()));
     hipLaunchKernelGGL(time_mlp_out_kernel, dim3(out_blocks, groups), dim3(kOutWaves * 64u), lds, st, p);
     return host::check_launch();
@@ -382,17 +383,23 @@ float* g_scratch_ptr[kMaxScratchDevices];
 hipError_t g_scratch_rc[kMaxScratchDevices];
 } // namespace
 
-// The current device's copy of `scratch`, or null (with the HIP error recorded) if its address is not available.
-float* scratch_on_current_device()
+// The current device's copy of `scratch`; null if its address is not available, with the HIP error in *rc.
+float* scratch_on_current_device(hipError_t* rc)
 {
     int dev = 0;
-    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxScratchDevices)
+    *rc = hipGetDevice(&dev);
+    if (*rc != hipSuccess)
         return nullptr;
+    if (dev < 0 || dev >= kMaxScratchDevices) {
+        *rc = hipErrorInvalidDevice;
+        return nullptr;
+    }
     std::call_once(g_scratch_once[dev], [dev] {
         void* ptr = nullptr;
         g_scratch_rc[dev] = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
         g_scratch_ptr[dev] = g_scratch_rc[dev] == hipSuccess ? static_cast<float*>(ptr) : nullptr;
     });
+    *rc = g_scratch_rc[dev];
     return g_scratch_ptr[dev];
 }
 
@@ -439,9 +446,10 @@ int mh3_time_embed_noalloc(const MH3TimeArgs* args, const float* t, const float*
     rc = time_embed_aliasing(args, t, w_in, b_in, w_out, b_out, nullptr, 0, temb, cond);
     if (rc != MH3_OK)
         return rc;
-    float* hid = scratch_on_current_device();
+    hipError_t e = hipSuccess;
+    float* hid = scratch_on_current_device(&e);
     if (!hid)
-        return MH3_ERR_HIP;
+        return host::hip_error(e);
     return time_embed_launch(args, t, w_in, b_in, w_out, b_out, hid, temb, cond, static_cast<hipStream_t>(stream));
 }
 

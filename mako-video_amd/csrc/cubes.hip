@@ -581,7 +581,8 @@ int check_topk_args(const MH3CubeArgs* a, const CubeGeo& g)
 // Dynamic LDS above the default limit for `kernel`, once per device.
 int set_lds_limit(const void* kernel, size_t bytes)
 {
-    return host::allow_dynamic_lds(kernel, bytes) == hipSuccess ? MH3_OK : MH3_ERR_HIP;
+    const hipError_t e = host::allow_dynamic_lds(kernel, bytes);
+    return e == hipSuccess ? MH3_OK : host::hip_error(e);
 }
 
 // Bytes from the start of a head-tile array (q or k) to the end of the last row the selector reads: its last head's

@@ -485,9 +485,8 @@ int launch_gemm(const MH3GemmArgs* a, const void* x, const void* w, const float*
         return MH3_ERR_PARAM;
     constexpr int WM = kGemmWM, WN = kGemmWN;
     const void* kernel = reinterpret_cast<const void*>(&gemm_kernel<WM, WN, MODE, EPI>);
-    static const int lds_ok = hipFuncSetAttribute(kernel, hipFuncAttributeMaxDynamicSharedMemorySize, int(kGemmLds));
-    if (lds_ok != hipSuccess)
-        return MH3_ERR_HIP;
+    if (const hipError_t e = host::allow_dynamic_lds(kernel, kGemmLds); e != hipSuccess)
+        return host::hip_error(e);
     const uint32_t mt = (a->m + kBM - 1) / kBM, nt = a->n / kCols;
     const uint64_t tiles = uint64_t(mt) * nt;
     if (tiles >= (uint64_t(1) << 31))

@@ -390,8 +390,8 @@ int launch_heads(HeadsParams p, uint32_t row_begin, uint32_t row_end, hipStream_
     size_t lds = (256u + ((p.rows_per_block + 3u) & ~3u) + 2u * size_t(p.rows_per_block) * p.half) * sizeof(float);
     if (lds < kHeadsLdsFloor)
         lds = kHeadsLdsFloor;
-    if (host::allow_dynamic_lds(reinterpret_cast<const void*>(&heads_kernel), lds) != hipSuccess)
-        return MH3_ERR_HIP;
+    if (const hipError_t e = host::allow_dynamic_lds(reinterpret_cast<const void*>(&heads_kernel), lds); e != hipSuccess)
+        return host::hip_error(e);
     hipLaunchKernelGGL(heads_kernel, dim3(uint32_t(blocks)), dim3(kHeadsThreads), lds, stream, p);
     return host::check_launch();
 }
@@ -448,8 +448,9 @@ extern "C" int mh3_heads_partial_pool(const MH3HeadsArgs* args, const MH3CubeArg
     pp.gt = cb.grid_t, pp.gh = cb.grid_h, pp.gw = cb.grid_w, pp.cw = (cb.grid_w + 3u) / 4u;
     pp.plane = ((cb.grid_h + 3u) / 4u) * pp.cw, pp.cubes = uint32_t(ncubes), pp.grid = grid ? 1u : 0u;
     const size_t lds = (256u + 64u + 2u * 64u * size_t(p.half)) * sizeof(float); // 26 KB at rot 96
-    if (host::allow_dynamic_lds(reinterpret_cast<const void*>(&heads_pool_kernel), lds) != hipSuccess)
-        return MH3_ERR_HIP;
+    if (const hipError_t e = host::allow_dynamic_lds(reinterpret_cast<const void*>(&heads_pool_kernel), lds);
+        e != hipSuccess)
+        return host::hip_error(e);
     hipLaunchKernelGGL(heads_pool_kernel, dim3(uint32_t(ncubes)), dim3(kPoolThreads), lds, st, pp);
     return host::check_launch();
 }

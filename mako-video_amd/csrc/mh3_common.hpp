@@ -156,6 +156,8 @@ namespace mh3::host {
 
 // Records the HIP error of the last launch on this thread; returns MH3_ERR_HIP if there was one.
 int check_launch();
+// Records `e` as this thread's last HIP error (mh3_last_hip_error) and returns MH3_ERR_HIP.
+int hip_error(hipError_t e);
 // The CU count of the current device (cached per device).
 int cu_count();
 // How many blocks of `kernel` fit on one CU with `block` threads and `lds` dynamic LDS bytes (cached by the caller).

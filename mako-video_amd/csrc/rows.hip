@@ -546,15 +546,18 @@ int launch_rows_wave(const RowsParams& p, hipStream_t stream)
     const size_t table = src == kCoefLds ? size_t(p.n_sets) * p.dim * kPlanes<OP> * sizeof(float) : 0;
     const size_t floor = OP == kGateAddMod ? kOrderLdsFloor : kWaveLdsFloor;
     const size_t lds = table > floor ? table : floor;
-    if (host::allow_dynamic_lds(k, lds) != hipSuccess)
-        return MH3_ERR_HIP;
+    if (const hipError_t e = host::allow_dynamic_lds(k, lds); e != hipSuccess)
+        return host::hip_error(e);
     // A row a wave; a persistent grid (rows_per_wave 0) measured slower.
     RowsParams arg = p;
     arg.rows_per_wave = 1;
     const uint64_t blocks = (uint64_t(p.rows) + waves - 1) / waves;
     void* args[] = {&arg};
-    if (hipLaunchKernel(k, dim3(uint32_t(blocks)), dim3(threads), args, lds, stream) != hipSuccess)
-        return host::check_launch() == MH3_OK ? MH3_ERR_HIP : MH3_ERR_HIP;
+    if (const hipError_t e = hipLaunchKernel(k, dim3(uint32_t(blocks)), dim3(threads), args, lds, stream);
+        e != hipSuccess) {
+        (void)hipGetLastError(); // the launch's error is reported here; clear it for the next call
+        return host::hip_error(e);
+    }
     return host::check_launch();
 }
 
@@ -589,8 +592,11 @@ int launch_rows_dt(const RowsParams& p, hipStream_t stream)
         blocks = cap;
     RowsParams arg = p;
     void* args[] = {&arg};
-    if (hipLaunchKernel(k, dim3(uint32_t(blocks)), dim3(threads), args, lds, stream) != hipSuccess)
-        return host::check_launch() == MH3_OK ? MH3_ERR_HIP : MH3_ERR_HIP;
+    if (const hipError_t e = hipLaunchKernel(k, dim3(uint32_t(blocks)), dim3(threads), args, lds, stream);
+        e != hipSuccess) {
+        (void)hipGetLastError(); // the launch's error is reported here; clear it for the next call
+        return host::hip_error(e);
+    }
     return host::check_launch();
 }
 

@@ -366,6 +366,21 @@ def test_time_embed_refuses_overlapping_outputs():
     assert mh.lib.mh3_time_embed_noalloc(C.byref(a), t, w_in, None, w_out, None, w_in, None, None) == mh.ERR_PARAM
 
 
+def test_hip_error_text_is_recorded():
+    """A valid call that fails in HIP itself returns MH3_ERR_HIP with HIP's own message in mh3_last_hip_error. Without
+    a GPU the variant that allocates nothing fails at the device lookup for its scratch array, after every check of
+    its arguments and before any launch."""
+    import torch
+    if torch.cuda.device_count() > 0:
+        pytest.skip("a visible GPU would take the call past the device lookup to a launch on these stand-in pointers")
+    a = time_args()
+    t, w_in, w_out = C.c_void_p(0x1000), C.c_void_p(0x100000), C.c_void_p(0x1000000)
+    temb, cond = C.c_void_p(0x20000000), C.c_void_p(0x30000000)
+    assert mh.lib.mh3_time_embed_noalloc(C.byref(a), t, w_in, None, w_out, None, temb, cond, None) == mh.ERR_HIP
+    text = mh.lib.mh3_last_hip_error().decode()
+    assert text and text != "no error", text
+
+
 def test_adaln_and_curve_refuse_overlapping_outputs():
     g = mh.GemmArgs()
     g.m, g.n, g.k = 3, 96768, 2688
