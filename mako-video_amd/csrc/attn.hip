@@ -32,7 +32,10 @@
 //   holds at once, rank the tile's place in its XCD's sequence), wrapping round. The XCD's resident tiles then sweep
 //   the key cubes together, so a K/V tile one of them fetches is still in L2 when the others that selected it reach
 //   it: the L2 hit rate at 768p went from 11-15% to 29-35% and the L2 misses fell by a fifth, for 2.4% less time
-//   (the DMA latency of each tile also bounds the kernel).
+//   (the DMA latency of each tile also bounds the kernel). The first 4 S tiles of an XCD walk from the start of their
+//   lists instead: they start in step (the whole first round at once, and the next rounds nearly so), and tiles in
+//   step share their K/V tiles by walking together. 5 heads at 768p: 7.37-7.40 ms against 7.96-7.98 rotated from
+//   the first tile and 7.73-7.75 never rotated; 40 heads: 54.0-54.4 against 54.2-54.6 (68.1 never rotated).
 // - Softmax in base 2 with the scale folded into the exponent. A query's running maximum moves only when a tile
 //   raises it by more than 8 (in log2 units): P stays below 2^8, and most tiles skip the rescale of O.
 #include "mh3_common.hpp"
@@ -48,6 +51,7 @@ typedef float floatx16 __attribute__((ext_vector_type(16)));
 constexpr uint32_t kAttnThreads = 128;
 constexpr bool kAttnXcd = true;   // map each XCD to a contiguous eighth of every head's query cubes
 constexpr bool kAttnSweep = true; // rotate each cube tile's pass list so an XCD's resident tiles sweep the keys together
+constexpr uint32_t kAttnInStep = 4; // rounds of an XCD's cube tiles that walk their lists unrotated (1, 2, 8: slower)
 constexpr int kAttnStages = 1;    // K/V stages in LDS (2 overlaps a tile's loads with the previous tile's MFMAs but
                                   // halves the workgroups a CU holds; one stage and two waves a SIMD measured faster)
 constexpr uint32_t kNoTile = 0xffffffffu;
@@ -209,8 +213,10 @@ __global__ __launch_bounds__(kAttnThreads, STAGES == 2 ? 1 : 2) void attn_sparse
     // The pass list is walked from position rot, wrapping round: a workgroup that starts when the XCD's resident ones
     // are a fraction f into their lists starts a fraction f into its own, so the resident tiles sweep the key cubes
     // together and a K/V tile fetched for one is still in that XCD's L2 when the others that selected it reach it.
+    // The first kAttnInStep rounds of an XCD's sequence start (nearly) together and walk from position 0 in step.
     // The order only changes the softmax's summation order.
-    const uint32_t rot = (!dense_q && p.sweep) ? uint32_t(uint64_t(rank % p.sweep) * n_sel / p.sweep) : 0u;
+    const bool rotated = !dense_q && p.sweep && rank >= kAttnInStep * p.sweep;
+    const uint32_t rot = rotated ? uint32_t(uint64_t(rank % p.sweep) * n_sel / p.sweep) : 0u;
     auto key_tile = [&](uint32_t e) -> uint32_t {
         if (e >= n_sel)
             return e - n_sel;
