@@ -180,8 +180,12 @@ __global__ __launch_bounds__(kAttnThreads, STAGES == 2 ? 1 : 2) void attn_sparse
     {
         const uint32_t b = blockIdx.x, dense_blocks = p.nd * p.heads;
         if (b < dense_blocks) {
-            h = b / p.nd;
-            qt = b - h * p.nd;
+            // With the XCD slices, XCD x takes the dense tiles of whole heads (the x-th eighth of them in order), so
+            // a head's dense tiles, which walk the same keys in the same order, share each K/V tile in one L2 (5
+            // heads at 768p: 7.29-7.32 ms against 7.47-7.48 with a head's tiles dealt over the 8 XCDs).
+            const uint32_t l = p.xcd_slices ? (b % 8u) * (dense_blocks / 8u) + b / 8u : b;
+            h = l / p.nd;
+            qt = l - h * p.nd;
         } else {
             const uint32_t r = b - dense_blocks;
             if (p.xcd_slices) {
