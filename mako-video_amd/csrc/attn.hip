@@ -51,7 +51,8 @@ typedef float floatx16 __attribute__((ext_vector_type(16)));
 constexpr uint32_t kAttnThreads = 128;
 constexpr bool kAttnXcd = true;   // map each XCD to a contiguous eighth of every head's query cubes
 constexpr bool kAttnSweep = true; // rotate each cube tile's pass list so an XCD's resident tiles sweep the keys together
-constexpr uint32_t kAttnInStep = 4; // rounds of an XCD's cube tiles that walk their lists unrotated (1, 2, 8: slower)
+constexpr uint32_t kAttnInStep = 4; // rounds of an XCD's cube tiles that walk their lists unrotated (1, 2, 8: slower;
+                                    // 3, 5, 6: within 1%)
 constexpr int kAttnStages = 1;    // K/V stages in LDS (2 overlaps a tile's loads with the previous tile's MFMAs but
                                   // halves the workgroups a CU holds; one stage and two waves a SIMD measured faster)
 constexpr uint32_t kNoTile = 0xffffffffu;
