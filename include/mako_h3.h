@@ -208,7 +208,8 @@ int mh3_cube_map(const MH3CubeMapArgs* args, int32_t* map, int32_t* counts, mh3_
  * cube_pool, cube_select and flash_attn_sparse_128 take as MH3_CUBES_GATHERED (cube c's 64 slots at rows 64 c ..,
  * then the dense rows). cos_t and sin_t are float [model_rows][rot / 2] (NULL when rot is 0); q_w and k_w are
  * float [128] shared by the heads (NULL: all 1). The outputs may overwrite their own inputs in place (map NULL, each
- * output at its input's position); otherwise they may not overlap qkv. */
+ * output at its input's position); otherwise they may not overlap qkv. No output may overlap q_w, k_w, cos_t, sin_t
+ * or map (MH3_ERR_PARAM). */
 typedef struct MH3HeadsArgs {
     uint32_t rows;       /* output rows */
     uint32_t model_rows; /* rows of qkv, cos_t and sin_t */
@@ -232,7 +233,8 @@ int mh3_heads_partial(const MH3HeadsArgs* args, const uint16_t* qkv, const float
  *   MH3_CUBES_GRID: no map (MH3_ERR_PARAM), output rows in the model's order, the grid's tokens at rows
  *                   row0 .. row0 + T H W - 1 within args->rows.
  * (MH3_ERR_SHAPE when the rows do not fit.) Rows outside them (the dense rows) get heads_partial alone. qc and kc are
- * float [heads][cubes][128], 16-byte aligned. */
+ * float [heads][cubes][128], 16-byte aligned. qc, kc and counts may not overlap each other, any input, or q, k and v
+ * (each taken as the span from its start to the last head's last row), else MH3_ERR_PARAM. */
 int mh3_heads_partial_pool(const MH3HeadsArgs* args, const MH3CubeArgs* cubes, const uint16_t* qkv, const float* q_w,
                            const float* k_w, const float* cos_t, const float* sin_t, const int32_t* map, uint16_t* q,
                            uint16_t* k, uint16_t* v, float* qc, float* kc, int32_t* counts, mh3_stream_t stream);
@@ -248,8 +250,8 @@ int mh3_heads_partial_pool(const MH3HeadsArgs* args, const MH3CubeArgs* cubes, c
  * Output rows are written where the queries lie: the grid layout writes the token rows and the dense rows (the
  * reference's write-back to the model's rows, with no gather or scatter pass); the gathered layout also writes a
  * cube's padding slots, as zeros. idx entries outside [0, cubes) are skipped; cnt is clamped to [0, out_stride].
- * out may not be q, k or v, nor overlap k or v, each taken as the span from its start to the last head's last row
- * read (MH3_ERR_PARAM). cubes.k and cubes.local are not used. */
+ * out may not overlap q, k, v, idx or cnt, q, k, v and out each taken as the span from its start to the last head's
+ * last row read or written (MH3_ERR_PARAM). cubes.k and cubes.local are not used. */
 typedef struct MH3AttnArgs {
     MH3CubeArgs cubes;   /* heads, head_dim (128), grid, layout, row0, head_stride, row_stride; out_stride: idx's
                             int32 entries per (head, query cube) */
@@ -365,7 +367,9 @@ int mh3_time_embed(const MH3TimeArgs* args, const float* t, const float* w_in, c
  * 3 levels of 5376 use 16,128), else MH3_ERR_UNSUPPORTED. Every call on a GPU shares that GPU's array, so calls that
  * overlap in time on one GPU (on different streams, or from several host threads) race; calls on one stream, or
  * ordered by events, do not. Each call writes the part of the array it reads before reading it. Same results as
- * mh3_time_embed, bit for bit. MH3_ERR_HIP if the array's address on the current device cannot be obtained. */
+ * mh3_time_embed, bit for bit. The call uses the current device's array, so a non-NULL stream must belong to the
+ * current device (MH3_ERR_PARAM otherwise). MH3_ERR_HIP if the array's address on the current device cannot be
+ * obtained. */
 int mh3_time_embed_noalloc(const MH3TimeArgs* args, const float* t, const float* w_in, const float* b_in,
                            const float* w_out, const float* b_out, float* temb, uint16_t* cond, mh3_stream_t stream);
 /* A block's AdaLN projection (and the final layer's, n = 2 D): mod[u][r] = w[r] . cond[u] + bias[r] in float

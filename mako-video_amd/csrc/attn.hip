@@ -454,13 +454,22 @@ extern "C" int mh3_flash_attn_sparse_128(const MH3AttnArgs* args, const uint16_t
     const uint64_t video = c.layout == MH3_CUBES_GRID ? uint64_t(p.gt) * p.gh * p.gw : 64ull * cubes;
     if (args->n_dense && args->dense_row0 < c.row0 + video && c.row0 < args->dense_row0 + args->n_dense)
         return MH3_ERR_PARAM;
-    // Nor may out overlap k or v, which other workgroups are still reading: each array spans from its start to the
-    // last head's last row (video or dense) that the call reads or writes.
+    // Nor may out overlap q, k, v or the pass lists, which other workgroups are still reading (each starts by reading
+    // its own query tile and list): q, k, v and out each span from the array's start to the last head's last row
+    // (video or dense) that the call reads or writes.
     const uint64_t last_row =
         std::max<uint64_t>(c.row0 + video, args->n_dense ? args->dense_row0 + args->n_dense : 0u) - 1u;
     const uint64_t span = ((uint64_t(c.heads) - 1u) * c.head_stride + last_row * c.row_stride + 128u) * 2u;
-    if (host::overlaps(out, span, k, span) || host::overlaps(out, span, v, span))
-        return MH3_ERR_PARAM;
+    {
+        const host::Span in[] = {{q, span},
+                                 {k, span},
+                                 {v, span},
+                                 {idx, uint64_t(c.heads) * cubes * c.out_stride * 4u},
+                                 {cnt, uint64_t(c.heads) * cubes * 4u}};
+        const host::Span o[] = {{out, span}};
+        if (host::any_overlap(in, o))
+            return MH3_ERR_PARAM;
+    }
     p.q = q, p.k = k, p.v = v, p.out = out, p.idx = idx, p.cnt = cnt;
     p.row0 = c.row0, p.dense_row0 = args->dense_row0, p.head_stride = c.head_stride, p.row_stride = c.row_stride;
     p.plane = uint32_t(plane), p.cubes = uint32_t(cubes), p.heads = c.heads, p.n_dense = args->n_dense;

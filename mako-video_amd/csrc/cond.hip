@@ -450,6 +450,17 @@ int mh3_time_embed_noalloc(const MH3TimeArgs* args, const float* t, const float*
     float* hid = scratch_on_current_device(&e);
     if (!hid)
         return host::hip_error(e);
+    if (stream) {
+        // The array's address is the current device's copy: a stream of another GPU would run the kernels there
+        // against this GPU's address.
+        int cur = 0;
+        hipDevice_t sdev = 0;
+        if ((e = hipGetDevice(&cur)) != hipSuccess ||
+            (e = hipStreamGetDevice(static_cast<hipStream_t>(stream), &sdev)) != hipSuccess)
+            return host::hip_error(e);
+        if (int(sdev) != cur)
+            return MH3_ERR_PARAM;
+    }
     return time_embed_launch(args, t, w_in, b_in, w_out, b_out, hid, temb, cond, static_cast<hipStream_t>(stream));
 }
 

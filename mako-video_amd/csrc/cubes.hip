@@ -594,26 +594,6 @@ uint64_t tile_span_bytes(const CubeGeo& g)
     return ((uint64_t(g.heads) - 1u) * g.head_stride + last_row * g.row_stride + 128u) * 2u;
 }
 
-// Whether any of the outputs (pointer, bytes; null pointers skipped) overlaps an input or another output: a launch
-// would read what its other workgroups are writing.
-struct Span {
-    const void* p;
-    uint64_t n;
-};
-template <size_t NI, size_t NO>
-bool any_overlap(const Span (&in)[NI], const Span (&out)[NO])
-{
-    for (size_t i = 0; i < NO; ++i) {
-        for (size_t j = 0; j < NI; ++j)
-            if (out[i].p && in[j].p && host::overlaps(out[i].p, out[i].n, in[j].p, in[j].n))
-                return true;
-        for (size_t j = i + 1; j < NO; ++j)
-            if (out[i].p && out[j].p && host::overlaps(out[i].p, out[i].n, out[j].p, out[j].n))
-                return true;
-    }
-    return false;
-}
-
 } // namespace
 
 extern "C" {
@@ -660,9 +640,9 @@ int mh3_cube_pool(const MH3CubeArgs* args, const uint16_t* q, const uint16_t* k,
         !host::aligned16(qc) || !host::aligned16(kc))
         return MH3_ERR_ALIGN;
     const uint64_t pooled = uint64_t(g.heads) * g.cubes * 128u * 4u;
-    const Span in[] = {{q, tile_span_bytes(g)}, {k, tile_span_bytes(g)}};
-    const Span out[] = {{qc, pooled}, {kc, pooled}, {counts, uint64_t(g.cubes) * 4u}};
-    if (any_overlap(in, out))
+    const host::Span in[] = {{q, tile_span_bytes(g)}, {k, tile_span_bytes(g)}};
+    const host::Span out[] = {{qc, pooled}, {kc, pooled}, {counts, uint64_t(g.cubes) * 4u}};
+    if (host::any_overlap(in, out))
         return MH3_ERR_PARAM;
     const uint32_t items = g.heads * g.cubes;
     hipLaunchKernelGGL(cube_pool_kernel, dim3((items + 3u) / 4u), dim3(256), 0, static_cast<hipStream_t>(stream), g,
@@ -681,9 +661,9 @@ int mh3_cube_scores(const MH3CubeArgs* args, const float* qc, const float* kc, f
     if (!host::aligned16(qc) || !host::aligned16(kc))
         return MH3_ERR_ALIGN;
     const uint64_t pooled = uint64_t(g.heads) * g.cubes * 128u * 4u;
-    const Span in[] = {{qc, pooled}, {kc, pooled}};
-    const Span out[] = {{s, uint64_t(g.heads) * g.cubes * g.cubes * 4u}};
-    if (any_overlap(in, out))
+    const host::Span in[] = {{qc, pooled}, {kc, pooled}};
+    const host::Span out[] = {{s, uint64_t(g.heads) * g.cubes * g.cubes * 4u}};
+    if (host::any_overlap(in, out))
         return MH3_ERR_PARAM;
     hipLaunchKernelGGL(cube_scores_kernel, dim3((g.cubes + 15u) / 16u, g.heads), dim3(256), 0,
                        static_cast<hipStream_t>(stream), g, qc, kc, s);
@@ -701,10 +681,10 @@ int mh3_cube_topk(const MH3CubeArgs* args, const float* s, int32_t* idx, int32_t
     if (!s || !idx || !cnt)
         return MH3_ERR_POINTER;
     {
-        const Span in[] = {{s, uint64_t(g.heads) * g.cubes * g.cubes * 4u}};
-        const Span out[] = {{idx, uint64_t(g.heads) * g.cubes * args->out_stride * 4u},
+        const host::Span in[] = {{s, uint64_t(g.heads) * g.cubes * g.cubes * 4u}};
+        const host::Span out[] = {{idx, uint64_t(g.heads) * g.cubes * args->out_stride * 4u},
                             {cnt, uint64_t(g.heads) * g.cubes * 4u}};
-        if (any_overlap(in, out))
+        if (host::any_overlap(in, out))
             return MH3_ERR_PARAM;
     }
     const uint32_t items = g.heads * g.cubes;
@@ -739,10 +719,10 @@ int mh3_cube_select(const MH3CubeArgs* args, const float* qc, const float* kc, i
         return MH3_ERR_ALIGN;
     {
         const uint64_t pooled = uint64_t(g.heads) * g.cubes * 128u * 4u;
-        const Span in[] = {{qc, pooled}, {kc, pooled}};
-        const Span out[] = {{idx, uint64_t(g.heads) * g.cubes * args->out_stride * 4u},
+        const host::Span in[] = {{qc, pooled}, {kc, pooled}};
+        const host::Span out[] = {{idx, uint64_t(g.heads) * g.cubes * args->out_stride * 4u},
                             {cnt, uint64_t(g.heads) * g.cubes * 4u}};
-        if (any_overlap(in, out))
+        if (host::any_overlap(in, out))
             return MH3_ERR_PARAM;
     }
     if (g.cubes > kSelectMaxCubes)

@@ -220,8 +220,10 @@ heads_pool_kernel(HeadsPoolParams pp)
     const uint64_t orow0 = pp.row0 + uint64_t(c) * 64u;
     float* wt = lds;
     int32_t* srcs = reinterpret_cast<int32_t*>(lds + 256);
+    // The cos and sin tables, at least 8 floats each: head_vector reads 8 values of them on every lane, rotating or
+    // not, so with no rotary (half 0) they still lie inside the allocation.
     float* ct = lds + 256 + 64;
-    float* st = ct + 64u * p.half;
+    float* st = ct + max(64u * p.half, 8u);
     stage_weights(wt, p.qw, p.kw, tid, kPoolThreads);
     const uint32_t cube_t = c / pp.plane, rem = c - cube_t * pp.plane, cube_y = rem / pp.cw, cube_x = rem - cube_y * pp.cw;
     // Slot l's model row (-1: none). Gathered: through the map (or l's own output row); grid: the token at the slot's
@@ -366,6 +368,15 @@ int heads_setup(const MH3HeadsArgs* args, const uint16_t* qkv, const float* q_w,
         if (!in_place)
             return MH3_ERR_PARAM;
     }
+    // Nor may an output overlap the norm weights, the rotary tables or the map.
+    const uint64_t tab = a.rot ? uint64_t(a.model_rows) * (a.rot / 2u) * 4u : 0u;
+    const host::Span small_in[] = {
+        {q_w, 512u}, {k_w, 512u}, {cos_t, tab}, {sin_t, tab}, {map, map ? uint64_t(a.rows) * 4u : 0u}};
+    for (int t = 0; t < 3; ++t) {
+        const host::Span o[] = {{outs[t], out_bytes}};
+        if (host::any_overlap(small_in, o))
+            return MH3_ERR_PARAM;
+    }
     p = HeadsParams{};
     p.qkv = qkv, p.qw = q_w, p.kw = k_w, p.cos_t = cos_t, p.sin_t = sin_t, p.map = map;
     p.out[0] = q, p.out[1] = k, p.out[2] = v;
@@ -436,6 +447,21 @@ extern "C" int mh3_heads_partial_pool(const MH3HeadsArgs* args, const MH3CubeArg
         return MH3_ERR_POINTER;
     if (!host::aligned16(qc) || !host::aligned16(kc))
         return MH3_ERR_ALIGN;
+    {
+        // The pooled outputs may not overlap any input, the head tiles this call writes, or each other: one
+        // workgroup a cube writes them while the others still read qkv and write their own rows.
+        const uint64_t qkv_bytes = ((uint64_t(args->model_rows) - 1) * args->qkv_stride + 3ull * args->heads * 128u) * 2u;
+        const uint64_t out_bytes = ((uint64_t(args->heads) - 1) * args->out_head_stride +
+                                    (uint64_t(args->rows) - 1) * args->out_row_stride + 128u) * 2u;
+        const uint64_t tab = args->rot ? uint64_t(args->model_rows) * (args->rot / 2u) * 4u : 0u;
+        const uint64_t pooled = ncubes * args->heads * 128u * 4u;
+        const host::Span in[] = {{qkv, qkv_bytes}, {q, out_bytes},   {k, out_bytes},
+                                 {v, out_bytes},   {q_w, 512u},      {k_w, 512u},
+                                 {cos_t, tab},     {sin_t, tab},     {map, map ? uint64_t(args->rows) * 4u : 0u}};
+        const host::Span out[] = {{qc, pooled}, {kc, pooled}, {counts, ncubes * 4u}};
+        if (host::any_overlap(in, out))
+            return MH3_ERR_PARAM;
+    }
     hipStream_t st = static_cast<hipStream_t>(stream);
     const uint32_t video0 = uint32_t(cb.row0), video1 = uint32_t(cb.row0 + span);
     int r = launch_heads(p, 0u, video0, st); // rows before the cubes, and after them (the dense rows)
@@ -447,7 +473,7 @@ extern "C" int mh3_heads_partial_pool(const MH3HeadsArgs* args, const MH3CubeArg
     pp.hp = p, pp.qc = qc, pp.kc = kc, pp.counts = counts, pp.row0 = cb.row0;
     pp.gt = cb.grid_t, pp.gh = cb.grid_h, pp.gw = cb.grid_w, pp.cw = (cb.grid_w + 3u) / 4u;
     pp.plane = ((cb.grid_h + 3u) / 4u) * pp.cw, pp.cubes = uint32_t(ncubes), pp.grid = grid ? 1u : 0u;
-    const size_t lds = (256u + 64u + 2u * 64u * size_t(p.half)) * sizeof(float); // 26 KB at rot 96
+    const size_t lds = (256u + 64u + 2u * std::max(64u * p.half, 8u)) * sizeof(float); // 26 KB at rot 96
     if (const hipError_t e = host::allow_dynamic_lds(reinterpret_cast<const void*>(&heads_pool_kernel), lds);
         e != hipSuccess)
         return host::hip_error(e);

@@ -173,4 +173,24 @@ inline bool overlaps(const void* a, uint64_t an, const void* b, uint64_t bn)
 // Lets `kernel` take `bytes` of dynamic LDS on the current device (hipFuncSetAttribute, once per kernel and device).
 hipError_t allow_dynamic_lds(const void* kernel, size_t bytes);
 
+// Whether any of the outputs (pointer, bytes; null pointers skipped) overlaps an input or another output: a launch
+// would read what its other workgroups are writing.
+struct Span {
+    const void* p;
+    uint64_t n;
+};
+template <size_t NI, size_t NO>
+bool any_overlap(const Span (&in)[NI], const Span (&out)[NO])
+{
+    for (size_t i = 0; i < NO; ++i) {
+        for (size_t j = 0; j < NI; ++j)
+            if (out[i].p && in[j].p && overlaps(out[i].p, out[i].n, in[j].p, in[j].n))
+                return true;
+        for (size_t j = i + 1; j < NO; ++j)
+            if (out[i].p && out[j].p && overlaps(out[i].p, out[i].n, out[j].p, out[j].n))
+                return true;
+    }
+    return false;
+}
+
 } // namespace mh3::host

@@ -250,6 +250,21 @@ def test_flash_attn_sparse_refuses_an_output_over_k_or_v():
     assert mh.lib.mh3_flash_attn_sparse_128(C.byref(a), q, k, v, FAKE, FAKE, before_k, None) == mh.ERR_PARAM
 
 
+def test_flash_attn_sparse_refuses_an_output_over_q_or_the_pass_lists():
+    """out may not partially overlap q (each workgroup reads its own query tile when it starts) nor the pass lists."""
+    a = attn_args()
+    q, k, v = C.c_void_p(0x100000), C.c_void_p(0x200000), C.c_void_p(0x300000)
+    idx, cnt = C.c_void_p(0x400000), C.c_void_p(0x500000)
+    span = (a.cubes.head_stride + 807 * a.cubes.row_stride + 128) * 2
+    inside_q = C.c_void_p(0x100000 + 256)                   # out one row after q's start
+    assert mh.lib.mh3_flash_attn_sparse_128(C.byref(a), q, k, v, idx, cnt, inside_q, None) == mh.ERR_PARAM
+    lists = 2 * 12 * a.cubes.out_stride * 4                 # heads x cubes x out_stride int32
+    over_idx = C.c_void_p(0x400000 + lists - 16 - span + 16)  # out's last bytes on idx's last entries
+    assert mh.lib.mh3_flash_attn_sparse_128(C.byref(a), q, k, v, idx, cnt, over_idx, None) == mh.ERR_PARAM
+    over_cnt = C.c_void_p(0x500000 + 64)
+    assert mh.lib.mh3_flash_attn_sparse_128(C.byref(a), q, k, v, idx, cnt, over_cnt, None) == mh.ERR_PARAM
+
+
 def test_quant_refuses_overlapping_outputs():
     a = mh.QuantArgs()
     a.rows, a.cols, a.dtype = 64, 128, mh.BF16             # w 16 KiB, q 8 KiB, scale 256 B
@@ -426,7 +441,7 @@ def test_heads_partial_pool_validation():
 
     base = 0x1000  # aligned; never dereferenced
 
-    def call(cube_kw=None, qc=base, hk=None, **ptrs):
+    def call(cube_kw=None, qc=base + 2**38, hk=None, counts=None, **ptrs):
         ca = mh.cube_args(heads, grid, layout=mh.CUBES_GATHERED, head_stride=rows * 128)
         for key, val in (cube_kw or {}).items():
             setattr(ca, key, val)
@@ -436,7 +451,7 @@ def test_heads_partial_pool_validation():
         p = dict(qkv=base, cos=base, q=base + 2**34, k=base + 2**35, kc=base + 2**36)
         p.update(ptrs)
         return mh.lib.mh3_heads_partial_pool(C.byref(a), C.byref(ca), p["qkv"], None, None, p["cos"], p["cos"],
-                                             p.get("map"), p["q"], p["k"], None, qc, p["kc"], None, None)
+                                             p.get("map"), p["q"], p["k"], None, qc, p["kc"], counts, None)
 
     assert mh.lib.mh3_heads_partial_pool(None, None, *([None] * 13)) == mh.ERR_POINTER
     assert call({"layout": 2}) == mh.ERR_PARAM
@@ -451,3 +466,14 @@ def test_heads_partial_pool_validation():
     assert call(qc=None) == mh.ERR_POINTER
     assert call(qc=base + 4) == mh.ERR_ALIGN
     assert call(kc=base + 2**36 + 8) == mh.ERR_ALIGN
+    # The pooled outputs may not overlap an input, the head tiles the call writes, or each other.
+    pooled = heads * cubes * 128 * 4
+    assert call(qc=base) == mh.ERR_PARAM                                 # qc on qkv
+    assert call(qc=base + 2**34 + 4096) == mh.ERR_PARAM                  # qc inside the q tiles
+    assert call(kc=base + 2**38 + pooled - 16) == mh.ERR_PARAM          # kc runs into qc's last float4
+    assert call(counts=base + 2**36 + 64) == mh.ERR_PARAM                # counts inside kc
+    assert call(counts=base + 2**37, map=base + 2**37) == mh.ERR_PARAM   # counts on the map
+    # heads_partial's outputs may not overlap the rotary tables or the map.
+    assert call(q=base) == mh.ERR_PARAM                                  # q on qkv, not in place
+    assert call(cos=base + 2**35 + 1024) == mh.ERR_PARAM                 # the cos table inside k
+    assert call(map=base + 2**34 + 256) == mh.ERR_PARAM                  # the map inside q
