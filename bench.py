@@ -125,8 +125,23 @@ def bench_block_order(mh, dev, steps, warmup):
         mh.rms_mod_rows(x, w, shift, scale, out=h)
     ms2, _ = time_launches(two, steps, warmup)
     nbytes = ROWS * DIM * 8
-    return {"ms": ms, "bytes": nbytes, "GBs": nbytes / ms / 1e6, "frac": nbytes / ms / 1e6 / HBM_PEAK_GBS,
-            "two_kernel_ms": ms2, "two_kernel_bytes": ROWS * DIM * 10, "shape": [ROWS, DIM]}
+    res = {"ms": ms, "bytes": nbytes, "GBs": nbytes / ms / 1e6, "frac": nbytes / ms / 1e6 / HBM_PEAK_GBS,
+           "two_kernel_ms": ms2, "two_kernel_bytes": ROWS * DIM * 10, "shape": [ROWS, DIM]}
+    del x, y, h
+    torch.cuda.empty_cache()
+    # The reference's float residual stream: x float, y (the out projection's bf16 output) and h (fc1's bf16 input)
+    # bf16; 12 bytes an element (read x 4 and y 2, write x 4 and h 2). And the modulated norm alone from the float x
+    # to the bf16 GEMM row (6 bytes an element).
+    xf = torch.randn((ROWS, DIM), generator=g, device=dev)
+    yb = torch.randn((ROWS, DIM), generator=g, device=dev).to(torch.bfloat16)
+    hb = torch.empty((ROWS, DIM), dtype=torch.bfloat16, device=dev)
+    fms, _ = time_launches(lambda: mh.gate_add_rms_mod_rows(xf, yb, gate, w, shift, scale, h=hb), steps, warmup)
+    rms, _ = time_launches(lambda: mh.rms_mod_rows(xf, w, shift, scale, out=hb), steps, warmup)
+    fb, rb = ROWS * DIM * 12, ROWS * DIM * 6
+    res["float_stream"] = {"ms": fms, "bytes": fb, "GBs": fb / fms / 1e6, "frac": fb / fms / 1e6 / HBM_PEAK_GBS,
+                           "rms_mod_f32_to_bf16": {"ms": rms, "bytes": rb, "GBs": rb / rms / 1e6,
+                                                   "frac": rb / rms / 1e6 / HBM_PEAK_GBS}}
+    return res
 
 
 def bench_copy(dev, steps, warmup):
@@ -181,10 +196,65 @@ def bench_stream(dev, steps, warmup):
         res[name] = {"ms": ms, "GBs": moved * nbytes / ms / 1e6, "frac": moved * nbytes / ms / 1e6 / HBM_PEAK_GBS,
                      "unroll": unroll, "grid": "flat" if per_cu == 0 else f"{per_cu} workgroups a CU",
                      "access": "buffer" if kind >= 4 else "global"}
+    # The fused row op's own shape with no arithmetic (one 5120-wide row a wave, all of a's row then all of b's, an
+    # 8-wave workgroup of 8 rows), at one, two and three workgroups a CU (the dynamic LDS sets it; the fused op runs
+    # two): the ceiling for that access pattern.
+    lib.mh3_probe_rows.argtypes = [C.c_void_p, C.c_void_p, C.c_void_p, C.c_uint32, C.c_uint32, C.c_uint32,
+                                   C.c_void_p]
+    rows_res = {}
+    for per_cu, lds in ((1, 81 * 1024), (2, 54 * 1024), (3, 41 * 1024)):
+        def run_rows():
+            rc = lib.mh3_probe_rows(a.data_ptr(), b.data_ptr(), c.data_ptr(), ROWS, DIM // 8, lds, stream)
+            if rc != 0:
+                raise RuntimeError(f"mh3_probe_rows returned {rc}")
+        ms, _ = time_launches(run_rows, max(5, steps // 2), 2)
+        rows_res[f"{per_cu}_workgroups_a_cu"] = {"ms": ms, "GBs": 3 * nbytes / ms / 1e6,
+                                                 "frac": 3 * nbytes / ms / 1e6 / HBM_PEAK_GBS}
+    best = max(rows_res.values(), key=lambda r: r["GBs"])
+    res["rows_r2w1"] = {**rows_res, "GBs": best["GBs"], "frac": best["frac"], "ms": best["ms"],
+                        "shape": "one row a wave, 10 vectors a lane of two inputs, one output, no arithmetic"}
     clk = khz.value * 1e3
     res["device"] = {"cus": cus.value, "peak_clock_mhz": khz.value / 1e3,
                      "bf16_mfma_peak_tflops": cus.value * clk * 4096 / 1e12,
                      "int8_mfma_peak_tops": cus.value * clk * 8192 / 1e12}
+    return res
+
+
+def bench_mfma_ceiling(dev, steps, warmup):
+    """The matrix cores' sustained rate on this GPU under its power limit: a register-only loop of
+    v_mfma_f32_32x32x16_bf16 (and of v_mfma_i32_32x32x32_i8), 8 independent accumulators a wave, two waves a SIMD,
+    one 8-wave workgroup a CU, the operands cycling through 8 fragments of random bits, ~40 ms a launch (the power
+    limit acts within it). The clock each workgroup ran at is its shader clock counter's advance over the 100 MHz
+    real-time counter's (s_memtime, s_memrealtime): the median over workgroups is reported."""
+    import ctypes as C
+
+    lib = C.CDLL(str(REPO / "mako-video_amd" / "lib" / "libmh3_stream_probe.so"))
+    lib.mh3_probe_mfma.argtypes = [C.c_int, C.c_uint32, C.c_uint32, C.c_void_p, C.c_void_p, C.c_void_p]
+    lib.mh3_probe_device.argtypes = [C.POINTER(C.c_int), C.POINTER(C.c_int)]
+    cus, khz = C.c_int(0), C.c_int(0)
+    if lib.mh3_probe_device(C.byref(cus), C.byref(khz)) != 0:
+        raise RuntimeError("mh3_probe_device failed")
+    blocks = cus.value
+    out = torch.empty(blocks * 512, dtype=torch.float32, device=dev)
+    clocks = torch.zeros(2 * blocks, dtype=torch.int64, device=dev)
+    stream = torch.cuda.current_stream().cuda_stream
+    res = {}
+    for kind, name, flops_per, peak in ((0, "bf16", 2 * 32 * 32 * 16, BF16_PEAK_TFLOPS),
+                                        (1, "int8", 2 * 32 * 32 * 32, INT8_PEAK_TOPS)):
+        iters = 40000 if kind == 0 else 20000  # ~40 ms a launch at 2 GHz
+
+        def run():
+            rc = lib.mh3_probe_mfma(kind, blocks, iters, out.data_ptr(), clocks.data_ptr(), stream)
+            if rc != 0:
+                raise RuntimeError(f"mh3_probe_mfma returned {rc}")
+        ms, _ = time_launches(run, max(3, steps // 4), max(1, warmup // 2))
+        ck = clocks.view(blocks, 2).double().cpu()
+        ghz = float((ck[:, 0] / ck[:, 1]).median()) * 0.1  # 100 MHz real-time counter
+        ops = float(blocks) * 512 / 64 * iters * 8 * flops_per
+        rate = ops / ms / 1e9
+        res[name] = {"ms": ms, "rate": rate, "unit": "TFLOP/s" if kind == 0 else "TOP/s", "frac": rate / peak,
+                     "clock_ghz": ghz,
+                     "mfma_busy_at_clock": rate / (cus.value * ghz * 1e9 * flops_per / 32 / 1e12 * 4) if ghz else None}
     return res
 
 
@@ -676,6 +746,13 @@ def bench_proj(mh, dev, steps, warmup):
         flops = 2.0 * ROWS * k * n
         res[name] = {"ms": ms, "tflops": flops / ms / 1e9, "mfma_util": flops / ms / 1e9 / BF16_PEAK_TFLOPS,
                      "shape": [ROWS, k, n], "weights": "int8 (W8A16)", "epilogue": epi}
+        if name == "out":
+            # The same on the reference's float residual stream: residual float [rows][5120] += gate * y.
+            yf = torch.zeros((ROWS, n), dtype=torch.float32, device=dev)
+            fms, _ = time_launches(lambda: mh.gemm_gate_add(x, w, yf, gate, w_scale=s), steps, warmup)
+            res[name]["float_residual_ms"] = fms
+            res[name]["float_residual_tflops"] = flops / fms / 1e9
+            del yf
         if name == "qkv":
             wb = (w.float() * s[:, None]).to(torch.bfloat16)
             bms, _ = time_launches(lambda: mh.gemm(x, wb, out=y), steps, warmup)
@@ -729,6 +806,38 @@ def bench_fc1(mh, dev, steps, warmup, compare):
         res["bf16_hipblaslt_tflops"] = flops / cms / 1e9
         del wt, y, wb
     return res
+
+
+def bench_hipblaslt_tuned(dev, steps, warmup, max_ms_per_solution=200):
+    """hipBLASLt's (and rocBLAS's) best solution for fc1's GEMM (x [129,536][5120] bf16 times w^T [5120][27,648] bf16,
+    no epilogue), found by PyTorch's TunableOp, which times every candidate solution for this shape; beside the
+    default solution torch.matmul picks. The tuning results file goes to a temporary directory."""
+    import tempfile
+
+    g = torch.Generator(device=dev).manual_seed(9)
+    x = torch.randn((ROWS, DIM), generator=g, device=dev).to(torch.bfloat16)
+    wt = torch.randn((DIM, 2 * FFN), generator=g, device=dev).to(torch.bfloat16)
+    y = torch.empty((ROWS, 2 * FFN), dtype=torch.bfloat16, device=dev)
+    flops = 2.0 * ROWS * DIM * 2 * FFN
+    dms, _ = time_launches(lambda: torch.matmul(x, wt, out=y), max(3, steps), warmup)
+    tun = torch.cuda.tunable
+    t0 = time.perf_counter()
+    with tempfile.TemporaryDirectory() as tmp:
+        tun.set_filename(str(Path(tmp) / "tunableop_results.csv"))
+        tun.enable(True)
+        tun.tuning_enable(True)
+        tun.set_max_tuning_duration(max_ms_per_solution)
+        tun.set_max_tuning_iterations(3)
+        torch.matmul(x, wt, out=y)  # tunes this shape
+        torch.cuda.synchronize()
+        tune_s = time.perf_counter() - t0
+        tun.tuning_enable(False)
+        tms, _ = time_launches(lambda: torch.matmul(x, wt, out=y), max(3, steps), warmup)
+        results = tun.get_results()
+        tun.enable(False)
+    return {"default_ms": dms, "default_tflops": flops / dms / 1e9, "tuned_ms": tms, "tuned_tflops": flops / tms / 1e9,
+            "tuned_mfma_util": flops / tms / 1e9 / BF16_PEAK_TFLOPS, "tuning_s": tune_s,
+            "results": [" ".join(map(str, r)) for r in results]}
 
 
 def bench_share(mh, dev, steps, warmup, gpus=8):
@@ -949,8 +1058,8 @@ def main() -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--only",
-                    default="fused,block_order,copy,swiglu,select,cond,heads,attn,proj,fc1,rms_f32,block,ref,share")
+    ap.add_argument("--only", default="fused,block_order,copy,swiglu,select,cond,heads,attn,proj,fc1,mfma,rms_f32,"
+                                      "block,ref,share")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-compare", action="store_true")
     args = ap.parse_args()
@@ -983,9 +1092,13 @@ def main() -> int:
         head = report.get("fused_rms_mod_gate_add")
         if head:
             report["stream_ceiling"]["fused_vs_r2w1"] = head["GBs"] / report["stream_ceiling"]["r2w1"]["GBs"]
+            rows2 = report["stream_ceiling"]["rows_r2w1"]["2_workgroups_a_cu"]
+            report["stream_ceiling"]["fused_vs_rows_r2w1"] = head["GBs"] / rows2["GBs"]
         order = report.get("gate_add_rms_mod")
         if order:
             report["stream_ceiling"]["block_order_vs_r2w2"] = order["GBs"] / report["stream_ceiling"]["r2w2"]["GBs"]
+            report["stream_ceiling"]["float_stream_block_order_vs_r2w2"] = (
+                order["float_stream"]["GBs"] / report["stream_ceiling"]["r2w2"]["GBs"])
         torch.cuda.empty_cache()
         done("copy")
     if "rms_f32" in ops:
@@ -1028,6 +1141,19 @@ def main() -> int:
                                                not args.no_compare)
         torch.cuda.empty_cache()
         done("fc1")
+    if "tuned" in ops:
+        report["hipblaslt_tuned_fc1"] = bench_hipblaslt_tuned(dev, max(3, args.steps // 2),
+                                                              max(1, args.warmup // 2))
+        torch.cuda.empty_cache()
+        done("tuned")
+    if "mfma" in ops:
+        ceil = bench_mfma_ceiling(dev, args.steps, args.warmup)
+        fc1 = report.get("fc1_w8a16_swiglu")
+        if fc1:
+            ceil["fc1_w8a16_vs_bf16_ceiling"] = fc1["tflops"] / ceil["bf16"]["rate"]
+            ceil["fc1_w8a8_vs_int8_ceiling"] = fc1["w8a8_fc1_tops"] / ceil["int8"]["rate"]
+        report["mfma_ceiling"] = ceil
+        done("mfma")
 
     if "block" in ops:
         blk = bench_block(mh, dev, 3, 1)

@@ -29,7 +29,7 @@
 extern "C" {
 #endif
 
-#define MH3_ABI_VERSION 3
+#define MH3_ABI_VERSION 4
 
 /* ---- error codes ------------------------------------------------------------------------------------------------ */
 enum {
@@ -89,8 +89,20 @@ typedef struct MH3RowsArgs {
      * interleaved vectors, such as the reference's [U][3][6][D] modulation table (h3_ref_test.cpp:229-241), whose
      * (level, tag) sets are 6 D floats apart. */
     uint32_t set_stride;
-    uint32_t reserved[2];
+    uint32_t flags; /* 0, or MH3_ROWS_* below (dtype MH3_F32 only) */
+    uint32_t reserved;
 } MH3RowsArgs;
+/* The reference's float residual stream (docs/architecture.md:69-70: activations are fp32 and go into the bf16 GEMMs
+ * rounded to bf16). With dtype MH3_F32, x (and the residual) are float rows and these flags make the GEMMs' rows bf16:
+ *   MH3_ROWS_NORM_BF16: the modulated norm's output (y of mh3_rms_mod_rows, h of mh3_gate_add_rms_mod_rows) is bf16,
+ *                       the float result rounded once to nearest even: the next GEMM's input;
+ *   MH3_ROWS_Y_BF16:    the gated addend y (mh3_gate_add_rows, mh3_gate_add_rms_mod_rows) is bf16, a GEMM's output.
+ * mh3_rms_mod_rows takes NORM_BF16, mh3_gate_add_rows Y_BF16, mh3_gate_add_rms_mod_rows NORM_BF16 alone or with
+ * Y_BF16 (its results then equal, bit for bit, mh3_gate_add_rows and mh3_rms_mod_rows with the same flags), and
+ * mh3_rms_mod_gate_add_rows none; any other flag, or a flag with dtype MH3_BF16, is MH3_ERR_PARAM. Under a flag
+ * dim % 8 == 0 and dim <= 6144 (MH3_ERR_UNSUPPORTED beyond), and a bf16 row array may not share memory with a float
+ * one (MH3_ERR_PARAM). */
+enum { MH3_ROWS_NORM_BF16 = 1u, MH3_ROWS_Y_BF16 = 2u };
 
 /* y = x * rsqrt(mean(x^2) + eps) * w * (1 + scale[s]) + shift[s]. y may equal x. */
 int mh3_rms_mod_rows(const MH3RowsArgs* args, const void* x, const float* w, const float* shift, const float* scale,
@@ -331,6 +343,13 @@ int mh3_gemm(const MH3GemmArgs* args, uint32_t form, const void* x, const float*
 int mh3_gemm_gate_add(const MH3GemmArgs* args, uint32_t form, const void* x, const float* x_scale, const void* w,
                       const float* w_scale, const float* gate, const uint8_t* set_of_row, uint16_t* residual,
                       mh3_stream_t stream);
+/* mh3_gemm_gate_add on the reference's float residual stream (docs/architecture.md:69-70: the GEMMs take bf16 rows,
+ * the residual stays float): residual is float [m][n], residual[row][col] = fmaf(gate[s][col], y, residual[row][col])
+ * with y the scaled float accumulator, in place; x is the bf16 (or int8) row the GEMM takes. The same shape, form and
+ * aliasing rules as mh3_gemm_gate_add. */
+int mh3_gemm_gate_add_f32(const MH3GemmArgs* args, uint32_t form, const void* x, const float* x_scale, const void* w,
+                          const float* w_scale, const float* gate, const uint8_t* set_of_row, float* residual,
+                          mh3_stream_t stream);
 
 /* ---- time conditioning: the producer of the modulation table ---------------------------------------------------
  * What turns a step's distinct noise levels t = 1 - sigma (one to three in H3) into the [U][3][6][D] modulation

@@ -166,17 +166,19 @@ public:
     hipStream_t stream() const { return s_; }
     void finish() const { check_hip(hipStreamSynchronize(s_), "finish"); }
 
-    // y = rmsnorm(x) * w * (1 + scale[s]) + shift[s]
+    // y = rmsnorm(x) * w * (1 + scale[s]) + shift[s]. flags (dtype MH3_F32): MH3_ROWS_NORM_BF16 gives the bf16 row
+    // the next GEMM takes from the float residual stream.
     void rms_mod_rows(uint32_t rows, uint32_t dim, uint32_t dtype, const void* x, const Modulation& m, void* y,
-                      float eps = 1e-6f) const
+                      float eps = 1e-6f, uint32_t flags = 0) const
     {
-        const MH3RowsArgs a = rows_args(rows, dim, dtype, m, eps);
+        const MH3RowsArgs a = rows_args(rows, dim, dtype, m, eps, flags);
         check(mh3_rms_mod_rows(&a, x, m.w, m.shift, m.scale, m.set_of_row, y, s_), "rms_mod_rows");
     }
-    // x += gate[s] * y
-    void gate_add_rows(uint32_t rows, uint32_t dim, uint32_t dtype, void* x, const void* y, const Modulation& m) const
+    // x += gate[s] * y. flags (dtype MH3_F32): MH3_ROWS_Y_BF16 adds a GEMM's bf16 output into the float stream.
+    void gate_add_rows(uint32_t rows, uint32_t dim, uint32_t dtype, void* x, const void* y, const Modulation& m,
+                       uint32_t flags = 0) const
     {
-        const MH3RowsArgs a = rows_args(rows, dim, dtype, m, 1.0f);
+        const MH3RowsArgs a = rows_args(rows, dim, dtype, m, 1.0f, flags);
         check(mh3_gate_add_rows(&a, x, y, m.gate, m.set_of_row, s_), "gate_add_rows");
     }
     // out = residual + gate[s] * rms_mod(x)
@@ -187,11 +189,12 @@ public:
         check(mh3_rms_mod_gate_add_rows(&a, x, residual, m.w, m.shift, m.scale, m.gate, m.set_of_row, out, s_),
               "rms_mod_gate_add_rows");
     }
-    // x += gate[s] * y; h = rms_mod(x)  (the block's order: gate_add_rows then rms_mod_rows, in one pass)
+    // x += gate[s] * y; h = rms_mod(x)  (the block's order: gate_add_rows then rms_mod_rows, in one pass). flags
+    // (dtype MH3_F32): MH3_ROWS_NORM_BF16, alone or with MH3_ROWS_Y_BF16, for the float residual stream.
     void gate_add_rms_mod_rows(uint32_t rows, uint32_t dim, uint32_t dtype, void* x, const void* y,
-                               const Modulation& m, void* h, float eps = 1e-6f) const
+                               const Modulation& m, void* h, float eps = 1e-6f, uint32_t flags = 0) const
     {
-        const MH3RowsArgs a = rows_args(rows, dim, dtype, m, eps);
+        const MH3RowsArgs a = rows_args(rows, dim, dtype, m, eps, flags);
         check(mh3_gate_add_rms_mod_rows(&a, x, y, m.gate, m.w, m.shift, m.scale, m.set_of_row, h, s_),
               "gate_add_rms_mod_rows");
     }
@@ -340,11 +343,20 @@ public:
         check(mh3_gemm_gate_add(&a, form, x, x_scale, w, w_scale, m.gate, m.set_of_row, residual, s_),
               form == MH3_GEMM_BF16 ? "Gemm::encode+gate_add_rows" : "gemm_i8+gate_add_rows");
     }
+    // The same on the float residual stream: residual float [rows][n] += gate[s] * (x w^T).
+    void gemm_gate_add(uint32_t rows, uint32_t n, uint32_t k, uint32_t form, const void* x, const float* x_scale,
+                       const void* w, const float* w_scale, const Modulation& m, float* residual) const
+    {
+        const MH3GemmArgs a{rows, n, k, m.n_sets, m.set_stride, 0};
+        check(mh3_gemm_gate_add_f32(&a, form, x, x_scale, w, w_scale, m.gate, m.set_of_row, residual, s_),
+              form == MH3_GEMM_BF16 ? "Gemm::encode+gate_add_rows" : "gemm_i8+gate_add_rows");
+    }
 
 private:
-    static MH3RowsArgs rows_args(uint32_t rows, uint32_t dim, uint32_t dtype, const Modulation& m, float eps)
+    static MH3RowsArgs rows_args(uint32_t rows, uint32_t dim, uint32_t dtype, const Modulation& m, float eps,
+                                 uint32_t flags = 0)
     {
-        return MH3RowsArgs{rows, dim, m.n_sets, dtype, eps, m.set_stride, {0, 0}};
+        return MH3RowsArgs{rows, dim, m.n_sets, dtype, eps, m.set_stride, flags, 0};
     }
     hipStream_t s_;
 };

@@ -107,10 +107,11 @@ enum GemmMode { kW8A16 = 0, kBf16 = 1, kW8A8 = 2 };
 //   kSwiGLU:  out[m][N] = silu(y gate column) * y up column; w holds N gate rows then N up rows (fc1);
 //   kStore:   out[m][N] = y; w holds N rows (the qkv projection);
 //   kGateAdd: out[m][N] += gate[set(row)] * y, in place on the bf16 residual (the out projection and fc2, with the
-//             reference's gate_add_rows folded in).
+//             reference's gate_add_rows folded in);
+//   kGateAddF32: the same on a float residual (the reference's float residual stream), out read as float [m][N].
 // With kSwiGLU a tile's 256 weight rows are 128 gate rows from n0 and the 128 matching up rows from N + n0; otherwise
 // they are 256 consecutive rows, so both halves of the wave's accumulators are output columns.
-enum GemmEpi { kSwiGLU = 0, kStore = 1, kGateAdd = 2 };
+enum GemmEpi { kSwiGLU = 0, kStore = 1, kGateAdd = 2, kGateAddF32 = 3 };
 
 // The epilogue's extra operands (kGateAdd): gate vectors [n_sets][gate_stride] floats, a set per row (NULL: set 0).
 struct GemmGate {
@@ -179,6 +180,18 @@ __device__ __forceinline__ void gemm_epilogue(Acc (&acc)[TM][2 * TN], u32x4_t* s
             const float4 v0 = *reinterpret_cast<const float4*>(stage + r * kEpiStride + c8);
             const float4 v1 = *reinterpret_cast<const float4*>(stage + r * kEpiStride + c8 + 4u);
             float o[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
+            if constexpr (EPI == kGateAddF32) {
+                // The float residual: 32 bytes a thread, x += gate * y with one float rounding.
+                const uint32_t set = gg.set_of_row ? min(uint32_t(gg.set_of_row[row]), gg.n_sets - 1u) : 0u;
+                const float* g = gg.gate + uint64_t(set) * gg.gate_stride + col0 + c8;
+                float4* fdst = reinterpret_cast<float4*>(reinterpret_cast<float*>(out) + uint64_t(row) * N + col0 + c8);
+                const float4 r0 = fdst[0], r1 = fdst[1];
+                fdst[0] = float4{fmaf(g[0], o[0], r0.x), fmaf(g[1], o[1], r0.y), fmaf(g[2], o[2], r0.z),
+                                 fmaf(g[3], o[3], r0.w)};
+                fdst[1] = float4{fmaf(g[4], o[4], r1.x), fmaf(g[5], o[5], r1.y), fmaf(g[6], o[6], r1.z),
+                                 fmaf(g[7], o[7], r1.w)};
+                continue;
+            }
             uint4* dst = reinterpret_cast<uint4*>(out + uint64_t(row) * N + col0 + c8);
             if constexpr (EPI == kGateAdd) {
                 const uint32_t set = gg.set_of_row ? min(uint32_t(gg.set_of_row[row]), gg.n_sets - 1u) : 0u;
@@ -466,20 +479,21 @@ int launch_gemm(const MH3GemmArgs* a, const void* x, const void* w, const float*
         return MH3_ERR_UNSUPPORTED; // 32-bit buffer offsets: a tile's A rows, and all of w
     if (!x || !w || (MODE != kBf16 && !scale) || (MODE == kW8A8 && !xscale) || !out)
         return MH3_ERR_POINTER;
-    if (EPI == kGateAdd && (!gg.gate || gg.n_sets == 0 || gg.n_sets > 256 || gg.gate_stride < a->n))
+    if ((EPI == kGateAdd || EPI == kGateAddF32) &&
+        (!gg.gate || gg.n_sets == 0 || gg.n_sets > 256 || gg.gate_stride < a->n))
         return gg.gate ? MH3_ERR_PARAM : MH3_ERR_POINTER;
     if (!host::aligned16(x) || !host::aligned16(w) || !host::aligned16(out))
         return MH3_ERR_ALIGN;
     // The output (for the gate-add epilogue, the residual updated in place) may not overlap an operand: while one
     // tile writes its columns, the other tiles of its row band still read the same rows of x.
-    const uint64_t out_bytes = uint64_t(a->m) * a->n * 2u;
+    const uint64_t out_bytes = uint64_t(a->m) * a->n * (EPI == kGateAddF32 ? 4u : 2u);
     if (host::overlaps(out, out_bytes, x, uint64_t(a->m) * a->k * kEA) ||
         host::overlaps(out, out_bytes, w, w_rows * a->k * kEB))
         return MH3_ERR_PARAM;
     // Nor the vectors every epilogue reads: the scales, the gate sets and the row-to-set map.
     if (host::overlaps(out, out_bytes, scale, scale ? w_rows * 4u : 0u) ||
         host::overlaps(out, out_bytes, xscale, xscale ? uint64_t(a->m) * 4u : 0u) ||
-        (EPI == kGateAdd &&
+        ((EPI == kGateAdd || EPI == kGateAddF32) &&
          (host::overlaps(out, out_bytes, gg.gate, (uint64_t(gg.n_sets) - 1u) * gg.gate_stride * 4u + a->n * 4ull) ||
           host::overlaps(out, out_bytes, gg.set_of_row, gg.set_of_row ? uint64_t(a->m) : 0u))))
         return MH3_ERR_PARAM;
@@ -555,4 +569,12 @@ extern "C" int mh3_gemm_gate_add(const MH3GemmArgs* a, uint32_t form, const void
 {
     return launch_by_form<mh3::kGateAdd>(a, form, x, x_scale, w, w_scale, residual, gate_of(a, gate, set_of_row),
                                          stream);
+}
+
+extern "C" int mh3_gemm_gate_add_f32(const MH3GemmArgs* a, uint32_t form, const void* x, const float* x_scale,
+                                     const void* w, const float* w_scale, const float* gate,
+                                     const uint8_t* set_of_row, float* residual, mh3_stream_t stream)
+{
+    return launch_by_form<mh3::kGateAddF32>(a, form, x, x_scale, w, w_scale, reinterpret_cast<uint16_t*>(residual),
+                                            gate_of(a, gate, set_of_row), stream);
 }

@@ -126,6 +126,7 @@ struct FastDiv {
 
 // ---- streaming memory access -----------------------------------------------------------------------------------------
 typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
 
 // Buffer descriptor word 3 for raw (stride 0) buffers with 32-bit byte offsets on gfx9: reads past num_records
 // return zero without touching memory, writes past it are dropped.

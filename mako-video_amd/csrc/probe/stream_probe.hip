@@ -19,9 +19,26 @@
 //   returns 0, -1 for a bad kind, unroll or null pointer, -2 for misaligned pointers, -3 for a launch failure.
 //   int mh3_probe_device(int* cus, int* max_clock_khz);  the current device's CU count and peak engine clock, from
 //   which the MFMA peak is CUs x clock x flops a clock a CU.
+//
+// Two more probes with the shapes of the hot path's own kernels:
+//   int mh3_probe_rows(const void* a, const void* b, void* c, uint32_t rows, uint32_t nvec, uint32_t lds_bytes,
+//                      void* stream);
+//     the fused row op's access pattern with no arithmetic: one row of nvec 16-byte vectors a wave (vector lane +
+//     64 j of the row, j < 10), all of a's row loaded, then all of b's, then c = a + b stored; 8-wave workgroups of 8
+//     consecutive rows, `lds_bytes` of dynamic LDS a workgroup (which sets how many share a CU), buffer loads and
+//     stores with the non-temporal hint. nvec <= 640.
+//   int mh3_probe_mfma(int kind, uint32_t blocks, uint32_t iters, float* out, uint64_t* clocks, void* stream);
+//     a register-only loop of matrix instructions, kind 0 v_mfma_f32_32x32x16_bf16, kind 1 v_mfma_i32_32x32x32_i8:
+//     8 waves a workgroup, each wave `iters` (a multiple of 8; rounded up) rounds of 8 independent accumulators,
+//     the operands cycling through 8
+//     register fragments of random bits (so the matrix core's inputs change from one instruction to the next, as in
+//     a GEMM). out gets one value a thread (keeps the results live); clocks gets, for each workgroup, the shader
+//     clock counter's and the 100 MHz real-time counter's advance over its loop (s_memtime, s_memrealtime), from
+//     which the clock the loop ran at follows.
 #include <hip/hip_runtime.h>
 
 #include <cstdint>
+#include <type_traits>
 
 namespace {
 
@@ -126,7 +143,133 @@ void launch_buffer(int unroll, hipStream_t s, const u32x4* a, const u32x4* b, u3
         hipLaunchKernelGGL((stream_buffer_kernel<MIX, 8>), grid, dim3(kThreads), 0, s, a, b, c, n);
 }
 
+// ---- the fused row op's shape ----------------------------------------------------------------------------------------
+constexpr uint32_t kRowVecs = 10; // 16-byte vectors a lane: a 5120-wide bf16 row
+
+__global__ __launch_bounds__(512) void rows_probe_kernel(const u32x4* a, const u32x4* b, u32x4* c, uint32_t rows,
+                                                         uint32_t nvec)
+{
+    const uint32_t lane = threadIdx.x & 63u, row = blockIdx.x * 8u + (threadIdx.x >> 6);
+    const uint32_t bytes = row < rows ? nvec * 16u : 0u, rr = row < rows ? row : 0u;
+    const auto ra = __builtin_amdgcn_make_buffer_rsrc(const_cast<u32x4*>(a + uint64_t(rr) * nvec), 0, int(bytes),
+                                                      kRsrcFlags);
+    const auto rb = __builtin_amdgcn_make_buffer_rsrc(const_cast<u32x4*>(b + uint64_t(rr) * nvec), 0, int(bytes),
+                                                      kRsrcFlags);
+    const auto rc = __builtin_amdgcn_make_buffer_rsrc(c + uint64_t(rr) * nvec, 0, int(bytes), kRsrcFlags);
+    u32x4 va[kRowVecs], vb[kRowVecs];
+#pragma unroll
+    for (uint32_t j = 0; j < kRowVecs; ++j)
+        va[j] = __builtin_amdgcn_raw_buffer_load_b128(ra, (lane + 64u * j) * 16u, 0, kNonTemporal);
+#pragma unroll
+    for (uint32_t j = 0; j < kRowVecs; ++j)
+        vb[j] = __builtin_amdgcn_raw_buffer_load_b128(rb, (lane + 64u * j) * 16u, 0, kNonTemporal);
+#pragma unroll
+    for (uint32_t j = 0; j < kRowVecs; ++j)
+        __builtin_amdgcn_raw_buffer_store_b128(va[j] + vb[j], rc, (lane + 64u * j) * 16u, 0, kNonTemporal);
+}
+
+// ---- the matrix cores' sustained rate ------------------------------------------------------------------------------
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float floatx16 __attribute__((ext_vector_type(16)));
+typedef int intx4 __attribute__((ext_vector_type(4)));
+typedef int intx16 __attribute__((ext_vector_type(16)));
+
+__device__ __forceinline__ uint32_t mix32(uint32_t x)
+{
+    x ^= x >> 16;
+    x *= 0x7feb352du;
+    x ^= x >> 15;
+    x *= 0x846ca68bu;
+    return x ^ (x >> 16);
+}
+
+template <int KIND>
+__global__ __launch_bounds__(512) void mfma_probe_kernel(uint32_t iters, float* out, uint64_t* clocks)
+{
+    constexpr int kFrag = 8, kAcc = 8;
+    // Operand fragments of random bits; bf16 ones with the exponent held to 2^-15 .. 2^0 so no sum overflows.
+    intx4 fa[kFrag], fb[kFrag];
+    const uint32_t seed = (blockIdx.x * 512u + threadIdx.x) * 64u;
+#pragma unroll
+    for (int f = 0; f < kFrag; ++f)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            uint32_t ra = mix32(seed + f * 8u + e), rb = mix32(seed + f * 8u + 4u + e);
+            if (KIND == 0) {
+                ra = (ra & 0x87ff87ffu) | 0x38003800u; // sign, 4 low exponent bits and 7 mantissa bits random
+                rb = (rb & 0x87ff87ffu) | 0x38003800u;
+            }
+            fa[f][e] = int(ra);
+            fb[f][e] = int(rb);
+        }
+    using Acc = typename std::conditional<KIND == 0, floatx16, intx16>::type;
+    Acc acc[kAcc];
+#pragma unroll
+    for (int i = 0; i < kAcc; ++i)
+        acc[i] = Acc{};
+    __syncthreads();
+    const uint64_t t0 = __builtin_amdgcn_s_memtime(), r0 = __builtin_amdgcn_s_memrealtime();
+    // Rounds of 8 (iters is taken in multiples of 8): the fragment of each instruction is then known at compile time.
+    for (uint32_t it = 0; it < iters; it += 8u) {
+#pragma unroll
+        for (int u = 0; u < 8; ++u)
+#pragma unroll
+            for (int i = 0; i < kAcc; ++i) {
+                const int f = (i + u) & (kFrag - 1), g = (i * 3 + u) & (kFrag - 1);
+                if constexpr (KIND == 0)
+                    acc[i] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
+                        __builtin_bit_cast(bf16x8, fa[f]), __builtin_bit_cast(bf16x8, fb[g]), acc[i], 0, 0, 0);
+                else
+                    acc[i] = __builtin_amdgcn_mfma_i32_32x32x32_i8(fa[f], fb[g], acc[i], 0, 0, 0);
+            }
+    }
+    float sum = 0.0f;
+#pragma unroll
+    for (int i = 0; i < kAcc; ++i)
+#pragma unroll
+        for (int e = 0; e < 16; ++e)
+            sum += float(acc[i][e]);
+    const uint64_t t1 = __builtin_amdgcn_s_memtime(), r1 = __builtin_amdgcn_s_memrealtime();
+    out[blockIdx.x * 512u + threadIdx.x] = sum;
+    if (threadIdx.x == 0) {
+        clocks[2u * blockIdx.x] = t1 - t0;
+        clocks[2u * blockIdx.x + 1u] = r1 - r0;
+    }
+}
+
 } // namespace
+
+extern "C" int mh3_probe_rows(const void* a, const void* b, void* c, uint32_t rows, uint32_t nvec, uint32_t lds_bytes,
+                              void* stream)
+{
+    if (!a || !b || !c || nvec == 0 || nvec > 64u * kRowVecs || lds_bytes > 160u * 1024u)
+        return -1;
+    if ((reinterpret_cast<uintptr_t>(a) | reinterpret_cast<uintptr_t>(b) | reinterpret_cast<uintptr_t>(c)) & 15u)
+        return -2;
+    if (rows == 0)
+        return 0;
+    const auto k = reinterpret_cast<const void*>(&rows_probe_kernel);
+    if (hipFuncSetAttribute(k, hipFuncAttributeMaxDynamicSharedMemorySize, int(lds_bytes)) != hipSuccess)
+        return -3;
+    hipLaunchKernelGGL(rows_probe_kernel, dim3((rows + 7u) / 8u), dim3(512), lds_bytes,
+                       static_cast<hipStream_t>(stream), static_cast<const u32x4*>(a), static_cast<const u32x4*>(b),
+                       static_cast<u32x4*>(c), rows, nvec);
+    return hipGetLastError() == hipSuccess ? 0 : -3;
+}
+
+extern "C" int mh3_probe_mfma(int kind, uint32_t blocks, uint32_t iters, float* out, uint64_t* clocks, void* stream)
+{
+    if ((kind != 0 && kind != 1) || blocks == 0 || !out || !clocks)
+        return -1;
+    if ((reinterpret_cast<uintptr_t>(clocks) & 7u) != 0)
+        return -2;
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    if (kind == 0)
+        hipLaunchKernelGGL(mfma_probe_kernel<0>, dim3(blocks), dim3(512), 0, s, iters, out, clocks);
+    else
+        hipLaunchKernelGGL(mfma_probe_kernel<1>, dim3(blocks), dim3(512), 0, s, iters, out, clocks);
+    return hipGetLastError() == hipSuccess ? 0 : -3;
+}
 
 extern "C" int mh3_probe_stream(int kind, const void* a, const void* b, void* c, uint64_t n, int unroll,
                                 uint32_t blocks, void* stream)

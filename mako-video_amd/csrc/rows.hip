@@ -444,6 +444,126 @@ __global__ __launch_bounds__(kWaveBlock) void rows_wave_kernel(RowsParams p)
     }
 }
 
+// ---- the float residual stream with bf16 GEMM operands ------------------------------------------------------------
+// The reference keeps the block's residual stream x in float and rounds the GEMMs' inputs to bf16
+// (docs/architecture.md:69-70). These kernels read and write float x and give or take the GEMMs' bf16 rows: the
+// modulated norm's output (the next GEMM's input, rounded once) and, with YB, the gated addend y (a GEMM's bf16
+// output). One wavefront a row, as in rows_wave_kernel; a lane's unit is 4 columns, 16 bytes of a float row and 8 of a
+// bf16 row: unit lane + 64 j, j < NU, so every load and store instruction covers one contiguous stretch of its row.
+// The coefficient table is rows_wave_kernel's, and so are the reduction (DPP row sums, four readlanes) and the
+// arithmetic, so each op gives the same bits whether fused (kGateAddMod) or run as its two parts.
+template <int OP, int YB, int NU, int SRC>
+__global__ __launch_bounds__(kWaveBlock) void rows_f32_stream_kernel(RowsParams p)
+{
+    using F = RowVec<MH3_F32>;
+    extern __shared__ float ctab[]; // kCoefLds: a[n_sets][dim], b[n_sets][dim] (and c for kGateAddMod)
+    const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
+    const uint32_t units = p.nvec; // 4-column units a row
+    const uint32_t coef_total = p.n_sets * p.dim;
+    for (uint32_t i = tid; SRC == kCoefLds && i < p.n_sets * units; i += blockDim.x) {
+        const uint32_t s = i / units, v = i - s * units;
+        float a[4], b[4], c[4];
+        coef_vec<OP, 4>(p, s, v * 4u, a, b, c);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            ctab[s * p.dim + v * 4u + e] = a[e];
+            ctab[coef_total + s * p.dim + v * 4u + e] = b[e];
+            if constexpr (OP == kGateAddMod)
+                ctab[2 * coef_total + s * p.dim + v * 4u + e] = c[e];
+        }
+    }
+    __syncthreads();
+    const uint32_t row = blockIdx.x * (blockDim.x >> 6) + wave;
+    if (row >= p.rows)
+        return;
+    const uint32_t set = p.set_of_row ? min(uint32_t(p.set_of_row[row]), p.n_sets - 1u) : 0u;
+    // The float row x (rms_mod: the input; the gate-add ops: the stream updated in place).
+    const u32x4_t* xsrc = OP == kRmsMod ? p.x : p.res;
+    const __amdgpu_buffer_rsrc_t sx = buffer_rsrc(xsrc + uint64_t(row) * units, units * 16u);
+    u32x4_t xv[NU];
+#pragma unroll
+    for (int j = 0; j < NU; ++j)
+        xv[j] = __builtin_amdgcn_raw_buffer_load_b128(sx, (lane + 64u * j) * 16u, 0, kNonTemporal);
+    if constexpr (OP == kGateAdd || OP == kGateAddMod) {
+        // x' = x + gate * y in float, stored; the norm below is of these values.
+        u32x4_t yv[NU];
+        u32x2_t yh[NU];
+        const char* ybase = reinterpret_cast<const char*>(p.x) + uint64_t(row) * units * (YB ? 8u : 16u);
+        const __amdgpu_buffer_rsrc_t sy = buffer_rsrc(ybase, units * (YB ? 8u : 16u));
+#pragma unroll
+        for (int j = 0; j < NU; ++j) {
+            if constexpr (YB)
+                yh[j] = __builtin_amdgcn_raw_buffer_load_b64(sy, (lane + 64u * j) * 8u, 0, kNonTemporal);
+            else
+                yv[j] = __builtin_amdgcn_raw_buffer_load_b128(sy, (lane + 64u * j) * 16u, 0, kNonTemporal);
+        }
+        const __amdgpu_buffer_rsrc_t so2 = buffer_rsrc(p.out2 + uint64_t(row) * units, units * 16u);
+        const float* tg = ctab + (OP == kGateAdd ? 0u : 2u * coef_total) + set * p.dim;
+#pragma unroll
+        for (int j = 0; j < NU; ++j) {
+            const uint32_t v = min(lane + 64u * j, units - 1u);
+            float g[4], f[4], y[4], o[4];
+            if constexpr (SRC == kCoefLds) {
+                const float4 g4 = *reinterpret_cast<const float4*>(tg + v * 4u);
+                g[0] = g4.x, g[1] = g4.y, g[2] = g4.z, g[3] = g4.w;
+            } else {
+                float ga[4], gb[4], gc[4];
+                coef_vec<OP, 4>(p, set, v * 4u, ga, gb, gc);
+#pragma unroll
+                for (int e = 0; e < 4; ++e)
+                    g[e] = OP == kGateAdd ? ga[e] : gc[e];
+            }
+            F::unpack(xv[j], f);
+            if constexpr (YB) {
+                y[0] = bf16_lo(yh[j][0]), y[1] = bf16_hi(yh[j][0]), y[2] = bf16_lo(yh[j][1]), y[3] = bf16_hi(yh[j][1]);
+            } else {
+                F::unpack(yv[j], y);
+            }
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+                o[e] = fmaf(g[e], y[e], f[e]);
+            xv[j] = F::pack4(o);
+            __builtin_amdgcn_raw_buffer_store_b128(xv[j], so2, (lane + 64u * j) * 16u, 0, kNonTemporal);
+        }
+    }
+    if constexpr (OP == kRmsMod || OP == kGateAddMod) {
+        float ss = 0.0f;
+#pragma unroll
+        for (int j = 0; j < NU; ++j)
+            ss = F::sumsq(xv[j], ss);
+        ss = row16_sum(ss);
+        const float total = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(ss), 0)) +
+                            __int_as_float(__builtin_amdgcn_readlane(__float_as_int(ss), 16)) +
+                            __int_as_float(__builtin_amdgcn_readlane(__float_as_int(ss), 32)) +
+                            __int_as_float(__builtin_amdgcn_readlane(__float_as_int(ss), 48));
+        const float inv = 1.0f / sqrtf(fmaf(total, p.inv_dim, p.eps));
+        const __amdgpu_buffer_rsrc_t so = buffer_rsrc(reinterpret_cast<const char*>(p.out) + uint64_t(row) * units * 8u,
+                                                      units * 8u);
+        const float* ta = ctab + set * p.dim;
+        const float* tb = ctab + coef_total + set * p.dim;
+#pragma unroll
+        for (int j = 0; j < NU; ++j) {
+            const uint32_t v = min(lane + 64u * j, units - 1u);
+            float f[4], o[4], a[4], b[4];
+            if constexpr (SRC == kCoefLds) {
+                const float4 a4 = *reinterpret_cast<const float4*>(ta + v * 4u);
+                const float4 b4 = *reinterpret_cast<const float4*>(tb + v * 4u);
+                a[0] = a4.x, a[1] = a4.y, a[2] = a4.z, a[3] = a4.w;
+                b[0] = b4.x, b[1] = b4.y, b[2] = b4.z, b[3] = b4.w;
+            } else {
+                float c[4];
+                coef_vec<OP, 4>(p, set, v * 4u, a, b, c);
+            }
+            F::unpack(xv[j], f);
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+                o[e] = fmaf(f[e] * inv, a[e], b[e]);
+            const u32x2_t h = {pack_bf16(o[0], o[1]), pack_bf16(o[2], o[3])};
+            __builtin_amdgcn_raw_buffer_store_b64(h, so, (lane + 64u * j) * 8u, 0, kNonTemporal);
+        }
+    }
+}
+
 // ---- swiglu ---------------------------------------------------------------------------------------------------------
 
 // silu(g) * u = g / (1 + exp(-g)) * u, with exp from v_exp_f32 and one reciprocal.
@@ -561,6 +681,49 @@ int launch_rows_wave(const RowsParams& p, hipStream_t stream)
     return host::check_launch();
 }
 
+// The float stream with bf16 GEMM rows (flags): one wavefront a row, NU 4-column units a lane.
+template <int OP, int YB, int SRC>
+const void* pick_f32_stream_kernel(uint32_t units)
+{
+    const uint32_t need = (units + 63u) / 64u;
+    if (need <= 4)
+        return reinterpret_cast<const void*>(&rows_f32_stream_kernel<OP, YB, 4, SRC>);
+    if (need <= 8)
+        return reinterpret_cast<const void*>(&rows_f32_stream_kernel<OP, YB, 8, SRC>);
+    if (need <= 16)
+        return reinterpret_cast<const void*>(&rows_f32_stream_kernel<OP, YB, 16, SRC>);
+    if (need <= 20)
+        return reinterpret_cast<const void*>(&rows_f32_stream_kernel<OP, YB, 20, SRC>);
+    return reinterpret_cast<const void*>(&rows_f32_stream_kernel<OP, YB, 24, SRC>);
+}
+
+template <int OP>
+int launch_rows_f32_stream(const RowsParams& p, uint32_t flags, hipStream_t stream)
+{
+    // The coefficients come from an LDS table the workgroup builds when it fits, else from the parameter vectors.
+    const bool in_lds = size_t(p.n_sets) * p.dim * kPlanes<OP> * sizeof(float) <= kCoefLdsMax;
+    const bool yb = (flags & MH3_ROWS_Y_BF16) != 0;
+    const void* k = in_lds ? (yb ? pick_f32_stream_kernel<OP, 1, kCoefLds>(p.nvec)
+                                 : pick_f32_stream_kernel<OP, 0, kCoefLds>(p.nvec))
+                           : (yb ? pick_f32_stream_kernel<OP, 1, kCoefGlobal>(p.nvec)
+                                 : pick_f32_stream_kernel<OP, 0, kCoefGlobal>(p.nvec));
+    const size_t table = in_lds ? size_t(p.n_sets) * p.dim * kPlanes<OP> * sizeof(float) : 0;
+    const size_t floor = OP == kGateAddMod ? kOrderLdsFloor : kWaveLdsFloor;
+    const size_t lds = table > floor ? table : floor;
+    if (const hipError_t e = host::allow_dynamic_lds(k, lds); e != hipSuccess)
+        return host::hip_error(e);
+    RowsParams arg = p;
+    const uint32_t waves = kWaveBlock / 64u;
+    const uint64_t blocks = (uint64_t(p.rows) + waves - 1) / waves;
+    void* args[] = {&arg};
+    if (const hipError_t e = hipLaunchKernel(k, dim3(uint32_t(blocks)), dim3(kWaveBlock), args, lds, stream);
+        e != hipSuccess) {
+        (void)hipGetLastError();
+        return host::hip_error(e);
+    }
+    return host::check_launch();
+}
+
 template <int DT, int OP>
 int launch_rows_dt(const RowsParams& p, hipStream_t stream)
 {
@@ -611,11 +774,18 @@ int launch_rows(const MH3RowsArgs* a, RowsParams p, hipStream_t stream)
     p.set_stride = a->set_stride ? a->set_stride : a->dim;
     p.eps = a->eps;
     p.inv_dim = 1.0f / float(a->dim);
+    if constexpr (OP != kFused) { // the fused op takes no flags (refused in its validation)
+        if (a->flags) {
+            p.nvec = a->dim / 4u; // 4-column units
+            return launch_rows_f32_stream<OP>(p, a->flags, stream);
+        }
+    }
     return a->dtype == MH3_BF16 ? launch_rows_dt<MH3_BF16, OP>(p, stream) : launch_rows_dt<MH3_F32, OP>(p, stream);
 }
 
-// Shared validation of the row entry points. `needs_eps` for the normed ops.
-int check_rows(const MH3RowsArgs* a, bool needs_eps)
+// Shared validation of the row entry points. `needs_eps` for the normed ops; `allowed` the flags the entry point
+// takes (with dtype MH3_F32 only: the float stream with bf16 GEMM rows).
+int check_rows(const MH3RowsArgs* a, bool needs_eps, uint32_t allowed)
 {
     if (!a)
         return MH3_ERR_POINTER;
@@ -623,33 +793,41 @@ int check_rows(const MH3RowsArgs* a, bool needs_eps)
         return MH3_ERR_PARAM;
     if (needs_eps && !(a->eps > 0.0f))
         return MH3_ERR_PARAM;
-    const uint32_t e = a->dtype == MH3_BF16 ? 8u : 4u;
+    if ((a->flags & ~allowed) != 0 || (a->flags && a->dtype != MH3_F32))
+        return MH3_ERR_PARAM;
+    const uint32_t e = a->dtype == MH3_BF16 || a->flags ? 8u : 4u;
     if (a->dim == 0 || a->dim % e != 0 || a->n_sets == 0 || a->n_sets > 256)
         return MH3_ERR_SHAPE;
     if (a->set_stride != 0 && (a->set_stride < a->dim || a->set_stride % 4 != 0))
         return MH3_ERR_PARAM;
-    if (a->dim / e > 4096u)
+    if (a->dim / e > (a->flags ? 12u * 64u : 4096u))
         return MH3_ERR_UNSUPPORTED;
     if (a->rows >= (1u << 31))
         return MH3_ERR_SHAPE;
     return MH3_OK;
 }
 
-// Aliasing rules of the row entry points. An output is a [rows][dim] array; it may equal an input row array where
-// `same_ok` (each wave or workgroup reads a row whole before it writes that row), but any other overlap with an input
-// row array races across rows.
-bool rows_clash(const MH3RowsArgs* a, const void* out, const void* in, bool same_ok)
+// Bytes of a [rows][dim] row array: of the stream's dtype, or bf16 where `bf16` (a GEMM's row under the flags).
+uint64_t row_bytes(const MH3RowsArgs* a, bool bf16)
 {
-    const uint64_t bytes = uint64_t(a->rows) * a->dim * (a->dtype == MH3_BF16 ? 2u : 4u);
-    return in && host::overlaps(out, bytes, in, bytes) && !(same_ok && out == in);
+    return uint64_t(a->rows) * a->dim * (bf16 || a->dtype == MH3_BF16 ? 2u : 4u);
+}
+
+// Aliasing rules of the row entry points. An output is a [rows][dim] array; it may equal an input row array of the
+// same element type where `same_ok` (each wave or workgroup reads a row whole before it writes that row), but any
+// other overlap with an input row array races across rows.
+bool rows_clash(const MH3RowsArgs* a, const void* out, bool out_bf16, const void* in, bool in_bf16, bool same_ok)
+{
+    return in && host::overlaps(out, row_bytes(a, out_bf16), in, row_bytes(a, in_bf16)) &&
+           !(same_ok && out == in && out_bf16 == in_bf16);
 }
 
 // Whether an output overlaps the vectors every workgroup reads: w [dim], shift / scale / gate (n_sets sets of dim
 // floats, set_stride apart) and set_of_row [rows].
-bool params_clash(const MH3RowsArgs* a, const void* out, const float* w, const float* shift, const float* scale,
-                  const float* gate, const uint8_t* sets)
+bool params_clash(const MH3RowsArgs* a, const void* out, bool out_bf16, const float* w, const float* shift,
+                  const float* scale, const float* gate, const uint8_t* sets)
 {
-    const uint64_t bytes = uint64_t(a->rows) * a->dim * (a->dtype == MH3_BF16 ? 2u : 4u);
+    const uint64_t bytes = row_bytes(a, out_bf16);
     const uint64_t vec = (uint64_t(a->n_sets - 1u) * (a->set_stride ? a->set_stride : a->dim) + a->dim) * 4u;
     return host::overlaps(out, bytes, w, w ? uint64_t(a->dim) * 4u : 0u) ||
            host::overlaps(out, bytes, shift, shift ? vec : 0u) || host::overlaps(out, bytes, scale, scale ? vec : 0u) ||
@@ -663,7 +841,7 @@ extern "C" {
 int mh3_rms_mod_rows(const MH3RowsArgs* args, const void* x, const float* w, const float* shift, const float* scale,
                      const uint8_t* set_of_row, void* y, mh3_stream_t stream)
 {
-    int rc = check_rows(args, true);
+    int rc = check_rows(args, true, MH3_ROWS_NORM_BF16);
     if (rc != MH3_OK)
         return rc;
     if (args->rows == 0)
@@ -673,7 +851,8 @@ int mh3_rms_mod_rows(const MH3RowsArgs* args, const void* x, const float* w, con
     if (!host::aligned16(x) || !host::aligned16(y) || !host::aligned16(w) || !host::aligned16(shift) ||
         !host::aligned16(scale))
         return MH3_ERR_ALIGN;
-    if (rows_clash(args, y, x, true) || params_clash(args, y, w, shift, scale, nullptr, set_of_row))
+    const bool yb = (args->flags & MH3_ROWS_NORM_BF16) != 0;
+    if (rows_clash(args, y, yb, x, false, true) || params_clash(args, y, yb, w, shift, scale, nullptr, set_of_row))
         return MH3_ERR_PARAM;
     RowsParams p{};
     p.x = static_cast<const u32x4_t*>(x);
@@ -688,7 +867,7 @@ int mh3_rms_mod_rows(const MH3RowsArgs* args, const void* x, const float* w, con
 int mh3_gate_add_rows(const MH3RowsArgs* args, void* x, const void* y, const float* gate, const uint8_t* set_of_row,
                       mh3_stream_t stream)
 {
-    int rc = check_rows(args, false);
+    int rc = check_rows(args, false, MH3_ROWS_Y_BF16);
     if (rc != MH3_OK)
         return rc;
     if (args->rows == 0)
@@ -697,12 +876,15 @@ int mh3_gate_add_rows(const MH3RowsArgs* args, void* x, const void* y, const flo
         return MH3_ERR_POINTER;
     if (!host::aligned16(x) || !host::aligned16(y) || !host::aligned16(gate))
         return MH3_ERR_ALIGN;
-    if (rows_clash(args, x, y, true) || params_clash(args, x, nullptr, nullptr, nullptr, gate, set_of_row))
+    const bool yb = (args->flags & MH3_ROWS_Y_BF16) != 0;
+    if (rows_clash(args, x, false, y, yb, true) ||
+        params_clash(args, x, false, nullptr, nullptr, nullptr, gate, set_of_row))
         return MH3_ERR_PARAM;
     RowsParams p{};
     p.x = static_cast<const u32x4_t*>(y);
     p.res = static_cast<const u32x4_t*>(x);
     p.out = static_cast<u32x4_t*>(x);
+    p.out2 = static_cast<u32x4_t*>(x); // the float stream's kernel writes the updated x here
     p.gate = gate;
     p.set_of_row = set_of_row;
     return launch_rows<kGateAdd>(args, p, static_cast<hipStream_t>(stream));
@@ -712,7 +894,7 @@ int mh3_rms_mod_gate_add_rows(const MH3RowsArgs* args, const void* x, const void
                               const float* shift, const float* scale, const float* gate, const uint8_t* set_of_row,
                               void* out, mh3_stream_t stream)
 {
-    int rc = check_rows(args, true);
+    int rc = check_rows(args, true, 0u);
     if (rc != MH3_OK)
         return rc;
     if (args->rows == 0)
@@ -722,8 +904,8 @@ int mh3_rms_mod_gate_add_rows(const MH3RowsArgs* args, const void* x, const void
     if (!host::aligned16(x) || !host::aligned16(residual) || !host::aligned16(out) || !host::aligned16(w) ||
         !host::aligned16(shift) || !host::aligned16(scale) || !host::aligned16(gate))
         return MH3_ERR_ALIGN;
-    if (rows_clash(args, out, x, true) || rows_clash(args, out, residual, true) ||
-        params_clash(args, out, w, shift, scale, gate, set_of_row))
+    if (rows_clash(args, out, false, x, false, true) || rows_clash(args, out, false, residual, false, true) ||
+        params_clash(args, out, false, w, shift, scale, gate, set_of_row))
         return MH3_ERR_PARAM;
     RowsParams p{};
     p.x = static_cast<const u32x4_t*>(x);
@@ -741,9 +923,12 @@ int mh3_gate_add_rms_mod_rows(const MH3RowsArgs* args, void* x, const void* y, c
                               const float* shift, const float* scale, const uint8_t* set_of_row, void* h,
                               mh3_stream_t stream)
 {
-    int rc = check_rows(args, true);
+    // Flags: none, a bf16 h, or a bf16 h from a bf16 y (a bf16 y alone would need a float norm of its own order).
+    int rc = check_rows(args, true, MH3_ROWS_NORM_BF16 | MH3_ROWS_Y_BF16);
     if (rc != MH3_OK)
         return rc;
+    if (args->flags == MH3_ROWS_Y_BF16)
+        return MH3_ERR_PARAM;
     if (args->rows == 0)
         return MH3_OK;
     if (!x || !y || !gate || !shift || !scale || !h)
@@ -753,9 +938,10 @@ int mh3_gate_add_rms_mod_rows(const MH3RowsArgs* args, void* x, const void* y, c
     if (!host::aligned16(x) || !host::aligned16(y) || !host::aligned16(h) || !host::aligned16(gate) ||
         !host::aligned16(w) || !host::aligned16(shift) || !host::aligned16(scale))
         return MH3_ERR_ALIGN;
-    if (rows_clash(args, h, x, false) || rows_clash(args, h, y, false) || rows_clash(args, x, y, true) ||
-        params_clash(args, h, w, shift, scale, gate, set_of_row) ||
-        params_clash(args, x, w, shift, scale, gate, set_of_row))
+    const bool hb = (args->flags & MH3_ROWS_NORM_BF16) != 0, yb = (args->flags & MH3_ROWS_Y_BF16) != 0;
+    if (rows_clash(args, h, hb, x, false, false) || rows_clash(args, h, hb, y, yb, false) ||
+        rows_clash(args, x, false, y, yb, true) || params_clash(args, h, hb, w, shift, scale, gate, set_of_row) ||
+        params_clash(args, x, false, w, shift, scale, gate, set_of_row))
         return MH3_ERR_PARAM;
     RowsParams p{};
     p.x = static_cast<const u32x4_t*>(y);

@@ -20,9 +20,10 @@ import torch
 
 _LIB_PATH = Path(os.environ.get("MAKO_H3_LIB", Path(__file__).resolve().parent.parent / "lib" / "libmako_h3.so"))
 
-ABI_VERSION = 3  # MH3_ABI_VERSION of include/mako_h3.h, whose structs this module mirrors
+ABI_VERSION = 4  # MH3_ABI_VERSION of include/mako_h3.h, whose structs this module mirrors
 OK, ERR_SHAPE, ERR_POINTER, ERR_ALIGN, ERR_PARAM, ERR_HIP, ERR_UNSUPPORTED = 0, -1, -2, -3, -4, -5, -6
 F32, BF16 = 0, 1
+ROWS_NORM_BF16, ROWS_Y_BF16 = 1, 2  # MH3RowsArgs.flags: the float stream's bf16 GEMM rows
 SWIGLU_SPLIT, SWIGLU_FUSED = 0, 1
 GEMM_W8A16, GEMM_BF16, GEMM_W8A8 = 0, 1, 2
 CUBES_GRID, CUBES_GATHERED = 0, 1
@@ -31,7 +32,7 @@ INT8_QKV, INT8_OUT, INT8_FC1, INT8_FC2, INT8_ALL = 1, 2, 4, 8, 15
 
 class RowsArgs(C.Structure):
     _fields_ = [("rows", C.c_uint32), ("dim", C.c_uint32), ("n_sets", C.c_uint32), ("dtype", C.c_uint32),
-                ("eps", C.c_float), ("set_stride", C.c_uint32), ("reserved", C.c_uint32 * 2)]
+                ("eps", C.c_float), ("set_stride", C.c_uint32), ("flags", C.c_uint32), ("reserved", C.c_uint32)]
 
 
 class SwigluArgs(C.Structure):
@@ -115,6 +116,7 @@ def _load() -> C.CDLL:
         "mh3_gemm_i8_swiglu": (I32, [C.POINTER(GemmArgs), P, P, P, P, P, P]),
         "mh3_gemm": (I32, [C.POINTER(GemmArgs), U32, P, P, P, P, P, P]),
         "mh3_gemm_gate_add": (I32, [C.POINTER(GemmArgs), U32, P, P, P, P, P, P, P, P]),
+        "mh3_gemm_gate_add_f32": (I32, [C.POINTER(GemmArgs), U32, P, P, P, P, P, P, P, P]),
     }
     for name, (res, args) in sig.items():
         f = getattr(lib, name)
@@ -235,23 +237,29 @@ def _mod_params(a, dim, n_sets, w, shift, scale, gate, set_of_row, rows):
         _need(set_of_row, "set_of_row", torch.uint8, rows)
 
 
-def rms_mod_rows(x, w, shift, scale, *, eps=1e-6, set_of_row=None, n_sets=1, out=None):
-    """y = x * rsqrt(mean(x^2) + eps) * w * (1 + scale[s]) + shift[s] per row (x: [rows][dim] f32 or bf16)."""
+def rms_mod_rows(x, w, shift, scale, *, eps=1e-6, set_of_row=None, n_sets=1, out=None, out_dtype=None):
+    """y = x * rsqrt(mean(x^2) + eps) * w * (1 + scale[s]) + shift[s] per row (x: [rows][dim] f32 or bf16). With a
+    float x and out_dtype bf16 (or a bf16 `out`), y is the bf16 row the next GEMM takes, rounded once."""
     a = _rows_args(x, n_sets, eps)
     _need(x, "x", x.dtype, x.numel())
     _mod_params(a, x.shape[1], n_sets, w, shift, scale, None, set_of_row, x.shape[0])
-    out = torch.empty_like(x) if out is None else out
-    _need(out, "out", x.dtype, x.numel())
+    odt = out.dtype if out is not None else (out_dtype or x.dtype)
+    if odt != x.dtype:
+        a.flags = ROWS_NORM_BF16
+    out = torch.empty(x.shape, dtype=odt, device=x.device) if out is None else out
+    _need(out, "out", odt, x.numel())
     _check(lib.mh3_rms_mod_rows(C.byref(a), _ptr(x), _ptr(w), _ptr(shift), _ptr(scale), _ptr(set_of_row), _ptr(out),
                                 _stream()), "rms_mod_rows")
     return out
 
 
 def gate_add_rows(x, y, gate, *, set_of_row=None, n_sets=1):
-    """x += gate[s] * y per row, in place; returns x."""
+    """x += gate[s] * y per row, in place; returns x. A float x may take a bf16 y (a GEMM's output)."""
     a = _rows_args(x, n_sets, 1.0)
     _need(x, "x", x.dtype, x.numel())
-    _need(y, "y", x.dtype, x.numel())
+    if y.dtype != x.dtype:
+        a.flags = ROWS_Y_BF16
+    _need(y, "y", y.dtype, x.numel())
     _mod_params(a, x.shape[1], n_sets, None, None, None, gate, set_of_row, x.shape[0])
     _check(lib.mh3_gate_add_rows(C.byref(a), _ptr(x), _ptr(y), _ptr(gate), _ptr(set_of_row), _stream()),
            "gate_add_rows")
@@ -271,15 +279,19 @@ def rms_mod_gate_add_rows(x, residual, w, shift, scale, gate, *, eps=1e-6, set_o
     return out
 
 
-def gate_add_rms_mod_rows(x, y, gate, w, shift, scale, *, eps=1e-6, set_of_row=None, n_sets=1, h=None):
+def gate_add_rms_mod_rows(x, y, gate, w, shift, scale, *, eps=1e-6, set_of_row=None, n_sets=1, h=None,
+                          h_dtype=None):
     """The block's order: x += gate[s] * y in place, then h = x * rsqrt(mean(x^2) + eps) * w * (1 + scale[s]) +
-    shift[s] of the updated x; one HBM pass. Returns h."""
+    shift[s] of the updated x; one HBM pass. Returns h. With a float x (the reference's float residual stream), h may
+    be bf16 (h_dtype, or a bf16 `h`: the next GEMM's input), and then y may be bf16 too (a GEMM's output)."""
     a = _rows_args(x, n_sets, eps)
     _need(x, "x", x.dtype, x.numel())
-    _need(y, "y", x.dtype, x.numel())
+    _need(y, "y", y.dtype, x.numel())
     _mod_params(a, x.shape[1], n_sets, w, shift, scale, gate, set_of_row, x.shape[0])
-    h = torch.empty_like(x) if h is None else h
-    _need(h, "h", x.dtype, x.numel())
+    hdt = h.dtype if h is not None else (h_dtype or x.dtype)
+    a.flags = (ROWS_NORM_BF16 if hdt != x.dtype else 0) | (ROWS_Y_BF16 if y.dtype != x.dtype else 0)
+    h = torch.empty(x.shape, dtype=hdt, device=x.device) if h is None else h
+    _need(h, "h", hdt, x.numel())
     _check(lib.mh3_gate_add_rms_mod_rows(C.byref(a), _ptr(x), _ptr(y), _ptr(gate), _ptr(w), _ptr(shift), _ptr(scale),
                                          _ptr(set_of_row), _ptr(h), _stream()), "gate_add_rms_mod_rows")
     return h
@@ -702,15 +714,18 @@ def gemm(x, w, *, x_scale=None, w_scale=None, out=None):
 
 
 def gemm_gate_add(x, w, residual, gate, *, x_scale=None, w_scale=None, set_of_row=None, n_sets=1):
-    """The out projection and fc2 with gate_add_rows folded in: residual += gate[s] * (x w^T), bf16 [m][n] in place,
-    s = set_of_row[row]; gate f32 [n_sets][n] (or a view with a set stride). Returns residual."""
+    """The out projection and fc2 with gate_add_rows folded in: residual += gate[s] * (x w^T), [m][n] in place,
+    s = set_of_row[row]; gate f32 [n_sets][n] (or a view with a set stride). residual is bf16, or float (the
+    reference's float residual stream). Returns residual."""
     a, form = _gemm_operands(x, w, x_scale, w_scale)
-    _need(residual, "residual", torch.bfloat16, a.m * a.n)
+    f32 = residual.dtype == torch.float32
+    _need(residual, "residual", torch.float32 if f32 else torch.bfloat16, a.m * a.n)
     stride = _set_stride(gate, "gate", a.n, n_sets)
     a.n_sets, a.gate_stride = n_sets, stride
     if set_of_row is not None:
         _need(set_of_row, "set_of_row", torch.uint8, a.m)
-    _check(lib.mh3_gemm_gate_add(C.byref(a), form, _ptr(x), _ptr(x_scale if form == GEMM_W8A8 else None), _ptr(w),
-                                 _ptr(w_scale if form != GEMM_BF16 else None), _ptr(gate), _ptr(set_of_row),
-                                 _ptr(residual), _stream()), "gemm_gate_add")
+    fn = lib.mh3_gemm_gate_add_f32 if f32 else lib.mh3_gemm_gate_add
+    _check(fn(C.byref(a), form, _ptr(x), _ptr(x_scale if form == GEMM_W8A8 else None), _ptr(w),
+              _ptr(w_scale if form != GEMM_BF16 else None), _ptr(gate), _ptr(set_of_row), _ptr(residual), _stream()),
+           "gemm_gate_add")
     return residual

@@ -89,33 +89,45 @@ static double inv_rms(uint32_t dim, float eps, int dtype, const void* x, uint64_
 
 /* docs/architecture.md:61: "RMS norm with weight times (1 + scale) plus shift, per row"; the row's set through
  * the offset table (architecture.md:49-52). */
-void mh3o_rms_mod_rows(uint32_t rows, uint32_t dim, float eps, int dtype, const void* x, const float* w,
-                       const float* shift, const float* scale, const uint8_t* set_of_row, void* y)
+void mh3o_rms_mod_rows2(uint32_t rows, uint32_t dim, float eps, int xdtype, int ydtype, const void* x, const float* w,
+                        const float* shift, const float* scale, const uint8_t* set_of_row, void* y)
 {
     for (uint64_t r = 0; r < rows; ++r) {
-        const double inv = inv_rms(dim, eps, dtype, x, r);
+        const double inv = inv_rms(dim, eps, xdtype, x, r);
         const uint64_t s = set_of_row ? set_of_row[r] : 0;
         const float* sh = shift + s * dim;
         const float* sc = scale + s * dim;
         for (uint32_t c = 0; c < dim; ++c) {
-            const double n = load(dtype, x, r * dim + c) * inv * (w ? (double)w[c] : 1.0);
-            store(dtype, y, r * dim + c, n * (1.0 + (double)sc[c]) + (double)sh[c]);
+            const double n = load(xdtype, x, r * dim + c) * inv * (w ? (double)w[c] : 1.0);
+            store(ydtype, y, r * dim + c, n * (1.0 + (double)sc[c]) + (double)sh[c]);
         }
     }
 }
 
+void mh3o_rms_mod_rows(uint32_t rows, uint32_t dim, float eps, int dtype, const void* x, const float* w,
+                       const float* shift, const float* scale, const uint8_t* set_of_row, void* y)
+{
+    mh3o_rms_mod_rows2(rows, dim, eps, dtype, dtype, x, w, shift, scale, set_of_row, y);
+}
+
 /* docs/architecture.md:64-65: "the output projection times the row's gate added back" (and the same after fc2). */
-void mh3o_gate_add_rows(uint32_t rows, uint32_t dim, int dtype, void* x, const void* y, const float* gate,
-                        const uint8_t* set_of_row)
+void mh3o_gate_add_rows2(uint32_t rows, uint32_t dim, int xdtype, int ydtype, void* x, const void* y,
+                         const float* gate, const uint8_t* set_of_row)
 {
     for (uint64_t r = 0; r < rows; ++r) {
         const uint64_t s = set_of_row ? set_of_row[r] : 0;
         const float* g = gate + s * dim;
         for (uint32_t c = 0; c < dim; ++c) {
             const uint64_t i = r * dim + c;
-            store(dtype, x, i, load(dtype, x, i) + (double)g[c] * load(dtype, y, i));
+            store(xdtype, x, i, load(xdtype, x, i) + (double)g[c] * load(ydtype, y, i));
         }
     }
+}
+
+void mh3o_gate_add_rows(uint32_t rows, uint32_t dim, int dtype, void* x, const void* y, const float* gate,
+                        const uint8_t* set_of_row)
+{
+    mh3o_gate_add_rows2(rows, dim, dtype, dtype, x, y, gate, set_of_row);
 }
 
 /* The fused form: out = residual + gate * modRMS(x), each output rounded once. */
@@ -504,7 +516,7 @@ void mh3o_gemm_i8_swiglu(uint32_t m, uint32_t n, uint32_t k, const int8_t* x, co
  * out += gate[s][col] * y with s = set_of_row[row] (NULL: 0), out bf16 in place, one rounding. */
 void mh3o_gemm(uint32_t m, uint32_t n, uint32_t k, int form, int epi, const void* x, const float* x_scale,
                const void* w, const float* w_scale, const float* gate, const uint8_t* set_of_row, uint32_t gate_stride,
-               uint16_t* out)
+               void* out)
 {
     double* xr = (double*)malloc(sizeof(double) * k);
     for (uint64_t r = 0; r < m; ++r) {
@@ -526,11 +538,14 @@ void mh3o_gemm(uint32_t m, uint32_t n, uint32_t k, int form, int epi, const void
                 if (form == 0)
                     y *= (double)w_scale[c];
             }
-            uint16_t* o = out + r * n + c;
+            uint16_t* o = (uint16_t*)out + r * n + c;
+            float* of = (float*)out + r * n + c;
             if (epi == 0)
                 *o = mh3o_bf16_from_double(y);
-            else
+            else if (epi == 1)
                 *o = mh3o_bf16_from_double((double)mh3o_bf16_to_float(*o) + (double)gate[set * gate_stride + c] * y);
+            else
+                *of = (float)((double)*of + (double)gate[set * gate_stride + c] * y);
         }
     }
     free(xr);

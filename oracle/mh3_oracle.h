@@ -76,6 +76,12 @@ void mh3o_rms_mod_rows(uint32_t rows, uint32_t dim, float eps, int dtype, const 
                        const float* shift, const float* scale, const uint8_t* set_of_row, void* y);
 void mh3o_gate_add_rows(uint32_t rows, uint32_t dim, int dtype, void* x, const void* y, const float* gate,
                         const uint8_t* set_of_row);
+/* The same with each row array's own element type: the reference's float residual stream (docs/architecture.md:
+ * 69-70) with bf16 GEMM rows, x float and y (the norm's output, or gate_add's addend) bf16. */
+void mh3o_rms_mod_rows2(uint32_t rows, uint32_t dim, float eps, int xdtype, int ydtype, const void* x, const float* w,
+                        const float* shift, const float* scale, const uint8_t* set_of_row, void* y);
+void mh3o_gate_add_rows2(uint32_t rows, uint32_t dim, int xdtype, int ydtype, void* x, const void* y,
+                         const float* gate, const uint8_t* set_of_row);
 void mh3o_rms_mod_gate_add_rows(uint32_t rows, uint32_t dim, float eps, int dtype, const void* x, const void* residual,
                                 const float* w, const float* shift, const float* scale, const float* gate,
                                 const uint8_t* set_of_row, void* out);
@@ -125,10 +131,11 @@ void mh3o_gemm_bf16_swiglu(uint32_t m, uint32_t n, uint32_t k, const uint16_t* x
 void mh3o_gemm_i8_swiglu(uint32_t m, uint32_t n, uint32_t k, const int8_t* x, const float* x_scale, const int8_t* w,
                          const float* w_scale, uint16_t* out);
 /* The qkv / out / fc2 projections: y = x w^T, w [n][k]; form 0 W8A16 (w int8 + w_scale), 1 bf16, 2 W8A8 (x int8 +
- * x_scale, w int8 + w_scale). epi 0: out = y; epi 1: out += gate[set][col] * y in place (the gate_add_rows epilogue). */
+ * x_scale, w int8 + w_scale). epi 0: out = y (bf16); epi 1: out += gate[set][col] * y in place (the gate_add_rows
+ * epilogue, bf16 out); epi 2: the same on a float out (the reference's float residual stream). */
 void mh3o_gemm(uint32_t m, uint32_t n, uint32_t k, int form, int epi, const void* x, const float* x_scale,
                const void* w, const float* w_scale, const float* gate, const uint8_t* set_of_row, uint32_t gate_stride,
-               uint16_t* out);
+               void* out);
 
 /* H3::Cubes' map: attention row -> model row (-1 for padding), then the dense rows; counts per cube (may be NULL).
  * Returns the number of map entries. */

@@ -59,6 +59,8 @@ _lib.mh3o_gemm_w8a16_swiglu.argtypes = [C.c_uint32] * 3 + [_P] * 4
 _lib.mh3o_gemm_bf16_swiglu.argtypes = [C.c_uint32] * 3 + [_P] * 3
 _lib.mh3o_gemm_i8_swiglu.argtypes = [C.c_uint32] * 3 + [_P] * 5
 _lib.mh3o_gemm.argtypes = [C.c_uint32] * 3 + [C.c_int] * 2 + [_P] * 6 + [C.c_uint32, _P]
+_lib.mh3o_rms_mod_rows2.argtypes = [C.c_uint32, C.c_uint32, C.c_float, C.c_int, C.c_int] + [_P] * 6
+_lib.mh3o_gate_add_rows2.argtypes = [C.c_uint32, C.c_uint32, C.c_int, C.c_int] + [_P] * 4
 _lib.mh3o_cube_map.restype = C.c_int64
 _lib.mh3o_cube_map.argtypes = [C.c_uint32] * 4 + [C.c_uint64, C.c_uint64, _P, _P]
 _lib.mh3o_time_embed.argtypes = [C.c_uint32] * 4 + [C.c_double] + [_P] * 7
@@ -105,17 +107,21 @@ def bf16_from_float(f: float) -> int:
 
 # ---- rows ------------------------------------------------------------------------------------------------------------
 
-def rms_mod_rows(x, w, shift, scale, eps=1e-6, set_of_row=None):
+def rms_mod_rows(x, w, shift, scale, eps=1e-6, set_of_row=None, out_dtype=None):
+    """x float32 or bf16 bits; y of x's type, or of out_dtype (np.uint16: bf16 bits) for a float x."""
     rows, dim = x.shape
-    y = np.empty_like(x)
-    _lib.mh3o_rms_mod_rows(rows, dim, eps, _dtype_code(x), _p(x), _p(w), _p(shift), _p(scale), _p(set_of_row), _p(y))
+    y = np.empty(x.shape, out_dtype or x.dtype)
+    _lib.mh3o_rms_mod_rows2(rows, dim, eps, _dtype_code(x), _dtype_code(y), _p(x), _p(w), _p(shift), _p(scale),
+                            _p(set_of_row), _p(y))
     return y
 
 
 def gate_add_rows(x, y, gate, set_of_row=None):
+    """x + gate * y, in x's type (y may be bf16 bits with a float x)."""
     x = x.copy()
     rows, dim = x.shape
-    _lib.mh3o_gate_add_rows(rows, dim, _dtype_code(x), _p(x), _p(y), _p(gate), _p(set_of_row))
+    _lib.mh3o_gate_add_rows2(rows, dim, _dtype_code(x), _dtype_code(y), _p(x), _p(np.ascontiguousarray(y)), _p(gate),
+                             _p(set_of_row))
     return x
 
 
@@ -266,13 +272,15 @@ def gemm(x, w, form, x_scale=None, w_scale=None):
 
 
 def gemm_gate_add(x, w, form, residual, gate, x_scale=None, w_scale=None, set_of_row=None):
-    """residual + gate[set(row)] * (x w^T), one rounding to bf16 bits; gate f32 [n_sets][n] (or [n])."""
+    """residual + gate[set(row)] * (x w^T), one rounding to bf16 bits (or to float for a float32 residual); gate f32
+    [n_sets][n] (or [n])."""
     m, k = x.shape
     n = w.shape[0]
-    out = np.array(residual, dtype=np.uint16, copy=True, order="C")
+    f32 = np.asarray(residual).dtype == np.float32
+    out = np.array(residual, dtype=np.float32 if f32 else np.uint16, copy=True, order="C")
     c = np.ascontiguousarray
     g = c(gate, dtype=np.float32).reshape(-1, n)
-    _lib.mh3o_gemm(m, n, k, form, 1, _p(c(x)), _p(None if x_scale is None else c(x_scale, dtype=np.float32)),
+    _lib.mh3o_gemm(m, n, k, form, 2 if f32 else 1, _p(c(x)), _p(None if x_scale is None else c(x_scale, dtype=np.float32)),
                    _p(c(w)), _p(None if w_scale is None else c(w_scale, dtype=np.float32)), _p(g),
                    _p(None if set_of_row is None else c(set_of_row, dtype=np.uint8)), n, _p(out))
     return out

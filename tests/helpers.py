@@ -115,7 +115,8 @@ def check_rows_f64(got: torch.Tensor, want: torch.Tensor, what: str, rtol=1e-2, 
 
 
 def check_gemm_full(out: torch.Tensor, x: torch.Tensor, w: torch.Tensor, what: str, *, x_scale=None, w_scale=None,
-                    epi: str = "store", residual0=None, gate=None, set_of_row=None, chunk: int = 4096):
+                    epi: str = "store", residual0=None, gate=None, set_of_row=None, chunk: int = 4096,
+                    rtol: float = 1e-2, row_frac: float = 1e-4):
     """Every element of a GEMM's output against float64 products on the GPU over the same operands, row chunk by row
     chunk: y = (x * x_scale[row]) (w * w_scale[col])^T, then epi "store" (out = y), "swiglu" (out = silu(y[:, :n]) *
     y[:, n:], n = out's width) or "gate_add" (out = residual0 + gate[set_of_row[row]] * y)."""
@@ -142,6 +143,95 @@ def check_gemm_full(out: torch.Tensor, x: torch.Tensor, w: torch.Tensor, what: s
             want = residual0[r0:r1].double() + gr * y
         else:
             want = y
-        rel, cos = check_rows_f64(out[r0:r1], want, f"{what} rows {r0}..{r1 - 1}")
+        rel, cos = check_rows_f64(out[r0:r1], want, f"{what} rows {r0}..{r1 - 1}", rtol, row_frac)
         worst_rel, worst_cos = max(worst_rel, rel), min(worst_cos, cos)
     return worst_rel, worst_cos
+
+
+# ---- sparse attention on the GPU, in float32 -------------------------------------------------------------------------
+
+def cube_rows_table(grid, layout: int, row0: int, device) -> torch.Tensor:
+    """int64 [cubes][64]: the row of cube c's slot l = (dt * 4 + dy) * 4 + dx, or -1 where (4 ct + dt, 4 cy + dy,
+    4 cx + dx) lies in the padding past the grid. layout 0 (grid): the token's row in the model's frame-major order;
+    layout 1 (gathered): row0 + 64 c + l."""
+    gt, gh, gw = grid
+    ct_n, ch, cw = (gt + 3) // 4, (gh + 3) // 4, (gw + 3) // 4
+    c = torch.arange(ct_n * ch * cw, device=device)[:, None]
+    slot = torch.arange(64, device=device)[None, :]
+    t = 4 * (c // (ch * cw)) + slot // 16
+    y = 4 * (c // cw % ch) + slot // 4 % 4
+    x = 4 * (c % cw) + slot % 4
+    inside = (t < gt) & (y < gh) & (x < gw)
+    row = row0 + 64 * c + slot if layout == 1 else row0 + (t * gh + y) * gw + x
+    return torch.where(inside, row, torch.full_like(row, -1))
+
+
+def attn_sparse_f32(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, idx: torch.Tensor, cnt: torch.Tensor, grid,
+                    dense_row0: int, n_dense: int, *, layout: int = 0, row0: int = 0, heads=None, cubes=None,
+                    dense: bool = True, scale: float | None = None, chunk: int = 64) -> dict:
+    """flash_attn_sparse_128's semantics restated with torch in float32 on the GPU, for checking whole launches.
+    q, k, v: bf16 [heads][rows][128]; idx int32 [heads][cubes][stride], cnt int32 [heads][cubes] (entries past cnt,
+    and entries outside [0, cubes), are skipped). The queries of cube c attend the tokens of its listed cubes and the
+    dense rows; a dense row's query attends every token and every dense row. Returns {h: (rows, out)} for each head
+    of `heads` (default all): the rows computed (the dense rows when `dense`, then the tokens of the query cubes
+    `cubes`, default all) and float32 [len(rows)][128] results."""
+    scale = 1.0 / 128 ** 0.5 if scale is None else scale
+    dev = q.device
+    table = cube_rows_table(grid, layout, row0, dev)
+    n_cubes = table.shape[0]
+    tokens = table[table >= 0]
+    drows = torch.arange(dense_row0, dense_row0 + n_dense, device=dev)
+    every_key = torch.cat([tokens, drows])
+    cubes = torch.arange(n_cubes, device=dev) if cubes is None else torch.as_tensor(cubes, device=dev).long()
+    res = {}
+    for h in (range(q.shape[0]) if heads is None else heads):
+        Q, K, V = q[h].float(), k[h].float(), v[h].float()
+        rows_out, outs = [], []
+        if dense and n_dense:
+            s = (Q[drows] @ K[every_key].t().contiguous()) * scale
+            outs.append(torch.softmax(s, -1) @ V[every_key])
+            rows_out.append(drows)
+        stride = idx.shape[2]
+        for c0 in range(0, len(cubes), chunk):
+            cs = cubes[c0:c0 + chunk]
+            lists = idx[h, cs].long()                                        # [B][stride]
+            live = (torch.arange(stride, device=dev)[None, :] < cnt[h, cs].long().clamp(0, stride)[:, None]) & \
+                (lists >= 0) & (lists < n_cubes)
+            kr = table[lists.clamp(0, n_cubes - 1)]                          # [B][stride][64]
+            key_ok = (live[..., None] & (kr >= 0)).flatten(1)
+            kr = kr.flatten(1)
+            if n_dense:
+                kr = torch.cat([kr, drows[None, :].expand(len(cs), -1)], 1)
+                key_ok = torch.cat([key_ok, torch.ones((len(cs), n_dense), dtype=torch.bool, device=dev)], 1)
+            kr = kr.clamp_min(0)
+            qr = table[cs]                                                   # [B][64]
+            qv = Q[qr.clamp_min(0)]                                          # [B][64][128]
+            s = torch.bmm(qv, K[kr].transpose(1, 2).contiguous()) * scale    # [B][64][L]
+            s = s.masked_fill(~key_ok[:, None, :], float("-inf"))
+            o = torch.bmm(torch.softmax(s, -1), V[kr])                       # [B][64][128]
+            tok = qr >= 0
+            rows_out.append(qr[tok])
+            outs.append(o[tok])
+        res[h] = (torch.cat(rows_out), torch.cat(outs))
+    return res
+
+
+def check_attn_f32(got: torch.Tensor, ref: dict, what: str, elem_row=1e-2, row_rms=6e-3):
+    """Sparse-attention outputs (bf16 [heads][rows][128]) against attn_sparse_f32's results, every listed row:
+    finite; each element within 1e-2 of itself plus `elem_row` of its row's RMS; each row's RMS error within `row_rms`
+    of the row's RMS. The bf16 P operand of the P V product rounds each probability by up to 2^-9 relative, and the
+    output's own bf16 rounding adds as much: together about 3e-3 of a row's RMS, spread over its 128 values.
+    Returns (worst element error / row RMS, worst row RMS error / row RMS)."""
+    worst_e, worst_r = 0.0, 0.0
+    for h, (rows, want) in ref.items():
+        g = got[h, rows].float()
+        assert bool(torch.isfinite(g).all()), f"{what} head {h}: non-finite outputs (an unwritten element)"
+        rms = want.pow(2).mean(1, keepdim=True).sqrt().clamp_min(1e-30)
+        err = (g - want).abs()
+        bad = err > 1e-2 * want.abs() + elem_row * rms
+        assert not bool(bad.any()), \
+            f"{what} head {h}: {int(bad.sum())} elements beyond tolerance, worst {float((err / rms).max()):.3g} of rms"
+        rerr = err.pow(2).mean(1, keepdim=True).sqrt() / rms
+        assert bool((rerr <= row_rms).all()), f"{what} head {h}: row RMS error {float(rerr.max()):.3g} of the row's RMS"
+        worst_e, worst_r = max(worst_e, float((err / rms).max())), max(worst_r, float(rerr.max()))
+    return worst_e, worst_r

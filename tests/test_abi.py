@@ -47,10 +47,10 @@ def test_stream_probe_library_loads_and_refuses_bad_calls():
 
 
 def test_abi_version_and_strings():
-    assert mh.lib.mh3_abi_version() == 3
+    assert mh.lib.mh3_abi_version() == 4
     # The Python structs mirror the header: its MH3_ABI_VERSION is the module's (import refuses another library's).
     header = (Path(__file__).resolve().parent.parent / "include" / "mako_h3.h").read_text()
-    assert re.search(r"#define MH3_ABI_VERSION (\d+)", header).group(1) == str(mh.ABI_VERSION) == "3"
+    assert re.search(r"#define MH3_ABI_VERSION (\d+)", header).group(1) == str(mh.ABI_VERSION) == "4"
     assert mh.strerror(mh.ERR_SHAPE) == "bad shape"
     assert mh.strerror(123) == "unknown error"
 
@@ -477,3 +477,46 @@ def test_heads_partial_pool_validation():
     assert call(q=base) == mh.ERR_PARAM                                  # q on qkv, not in place
     assert call(cos=base + 2**35 + 1024) == mh.ERR_PARAM                 # the cos table inside k
     assert call(map=base + 2**34 + 256) == mh.ERR_PARAM                  # the map inside q
+
+
+@pytest.mark.parametrize("call,kw,code", [
+    ("rms_mod", {"flags": mh.ROWS_NORM_BF16}, mh.ERR_PARAM),                       # a flag with a bf16 stream
+    ("rms_mod", {"dtype": mh.F32, "flags": 4}, mh.ERR_PARAM),                      # an unknown flag
+    ("rms_mod", {"dtype": mh.F32, "flags": mh.ROWS_Y_BF16}, mh.ERR_PARAM),         # no y to take
+    ("gate_add", {"dtype": mh.F32, "flags": mh.ROWS_NORM_BF16}, mh.ERR_PARAM),     # no norm to give
+    ("fused", {"dtype": mh.F32, "flags": mh.ROWS_NORM_BF16}, mh.ERR_PARAM),        # the fused op takes none
+    ("order", {"dtype": mh.F32, "flags": mh.ROWS_Y_BF16}, mh.ERR_PARAM),           # a bf16 y needs a bf16 h
+    ("rms_mod", {"dtype": mh.F32, "flags": mh.ROWS_NORM_BF16, "dim": 6152}, mh.ERR_UNSUPPORTED),
+    ("rms_mod", {"dtype": mh.F32, "flags": mh.ROWS_NORM_BF16, "dim": 5124}, mh.ERR_SHAPE),
+])
+def test_float_stream_flags_validation(call, kw, code):
+    """The float residual stream's flags: only with a float stream, only where the entry point takes them, and within
+    the widths its kernel holds."""
+    a = rows_args(**kw)
+    if call == "rms_mod":
+        rc = mh.lib.mh3_rms_mod_rows(C.byref(a), FAKE, FAKE, FAKE, FAKE, None, C.c_void_p(0x10000000), None)
+    elif call == "gate_add":
+        rc = mh.lib.mh3_gate_add_rows(C.byref(a), FAKE, C.c_void_p(0x10000000), FAKE, None, None)
+    elif call == "fused":
+        rc = mh.lib.mh3_rms_mod_gate_add_rows(C.byref(a), FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, None,
+                                              C.c_void_p(0x10000000), None)
+    else:
+        rc = mh.lib.mh3_gate_add_rms_mod_rows(C.byref(a), FAKE, C.c_void_p(0x10000000), FAKE, FAKE, FAKE, FAKE, None,
+                                              C.c_void_p(0x20000000), None)
+    assert rc == code
+
+
+def test_float_stream_outputs_may_not_share_the_float_rows():
+    """A bf16 output may not sit on the float x, not even at its start (its rows are half as long, so they race the
+    float rows); the float residual of the GEMM epilogue may not overlap x."""
+    a = rows_args(rows=64, dim=5120, dtype=mh.F32, flags=mh.ROWS_NORM_BF16)
+    x, v = C.c_void_p(0x1000000), C.c_void_p(0x9000000)
+    assert mh.lib.mh3_rms_mod_rows(C.byref(a), x, v, v, v, None, x, None) == mh.ERR_PARAM
+    assert mh.lib.mh3_rms_mod_rows(C.byref(a), x, v, v, v, None, C.c_void_p(0x1000000 + 64 * 5120 * 4 - 16),
+                                   None) == mh.ERR_PARAM
+    g = mh.GemmArgs()
+    g.m, g.n, g.k = 512, 256, 512
+    xg, wg = C.c_void_p(0x1000000), C.c_void_p(0x2000000)
+    inside_x = C.c_void_p(0x1000000 + 512 * 512 * 2 - 16)   # the residual's first float4 on x's last bytes
+    assert mh.lib.mh3_gemm_gate_add_f32(C.byref(g), mh.GEMM_BF16, xg, None, wg, None, v, None, inside_x, None) == \
+        mh.ERR_PARAM

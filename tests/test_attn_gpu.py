@@ -8,7 +8,8 @@ import torch
 
 import mako_h3 as mh
 import oracle as orc
-from helpers import bits_to_f64, diff, from_bits, randn_bf16_bits, to_bits
+from helpers import (attn_sparse_f32, bits_to_f64, check_attn_f32, diff, from_bits, nan_filled, randn_bf16_bits,
+                     to_bits)
 
 pytestmark = pytest.mark.gpu
 
@@ -56,6 +57,17 @@ def test_flash_attn_sparse_matches_oracle(dev, grid, layout, row0, dense_row0, n
     want = orc.attn_sparse(q, k, v, idx, cnt, grid, dense_row0, n_dense, layout, row0)
     got = run(dev, q, k, v, idx, cnt, grid, layout, row0, dense_row0, n_dense)
     check(got, want, f"attn {grid} layout {layout}")
+    # The float32 GPU restatement the whole-launch tests use agrees with the oracle (rounded to bf16) on every row.
+    t = lambda x: torch.from_numpy(np.ascontiguousarray(x)).to(dev)  # noqa: E731
+    ref = attn_sparse_f32(from_bits(q, dev), from_bits(k, dev), from_bits(v, dev), t(idx), t(cnt), grid, dense_row0,
+                          n_dense, layout=layout, row0=row0)
+    w64 = torch.from_numpy(bits_to_f64(want)).to(dev)
+    for h, (rows, out) in ref.items():
+        w = w64[h, rows]
+        rms = w.pow(2).mean(1, keepdim=True).sqrt()
+        # within the oracle's one bf16 rounding (half a unit in the last place: 2^-8 relative at most)
+        assert bool(((out.double() - w).abs() <= (2 ** -8 + 1e-5) * w.abs() + 1e-4 * rms).all()), \
+            f"f32 restatement head {h}"
     if layout == orc.CUBES_GATHERED:
         vrow = np.concatenate([orc.attn_tile_rows(grid, layout, row0, dense_row0, n_dense, (n_dense + 63) // 64 + c)
                                for c in range(C)])
@@ -155,11 +167,50 @@ def test_flash_attn_sparse_768p_sampled(dev):
         check(ob[h, r], want[h, r], f"768p head {h} tile {tile}")
 
 
+def test_flash_attn_sparse_rotated_walk_every_tile(dev):
+    """Enough cube tiles an XCD that most walk their pass lists from a rotated start: 160 heads of a 16 x 16 x 16 grid
+    (64 cubes, one dense tile), so each XCD runs 1280 cube tiles in sequence, and tiles from the fourth round of the
+    XCD's resident workgroups on (rank 512 and up at 4 workgroups a CU on 256 CUs) start a fraction of the way into
+    their lists. Every output row against the float32 restatement, the output buffer NaN-filled first; a sample of
+    rotated tiles against the oracle."""
+    grid, heads, n_dense = (16, 16, 16), 160, 64
+    video = 16 * 16 * 16
+    rows = video + n_dense
+    C = orc.cube_count(*grid)
+    g = torch.Generator(device=dev).manual_seed(41)
+    q, k, v = [torch.randn((heads, rows, 128), generator=g, device=dev).to(torch.bfloat16) for _ in range(3)]
+    rng = np.random.default_rng(42)
+    idx_n, cnt_n = orc.cube_topk(rng.standard_normal((heads, C, C)), grid, 6, 1, out_stride=8)
+    idx, cnt = torch.from_numpy(idx_n).to(dev), torch.from_numpy(cnt_n).to(dev)
+    a = mh.cube_args(heads, grid, head_stride=rows * 128, out_stride=8)
+    out = mh.flash_attn_sparse_128(a, q, k, v, idx, cnt, dense_row0=video, n_dense=n_dense,
+                                   out=nan_filled((heads, rows, 128), dev))
+    torch.cuda.synchronize()
+    assert bool(torch.isfinite(out).all()), "an output row left unwritten"
+    worst = (0.0, 0.0)
+    for h0 in range(0, heads, 40):
+        ref = attn_sparse_f32(q, k, v, idx, cnt, grid, video, n_dense, heads=range(h0, h0 + 40), chunk=1024)
+        e, r = check_attn_f32(out, ref, "rotated walk")
+        worst = (max(worst[0], e), max(worst[1], r))
+    print(f"rotated walk: worst element error {worst[0]:.3g}, worst row RMS error {worst[1]:.3g} of the row's RMS")
+    # Oracle: two cube tiles of each of the last eight heads (XCD ranks well past 512), every XCD slice covered.
+    hs = list(range(heads - 8, heads))
+    tiles = [(j, 1 + ((j % 8) * C) // 8 + int(rng.integers(0, C // 8))) for j in range(8)]
+    tiles += [(j, 1 + int(rng.integers(0, C))) for j in range(8)]
+    sub = lambda x: to_bits(x[hs])  # noqa: E731
+    qb, kb, vb, ob = sub(q), sub(k), sub(v), sub(out)
+    want = orc.attn_sparse(qb, kb, vb, idx_n[hs], cnt_n[hs], grid, video, n_dense, tiles=tiles)
+    for lh, tile in tiles:
+        r = orc.attn_tile_rows(grid, orc.CUBES_GRID, 0, video, n_dense, tile)
+        check(ob[lh, r], want[lh, r], f"rotated walk: head {hs[lh]} tile {tile}")
+
+
 def test_flash_attn_sparse_768p_40_heads(dev):
     """The launch bench.py times: 40 heads of the 768p shape (2016 cubes, 512 text rows after the video rows), whose
     tile count lets each XCD take a contiguous eighth of every head's query cubes with rotated pass lists, the pass
-    lists from cube_select at ratio 0.1 (k = 202), local 1. Every output is finite, and tiles of every head --
-    one dense tile of each fifth head, cube tiles spread over all XCD slices -- against the oracle."""
+    lists from cube_select at ratio 0.1 (k = 202), local 1. The output buffer is NaN-filled first and every row is
+    finite after; every dense tile and the cube tiles of three whole heads against the float32 restatement; tiles of
+    every head -- one dense tile of each fifth head, cube tiles spread over all XCD slices -- against the oracle."""
     grid, heads, n_dense = (32, 48, 84), 40, 512
     video = 32 * 48 * 84
     rows = video + n_dense
@@ -177,9 +228,24 @@ def test_flash_attn_sparse_768p_40_heads(dev):
     a = mh.cube_args(heads, grid, head_stride=rows * 128, k=kk, local=1)
     qc, kc = mh.cube_pool(a, q, k)
     idx, cnt = mh.cube_select(a, qc, kc)
-    out = mh.flash_attn_sparse_128(a, q, k, v, idx, cnt, dense_row0=video, n_dense=n_dense)
+    out = mh.flash_attn_sparse_128(a, q, k, v, idx, cnt, dense_row0=video, n_dense=n_dense,
+                                   out=nan_filled((heads, rows, 128), dev))
     torch.cuda.synchronize()
-    assert bool(torch.isfinite(out).all())
+    assert bool(torch.isfinite(out).all()), "an output row left unwritten"
+    # Every dense tile of every head, and every cube tile of three whole heads (head 0's tiles are among each XCD's
+    # first, which walk their lists unrotated; heads 2 and 39 are past the fourth round and rotated), against the
+    # float32 restatement.
+    worst = (0.0, 0.0)
+    for h0 in range(0, heads, 8):
+        ref = attn_sparse_f32(q, k, v, idx, cnt, grid, video, n_dense, heads=range(h0, h0 + 8),
+                              cubes=torch.empty(0, dtype=torch.long))
+        e, r = check_attn_f32(out, ref, "768p dense tiles")
+        worst = (max(worst[0], e), max(worst[1], r))
+    for h in (0, 2, heads - 1):
+        ref = attn_sparse_f32(q, k, v, idx, cnt, grid, video, n_dense, heads=[h], dense=False)
+        e, r = check_attn_f32(out, ref, "768p cube tiles")
+        worst = (max(worst[0], e), max(worst[1], r))
+    print(f"768p 40 heads: worst element error {worst[0]:.3g}, worst row RMS error {worst[1]:.3g} of the row's RMS")
     nd = n_dense // 64
     rng = np.random.default_rng(16)
     # cube c of head h lands in XCD slice c * 8 // C; cover every slice across the heads

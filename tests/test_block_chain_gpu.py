@@ -198,3 +198,70 @@ def test_one_block_in_the_models_row_order(dev):
     rel, cos = diff(bits_to_f64(to_bits(x2)), bits_to_f64(ox2), D)
     print(f"whole block in the model's rows against the oracle's chain: rel {rel:.3g}, min row cos {cos:.7f}")
     assert rel < 2e-3 and cos > 0.99999, f"whole block (model's rows): rel {rel:.3g} cos {cos:.7f}"
+
+
+@pytest.mark.parametrize("order", ["epilogue", "block_order"])
+def test_one_block_on_the_float_residual_stream(dev, order):
+    """The block in the reference's numerics (docs/architecture.md:69-70): the residual stream x stays float and only
+    the GEMMs' inputs are bf16, with no cast pass. rms_mod_rows turns the float x into the bf16 row the QKV GEMM and
+    fc1 take; the out projection and fc2 add gate * y into the float x in their epilogue ("epilogue"), or the out
+    projection stores a bf16 y and gate_add_rms_mod_rows adds it into the float x and gives fc1's bf16 row in one pass
+    ("block_order"). Rows in the model's order, as bench.py's block leg runs them. The whole block against the oracle's
+    chain on the same float stream, by the reference's comparison metric."""
+    rng = np.random.default_rng(47)
+    t = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(dev)  # noqa: E731
+    npv = lambda a: a.cpu().numpy()  # noqa: E731
+    video = GRID[0] * GRID[1] * GRID[2]
+    rows = video + N_DENSE
+
+    def w8(n, k):
+        return mh.quant_rows_i8(t((0.05 * rng.standard_normal((n, k))).astype(np.float32)))
+    wqkv, sqkv = w8(3 * HEADS * 128, D)
+    wo, so = w8(D, HEADS * 128)
+    w1, s1 = w8(2 * FFN, D)
+    w2, s2 = w8(D, FFN)
+    n1, n2 = [(1 + 0.02 * rng.standard_normal(D)).astype(np.float32) for _ in range(2)]
+    sh_a, sc_a, ga_a, sh_m, sc_m, ga_m = [(0.1 * rng.standard_normal((1, D))).astype(np.float32) for _ in range(6)]
+    qw, kw = [(1 + 0.1 * rng.standard_normal(128)).astype(np.float32) for _ in range(2)]
+    ang = rng.uniform(-np.pi, np.pi, (rows, ROT // 2))
+    cs, sn = np.cos(ang).astype(np.float32), np.sin(ang).astype(np.float32)
+    x0 = rng.standard_normal((rows, D)).astype(np.float32)
+
+    x = t(x0)
+    bf = torch.bfloat16
+    h = mh.rms_mod_rows(x, t(n1), t(sh_a[0]), t(sc_a[0]), out_dtype=bf)
+    qkv = mh.gemm(h, wqkv, w_scale=sqkv)
+    q, k, v, qc, kc = mh.heads_partial_pool(qkv, HEADS, GRID, t(qw), t(kw), t(cs), t(sn), rot=ROT, layout="rows",
+                                            cube_layout=mh.CUBES_GRID)
+    kk = mh.topk_k(0.25, mh.cube_count(*GRID))
+    a = mh.cube_args(HEADS, GRID, head_stride=128, row_stride=HEADS * 128, k=kk, local=1)
+    idx, cnt = mh.cube_select(a, qc, kc)
+    att = mh.flash_attn_sparse_128(a, q, k, v, idx, cnt, dense_row0=video, n_dense=N_DENSE)
+    if order == "epilogue":
+        mh.gemm_gate_add(att, wo, x, t(ga_a[0]), w_scale=so)
+        h2 = mh.rms_mod_rows(x, t(n2), t(sh_m[0]), t(sc_m[0]), out_dtype=bf)
+    else:
+        y = mh.gemm(att, wo, w_scale=so)
+        h2 = mh.gate_add_rms_mod_rows(x, y, t(ga_a[0]), t(n2), t(sh_m[0]), t(sc_m[0]), h_dtype=bf)
+    assert x.dtype == torch.float32 and h2.dtype == bf
+    f = mh.gemm_w8a16_swiglu(h2, w1, s1)
+    mh.gemm_gate_add(f, w2, x, t(ga_m[0]), w_scale=s2)
+
+    # The oracle's chain on the same float stream, on the GPU's selection.
+    row = lambda a_: a_.reshape(1, D)  # noqa: E731
+    oh = orc.rms_mod_rows(x0, n1, row(sh_a), row(sc_a), out_dtype=np.uint16)
+    oqkv = orc.gemm(oh, npv(wqkv), orc.GEMM_W8A16, w_scale=npv(sqkv))
+    oq, ok, ov = orc.heads_partial(oqkv, HEADS, qw, kw, cs, sn, rot=ROT)
+    oatt = orc.attn_sparse(oq, ok, ov, npv(idx), npv(cnt), GRID, video, N_DENSE, layout=orc.CUBES_GRID)
+    oatt_rows = np.ascontiguousarray(oatt.transpose(1, 0, 2)).reshape(rows, HEADS * 128)
+    if order == "epilogue":
+        ox1 = orc.gemm_gate_add(oatt_rows, npv(wo), orc.GEMM_W8A16, x0, ga_a, w_scale=npv(so))
+    else:
+        ox1 = orc.gate_add_rows(x0, orc.gemm(oatt_rows, npv(wo), orc.GEMM_W8A16, w_scale=npv(so)), ga_a)
+    oh2 = orc.rms_mod_rows(ox1, n2, row(sh_m), row(sc_m), out_dtype=np.uint16)
+    of = orc.gemm_w8a16_swiglu(oh2, npv(w1), npv(s1))
+    ox2 = orc.gemm_gate_add(of, npv(w2), orc.GEMM_W8A16, ox1, ga_m, w_scale=npv(s2))
+    assert ox2.dtype == np.float32
+    rel, cos = diff(npv(x).astype(np.float64), ox2.astype(np.float64), D)
+    print(f"whole block on the float stream ({order}) against the oracle's chain: rel {rel:.3g}, min row cos {cos:.7f}")
+    assert rel < 2e-3 and cos > 0.99999, f"whole block, float stream ({order}): rel {rel:.3g} cos {cos:.7f}"

@@ -406,3 +406,41 @@ def test_golden_fixtures_reproduce():
         got = make_golden.run_case(case, data)
         for name, arr in got.items():
             assert (arr == data[name]).all(), f"{case['name']}: {name} changed"
+
+
+# ---- the float residual stream with bf16 GEMM rows ------------------------------------------------------------------
+
+def test_rms_mod_rows_float_to_bf16_is_rounded_float64():
+    """A float x normed into the bf16 row a GEMM takes: torch's float64 rms_norm restatement, rounded once to bf16
+    (within half a bf16 step of it, and equal to torch's own rounding nearly everywhere); set rows pick their sets."""
+    rng = np.random.default_rng(40)
+    x = rng.standard_normal((48, 768)).astype(np.float32)
+    w, shift, scale, _ = params(rng, 768, 3)
+    sets = rng.integers(0, 3, 48).astype(np.uint8)
+    got = orc.rms_mod_rows(x, w, shift, scale, 1e-6, sets, out_dtype=np.uint16)
+    assert got.dtype == np.uint16
+    want = torch_mod_rms(x.astype(np.float64), w, shift[sets], scale[sets], 1e-6)
+    g = bits_to_f64(got)
+    assert np.all(np.abs(g - want) <= 2 ** -8 * np.abs(want) + 1e-30)
+    tb = torch.from_numpy(want).to(torch.bfloat16).view(torch.int16).numpy().view(np.uint16)
+    assert (got == tb).mean() > 0.999
+    # the float output of the same rows, rounded to bf16, is the same row (one rounding either way, from double)
+    f = orc.rms_mod_rows(x, w, shift, scale, 1e-6, sets)
+    assert np.abs(bits_to_f64(got) - f.astype(np.float64)).max() <= 2 ** -8 * np.abs(f).max()
+
+
+def test_gate_add_rows_float_x_bf16_y():
+    """x (float) += gate * y (bf16): y's bf16 values decoded exactly (gate 1 and x 0 give y's values bit for bit),
+    gate 0 leaves x bit-exact, and the sum matches float64 within half a float step."""
+    rng = np.random.default_rng(41)
+    x = rng.standard_normal((16, 512)).astype(np.float32)
+    y = randn_bf16_bits(rng, (16, 512))
+    gate = (0.1 * rng.standard_normal((2, 512))).astype(np.float32)
+    sets = rng.integers(0, 2, 16).astype(np.uint8)
+    got = orc.gate_add_rows(x, y, gate, sets)
+    assert got.dtype == np.float32
+    want = x.astype(np.float64) + gate[sets].astype(np.float64) * bits_to_f64(y)
+    assert np.all(np.abs(got - want) <= 2 ** -24 * np.abs(want))
+    assert (orc.gate_add_rows(x, y, np.zeros_like(gate), sets) == x).all()
+    ones = np.ones((1, 512), np.float32)
+    assert (orc.gate_add_rows(np.zeros_like(x), y, ones) == bits_to_f64(y).astype(np.float32)).all()

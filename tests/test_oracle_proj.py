@@ -79,3 +79,20 @@ def test_gemm_gate_add_epilogue():
     assert np.all(np.abs(g - t) <= 2 ** -8 * (np.abs(t) + np.abs(g) + gy) + 1e-30)
     zero = orc.gemm_gate_add(x, w, orc.GEMM_W8A16, res, np.zeros(n, np.float32), None, ws)
     assert np.array_equal(zero, res)
+
+
+def test_gemm_gate_add_float_residual():
+    """The gate-add epilogue on a float residual (the reference's float residual stream): the float64 product added
+    to the residual, rounded once to float; gate 0 leaves the residual bit-exact."""
+    rng = np.random.default_rng(3)
+    m, n, k = 7, 40, 64
+    for form in (orc.GEMM_W8A16, orc.GEMM_BF16, orc.GEMM_W8A8):
+        x, xs, w, ws = operands(rng, form, m, n, k)
+        res = rng.standard_normal((m, n)).astype(np.float32)
+        gate = (0.1 * rng.standard_normal((2, n))).astype(np.float32)
+        sets = rng.integers(0, 2, m).astype(np.uint8)
+        got = orc.gemm_gate_add(x, w, form, res, gate, xs, ws, sets)
+        assert got.dtype == np.float32
+        want = res.astype(np.float64) + gate[sets].astype(np.float64) * torch_y(x, w, form, xs, ws)
+        assert np.all(np.abs(got - want) <= 2 ** -24 * np.abs(want) + 1e-12), form
+        assert (orc.gemm_gate_add(x, w, form, res, np.zeros(n, np.float32), xs, ws) == res).all(), form
