@@ -798,25 +798,30 @@ def bench_fc1(mh, dev, steps, warmup, compare):
     res["w8a8_fc1_int8_mfma_util"] = flops / ims / 1e9 / INT8_PEAK_TOPS
     del xq, xs
     if compare:
+        # hipBLASLt's bf16 GEMM on the same weight layout (w [2 F][5120], x w^T: its fastest form here) and on w^T
+        # stored [5120][2 F]; no epilogue.
         wb = (w.float() * s[:, None]).to(torch.bfloat16)
-        wt = wb.t().contiguous()
         y = torch.empty((ROWS, 2 * FFN), dtype=torch.bfloat16, device=dev)
-        cms, _ = time_launches(lambda: torch.matmul(x, wt, out=y), max(3, steps // 2), 2)
+        cms, _ = time_launches(lambda: torch.matmul(x, wb.t(), out=y), max(3, steps // 2), 2)
         res["bf16_hipblaslt_gemm_ms"] = cms
         res["bf16_hipblaslt_tflops"] = flops / cms / 1e9
+        wt = wb.t().contiguous()
+        nms, _ = time_launches(lambda: torch.matmul(x, wt, out=y), max(3, steps // 2), 2)
+        res["bf16_hipblaslt_gemm_wt_ms"] = nms
         del wt, y, wb
     return res
 
 
 def bench_hipblaslt_tuned(dev, steps, warmup, max_ms_per_solution=200):
-    """hipBLASLt's (and rocBLAS's) best solution for fc1's GEMM (x [129,536][5120] bf16 times w^T [5120][27,648] bf16,
-    no epilogue), found by PyTorch's TunableOp, which times every candidate solution for this shape; beside the
-    default solution torch.matmul picks. The tuning results file goes to a temporary directory."""
+    """hipBLASLt's (and rocBLAS's) best solution for fc1's GEMM (x [129,536][5120] bf16 times w^T, w the weight's
+    [27,648][5120] rows, no epilogue), found by PyTorch's TunableOp, which times every candidate solution for this
+    shape; beside the default solution torch.matmul picks. The tuning results file goes to a temporary directory."""
     import tempfile
 
     g = torch.Generator(device=dev).manual_seed(9)
     x = torch.randn((ROWS, DIM), generator=g, device=dev).to(torch.bfloat16)
-    wt = torch.randn((DIM, 2 * FFN), generator=g, device=dev).to(torch.bfloat16)
+    w = torch.randn((2 * FFN, DIM), generator=g, device=dev).to(torch.bfloat16)  # the weight's [out][in] rows
+    wt = w.t()
     y = torch.empty((ROWS, 2 * FFN), dtype=torch.bfloat16, device=dev)
     flops = 2.0 * ROWS * DIM * 2 * FFN
     dms, _ = time_launches(lambda: torch.matmul(x, wt, out=y), max(3, steps), warmup)

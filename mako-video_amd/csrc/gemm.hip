@@ -34,6 +34,7 @@ namespace mh3 {
 
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef float floatx16 __attribute__((ext_vector_type(16)));
+typedef float floatx4 __attribute__((ext_vector_type(4)));
 
 constexpr uint32_t kBM = 256, kBN = 128, kBK = 64;
 // LDS: a ring of 3 A stages (256 rows x 64 k bf16 = 2048 16-byte chunks each), then 2 B stages (256 B-rows x 64 k,
@@ -99,6 +100,10 @@ __device__ __forceinline__ void lds_barrier()
 
 constexpr int kGemmWM = 2; // wavefronts along the tile's rows
 constexpr int kGemmWN = 4; // wavefronts along its columns
+// MFMA tile shape: 16 x 16 (v_mfma_f32_16x16x32_bf16, v_mfma_i32_16x16x64_i8). The matrix cores sustain a higher
+// clock on it than on the 32 x 32 forms under the same power limit (a register-only loop of random operands: 1.91
+// against 1.69-1.76 GHz at 98% busy), with the same LDS bytes a flop for the same wave tile.
+constexpr int kGemmShape = 16;
 
 // The three fc1 forms: int8 weights widened to bf16 with bf16 activations (weight-only), bf16 weights, and int8
 // weights with int8 activations (each row of x with its own scale) on the int8 MFMA.
@@ -124,13 +129,14 @@ typedef int int32x4 __attribute__((ext_vector_type(4)));
 typedef int int32x16 __attribute__((ext_vector_type(16)));
 
 // The epilogue shared by the GEMM kernels, through the LDS (idle after the last K-step). acc[a][b][e] is y[r][c]
-// with tile row r = wm (256 / WM) + a 32 + 8 (e / 4) + 4 (lane / 32) + e % 4 and c = lane % 32 + 32 b + wn 32 TN
-// within the tile's first 128 w rows (b < TN) or, for acc[a][TN + b], the same position in its second 128. A
+// with c = lane % SH + SH b + wn SH TN within the tile's first 128 w rows (b < TN) or, for acc[a][TN + b], the same
+// position in its second 128, and tile row r = wm (256 / WM) + a 32 + 8 (e / 4) + 4 (lane / 32) + e % 4 for the
+// 32 x 32 MFMA tiles (SH 32), r = wm (256 / WM) + a 16 + 4 (lane / 16) + e for the 16 x 16 ones (SH 16). A
 // 128-column half of the tile at a time, each wave writes its scaled results as floats into a [256][kEpiStride] LDS
 // tile (the two half-waves' rows, 4 apart, fall on disjoint banks); then each thread takes 8 consecutive columns of
 // a row, so the output, and with kGateAdd the residual, moves in 16-byte accesses, 16 threads to a row's 256 bytes.
 // The results round to bf16 once, at the end, as they would written straight from the registers.
-template <int WM, int WN, int MODE, int EPI, int TM, int TN, typename Acc>
+template <int WM, int WN, int MODE, int EPI, int SH, int TM, int TN, typename Acc>
 __device__ __forceinline__ void gemm_epilogue(Acc (&acc)[TM][2 * TN], u32x4_t* smem, uint32_t M, uint32_t N,
                                               uint32_t m0, uint32_t w_lo, uint32_t w_hi,
                                               const float* __restrict__ scale, const float* __restrict__ xscale,
@@ -138,7 +144,8 @@ __device__ __forceinline__ void gemm_epilogue(Acc (&acc)[TM][2 * TN], u32x4_t* s
 {
     constexpr uint32_t kThreads = WM * WN * 64;
     const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6, wm = wave / WN, wn = wave % WN;
-    const uint32_t half = lane >> 5, r32 = lane & 31u;
+    const uint32_t half = lane >> 5, rl = lane % uint32_t(SH);
+    constexpr int NE = SH * SH / 64; // accumulator elements a lane: 16 (32 x 32) or 4 (16 x 16)
     constexpr uint32_t kEpiStride = kBN + 8u; // floats a staged row: 4 rows apart = 32 banks apart
     static_assert(kBM * kEpiStride * sizeof(float) <= kGemmLds, "the staged half-tile fits in the LDS");
     constexpr int kHalves = EPI == kSwiGLU ? 1 : 2;
@@ -150,14 +157,15 @@ __device__ __forceinline__ void gemm_epilogue(Acc (&acc)[TM][2 * TN], u32x4_t* s
             lds_barrier(); // the first half is read out
 #pragma unroll
         for (int b = 0; b < TN; ++b) {
-            const uint32_t c = wn * 32u * TN + uint32_t(b) * 32u + r32;
+            const uint32_t c = wn * uint32_t(SH) * TN + uint32_t(b) * uint32_t(SH) + rl;
             const float s_lo = MODE != kBf16 ? scale[w_lo + c] : 1.0f, s_hi = MODE != kBf16 ? scale[w_hi + c] : 1.0f;
 #pragma unroll
             for (int a = 0; a < TM; ++a) {
 #pragma unroll
-                for (int e = 0; e < 16; ++e) {
-                    const uint32_t r = wm * (kBM / WM) + uint32_t(a) * 32u + 8u * (uint32_t(e) >> 2) + 4u * half +
-                                       (uint32_t(e) & 3u);
+                for (int e = 0; e < NE; ++e) {
+                    const uint32_t r = SH == 32 ? wm * (kBM / WM) + uint32_t(a) * 32u + 8u * (uint32_t(e) >> 2) +
+                                                      4u * half + (uint32_t(e) & 3u)
+                                                : wm * (kBM / WM) + uint32_t(a) * 16u + 4u * (lane >> 4) + uint32_t(e);
                     const float sx = MODE == kW8A8 ? xscale[min(m0 + r, M - 1u)] : 1.0f;
                     float v;
                     if constexpr (EPI == kSwiGLU) {
@@ -210,9 +218,10 @@ __device__ __forceinline__ void gemm_epilogue(Acc (&acc)[TM][2 * TN], u32x4_t* s
 }
 
 // WM x WN wavefronts: wave (wm, wn) computes rows wm * (256 / WM) ... of the tile against its TN gate column tiles
-// (32 columns each, from wn * 32 TN) and the TN matching up column tiles. Every LDS row holds 128 bytes of k: 64 k of
-// bf16 or 128 k of int8, so a K-step is 64 or 128 k.
-template <int WM, int WN, int MODE, int EPI>
+// (SH columns each, from wn * SH TN) and the TN matching up column tiles, on SH x SH MFMA tiles: SH 32
+// (v_mfma_f32_32x32x16_bf16, v_mfma_i32_32x32x32_i8) or SH 16 (v_mfma_f32_16x16x32_bf16, v_mfma_i32_16x16x64_i8).
+// Every LDS row holds 128 bytes of k: 64 k of bf16 or 128 k of int8, so a K-step is 64 or 128 k.
+template <int WM, int WN, int MODE, int EPI, int SH>
 __global__ __launch_bounds__(kGemmWM * kGemmWN * 64) void gemm_kernel(
     const void* __restrict__ xv, const void* __restrict__ wv, const float* __restrict__ scale,
     const float* __restrict__ xscale, uint16_t* __restrict__ out, uint32_t M, uint32_t N, uint32_t K, uint32_t mt,
@@ -222,9 +231,13 @@ __global__ __launch_bounds__(kGemmWM * kGemmWN * 64) void gemm_kernel(
     constexpr uint32_t kEA = MODE == kW8A8 ? 1u : 2u;     // bytes of an x element
     constexpr uint32_t kEB = MODE == kBf16 ? 2u : 1u;     // bytes of a w element
     constexpr uint32_t kKS = 128u / kEA;                  // k of a K-step
-    using Acc = typename std::conditional<MODE == kW8A8, int32x16, floatx16>::type;
+    using Acc = typename std::conditional<SH == 32, typename std::conditional<MODE == kW8A8, int32x16, floatx16>::type,
+                                          typename std::conditional<MODE == kW8A8, int32x4, floatx4>::type>::type;
     constexpr uint32_t kThreads = WM * WN * 64, kWaves = WM * WN;
-    constexpr int TM = int(kBM / WM / 32), TN = int(kBN / WN / 32); // MFMA tiles: rows, and gate (= up) columns
+    constexpr int TM = int(kBM / WM / SH), TN = int(kBN / WN / SH); // MFMA tiles: rows, and gate (= up) columns
+    // Row tiles whose A fragments a sub-step holds: all of them (SH 32), or half (SH 16: a sub-step is one 32-k half
+    // of the K-step over one half of the wave's rows, so its fragments take no more registers than SH 32's).
+    constexpr int FA = SH == 32 ? TM : TM / 2;
     extern __shared__ u32x4_t smem[];
     uint32_t tm, tn;
     tile_of(mt, nt, tm, tn);
@@ -311,26 +324,39 @@ __global__ __launch_bounds__(kGemmWM * kGemmWN * 64) void gemm_kernel(
             lds_dma16(rw, stage + i * 64, bd_off[i], int(kt * 128u));
     };
 
-    // MFMA operands of sub-step ks (16 k) of tile kt: A rows wm*(256/WM) + t*32 + lane%32, B rows (gate)
-    // wn*32TN + t*32 + lane%32 and (up) 128 + the same, k-chunk ks*2 + lane/32. Every row a lane reads has
-    // (row >> 1) & 7 = (lane % 32 >> 1) & 7, so one offset per sub-step serves all tiles; t moves it by 32 rows.
-    const uint32_t half = lane >> 5, r32 = lane & 31u, fsx = (r32 >> 1) & 7u;
-    const uint32_t fa_base = (wm * (kBM / WM) + r32) * 128u, fb_base = (wn * 32u * TN + r32) * 128u;
+    // MFMA operands, 16 bytes a lane (8 bf16 or 16 int8 of k). SH 32, sub-step ks (a quarter of the K-step): A rows
+    // wm*(256/WM) + t*32 + lane%32, B rows (gate) wn*32TN + t*32 + lane%32 and (up) 128 + the same, k-chunk
+    // ks*2 + lane/32. SH 16, sub-step ks: k-half h = ks/2 and the wave's row tiles (ks%2)*FA .. +FA-1, A rows
+    // wm*(256/WM) + t*16 + lane%16, B rows wn*16TN + t*16 + lane%16 (and 128 + that), k-chunk 4h + lane/16. Every row
+    // a lane reads has (row >> 1) & 7 = (lane % SH >> 1) & 7, so one offset per sub-step serves all tiles; t moves it
+    // by SH rows. (The 16 rows a quarter-wave reads at one chunk then cover the 64 banks once.)
+    const uint32_t rs = lane % uint32_t(SH), fsx = (rs >> 1) & 7u;
+    const uint32_t fa_base = (wm * (kBM / WM) + rs) * 128u, fb_base = (wn * uint32_t(SH) * TN + rs) * 128u;
+    constexpr uint32_t kRowBytes = uint32_t(SH) * 128u; // one MFMA tile's rows in a stage
     uint32_t fko[4];
 #pragma unroll
     for (uint32_t ks = 0; ks < 4; ++ks)
-        fko[ks] = ((ks * 2u + half) ^ fsx) * 16u;
-    auto frags = [&](uint32_t kt, uint32_t ks, bf16x8_t (&fa)[TM], bf16x8_t (&fb)[2 * TN]) {
-        const char* A = lds + (kt % kAStages) * kStageChunks * 16u + fa_base + fko[ks];
+        fko[ks] = SH == 32 ? ((ks * 2u + (lane >> 5)) ^ fsx) * 16u : (((ks >> 1) * 4u + (lane >> 4)) ^ fsx) * 16u;
+    auto frags_a = [&](uint32_t kt, uint32_t ks, bf16x8_t (&fa)[FA]) {
+        const uint32_t t0 = SH == 32 ? 0u : (ks & 1u) * uint32_t(FA);
+        const char* A = lds + (kt % kAStages) * kStageChunks * 16u + fa_base + fko[ks] + t0 * kRowBytes;
+#pragma unroll
+        for (int t = 0; t < FA; ++t)
+            fa[t] = *reinterpret_cast<const bf16x8_t*>(A + t * kRowBytes);
+    };
+    auto frags_b = [&](uint32_t kt, uint32_t ks, bf16x8_t (&fb)[2 * TN]) {
         const char* B = lds + (kBBase + (kt % kBStages) * kStageChunks) * 16u + fb_base + fko[ks];
 #pragma unroll
-        for (int t = 0; t < TM; ++t)
-            fa[t] = *reinterpret_cast<const bf16x8_t*>(A + t * 4096);
-#pragma unroll
         for (int t = 0; t < TN; ++t) {
-            fb[t] = *reinterpret_cast<const bf16x8_t*>(B + t * 4096);
-            fb[TN + t] = *reinterpret_cast<const bf16x8_t*>(B + kBN * 128 + t * 4096);
+            fb[t] = *reinterpret_cast<const bf16x8_t*>(B + t * kRowBytes);
+            fb[TN + t] = *reinterpret_cast<const bf16x8_t*>(B + kBN * 128 + t * kRowBytes);
         }
+    };
+    // Sub-step ks's fragments; SH 16 reads B only at the start of a k-half (the second sub-step of a half keeps it).
+    auto frags = [&](uint32_t kt, uint32_t ks, bf16x8_t (&fa)[FA], bf16x8_t (&fb)[2 * TN]) {
+        frags_a(kt, ks, fa);
+        if (SH == 32 || (ks & 1u) == 0u)
+            frags_b(kt, ks, fb);
     };
 
     Acc acc[TM][2 * TN];
@@ -338,31 +364,40 @@ __global__ __launch_bounds__(kGemmWM * kGemmWN * 64) void gemm_kernel(
     for (int a = 0; a < TM; ++a)
 #pragma unroll
         for (int b = 0; b < 2 * TN; ++b)
+            acc[a][b] = Acc{};
+    // One MFMA: acc[a][b] += A fragment fa * B fragment fb.
+    auto mfma = [&](Acc& c, const bf16x8_t& fa, const bf16x8_t& fb) {
+        if constexpr (SH == 32 && MODE == kW8A8)
+            c = __builtin_amdgcn_mfma_i32_32x32x32_i8(__builtin_bit_cast(int32x4, fa), __builtin_bit_cast(int32x4, fb),
+                                                      c, 0, 0, 0);
+        else if constexpr (SH == 32)
+            c = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa, fb, c, 0, 0, 0);
+        else if constexpr (MODE == kW8A8)
+            c = __builtin_amdgcn_mfma_i32_16x16x64_i8(__builtin_bit_cast(int32x4, fa), __builtin_bit_cast(int32x4, fb),
+                                                      c, 0, 0, 0);
+        else
+            c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fa, fb, c, 0, 0, 0);
+    };
+    // Sub-step ks's MFMAs: its FA row tiles (from t0) against the 2 TN column tiles.
+    auto mfmas = [&](uint32_t ks, const bf16x8_t (&fa)[FA], const bf16x8_t (&fb)[2 * TN]) {
+        const int t0 = SH == 32 ? 0 : int(ks & 1u) * FA;
 #pragma unroll
-            for (int e = 0; e < 16; ++e)
-                acc[a][b][e] = 0;
-    auto mfmas = [&](const bf16x8_t (&fa)[TM], const bf16x8_t (&fb)[2 * TN]) {
+        for (int a = 0; a < FA; ++a)
 #pragma unroll
-        for (int a = 0; a < TM; ++a)
-#pragma unroll
-            for (int b = 0; b < 2 * TN; ++b) {
-                if constexpr (MODE == kW8A8)
-                    acc[a][b] = __builtin_amdgcn_mfma_i32_32x32x32_i8(__builtin_bit_cast(int32x4, fa[a]),
-                                                                      __builtin_bit_cast(int32x4, fb[b]), acc[a][b],
-                                                                      0, 0, 0);
-                else
-                    acc[a][b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[a], fb[b], acc[a][b], 0, 0, 0);
-            }
+            for (int b = 0; b < 2 * TN; ++b)
+                mfma(acc[t0 + a][b], fa[a], fb[b]);
     };
     // The same MFMAs with B pieces p0 .. p0 + np - 1 of tile kt placed between them, at even spacing, so the
     // widening's VALU work issues while the matrix core is busy.
-    auto mfmas_b = [&](const bf16x8_t (&fa)[TM], const bf16x8_t (&fb)[2 * TN], uint32_t kt, int p0, int np) {
-        constexpr int n = TM * 2 * TN;
+    auto mfmas_b = [&](uint32_t ks, const bf16x8_t (&fa)[FA], const bf16x8_t (&fb)[2 * TN], uint32_t kt, int p0,
+                       int np) {
+        constexpr int n = FA * 2 * TN;
+        const int t0 = SH == 32 ? 0 : int(ks & 1u) * FA;
 #pragma unroll
         for (int j = 0; j < n; ++j) {
             const int a = j / (2 * TN), b = j % (2 * TN);
             if constexpr (MODE == kW8A16)
-                acc[a][b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[a], fb[b], acc[a][b], 0, 0, 0);
+                mfma(acc[t0 + a][b], fa[a], fb[b]);
             __builtin_amdgcn_sched_barrier(0);
             if (j % (n / np) == 0 && j / (n / np) < np) {
                 b_piece(kt, rb, p0 + j / (n / np));
@@ -393,7 +428,9 @@ __global__ __launch_bounds__(kGemmWM * kGemmWN * 64) void gemm_kernel(
     // would turn every LDS wait in it into a full wait (scalar loads complete out of order).
     asm volatile("" ::"s"(scale), "s"(xscale), "s"(out), "s"(gg.gate), "s"(gg.set_of_row));
     lds_barrier();
-    bf16x8_t fa[2][TM], fb[2][2 * TN];
+    // Fragment double buffers: A by sub-step parity; B by sub-step parity (SH 32) or by k-half (SH 16, where a
+    // half's two sub-steps share one B set).
+    bf16x8_t fa[2][FA], fb[2][2 * TN];
     frags(0, 0, fa[0], fb[0]);
 
     // One K-step over tile kt (four sub-steps of 16 k). Tile kt+1's B is widened from registers into LDS in four
@@ -404,22 +441,24 @@ __global__ __launch_bounds__(kGemmWM * kGemmWN * 64) void gemm_kernel(
     // fragments load. LDS stages written in step kt (A stage (kt+2) % 3, B stage (kt+1) % 2) were last read before
     // step kt-1's barrier. The last step is a separate instance (kLast) so that the loop body has no branch around
     // the barrier: at such a join the compiler's LDS wait would also cover tile kt+1's fragment reads.
+    // B sets of sub-steps 0..3: SH 32 alternates (0, 1, 0, 1); SH 16 keeps one a k-half (0, 0, 1, 1).
+    constexpr int B1 = SH == 32 ? 1 : 0, B2 = SH == 32 ? 0 : 1, B3 = 1;
     auto kstep = [&](uint32_t kt, auto last) {
         constexpr bool kLast = decltype(last)::value;
         if constexpr (!I8 && !kLast)
             b_dma(kt + 1); // into B stage (kt+1) % 2, last read before step kt-1's barrier
-        frags(kt, 1, fa[1], fb[1]);
+        frags(kt, 1, fa[1], fb[B1]);
         __builtin_amdgcn_sched_barrier(0);
         if constexpr (kLast || !I8)
-            mfmas(fa[0], fb[0]);
+            mfmas(0, fa[0], fb[0]);
         else
-            mfmas_b(fa[0], fb[0], kt + 1, 0, BI);
-        frags(kt, 2, fa[0], fb[0]);
+            mfmas_b(0, fa[0], fb[0], kt + 1, 0, BI);
+        frags(kt, 2, fa[0], fb[B2]);
         __builtin_amdgcn_sched_barrier(0);
         if constexpr (kLast || !I8)
-            mfmas(fa[1], fb[1]);
+            mfmas(1, fa[1], fb[B1]);
         else
-            mfmas_b(fa[1], fb[1], kt + 1, BI, BI);
+            mfmas_b(1, fa[1], fb[B1], kt + 1, BI, BI);
         if constexpr (!kLast) {
             if constexpr (I8) {
                 __builtin_amdgcn_s_waitcnt(waitcnt_vm(0)); // tile kt+1's A complete too
@@ -431,9 +470,9 @@ __global__ __launch_bounds__(kGemmWM * kGemmWN * 64) void gemm_kernel(
                 a_issue(kt + 2);
             }
         }
-        frags(kt, 3, fa[1], fb[1]);
+        frags(kt, 3, fa[1], fb[B3]);
         __builtin_amdgcn_sched_barrier(0);
-        mfmas(fa[0], fb[0]);
+        mfmas(2, fa[0], fb[B2]);
         __builtin_amdgcn_sched_barrier(0);
         if constexpr (!kLast) {
             if constexpr (!I8) {
@@ -447,13 +486,13 @@ __global__ __launch_bounds__(kGemmWM * kGemmWN * 64) void gemm_kernel(
             frags(kt + 1, 0, fa[0], fb[0]);
         }
         __builtin_amdgcn_sched_barrier(0);
-        mfmas(fa[1], fb[1]);
+        mfmas(3, fa[1], fb[B3]);
     };
     for (uint32_t kt = 0; kt + 1 < KT; ++kt)
         kstep(kt, std::false_type{});
     kstep(KT - 1, std::true_type{});
 
-    gemm_epilogue<WM, WN, MODE, EPI, TM, TN>(acc, smem, M, N, m0, w_lo, w_hi, scale, xscale, out, gg);
+    gemm_epilogue<WM, WN, MODE, EPI, SH, TM, TN>(acc, smem, M, N, m0, w_lo, w_hi, scale, xscale, out, gg);
 }
 
 } // namespace mh3
@@ -497,15 +536,15 @@ int launch_gemm(const MH3GemmArgs* a, const void* x, const void* w, const float*
          (host::overlaps(out, out_bytes, gg.gate, (uint64_t(gg.n_sets) - 1u) * gg.gate_stride * 4u + a->n * 4ull) ||
           host::overlaps(out, out_bytes, gg.set_of_row, gg.set_of_row ? uint64_t(a->m) : 0u))))
         return MH3_ERR_PARAM;
-    constexpr int WM = kGemmWM, WN = kGemmWN;
-    const void* kernel = reinterpret_cast<const void*>(&gemm_kernel<WM, WN, MODE, EPI>);
+    constexpr int WM = kGemmWM, WN = kGemmWN, SH = kGemmShape;
+    const void* kernel = reinterpret_cast<const void*>(&gemm_kernel<WM, WN, MODE, EPI, SH>);
     if (const hipError_t e = host::allow_dynamic_lds(kernel, kGemmLds); e != hipSuccess)
         return host::hip_error(e);
     const uint32_t mt = (a->m + kBM - 1) / kBM, nt = a->n / kCols;
     const uint64_t tiles = uint64_t(mt) * nt;
     if (tiles >= (uint64_t(1) << 31))
         return MH3_ERR_SHAPE;
-    hipLaunchKernelGGL((gemm_kernel<WM, WN, MODE, EPI>), dim3(uint32_t(tiles)), dim3(WM * WN * 64), kGemmLds,
+    hipLaunchKernelGGL((gemm_kernel<WM, WN, MODE, EPI, SH>), dim3(uint32_t(tiles)), dim3(WM * WN * 64), kGemmLds,
                        static_cast<hipStream_t>(stream), x, w, scale, xscale, out, a->m, a->n, a->k, mt, nt, gg);
     return host::check_launch();
 }
