@@ -221,11 +221,12 @@ def bench_stream(dev, steps, warmup):
 
 
 def bench_mfma_ceiling(dev, steps, warmup):
-    """The matrix cores' sustained rate on this GPU under its power limit: a register-only loop of
-    v_mfma_f32_32x32x16_bf16 (and of v_mfma_i32_32x32x32_i8), 8 independent accumulators a wave, two waves a SIMD,
-    one 8-wave workgroup a CU, the operands cycling through 8 fragments of random bits, ~40 ms a launch (the power
-    limit acts within it). The clock each workgroup ran at is its shader clock counter's advance over the 100 MHz
-    real-time counter's (s_memtime, s_memrealtime): the median over workgroups is reported."""
+    """The matrix cores' sustained rate on this GPU under its power limit: a register-only loop of the GEMMs' own
+    instructions, v_mfma_f32_16x16x32_bf16 and v_mfma_i32_16x16x64_i8 (and of the 32 x 32 forms beside them), 16 (8)
+    independent accumulators a wave, two waves a SIMD, one 8-wave workgroup a CU, the operands cycling through 8
+    fragments of random bits, ~40 ms a launch (the power limit acts within it). The clock each workgroup ran at is its
+    shader clock counter's advance over the 100 MHz real-time counter's (s_memtime, s_memrealtime): the median over
+    workgroups is reported."""
     import ctypes as C
 
     lib = C.CDLL(str(REPO / "mako-video_amd" / "lib" / "libmh3_stream_probe.so"))
@@ -239,9 +240,12 @@ def bench_mfma_ceiling(dev, steps, warmup):
     clocks = torch.zeros(2 * blocks, dtype=torch.int64, device=dev)
     stream = torch.cuda.current_stream().cuda_stream
     res = {}
-    for kind, name, flops_per, peak in ((0, "bf16", 2 * 32 * 32 * 16, BF16_PEAK_TFLOPS),
-                                        (1, "int8", 2 * 32 * 32 * 32, INT8_PEAK_TOPS)):
-        iters = 40000 if kind == 0 else 20000  # ~40 ms a launch at 2 GHz
+    # (kind, name, ops an instruction, accumulators a wave, cycles an instruction at the nameplate rate, peak)
+    for kind, name, flops_per, accs, cyc, peak in ((0, "bf16", 2 * 16 * 16 * 32, 16, 16, BF16_PEAK_TFLOPS),
+                                                   (1, "int8", 2 * 16 * 16 * 64, 16, 16, INT8_PEAK_TOPS),
+                                                   (2, "bf16_32x32", 2 * 32 * 32 * 16, 8, 32, BF16_PEAK_TFLOPS),
+                                                   (3, "int8_32x32", 2 * 32 * 32 * 32, 8, 32, INT8_PEAK_TOPS)):
+        iters = 40000 if kind in (0, 2) else 20000  # ~40 ms a launch at 2 GHz
 
         def run():
             rc = lib.mh3_probe_mfma(kind, blocks, iters, out.data_ptr(), clocks.data_ptr(), stream)
@@ -250,11 +254,11 @@ def bench_mfma_ceiling(dev, steps, warmup):
         ms, _ = time_launches(run, max(3, steps // 4), max(1, warmup // 2))
         ck = clocks.view(blocks, 2).double().cpu()
         ghz = float((ck[:, 0] / ck[:, 1]).median()) * 0.1  # 100 MHz real-time counter
-        ops = float(blocks) * 512 / 64 * iters * 8 * flops_per
+        ops = float(blocks) * 512 / 64 * iters * accs * flops_per
         rate = ops / ms / 1e9
-        res[name] = {"ms": ms, "rate": rate, "unit": "TFLOP/s" if kind == 0 else "TOP/s", "frac": rate / peak,
+        res[name] = {"ms": ms, "rate": rate, "unit": "TOP/s" if "int8" in name else "TFLOP/s", "frac": rate / peak,
                      "clock_ghz": ghz,
-                     "mfma_busy_at_clock": rate / (cus.value * ghz * 1e9 * flops_per / 32 / 1e12 * 4) if ghz else None}
+                     "mfma_busy_at_clock": rate / (cus.value * ghz * 1e9 * 4 * flops_per / cyc / 1e12) if ghz else None}
     return res
 
 

@@ -28,9 +28,10 @@
 //     consecutive rows, `lds_bytes` of dynamic LDS a workgroup (which sets how many share a CU), buffer loads and
 //     stores with the non-temporal hint. nvec <= 640.
 //   int mh3_probe_mfma(int kind, uint32_t blocks, uint32_t iters, float* out, uint64_t* clocks, void* stream);
-//     a register-only loop of matrix instructions, kind 0 v_mfma_f32_32x32x16_bf16, kind 1 v_mfma_i32_32x32x32_i8:
-//     8 waves a workgroup, each wave `iters` (a multiple of 8; rounded up) rounds of 8 independent accumulators,
-//     the operands cycling through 8
+//     a register-only loop of matrix instructions, kind 0 v_mfma_f32_16x16x32_bf16, 1 v_mfma_i32_16x16x64_i8 (the
+//     GEMMs' forms), 2 v_mfma_f32_32x32x16_bf16, 3 v_mfma_i32_32x32x32_i8: 8 waves a workgroup, each wave `iters` (a
+//     multiple of 8; rounded up) rounds of 16 (16 x 16) or 8 (32 x 32) independent accumulators, the operands cycling
+//     through 8
 //     register fragments of random bits (so the matrix core's inputs change from one instruction to the next, as in
 //     a GEMM). out gets one value a thread (keeps the results live); clocks gets, for each workgroup, the shader
 //     clock counter's and the 100 MHz real-time counter's advance over its loop (s_memtime, s_memrealtime), from
@@ -183,10 +184,15 @@ __device__ __forceinline__ uint32_t mix32(uint32_t x)
     return x ^ (x >> 16);
 }
 
+typedef float floatx4 __attribute__((ext_vector_type(4)));
+
+// KIND 0: v_mfma_f32_16x16x32_bf16, 1: v_mfma_i32_16x16x64_i8 (the GEMMs' forms), 2: v_mfma_f32_32x32x16_bf16,
+// 3: v_mfma_i32_32x32x32_i8. 16 independent 16 x 16 accumulators a wave, or 8 of 32 x 32 (64 or 128 registers).
 template <int KIND>
 __global__ __launch_bounds__(512) void mfma_probe_kernel(uint32_t iters, float* out, uint64_t* clocks)
 {
-    constexpr int kFrag = 8, kAcc = 8;
+    constexpr bool kI8 = KIND == 1 || KIND == 3, k32 = KIND >= 2;
+    constexpr int kFrag = 8, kAcc = k32 ? 8 : 16;
     // Operand fragments of random bits; bf16 ones with the exponent held to 2^-15 .. 2^0 so no sum overflows.
     intx4 fa[kFrag], fb[kFrag];
     const uint32_t seed = (blockIdx.x * 512u + threadIdx.x) * 64u;
@@ -195,14 +201,16 @@ __global__ __launch_bounds__(512) void mfma_probe_kernel(uint32_t iters, float* 
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
             uint32_t ra = mix32(seed + f * 8u + e), rb = mix32(seed + f * 8u + 4u + e);
-            if (KIND == 0) {
+            if (!kI8) {
                 ra = (ra & 0x87ff87ffu) | 0x38003800u; // sign, 4 low exponent bits and 7 mantissa bits random
                 rb = (rb & 0x87ff87ffu) | 0x38003800u;
             }
             fa[f][e] = int(ra);
             fb[f][e] = int(rb);
         }
-    using Acc = typename std::conditional<KIND == 0, floatx16, intx16>::type;
+    using Acc = typename std::conditional<
+        k32, typename std::conditional<kI8, intx16, floatx16>::type,
+        typename std::conditional<kI8, intx4, floatx4>::type>::type;
     Acc acc[kAcc];
 #pragma unroll
     for (int i = 0; i < kAcc; ++i)
@@ -217,6 +225,11 @@ __global__ __launch_bounds__(512) void mfma_probe_kernel(uint32_t iters, float* 
             for (int i = 0; i < kAcc; ++i) {
                 const int f = (i + u) & (kFrag - 1), g = (i * 3 + u) & (kFrag - 1);
                 if constexpr (KIND == 0)
+                    acc[i] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+                        __builtin_bit_cast(bf16x8, fa[f]), __builtin_bit_cast(bf16x8, fb[g]), acc[i], 0, 0, 0);
+                else if constexpr (KIND == 1)
+                    acc[i] = __builtin_amdgcn_mfma_i32_16x16x64_i8(fa[f], fb[g], acc[i], 0, 0, 0);
+                else if constexpr (KIND == 2)
                     acc[i] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
                         __builtin_bit_cast(bf16x8, fa[f]), __builtin_bit_cast(bf16x8, fb[g]), acc[i], 0, 0, 0);
                 else
@@ -227,7 +240,7 @@ __global__ __launch_bounds__(512) void mfma_probe_kernel(uint32_t iters, float* 
 #pragma unroll
     for (int i = 0; i < kAcc; ++i)
 #pragma unroll
-        for (int e = 0; e < 16; ++e)
+        for (int e = 0; e < (k32 ? 16 : 4); ++e)
             sum += float(acc[i][e]);
     const uint64_t t1 = __builtin_amdgcn_s_memtime(), r1 = __builtin_amdgcn_s_memrealtime();
     out[blockIdx.x * 512u + threadIdx.x] = sum;
@@ -259,15 +272,19 @@ extern "C" int mh3_probe_rows(const void* a, const void* b, void* c, uint32_t ro
 
 extern "C" int mh3_probe_mfma(int kind, uint32_t blocks, uint32_t iters, float* out, uint64_t* clocks, void* stream)
 {
-    if ((kind != 0 && kind != 1) || blocks == 0 || !out || !clocks)
+    if (kind < 0 || kind > 3 || blocks == 0 || !out || !clocks)
         return -1;
     if ((reinterpret_cast<uintptr_t>(clocks) & 7u) != 0)
         return -2;
     hipStream_t s = static_cast<hipStream_t>(stream);
     if (kind == 0)
         hipLaunchKernelGGL(mfma_probe_kernel<0>, dim3(blocks), dim3(512), 0, s, iters, out, clocks);
-    else
+    else if (kind == 1)
         hipLaunchKernelGGL(mfma_probe_kernel<1>, dim3(blocks), dim3(512), 0, s, iters, out, clocks);
+    else if (kind == 2)
+        hipLaunchKernelGGL(mfma_probe_kernel<2>, dim3(blocks), dim3(512), 0, s, iters, out, clocks);
+    else
+        hipLaunchKernelGGL(mfma_probe_kernel<3>, dim3(blocks), dim3(512), 0, s, iters, out, clocks);
     return hipGetLastError() == hipSuccess ? 0 : -3;
 }
 
