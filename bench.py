@@ -41,7 +41,6 @@ sys.path.insert(0, str(REPO / "mako-video_amd"))
 HBM_PEAK_GBS = 8000.0          # MI355X HBM3E
 BF16_PEAK_TFLOPS = 2500.0      # dense bf16 MFMA
 INT8_PEAK_TOPS = 5000.0        # dense int8 MFMA
-FP32_MFMA_PEAK_TFLOPS = 157.3  # dense fp32 MFMA
 METRIC = "ms/op + achieved HBM GB/s (% peak) at 768p rows; int8 GEMM MFMA util %"
 
 ROWS, DIM, FFN = 32 * 48 * 84 + 512, 5120, 13824
@@ -367,7 +366,8 @@ def bench_select(mh, dev, steps, warmup):
             "alg_bytes": alg_bytes, "GBs": alg_bytes / total_ms / 1e6,
             "frac": alg_bytes / total_ms / 1e6 / HBM_PEAK_GBS,
             "score_gflop": flops / 1e9, "select_TFLOPs": flops / sel_ms / 1e9,
-            "select_fp32_mfma_frac": flops / sel_ms / 1e9 / FP32_MFMA_PEAK_TFLOPS,
+            # The scores are three bf16 MFMA products of split float operands: 3 x the flops on the bf16 matrix cores.
+            "select_split_bf16_mfma_frac": 3.0 * flops / sel_ms / 1e9 / BF16_PEAK_TFLOPS,
             "select_bytes": sel_bytes, "unfused_scores_ms": scores_ms, "unfused_topk_ms": topk_ms}
 
 

@@ -7,8 +7,9 @@
 //   of the cube's x position x, so each load instruction reads four adjacent rows (1 KiB contiguous per head in the
 //   grid layout) and each quad of lanes one aligned 64-byte piece of a row; all 32 loads of a lane are in flight at
 //   once. Lane sums in float, then two lane exchanges across the 16-lane rows.
-// - scores: v_mfma_f32_16x16x4_f32 on 16 x 16 blocks; the 128-long contraction is split over the MFMA's 4 k-lanes so
-//   that each operand load of the wave reads 64 contiguous bytes of each of the block's 16 rows.
+// - scores: float dot products on 16 x 16 blocks from the four bf16 MFMA products of operands split into bf16 high
+//   and low parts (v_mfma_f32_16x16x32_bf16): a quarter of the matrix-core clocks of v_mfma_f32_16x16x4_f32, within
+//   1e-5 of the row's largest score; each operand load of the wave reads 64 contiguous bytes of each of 16 rows.
 // - top-k: one wavefront per (head, query cube) holds the row's scores as order-preserving 32-bit keys in VGPRs, lane l
 //   owning cubes 32 l ... 32 l + 31. A 128-bin histogram of the scores, linear in value between the row's minimum and
 //   maximum (LDS atomics, one pass), brackets the k-th largest key to one bin's keys; where that bin holds more than
@@ -26,6 +27,7 @@
 namespace mh3 {
 
 typedef float floatx4 __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 
 struct CubeGeo {
     uint32_t gt, gh, gw;   // video grid
@@ -107,39 +109,102 @@ __global__ __launch_bounds__(256) void cube_pool_kernel(CubeGeo g, const uint16_
         counts[c] = int32_t(nt * ny * nx);
 }
 
-// The 32 contraction operands of lane l for a 16-row block starting at r0: row r0 + l % 16 (clamped to the last row);
-// operand 4 v + u is dimension 16 v + 4 (l / 16) + u, so the 32 MFMA steps cover all 128 dimensions once. The loads
-// take another lane order: lane l reads row r0 + l / 4, dimensions 16 v + 4 (l % 4) .. + 3, so each quad of lanes
-// fetches one aligned 64-byte piece of a row (a quad spread over four rows costs the address unit four accesses and
-// held these loads to about 16 bytes a clock a CU); a lane exchange (ds_bpermute, lane l from lane 4 (l % 16) + l / 16)
-// then gives each lane its MFMA operands.
-__device__ __forceinline__ void load_operand(const float* __restrict__ base, uint32_t r0, uint32_t rows, float (&v)[32])
+// A 16-row block's operands for the bf16 MFMA (v_mfma_f32_16x16x32_bf16, four steps of k = 32). Lane l of a step
+// holds row r0 + l % 16 (clamped to the last row) at 8 k-values; over the four steps, lane l's 32 operands are
+// dimensions 16 v + 4 (l / 16) + u (operand 4 v + u, step s taking operands 8 s .. 8 s + 7), the same for q and k,
+// so the contraction covers the 128 dimensions once. The loads take another lane order: lane l reads row r0 + l / 4,
+// dimensions 16 v + 4 (l % 4) .. + 3, so each quad of lanes fetches one aligned 64-byte piece of a row (a quad spread
+// over four rows costs the address unit four accesses and held these loads to about 16 bytes a clock a CU); a lane
+// exchange (ds_bpermute, lane l from lane 4 (l % 16) + l / 16) then gives each lane its operands.
+struct RawRows {
+    float4 t[8]; // lane l: row r0 + l / 4, dimensions 16 i + 4 (l % 4) .. + 3
+};
+
+__device__ __forceinline__ void load_raw(const float* __restrict__ base, uint32_t r0, uint32_t rows, RawRows& raw)
 {
     const uint32_t lane = threadIdx.x & 63u;
     uint32_t r = r0 + (lane >> 2);
     r = r < rows ? r : rows - 1u;
     const float* p = base + uint64_t(r) * 128u + (lane & 3u) * 4u;
-    const int src = int(4u * (4u * (lane & 15u) + (lane >> 4)));
-    float4 t[8];
 #pragma unroll
     for (int i = 0; i < 8; ++i)
-        t[i] = *reinterpret_cast<const float4*>(p + 16 * i);
+        raw.t[i] = *reinterpret_cast<const float4*>(p + 16 * i);
+}
+
+// Each float operand x is split into two bf16 parts, x = hi + lo + r with hi = bf16(x) and lo = bf16(x - hi), both
+// rounded to nearest even (x - hi is exact in float), so |r| <= 2^-18 |x|. The split is made before the lane
+// exchange, on pairs of adjacent operands, so the exchange moves 32 packed words, as many as the floats would take.
+struct SplitRow {
+    bf16x8_t hi[4], lo[4];
+};
+
+__device__ __forceinline__ void split_exchange(const RawRows& raw, SplitRow& o)
+{
+    const uint32_t lane = threadIdx.x & 63u;
+    const int src = int(4u * (4u * (lane & 15u) + (lane >> 4)));
+    uint32_t h[16], l[16]; // h[2 i + j]: operands 4 i + 2 j and 4 i + 2 j + 1 of the lane
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
-        const float c[4] = {t[i].x, t[i].y, t[i].z, t[i].w};
+        const float c[4] = {raw.t[i].x, raw.t[i].y, raw.t[i].z, raw.t[i].w};
 #pragma unroll
-        for (int u = 0; u < 4; ++u)
-            v[4 * i + u] = __int_as_float(__builtin_amdgcn_ds_bpermute(src, __float_as_int(c[u])));
+        for (int j = 0; j < 2; ++j) {
+            const float a = c[2 * j], b = c[2 * j + 1];
+            const uint32_t hp = pack_bf16(a, b);
+            const uint32_t lp = pack_bf16(a - bf16_lo(hp), b - bf16_hi(hp));
+            h[2 * i + j] = uint32_t(__builtin_amdgcn_ds_bpermute(src, int(hp)));
+            l[2 * i + j] = uint32_t(__builtin_amdgcn_ds_bpermute(src, int(lp)));
+        }
+    }
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+        o.hi[s] = __builtin_bit_cast(bf16x8_t, uint4{h[4 * s], h[4 * s + 1], h[4 * s + 2], h[4 * s + 3]});
+        o.lo[s] = __builtin_bit_cast(bf16x8_t, uint4{l[4 * s], l[4 * s + 1], l[4 * s + 2], l[4 * s + 3]});
     }
 }
 
-// acc[v] = q[i0 + 4 (l / 16) + v] . k[j0 + l % 16] over the 128 dimensions (v_mfma_f32_16x16x4_f32 layout).
-__device__ __forceinline__ floatx4 score_block(const float (&qa)[32], const float (&kb)[32])
+// acc[v] = q[i0 + 4 (l / 16) + v] . k[j0 + l % 16] from the four bf16 products of the split operands, q.k =
+// qlo.klo + qlo.khi + qhi.klo + qhi.khi, accumulated in float by the MFMA, the small products first. A product of
+// bf16 values is exact in float, so a term's error is the split's remainders, at most about 2^-17 |q_d k_d|: over
+// 2016 x 2016 scores of N(0, 1) rows the largest error is 6.3e-6 of the row's largest score (9.2e-6 without the
+// qlo.klo product, 8.7e-7 for a float contraction), and it matters to the selection only where two scores tie to
+// that order. The bf16 MFMAs (k = 32) take 256 clocks a block against 1024 for the 32 v_mfma_f32_16x16x4_f32 of a
+// float contraction.
+__device__ __forceinline__ floatx4 score_block(const SplitRow& q, const SplitRow& k)
 {
     floatx4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-    for (int s = 0; s < 32; ++s)
-        acc = __builtin_amdgcn_mfma_f32_16x16x4f32(qa[s], kb[s], acc, 0, 0, 0);
+    for (int s = 0; s < 4; ++s)
+        acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(q.lo[s], k.lo[s], acc, 0, 0, 0);
+#pragma unroll
+    for (int s = 0; s < 4; ++s)
+        acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(q.lo[s], k.hi[s], acc, 0, 0, 0);
+#pragma unroll
+    for (int s = 0; s < 4; ++s)
+        acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(q.hi[s], k.lo[s], acc, 0, 0, 0);
+#pragma unroll
+    for (int s = 0; s < 4; ++s)
+        acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(q.hi[s], k.hi[s], acc, 0, 0, 0);
+    return acc;
+}
+
+// The same four scores by float FMAs in dimension order, straight from memory. An infinite or NaN operand, or one so
+// large that bf16(x) overflows, makes the split's parts infinite or NaN, and with them the block's scores: a block
+// with a non-finite score (the test is wave-uniform) is scored again here. Rare, so written for few registers.
+__device__ __forceinline__ floatx4 score_block_direct(const float* __restrict__ qh, const float* __restrict__ kh,
+                                                      uint32_t i0, uint32_t j0, uint32_t rows)
+{
+    const uint32_t lane = threadIdx.x & 63u;
+    const uint32_t kr = min(j0 + (lane & 15u), rows - 1u);
+    floatx4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+    for (uint32_t d = 0; d < 128u; d += 4u) {
+        const float4 kv = *reinterpret_cast<const float4*>(kh + uint64_t(kr) * 128u + d);
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+            const uint32_t qr = min(i0 + 4u * (lane >> 4) + uint32_t(v), rows - 1u);
+            const float4 qv = *reinterpret_cast<const float4*>(qh + uint64_t(qr) * 128u + d);
+            acc[v] = fmaf(qv.w, kv.w, fmaf(qv.z, kv.z, fmaf(qv.y, kv.y, fmaf(qv.x, kv.x, acc[v]))));
+        }
+    }
     return acc;
 }
 
@@ -157,18 +222,26 @@ constexpr uint32_t kPaddedRow = 64u * (KPL + 4);
 
 // Scores of query block [i0, i0 + 16) of head h against every key cube; the wave takes key blocks wave, wave + waves...
 // Writes s[r][j] for r < 16, j < cubes into `dst` at r * ld + j, or at r * ld + pad_word<32>(j) when PAD (rows past
-// the last query cube skipped). The key blocks stream through a DEPTH-deep register ring: block b + DEPTH waves loads
-// while block b's MFMAs run.
+// the last query cube skipped). With DEPTH > 0 the key blocks stream through a DEPTH-deep register ring (block
+// b + DEPTH waves loads while block b's MFMAs run); with DEPTH 0 each block is loaded when it is scored.
 template <bool PAD, int DEPTH>
 __device__ __forceinline__ void score_rows(const CubeGeo& g, const float* __restrict__ qh, const float* __restrict__ kh,
                                            uint32_t i0, float* dst, uint64_t ld, uint32_t wave, uint32_t waves)
 {
     const uint32_t lane = threadIdx.x & 63u;
-    float qa[32];
-    load_operand(qh, i0, g.cubes, qa);
     const uint32_t kblocks = (g.cubes + 15u) / 16u;
-    auto emit = [&](uint32_t kb_i, const floatx4& acc) {
-        const uint32_t j = kb_i * 16u + (lane & 15u);
+    SplitRow qs;
+    {
+        RawRows qraw;
+        load_raw(qh, i0, g.cubes, qraw);
+        split_exchange(qraw, qs);
+    }
+    auto finish = [&](uint32_t b, floatx4 acc) {
+        const bool finite = __builtin_isfinite(acc[0]) && __builtin_isfinite(acc[1]) && __builtin_isfinite(acc[2]) &&
+                            __builtin_isfinite(acc[3]);
+        if (__ballot(!finite))
+            acc = score_block_direct(qh, kh, i0, b * 16u, g.cubes);
+        const uint32_t j = b * 16u + (lane & 15u);
 #pragma unroll
         for (int v = 0; v < 4; ++v) {
             const uint32_t r = (lane >> 4) * 4u + uint32_t(v);
@@ -176,28 +249,40 @@ __device__ __forceinline__ void score_rows(const CubeGeo& g, const float* __rest
                 dst[r * ld + (PAD ? pad_word<32>(j) : j)] = acc[v] * kScoreScale;
         }
     };
-    float kr[DEPTH][32];
+    if constexpr (DEPTH == 0) {
+        for (uint32_t b = wave; b < kblocks; b += waves) {
+            SplitRow ks;
+            {
+                RawRows raw;
+                load_raw(kh, b * 16u, g.cubes, raw);
+                split_exchange(raw, ks);
+            }
+            finish(b, score_block(qs, ks));
+        }
+    } else {
+        RawRows kr[DEPTH];
 #pragma unroll
-    for (int d = 0; d < DEPTH; ++d)
-        if (wave + uint32_t(d) * waves < kblocks)
-            load_operand(kh, (wave + uint32_t(d) * waves) * 16u, g.cubes, kr[d]);
-    for (uint32_t b0 = wave; b0 < kblocks; b0 += DEPTH * waves) {
+        for (int d = 0; d < DEPTH; ++d)
+            if (wave + uint32_t(d) * waves < kblocks)
+                load_raw(kh, (wave + uint32_t(d) * waves) * 16u, g.cubes, kr[d]);
+        for (uint32_t b0 = wave; b0 < kblocks; b0 += DEPTH * waves) {
 #pragma unroll
-        for (int d = 0; d < DEPTH; ++d) {
-            const uint32_t b = b0 + uint32_t(d) * waves;
-            if (b >= kblocks)
-                break;
-            const floatx4 acc = score_block(qa, kr[d]);
-            if (b + DEPTH * waves < kblocks)
-                load_operand(kh, (b + DEPTH * waves) * 16u, g.cubes, kr[d]);
-            emit(b, acc);
+            for (int d = 0; d < DEPTH; ++d) {
+                const uint32_t b = b0 + uint32_t(d) * waves;
+                if (b >= kblocks)
+                    break;
+                SplitRow ks;
+                split_exchange(kr[d], ks);
+                if (b + DEPTH * waves < kblocks)
+                    load_raw(kh, (b + DEPTH * waves) * 16u, g.cubes, kr[d]);
+                finish(b, score_block(qs, ks));
+            }
         }
     }
 }
 
-// Key blocks in flight a wave in cube_scores. Deeper rings measured slower at 768p (3: +0.5%, 4: +2%, 6: +13%): the
-// fp32 MFMAs, not the operand loads, set the pace once two are in flight.
-constexpr int kScoreDepth = 2;
+// Key blocks in flight a wave in cube_scores: one (0.467-0.469 ms at 768p against 0.478 for two, alternated).
+constexpr int kScoreDepth = 1;
 
 __global__ __launch_bounds__(256) void cube_scores_kernel(CubeGeo g, const float* __restrict__ qc,
                                                           const float* __restrict__ kc, float* __restrict__ s)
@@ -458,12 +543,13 @@ __global__ __launch_bounds__(256) void cube_topk_kernel(CubeGeo g, const float* 
 
 // cube_select: a persistent workgroup of 16 waves loops over tiles (16 query cubes of a head, dealt round robin).
 // Iteration j: each wave ranks its own row of tile t_(j-1) from registers (VALU work), then scores its share of the
-// key blocks of tile t_j into the LDS tile (fp32 MFMAs); barrier; each wave copies its row of t_j into registers as
-// keys; barrier (the tile is free again). Waves finish ranking at different times, so on each SIMD some waves
-// already run MFMAs while others still rank. A wave scores one key block at a time (one 32-MFMA chain, the next
-// block's operands loaded after it): two interleaved chains measured 3% slower once the operand loads were
-// coalesced. Staggering the order on purpose (half the waves scoring first) keeps a row of keys live across the
-// scoring and measured the same (16 registers spilled at 1024 threads' 128).
+// key blocks of tile t_j into the LDS tile (split bf16 MFMAs); barrier; each wave copies its row of t_j into
+// registers as keys; barrier (the tile is free again). Waves finish ranking at different times, so on each SIMD some
+// waves already score while others still rank. A wave loads each key block when it scores it (no register ring):
+// at 1024 threads a wave has 128 registers, and a one-block ring spilled 24 of them (0.715-0.727 ms at 768p against
+// 0.600-0.618 without it, alternated). Measured and slower: half the waves scoring first and ranking after (a row
+// of keys live across the scoring spills 35 registers), and waves in two roles, eight scoring while eight rank two
+// rows each (1.07 ms: two rows of keys spill 62 registers).
 constexpr int kSelectThreads = 1024;
 constexpr uint32_t kSelectRows = 16;
 constexpr uint32_t kSelectMaxCubes = 2048;
@@ -485,7 +571,7 @@ __global__ __launch_bounds__(kSelectThreads) void cube_select_kernel(CubeGeo g, 
     const uint32_t row_tiles = (g.cubes + kSelectRows - 1u) / kSelectRows, tiles = row_tiles * g.heads;
     auto score = [&](uint32_t t) {
         const uint32_t h = t / row_tiles, i0 = (t - h * row_tiles) * kSelectRows;
-        score_rows<true, 1>(g, qc + h * plane, kc + h * plane, i0, tile, kPaddedRow<32>, wave, waves);
+        score_rows<true, 0>(g, qc + h * plane, kc + h * plane, i0, tile, kPaddedRow<32>, wave, waves);
     };
     RowKeys<32> rk;
     auto rank = [&](uint32_t t) {

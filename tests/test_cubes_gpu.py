@@ -75,6 +75,48 @@ def test_cube_scores(dev, cubes_grid):
     assert (np.abs(s - want) <= 1e-5 * scale).all()
 
 
+def test_cube_scores_special_values(dev):
+    """Scores are four bf16 products of split operands unless a 16 x 16 block has a non-finite score; such a block
+    (an infinite or NaN operand, or one so large that its bf16 rounding overflows) is scored by float FMAs instead.
+    Against float64: +inf in q gives +-inf by k's sign along that row, NaN in k gives a NaN column, 3.4e38 in q (whose
+    bf16 rounding is infinite) against keys 1e-4 small in that dimension stays finite and within 1e-5; every block
+    without such an operand is unchanged."""
+    rng = np.random.default_rng(21)
+    grid = (16, 16, 16)  # 64 cubes: 4 x 4 blocks a head, so most blocks keep the split products
+    heads, cubes = 2, mh.cube_count(*grid)
+    qc = rng.standard_normal((heads, cubes, 128)).astype(np.float32)
+    kc = rng.standard_normal((heads, cubes, 128)).astype(np.float32)
+    qc[0, 3, 5] = np.inf
+    kc[0, 7, 9] = np.nan
+    qc[1, 10, 0] = 3.4e38
+    kc[1, :, 0] *= 1e-4
+    a = mh.cube_args(heads, grid)
+    tq, tk = torch.from_numpy(qc).to(dev), torch.from_numpy(kc).to(dev)
+    s = mh.cube_scores(a, tq, tk).cpu().numpy()
+    with np.errstate(invalid="ignore", over="ignore"):
+        want = orc.cube_scores(qc, kc)
+    assert (np.isnan(s) == np.isnan(want)).all()
+    assert np.isnan(s[0, :, 7]).all() and np.isnan(s).sum() == cubes
+    inf = np.isinf(s)
+    assert (inf == np.isinf(want)).all() and inf.sum() == cubes - 1
+    assert (np.sign(s[inf]) == np.sign(want[inf])).all()
+    fin = np.isfinite(want)
+    scale = np.abs(np.where(fin, want, 0)).max(axis=2, keepdims=True)
+    err = np.abs(np.where(fin, s, 0) - np.where(fin, want, 0))
+    assert (err[fin] <= (1e-5 * np.broadcast_to(scale, s.shape))[fin]).all()
+    assert np.isfinite(s[1, 10]).all() and np.abs(s[1, 10]).max() > 1e30
+    # The selection over these scores (no NaN: head 0 without its NaN key) equals cube_scores + cube_topk.
+    kc[0, 7, 9] = 0.0
+    tk = torch.from_numpy(kc).to(dev)
+    a = mh.cube_args(heads, grid, k=20, local=1, out_stride=23)
+    s = mh.cube_scores(a, tq, tk)
+    idx, cnt = mh.cube_topk(a, s)
+    sidx, scnt = mh.cube_select(a, tq, tk)
+    assert (scnt.cpu() == cnt.cpu()).all() and (sidx.cpu() == idx.cpu()).all()
+    widx, wcnt = orc.cube_topk(s.cpu().numpy().astype(np.float64), grid, 20, 1, out_stride=23)
+    assert (cnt.cpu().numpy() == wcnt).all() and (idx.cpu().numpy() == widx).all()
+
+
 @pytest.mark.parametrize("grid", [(8, 8, 12), (5, 7, 9), (16, 16, 16)])
 @pytest.mark.parametrize("local", [0, 1, 3])
 @pytest.mark.parametrize("ratio", [0.0001, 0.1, 0.25, 0.9, 1.0])
