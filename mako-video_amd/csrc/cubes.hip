@@ -18,7 +18,8 @@
 //   The selection is a per-lane bit mask; wave prefix sums over lanes rank the ties (lowest index first) and place
 //   each lane's indices, so the output is ascending with no per-element ballots.
 // - cube_select keeps a 16 x C score tile in LDS between the two phases, so the scores never reach HBM. Its
-//   workgroups are persistent (one a CU) and overlap one tile's ranking with the next tile's scoring across waves.
+//   workgroups are persistent (one a CU); scoring waves and ranking waves overlap one tile's ranking with the next
+//   tile's scoring.
 #include "mh3_common.hpp"
 
 #include <algorithm>
@@ -541,21 +542,26 @@ __global__ __launch_bounds__(256) void cube_topk_kernel(CubeGeo g, const float* 
                   cand + 64);
 }
 
-// cube_select: a persistent workgroup of 16 waves loops over tiles (16 query cubes of a head, dealt round robin).
-// Iteration j: each wave ranks its own row of tile t_(j-1) from registers (VALU work), then scores its share of the
-// key blocks of tile t_j into the LDS tile (split bf16 MFMAs); barrier; each wave copies its row of t_j into
-// registers as keys; barrier (the tile is free again). Waves finish ranking at different times, so on each SIMD some
-// waves already score while others still rank. A wave loads each key block when it scores it (no register ring):
-// at 1024 threads a wave has 128 registers, and a one-block ring spilled 24 of them (0.715-0.727 ms at 768p against
-// 0.600-0.618 without it, alternated). Measured and slower: half the waves scoring first and ranking after (a row
-// of keys live across the scoring spills 35 registers), and waves in two roles, eight scoring while eight rank two
-// rows each (1.07 ms: two rows of keys spill 62 registers).
-constexpr int kSelectThreads = 1024;
+// cube_select: a persistent workgroup of 12 waves loops over tiles (16 query cubes of a head, dealt round robin), in
+// two roles: 4 scoring waves (one a SIMD) and 8 ranking waves (two a SIMD, rows r and r + 8 of a tile each).
+// Iteration j: the scoring waves score the key blocks of tile t_j into the LDS tile (split bf16 MFMAs, the next key
+// block's loads in flight while a block's MFMAs run) while the ranking waves rank their rows of t_(j-1) from
+// registers (VALU work); barrier; the ranking waves copy their rows of t_j into registers as keys; barrier (the tile
+// is free again). The roles run side by side on every SIMD, one's loads and MFMAs beside the other's VALU work, and
+// in separate loops with the same barriers, so neither holds the other's registers (168 a wave at 768 threads).
+// Measured at 768p (alternated): 0.585-0.607 ms against 0.611-0.629 for 16 waves that each score and then rank one
+// row (there scoring and ranking barely overlap: the split's VALU work competes with the ranking's); scoring alone
+// 0.51 ms, ranking alone 0.43 ms. Slower: 8 scoring waves at 1024 threads (0.62-0.64 ms, 128 registers a wave with
+// spills), scoring without the one-block ring (0.66-0.68 ms), a two-block ring (0.87 ms: 17 registers spilled in the
+// loop). A timing copy without the split's VALU work and lane exchange (its outputs wrong) ran 0.51-0.56 ms: split
+// copies of qc and kc prepared ahead would gain at most that, less the pass that writes them.
+constexpr uint32_t kSelectScorers = 4, kSelectRankers = 8;
+constexpr int kSelectThreads = int(64 * (kSelectScorers + kSelectRankers));
 constexpr uint32_t kSelectRows = 16;
 constexpr uint32_t kSelectMaxCubes = 2048;
-static_assert(kSelectRows * 64 == kSelectThreads, "one row of a tile a wave");
+static_assert(2 * kSelectRankers == kSelectRows, "two rows of a tile a ranking wave");
 constexpr size_t kSelectLds =
-    (size_t(kSelectRows) * kPaddedRow<32> + (kSelectThreads / 64) * (64u + kHistBins)) * sizeof(float);
+    (size_t(kSelectRows) * kPaddedRow<32> + kSelectRankers * (64u + kHistBins)) * sizeof(float);
 static_assert(kSelectLds <= 160 * 1024, "the select tile, candidates and histograms fit gfx950's LDS");
 
 __global__ __launch_bounds__(kSelectThreads) void cube_select_kernel(CubeGeo g, const float* __restrict__ qc,
@@ -564,32 +570,40 @@ __global__ __launch_bounds__(kSelectThreads) void cube_select_kernel(CubeGeo g, 
                                                                      int32_t* __restrict__ idx,
                                                                      int32_t* __restrict__ cnt)
 {
-    extern __shared__ float tile[]; // [16][padded row], then 64 candidate words and a histogram per wave
-    const uint32_t wave = threadIdx.x >> 6, waves = kSelectThreads / 64;
-    uint32_t* cand = reinterpret_cast<uint32_t*>(tile + kSelectRows * kPaddedRow<32>) + wave * (64u + kHistBins);
+    extern __shared__ float tile[]; // [16][padded row], then 64 candidate words and a histogram per ranking wave
+    const uint32_t wave = threadIdx.x >> 6;
     const uint64_t plane = uint64_t(g.cubes) * 128u;
     const uint32_t row_tiles = (g.cubes + kSelectRows - 1u) / kSelectRows, tiles = row_tiles * g.heads;
-    auto score = [&](uint32_t t) {
-        const uint32_t h = t / row_tiles, i0 = (t - h * row_tiles) * kSelectRows;
-        score_rows<true, 0>(g, qc + h * plane, kc + h * plane, i0, tile, kPaddedRow<32>, wave, waves);
-    };
-    RowKeys<32> rk;
-    auto rank = [&](uint32_t t) {
-        const uint32_t h = t / row_tiles, i = (t - h * row_tiles) * kSelectRows + wave;
+    if (wave < kSelectScorers) {
+        for (uint32_t t = blockIdx.x; t < tiles; t += gridDim.x) {
+            const uint32_t h = t / row_tiles, i0 = (t - h * row_tiles) * kSelectRows;
+            score_rows<true, 1>(g, qc + h * plane, kc + h * plane, i0, tile, kPaddedRow<32>, wave, kSelectScorers);
+            __syncthreads(); // tile t scored
+            __syncthreads(); // the ranking waves hold every row of t: the tile is free
+        }
+        return;
+    }
+    const uint32_t r0 = wave - kSelectScorers; // rows r0 and r0 + 8 of each tile
+    uint32_t* cand = reinterpret_cast<uint32_t*>(tile + kSelectRows * kPaddedRow<32>) + r0 * (64u + kHistBins);
+    auto rank_row = [&](uint32_t t, uint32_t r, const RowKeys<32>& keys) {
+        const uint32_t h = t / row_tiles, i = (t - h * row_tiles) * kSelectRows + r;
         if (i < g.cubes) {
             const uint64_t item = uint64_t(h) * g.cubes + i;
-            topk_keys<32>(rk, g, i, k, local, idx + item * out_stride, out_stride, cnt + item, cand, cand + 64);
+            topk_keys<32>(keys, g, i, k, local, idx + item * out_stride, out_stride, cnt + item, cand, cand + 64);
         }
     };
+    RowKeys<32> rka, rkb;
     for (uint32_t j = 0;; ++j) {
         const uint32_t t = blockIdx.x + j * gridDim.x;
-        if (j > 0u)
-            rank(t - gridDim.x);
+        if (j > 0u) {
+            rank_row(t - gridDim.x, r0, rka);
+            rank_row(t - gridDim.x, r0 + kSelectRankers, rkb);
+        }
         if (t >= tiles)
             break;
-        score(t);
         __syncthreads(); // tile t scored
-        load_keys<32>(tile + wave * kPaddedRow<32>, g.cubes, rk);
+        load_keys<32>(tile + r0 * kPaddedRow<32>, g.cubes, rka);
+        load_keys<32>(tile + (r0 + kSelectRankers) * kPaddedRow<32>, g.cubes, rkb);
         __syncthreads(); // every row of t in registers: the tile is free
     }
 }
