@@ -152,7 +152,11 @@ int mh3_swiglu_rows(const MH3SwigluArgs* args, const void* gate, const void* up,
  *                       skipped by their grid position, whatever they hold.
  * cube_pool:  qc[h][c][:] = mean of q over cube c's valid rows (float), same for k; counts[c] = valid rows (int32,
  *             may be NULL).
- * cube_scores: s[h][i][j] = qc[h][i] . kc[h][j] / sqrt(head_dim), float [heads][cubes][cubes].
+ * cube_scores: s[h][i][j] = qc[h][i] . kc[h][j] / sqrt(head_dim), float [heads][cubes][cubes]. The dot products
+ *             are the four bf16 MFMA products of each float's bf16 high and low parts, accumulated in float: within
+ *             about 1e-5 of the row's largest score (a float contraction: 1e-6); a 16 x 16 block with a non-finite
+ *             score (infinite or NaN operands, or ones beyond bf16's range) is computed by float FMAs instead.
+ *             cube_select computes the same scores bit for bit.
  * cube_topk:  per (h, query cube i): the k cubes of highest s[h][i][:] (equal scores: lower cube index first),
  *             united with the local cubes (local 1: i itself; 3: also the cubes of the same (cy, cx) one frame group
  *             before and after, where they exist), written as ascending int32 cube indices
