@@ -4,26 +4,29 @@
 // bf16 weights is the dense fc1 of the `--int8 none` path (the reference's bf16 `Gemm::encode`,
 // docs/performance.md:52-69): its B tiles then stream into LDS like A's, one K-step ahead, and there is no scale.
 // With int8 x as well (W8A8, the reference's own `gemm_i8`: activations quantized per row) both operands stream
-// into LDS and the int8 MFMA (v_mfma_i32_32x32x32_i8, exact int32 sums) takes 128 k a K-step; the epilogue applies
+// into LDS and the int8 MFMA (v_mfma_i32_16x16x64_i8, exact int32 sums) takes 128 k a K-step; the epilogue applies
 // both scales. Two more epilogues make the same kernel the qkv projection (a plain store) and the out and fc2
 // projections (gate_add_rows folded in: the residual += gate * y, in place).
 //
-// Design (gfx950, v_mfma_f32_32x32x16_bf16):
+// Design (gfx950, v_mfma_f32_16x16x32_bf16):
 // - A workgroup of 8 wavefronts (2 along rows x 4 along columns) computes a 256-row x 128-column output tile, i.e.
 //   the 128 gate columns [n0, n0+128) and the 128 up columns [n + n0, n + n0 + 128) of y, so the SwiGLU epilogue has
-//   both halves in registers. Each wave owns 128 rows x (32 gate + 32 up) columns: 4 x 2 MFMA tiles of 32 x 32.
+//   both halves in registers. Each wave owns 128 rows x (32 gate + 32 up) columns: 8 x 4 MFMA tiles of 16 x 16.
 // - K advances 64 at a time. A (x, bf16) streams from HBM straight into a 3-stage LDS ring with buffer loads that
 //   write LDS (no VGPR round trip); B (int8 w) is loaded as 16-byte vectors into registers one K-step ahead and
 //   widened to bf16 into a 2-stage LDS ring (exact: |w| <= 127 fits bf16's 8-bit significand), so dequantization
 //   costs no extra HBM traffic and the scale is applied once to the float accumulator in the epilogue:
 //   x (W diag s) = (x W) diag s. The five stages fill gfx950's 160 KiB of LDS.
 // - LDS rows are 128 bytes; the 16-byte chunk c of row r is stored at chunk c ^ ((r >> 1) & 7), so the MFMA operand
-//   reads (32 rows at one chunk per half-wave) hit distinct banks, and B's 16-byte writes are spread over 8 chunk
+//   reads (16 rows at one chunk per quarter-wave) hit distinct banks, and B's 16-byte writes are spread over 8 chunk
 //   columns per 8 lanes by the chunk-to-thread mapping.
 // - Workgroups are mapped XCD-aware: the hardware deals workgroup b to XCD b % 8, so consecutive tiles are renumbered
 //   onto one XCD, and grouped 4 row-tiles a band so the tiles running together on an XCD share x and w in its L2.
 // - The epilogue goes through the LDS, idle by then: results staged as floats, then written (and the gate-add
 //   residual read) in coalesced 16-byte accesses.
+// - 16 x 16 MFMA tiles rather than 32 x 32: the matrix cores sustain a higher clock on them under the same power
+//   limit (a register-only loop of random operands: 1.91 against 1.69-1.76 GHz at 98% busy), with the same LDS bytes
+//   a flop for the same wave tile.
 // - 4 wavefronts of 128 x 128 (fewer LDS bytes a MFMA) measured 10-15% slower than these 8: with one wave a SIMD
 //   nothing hides the fragment reads and the barrier.
 #include "mh3_common.hpp"
@@ -33,7 +36,6 @@
 namespace mh3 {
 
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
-typedef float floatx16 __attribute__((ext_vector_type(16)));
 typedef float floatx4 __attribute__((ext_vector_type(4)));
 
 constexpr uint32_t kBM = 256, kBN = 128, kBK = 64;
@@ -100,10 +102,6 @@ __device__ __forceinline__ void lds_barrier()
 
 constexpr int kGemmWM = 2; // wavefronts along the tile's rows
 constexpr int kGemmWN = 4; // wavefronts along its columns
-// MFMA tile shape: 16 x 16 (v_mfma_f32_16x16x32_bf16, v_mfma_i32_16x16x64_i8). The matrix cores sustain a higher
-// clock on it than on the 32 x 32 forms under the same power limit (a register-only loop of random operands: 1.91
-// against 1.69-1.76 GHz at 98% busy), with the same LDS bytes a flop for the same wave tile.
-constexpr int kGemmShape = 16;
 
 // The three fc1 forms: int8 weights widened to bf16 with bf16 activations (weight-only), bf16 weights, and int8
 // weights with int8 activations (each row of x with its own scale) on the int8 MFMA.
@@ -126,17 +124,15 @@ struct GemmGate {
 };
 
 typedef int int32x4 __attribute__((ext_vector_type(4)));
-typedef int int32x16 __attribute__((ext_vector_type(16)));
 
 // The epilogue shared by the GEMM kernels, through the LDS (idle after the last K-step). acc[a][b][e] is y[r][c]
-// with c = lane % SH + SH b + wn SH TN within the tile's first 128 w rows (b < TN) or, for acc[a][TN + b], the same
-// position in its second 128, and tile row r = wm (256 / WM) + a 32 + 8 (e / 4) + 4 (lane / 32) + e % 4 for the
-// 32 x 32 MFMA tiles (SH 32), r = wm (256 / WM) + a 16 + 4 (lane / 16) + e for the 16 x 16 ones (SH 16). A
+// with c = lane % 16 + 16 b + wn 16 TN within the tile's first 128 w rows (b < TN) or, for acc[a][TN + b], the same
+// position in its second 128, and tile row r = wm (256 / WM) + a 16 + 4 (lane / 16) + e. A
 // 128-column half of the tile at a time, each wave writes its scaled results as floats into a [256][kEpiStride] LDS
 // tile (the two half-waves' rows, 4 apart, fall on disjoint banks); then each thread takes 8 consecutive columns of
 // a row, so the output, and with kGateAdd the residual, moves in 16-byte accesses, 16 threads to a row's 256 bytes.
 // The results round to bf16 once, at the end, as they would written straight from the registers.
-template <int WM, int WN, int MODE, int EPI, int SH, int TM, int TN, typename Acc>
+template <int WM, int WN, int MODE, int EPI, int TM, int TN, typename Acc>
 __device__ __forceinline__ void gemm_epilogue(Acc (&acc)[TM][2 * TN], u32x4_t* smem, uint32_t M, uint32_t N,
                                               uint32_t m0, uint32_t w_lo, uint32_t w_hi,
                                               const float* __restrict__ scale, const float* __restrict__ xscale,
@@ -144,8 +140,7 @@ __device__ __forceinline__ void gemm_epilogue(Acc (&acc)[TM][2 * TN], u32x4_t* s
 {
     constexpr uint32_t kThreads = WM * WN * 64;
     const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6, wm = wave / WN, wn = wave % WN;
-    const uint32_t half = lane >> 5, rl = lane % uint32_t(SH);
-    constexpr int NE = SH * SH / 64; // accumulator elements a lane: 16 (32 x 32) or 4 (16 x 16)
+    const uint32_t rl = lane % 16u;
     constexpr uint32_t kEpiStride = kBN + 8u; // floats a staged row: 4 rows apart = 32 banks apart
     static_assert(kBM * kEpiStride * sizeof(float) <= kGemmLds, "the staged half-tile fits in the LDS");
     constexpr int kHalves = EPI == kSwiGLU ? 1 : 2;
@@ -157,15 +152,13 @@ __device__ __forceinline__ void gemm_epilogue(Acc (&acc)[TM][2 * TN], u32x4_t* s
             lds_barrier(); // the first half is read out
 #pragma unroll
         for (int b = 0; b < TN; ++b) {
-            const uint32_t c = wn * uint32_t(SH) * TN + uint32_t(b) * uint32_t(SH) + rl;
+            const uint32_t c = wn * 16u * TN + uint32_t(b) * 16u + rl;
             const float s_lo = MODE != kBf16 ? scale[w_lo + c] : 1.0f, s_hi = MODE != kBf16 ? scale[w_hi + c] : 1.0f;
 #pragma unroll
             for (int a = 0; a < TM; ++a) {
 #pragma unroll
-                for (int e = 0; e < NE; ++e) {
-                    const uint32_t r = SH == 32 ? wm * (kBM / WM) + uint32_t(a) * 32u + 8u * (uint32_t(e) >> 2) +
-                                                      4u * half + (uint32_t(e) & 3u)
-                                                : wm * (kBM / WM) + uint32_t(a) * 16u + 4u * (lane >> 4) + uint32_t(e);
+                for (int e = 0; e < 4; ++e) {
+                    const uint32_t r = wm * (kBM / WM) + uint32_t(a) * 16u + 4u * (lane >> 4) + uint32_t(e);
                     const float sx = MODE == kW8A8 ? xscale[min(m0 + r, M - 1u)] : 1.0f;
                     float v;
                     if constexpr (EPI == kSwiGLU) {
@@ -218,10 +211,10 @@ __device__ __forceinline__ void gemm_epilogue(Acc (&acc)[TM][2 * TN], u32x4_t* s
 }
 
 // WM x WN wavefronts: wave (wm, wn) computes rows wm * (256 / WM) ... of the tile against its TN gate column tiles
-// (SH columns each, from wn * SH TN) and the TN matching up column tiles, on SH x SH MFMA tiles: SH 32
-// (v_mfma_f32_32x32x16_bf16, v_mfma_i32_32x32x32_i8) or SH 16 (v_mfma_f32_16x16x32_bf16, v_mfma_i32_16x16x64_i8).
-// Every LDS row holds 128 bytes of k: 64 k of bf16 or 128 k of int8, so a K-step is 64 or 128 k.
-template <int WM, int WN, int MODE, int EPI, int SH>
+// (16 columns each, from wn * 16 TN) and the TN matching up column tiles, on 16 x 16 MFMA tiles
+// (v_mfma_f32_16x16x32_bf16, v_mfma_i32_16x16x64_i8). Every LDS row holds 128 bytes of k: 64 k of bf16 or 128 k of
+// int8, so a K-step is 64 or 128 k.
+template <int WM, int WN, int MODE, int EPI>
 __global__ __launch_bounds__(kGemmWM * kGemmWN * 64) void gemm_kernel(
     const void* __restrict__ xv, const void* __restrict__ wv, const float* __restrict__ scale,
     const float* __restrict__ xscale, uint16_t* __restrict__ out, uint32_t M, uint32_t N, uint32_t K, uint32_t mt,
@@ -231,13 +224,12 @@ __global__ __launch_bounds__(kGemmWM * kGemmWN * 64) void gemm_kernel(
     constexpr uint32_t kEA = MODE == kW8A8 ? 1u : 2u;     // bytes of an x element
     constexpr uint32_t kEB = MODE == kBf16 ? 2u : 1u;     // bytes of a w element
     constexpr uint32_t kKS = 128u / kEA;                  // k of a K-step
-    using Acc = typename std::conditional<SH == 32, typename std::conditional<MODE == kW8A8, int32x16, floatx16>::type,
-                                          typename std::conditional<MODE == kW8A8, int32x4, floatx4>::type>::type;
+    using Acc = typename std::conditional<MODE == kW8A8, int32x4, floatx4>::type;
     constexpr uint32_t kThreads = WM * WN * 64, kWaves = WM * WN;
-    constexpr int TM = int(kBM / WM / SH), TN = int(kBN / WN / SH); // MFMA tiles: rows, and gate (= up) columns
-    // Row tiles whose A fragments a sub-step holds: all of them (SH 32), or half (SH 16: a sub-step is one 32-k half
-    // of the K-step over one half of the wave's rows, so its fragments take no more registers than SH 32's).
-    constexpr int FA = SH == 32 ? TM : TM / 2;
+    constexpr int TM = int(kBM / WM / 16), TN = int(kBN / WN / 16); // MFMA tiles: rows, and gate (= up) columns
+    // Row tiles whose A fragments a sub-step holds: half of them (a sub-step is one 32-k half of the K-step over one
+    // half of the wave's rows).
+    constexpr int FA = TM / 2;
     extern __shared__ u32x4_t smem[];
     uint32_t tm, tn;
     tile_of(mt, nt, tm, tn);
@@ -324,21 +316,20 @@ __global__ __launch_bounds__(kGemmWM * kGemmWN * 64) void gemm_kernel(
             lds_dma16(rw, stage + i * 64, bd_off[i], int(kt * 128u));
     };
 
-    // MFMA operands, 16 bytes a lane (8 bf16 or 16 int8 of k). SH 32, sub-step ks (a quarter of the K-step): A rows
-    // wm*(256/WM) + t*32 + lane%32, B rows (gate) wn*32TN + t*32 + lane%32 and (up) 128 + the same, k-chunk
-    // ks*2 + lane/32. SH 16, sub-step ks: k-half h = ks/2 and the wave's row tiles (ks%2)*FA .. +FA-1, A rows
-    // wm*(256/WM) + t*16 + lane%16, B rows wn*16TN + t*16 + lane%16 (and 128 + that), k-chunk 4h + lane/16. Every row
-    // a lane reads has (row >> 1) & 7 = (lane % SH >> 1) & 7, so one offset per sub-step serves all tiles; t moves it
-    // by SH rows. (The 16 rows a quarter-wave reads at one chunk then cover the 64 banks once.)
-    const uint32_t rs = lane % uint32_t(SH), fsx = (rs >> 1) & 7u;
-    const uint32_t fa_base = (wm * (kBM / WM) + rs) * 128u, fb_base = (wn * uint32_t(SH) * TN + rs) * 128u;
-    constexpr uint32_t kRowBytes = uint32_t(SH) * 128u; // one MFMA tile's rows in a stage
+    // MFMA operands, 16 bytes a lane (8 bf16 or 16 int8 of k). Sub-step ks: k-half h = ks/2 and the wave's row tiles
+    // (ks%2)*FA .. +FA-1, A rows wm*(256/WM) + t*16 + lane%16, B rows wn*16TN + t*16 + lane%16 (and 128 + that),
+    // k-chunk 4h + lane/16. Every row a lane reads has (row >> 1) & 7 = (lane % 16 >> 1) & 7, so one offset per
+    // sub-step serves all tiles; t moves it by 16 rows. (The 16 rows a quarter-wave reads at one chunk then cover the
+    // 64 banks once.)
+    const uint32_t rs = lane % 16u, fsx = (rs >> 1) & 7u;
+    const uint32_t fa_base = (wm * (kBM / WM) + rs) * 128u, fb_base = (wn * 16u * TN + rs) * 128u;
+    constexpr uint32_t kRowBytes = 16u * 128u; // one MFMA tile's rows in a stage
     uint32_t fko[4];
 #pragma unroll
     for (uint32_t ks = 0; ks < 4; ++ks)
-        fko[ks] = SH == 32 ? ((ks * 2u + (lane >> 5)) ^ fsx) * 16u : (((ks >> 1) * 4u + (lane >> 4)) ^ fsx) * 16u;
+        fko[ks] = (((ks >> 1) * 4u + (lane >> 4)) ^ fsx) * 16u;
     auto frags_a = [&](uint32_t kt, uint32_t ks, bf16x8_t (&fa)[FA]) {
-        const uint32_t t0 = SH == 32 ? 0u : (ks & 1u) * uint32_t(FA);
+        const uint32_t t0 = (ks & 1u) * uint32_t(FA);
         const char* A = lds + (kt % kAStages) * kStageChunks * 16u + fa_base + fko[ks] + t0 * kRowBytes;
 #pragma unroll
         for (int t = 0; t < FA; ++t)
@@ -352,10 +343,10 @@ __global__ __launch_bounds__(kGemmWM * kGemmWN * 64) void gemm_kernel(
             fb[TN + t] = *reinterpret_cast<const bf16x8_t*>(B + kBN * 128 + t * kRowBytes);
         }
     };
-    // Sub-step ks's fragments; SH 16 reads B only at the start of a k-half (the second sub-step of a half keeps it).
+    // Sub-step ks's fragments; B only at the start of a k-half (the second sub-step of a half keeps it).
     auto frags = [&](uint32_t kt, uint32_t ks, bf16x8_t (&fa)[FA], bf16x8_t (&fb)[2 * TN]) {
         frags_a(kt, ks, fa);
-        if (SH == 32 || (ks & 1u) == 0u)
+        if ((ks & 1u) == 0u)
             frags_b(kt, ks, fb);
     };
 
@@ -367,12 +358,7 @@ __global__ __launch_bounds__(kGemmWM * kGemmWN * 64) void gemm_kernel(
             acc[a][b] = Acc{};
     // One MFMA: acc[a][b] += A fragment fa * B fragment fb.
     auto mfma = [&](Acc& c, const bf16x8_t& fa, const bf16x8_t& fb) {
-        if constexpr (SH == 32 && MODE == kW8A8)
-            c = __builtin_amdgcn_mfma_i32_32x32x32_i8(__builtin_bit_cast(int32x4, fa), __builtin_bit_cast(int32x4, fb),
-                                                      c, 0, 0, 0);
-        else if constexpr (SH == 32)
-            c = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa, fb, c, 0, 0, 0);
-        else if constexpr (MODE == kW8A8)
+        if constexpr (MODE == kW8A8)
             c = __builtin_amdgcn_mfma_i32_16x16x64_i8(__builtin_bit_cast(int32x4, fa), __builtin_bit_cast(int32x4, fb),
                                                       c, 0, 0, 0);
         else
@@ -380,7 +366,7 @@ __global__ __launch_bounds__(kGemmWM * kGemmWN * 64) void gemm_kernel(
     };
     // Sub-step ks's MFMAs: its FA row tiles (from t0) against the 2 TN column tiles.
     auto mfmas = [&](uint32_t ks, const bf16x8_t (&fa)[FA], const bf16x8_t (&fb)[2 * TN]) {
-        const int t0 = SH == 32 ? 0 : int(ks & 1u) * FA;
+        const int t0 = int(ks & 1u) * FA;
 #pragma unroll
         for (int a = 0; a < FA; ++a)
 #pragma unroll
@@ -392,7 +378,7 @@ __global__ __launch_bounds__(kGemmWM * kGemmWN * 64) void gemm_kernel(
     auto mfmas_b = [&](uint32_t ks, const bf16x8_t (&fa)[FA], const bf16x8_t (&fb)[2 * TN], uint32_t kt, int p0,
                        int np) {
         constexpr int n = FA * 2 * TN;
-        const int t0 = SH == 32 ? 0 : int(ks & 1u) * FA;
+        const int t0 = int(ks & 1u) * FA;
 #pragma unroll
         for (int j = 0; j < n; ++j) {
             const int a = j / (2 * TN), b = j % (2 * TN);
@@ -428,8 +414,7 @@ __global__ __launch_bounds__(kGemmWM * kGemmWN * 64) void gemm_kernel(
     // would turn every LDS wait in it into a full wait (scalar loads complete out of order).
     asm volatile("" ::"s"(scale), "s"(xscale), "s"(out), "s"(gg.gate), "s"(gg.set_of_row));
     lds_barrier();
-    // Fragment double buffers: A by sub-step parity; B by sub-step parity (SH 32) or by k-half (SH 16, where a
-    // half's two sub-steps share one B set).
+    // Fragment double buffers: A by sub-step parity, B by k-half (a half's two sub-steps share one B set).
     bf16x8_t fa[2][FA], fb[2][2 * TN];
     frags(0, 0, fa[0], fb[0]);
 
@@ -441,8 +426,8 @@ __global__ __launch_bounds__(kGemmWM * kGemmWN * 64) void gemm_kernel(
     // fragments load. LDS stages written in step kt (A stage (kt+2) % 3, B stage (kt+1) % 2) were last read before
     // step kt-1's barrier. The last step is a separate instance (kLast) so that the loop body has no branch around
     // the barrier: at such a join the compiler's LDS wait would also cover tile kt+1's fragment reads.
-    // B sets of sub-steps 0..3: SH 32 alternates (0, 1, 0, 1); SH 16 keeps one a k-half (0, 0, 1, 1).
-    constexpr int B1 = SH == 32 ? 1 : 0, B2 = SH == 32 ? 0 : 1, B3 = 1;
+    // B sets of sub-steps 0..3: one a k-half (0, 0, 1, 1).
+    constexpr int B1 = 0, B2 = 1, B3 = 1;
     auto kstep = [&](uint32_t kt, auto last) {
         constexpr bool kLast = decltype(last)::value;
         if constexpr (!I8 && !kLast)
@@ -492,7 +477,7 @@ __global__ __launch_bounds__(kGemmWM * kGemmWN * 64) void gemm_kernel(
         kstep(kt, std::false_type{});
     kstep(KT - 1, std::true_type{});
 
-    gemm_epilogue<WM, WN, MODE, EPI, SH, TM, TN>(acc, smem, M, N, m0, w_lo, w_hi, scale, xscale, out, gg);
+    gemm_epilogue<WM, WN, MODE, EPI, TM, TN>(acc, smem, M, N, m0, w_lo, w_hi, scale, xscale, out, gg);
 }
 
 } // namespace mh3
@@ -536,15 +521,15 @@ int launch_gemm(const MH3GemmArgs* a, const void* x, const void* w, const float*
          (host::overlaps(out, out_bytes, gg.gate, (uint64_t(gg.n_sets) - 1u) * gg.gate_stride * 4u + a->n * 4ull) ||
           host::overlaps(out, out_bytes, gg.set_of_row, gg.set_of_row ? uint64_t(a->m) : 0u))))
         return MH3_ERR_PARAM;
-    constexpr int WM = kGemmWM, WN = kGemmWN, SH = kGemmShape;
-    const void* kernel = reinterpret_cast<const void*>(&gemm_kernel<WM, WN, MODE, EPI, SH>);
+    constexpr int WM = kGemmWM, WN = kGemmWN;
+    const void* kernel = reinterpret_cast<const void*>(&gemm_kernel<WM, WN, MODE, EPI>);
     if (const hipError_t e = host::allow_dynamic_lds(kernel, kGemmLds); e != hipSuccess)
         return host::hip_error(e);
     const uint32_t mt = (a->m + kBM - 1) / kBM, nt = a->n / kCols;
     const uint64_t tiles = uint64_t(mt) * nt;
     if (tiles >= (uint64_t(1) << 31))
         return MH3_ERR_SHAPE;
-    hipLaunchKernelGGL((gemm_kernel<WM, WN, MODE, EPI, SH>), dim3(uint32_t(tiles)), dim3(WM * WN * 64), kGemmLds,
+    hipLaunchKernelGGL((gemm_kernel<WM, WN, MODE, EPI>), dim3(uint32_t(tiles)), dim3(WM * WN * 64), kGemmLds,
                        static_cast<hipStream_t>(stream), x, w, scale, xscale, out, a->m, a->n, a->k, mt, nt, gg);
     return host::check_launch();
 }
