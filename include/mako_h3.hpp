@@ -251,6 +251,14 @@ public:
         check(mh3_time_embed(&a, t, w_in, b_in, w_out, b_out, workspace, workspace_bytes, temb, cond, s_),
               "time_embed");
     }
+    // The same without a workspace, for callers that cannot allocate (code under HIP graph capture, serving loops):
+    // the hidden layer in the library's own per-GPU array (levels x hidden at most 65,536 floats). Calls that
+    // overlap in time on one GPU share that array and race; calls on one stream do not.
+    void time_embed_noalloc(const MH3TimeArgs& a, const float* t, const float* w_in, const float* b_in,
+                            const float* w_out, const float* b_out, float* temb, uint16_t* cond) const
+    {
+        check(mh3_time_embed_noalloc(&a, t, w_in, b_in, w_out, b_out, temb, cond, s_), "time_embed");
+    }
     // A block's AdaLN projection: mod[levels][n] = w cond^T + bias, n = 3 x 6 x dim (the [U][3][6][D] table whose
     // (level, tag) sets the row kernels read at set_stride = 6 dim).
     void adaln_mod(uint32_t levels, uint32_t n, uint32_t k, const uint16_t* cond, const uint16_t* w, const float* bias,

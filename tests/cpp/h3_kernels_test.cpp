@@ -431,6 +431,14 @@ void cond()
     mh3o_time_embed(levels, fd, hid, od, 10000.0, t.data(), w_in.data(), b_in.data(), w_out.data(), b_out.data(),
                     wt.data(), wcond.data());
     compare("time embedding (256 -> 1024 -> 512, 3 levels)", of_f32(temb.download()), of_f32(wt), od, 1e-4, 1e-5);
+    {
+        // Without a workspace: the same bits as the call above.
+        DeviceBuffer<float> temb2(temb.size());
+        DeviceBuffer<uint16_t> cond2(cond.size());
+        k.time_embed_noalloc(ta, dt.get(), dwi.get(), dbi.get(), dwo.get(), dbo.get(), temb2.get(), cond2.get());
+        check(temb2.download() == temb.download() && cond2.download() == cond.download(),
+              "time embedding without a workspace, bit for bit the same as with one");
+    }
     // The projection over the GPU's own cond, so that it is tested alone.
     std::vector<uint16_t> wa(size_t(n) * od);
     for (auto& x : wa)
