@@ -340,14 +340,16 @@ def bench_select(mh, dev, steps, warmup):
     kc = torch.empty_like(qc)
     idx = torch.empty((HEADS, cubes, kk + 1), dtype=torch.int32, device=dev)
     cnt = torch.empty((HEADS, cubes), dtype=torch.int32, device=dev)
+    ws = torch.empty(mh.cube_select_workspace_bytes(a), dtype=torch.uint8, device=dev)
     pool_ms, _ = time_launches(lambda: mh.cube_pool(a, q, k, qc=qc, kc=kc), steps, warmup)
-    sel_ms, _ = time_launches(lambda: mh.cube_select(a, qc, kc, idx=idx, cnt=cnt), steps, warmup)
+    sel_ms, _ = time_launches(lambda: mh.cube_select(a, qc, kc, workspace=ws, idx=idx, cnt=cnt), steps, warmup)
     # The pooled inputs (83 MB) fit in the MALL, so back-to-back launches start warm; this timing starts each cold.
-    sel_cold_ms, _ = time_launches(lambda: mh.cube_select(a, qc, kc, idx=idx, cnt=cnt), steps, warmup, cold=True)
+    sel_cold_ms, _ = time_launches(lambda: mh.cube_select(a, qc, kc, workspace=ws, idx=idx, cnt=cnt), steps, warmup,
+                                   cold=True)
 
     def both():
         mh.cube_pool(a, q, k, qc=qc, kc=kc)
-        mh.cube_select(a, qc, kc, idx=idx, cnt=cnt)
+        mh.cube_select(a, qc, kc, workspace=ws, idx=idx, cnt=cnt)
     total_ms, _ = time_launches(both, steps, warmup)
     total_median = LAST_MEDIAN_MS[0]
     # The unfused pair, scores through HBM: for comparison with the fused select.
@@ -603,10 +605,11 @@ def bench_reference_shapes(mh, dev, steps, warmup):
     kc = torch.empty_like(qc)
     idx = torch.empty((H3_HEADS, cubes, kk + 1), dtype=torch.int32, device=dev)
     cnt = torch.empty((H3_HEADS, cubes), dtype=torch.int32, device=dev)
+    ws = torch.empty(mh.cube_select_workspace_bytes(a), dtype=torch.uint8, device=dev)
 
     def select():
         mh.cube_pool(a, q, k, qc=qc, kc=kc)
-        mh.cube_select(a, qc, kc, idx=idx, cnt=cnt)
+        mh.cube_select(a, qc, kc, workspace=ws, idx=idx, cnt=cnt)
     ms, _ = time_launches(select, steps, warmup)
     out["sparse_selection_per_forward"] = entry(ms * H3_BLOCKS, 300.0,
                                                 "cube_pool + cube_select, 56 heads, 400 cubes, k = 40, x 50 blocks")
@@ -682,6 +685,7 @@ def bench_block(mh, dev, steps, warmup):
     kc = torch.empty_like(qc)
     idx = torch.empty((HEADS, cubes, kk + 1), dtype=torch.int32, device=dev)
     cnt = torch.empty((HEADS, cubes), dtype=torch.int32, device=dev)
+    ws = torch.empty(mh.cube_select_workspace_bytes(a), dtype=torch.uint8, device=dev)
     att = torch.empty((ROWS, HEADS * 128), dtype=torch.bfloat16, device=dev)
     f = torch.empty((ROWS, FFN), dtype=torch.bfloat16, device=dev)
 
@@ -690,7 +694,7 @@ def bench_block(mh, dev, steps, warmup):
         mh.gemm(h, wqkv, w_scale=sqkv, out=qkv)
         mh.heads_partial_pool(qkv, HEADS, GRID, None, None, cs, sn, rot=96, layout="rows", cube_layout=mh.CUBES_GRID,
                               q=q, k=k, v=v, qc=qc, kc=kc)
-        mh.cube_select(a, qc, kc, idx=idx, cnt=cnt)
+        mh.cube_select(a, qc, kc, workspace=ws, idx=idx, cnt=cnt)
         mh.flash_attn_sparse_128(a, q, k, v, idx, cnt, dense_row0=video, n_dense=n_dense, out=att)
         mh.gemm_gate_add(att, wo, x, ga_a, w_scale=so)
         mh.rms_mod_rows(x, n2, sh_m, sc_m, out=h)
@@ -716,7 +720,7 @@ def bench_block(mh, dev, steps, warmup):
         mh.gemm(quant(h), wqkv, x_scale=xs, w_scale=sqkv, out=qkv)
         mh.heads_partial_pool(qkv, HEADS, GRID, None, None, cs, sn, rot=96, layout="rows", cube_layout=mh.CUBES_GRID,
                               q=q, k=k, v=v, qc=qc, kc=kc)
-        mh.cube_select(a, qc, kc, idx=idx, cnt=cnt)
+        mh.cube_select(a, qc, kc, workspace=ws, idx=idx, cnt=cnt)
         mh.flash_attn_sparse_128(a, q, k, v, idx, cnt, dense_row0=video, n_dense=n_dense, out=att)
         mh.gemm_gate_add(quant(att), wo, x, ga_a, x_scale=xs, w_scale=so)
         mh.rms_mod_rows(x, n2, sh_m, sc_m, out=h)
@@ -892,10 +896,11 @@ def bench_share(mh, dev, steps, warmup, gpus=8):
     kc = torch.empty_like(qc)
     idx = torch.empty((heads, cubes, kk + 1), dtype=torch.int32, device=dev)
     cnt = torch.empty((heads, cubes), dtype=torch.int32, device=dev)
+    ws = torch.empty(mh.cube_select_workspace_bytes(a), dtype=torch.uint8, device=dev)
 
     def selector():
         mh.cube_pool(a, q, k, qc=qc, kc=kc)
-        mh.cube_select(a, qc, kc, idx=idx, cnt=cnt)
+        mh.cube_select(a, qc, kc, workspace=ws, idx=idx, cnt=cnt)
     ms, _ = time_launches(selector, steps, warmup)
     nb = 2 * heads * video * 128 * 2 + heads * cubes * (kk + 1) * 4
     res["cube_selector"] = {"ms": ms, "GBs": nb / ms / 1e6, "frac": nb / ms / 1e6 / HBM_PEAK_GBS}

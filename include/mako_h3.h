@@ -163,7 +163,10 @@ int mh3_swiglu_rows(const MH3SwigluArgs* args, const void* gate, const void* up,
  *             idx[h][i][0 .. cnt[h][i]) with idx[h][i][cnt .. out_stride) = -1; cnt[h][i] = k + the local cubes not
  *             already among the k. out_stride >= k + local.
  * cube_select: cube_scores and cube_topk fused; the scores stay on chip. Up to 2048 cubes (MH3_ERR_UNSUPPORTED
- *             beyond: use cube_scores + cube_topk, which take up to 4096).
+ *             beyond: use cube_scores + cube_topk, which take up to 4096). `workspace` (device memory, 16-byte
+ *             aligned, at least mh3_cube_select_workspace_bytes(args) bytes, MH3_ERR_SHAPE if smaller; the call
+ *             overwrites it, so calls that overlap in time need their own) holds kc split into the bf16 parts the
+ *             matrix cores take, prepared once a call for all of its query cubes.
  * Each call's outputs may not overlap its inputs or each other (MH3_ERR_PARAM): for q and k the span from the array's
  * start to the last head's last row read.
  * mh3_cube_count() gives the number of cubes of a grid; mh3_topk_k() gives k for a ratio. */
@@ -186,8 +189,9 @@ int mh3_cube_pool(const MH3CubeArgs* args, const uint16_t* q, const uint16_t* k,
                   int32_t* counts, mh3_stream_t stream);
 int mh3_cube_scores(const MH3CubeArgs* args, const float* qc, const float* kc, float* s, mh3_stream_t stream);
 int mh3_cube_topk(const MH3CubeArgs* args, const float* s, int32_t* idx, int32_t* cnt, mh3_stream_t stream);
-int mh3_cube_select(const MH3CubeArgs* args, const float* qc, const float* kc, int32_t* idx, int32_t* cnt,
-                    mh3_stream_t stream);
+int64_t mh3_cube_select_workspace_bytes(const MH3CubeArgs* args); /* a negative code for invalid args */
+int mh3_cube_select(const MH3CubeArgs* args, const float* qc, const float* kc, void* workspace,
+                    uint64_t workspace_bytes, int32_t* idx, int32_t* cnt, mh3_stream_t stream);
 
 /* H3::Cubes' map (docs/architecture.md:120-125), built in the reference's begin(): the attention's row order, the
  * generated video rows in 4x4x4 cubes of (latent frame, patch row, patch column), the grid padded to multiples of 4

@@ -221,11 +221,20 @@ public:
         const MH3CubeArgs a = c.args();
         check(mh3_cube_topk(&a, s, idx, cnt, s_), "cube_topk");
     }
-    // cube_scores + cube_topk with the scores on chip
-    void cube_select(const Cubes& c, const float* qc, const float* kc, int32_t* idx, int32_t* cnt) const
+    // cube_scores + cube_topk with the scores on chip; `workspace` of at least cube_select_workspace_bytes() bytes
+    // holds the split key operands (overwritten by every call).
+    static uint64_t cube_select_workspace_bytes(const Cubes& c)
     {
         const MH3CubeArgs a = c.args();
-        check(mh3_cube_select(&a, qc, kc, idx, cnt, s_), "cube_scores+cube_topk");
+        const int64_t n = mh3_cube_select_workspace_bytes(&a);
+        check(n < 0 ? int(n) : MH3_OK, "cube_select_workspace_bytes");
+        return uint64_t(n);
+    }
+    void cube_select(const Cubes& c, const float* qc, const float* kc, void* workspace, uint64_t workspace_bytes,
+                     int32_t* idx, int32_t* cnt) const
+    {
+        const MH3CubeArgs a = c.args();
+        check(mh3_cube_select(&a, qc, kc, workspace, workspace_bytes, idx, cnt, s_), "cube_scores+cube_topk");
     }
 
     // H3::Cubes' map of begin(): attention row -> model row (-1 for a cube's padding slot), the cubes' 64 rows each

@@ -10,16 +10,17 @@
 // - scores: float dot products on 16 x 16 blocks from the four bf16 MFMA products of operands split into bf16 high
 //   and low parts (v_mfma_f32_16x16x32_bf16): a quarter of the matrix-core clocks of v_mfma_f32_16x16x4_f32, within
 //   1e-5 of the row's largest score; each operand load of the wave reads 64 contiguous bytes of each of 16 rows.
-// - top-k: one wavefront per (head, query cube) holds the row's scores as order-preserving 32-bit keys in VGPRs, lane l
-//   owning cubes 32 l ... 32 l + 31. A 128-bin histogram of the scores, linear in value between the row's minimum and
-//   maximum (LDS atomics, one pass), brackets the k-th largest key to one bin's keys; where that bin holds more than
-//   64 keys a binary search over the key range (per-lane counts, a DPP wave sum) narrows it further, and at most 64
-//   candidates, one to a lane, finish the search.
+// - top-k: one wavefront per (head, query cube) holds the row's scores as floats in VGPRs, lane l owning cubes
+//   32 l ... 32 l + 31. A 128-bin histogram of the scores, linear in value between the row's minimum and maximum (LDS
+//   atomics, one pass), brackets the k-th largest to one bin; a bin of more than 64 scores is binned again over its
+//   own range, and at most 64 candidates, one to a lane, finish the search by ballots. Rows with an infinite or NaN
+//   score are ranked as order-preserving 32-bit keys by a bisection of the key range.
 //   The selection is a per-lane bit mask; wave prefix sums over lanes rank the ties (lowest index first) and place
 //   each lane's indices, so the output is ascending with no per-element ballots.
-// - cube_select keeps a 16 x C score tile in LDS between the two phases, so the scores never reach HBM. Its
-//   workgroups are persistent (one a CU); scoring waves and ranking waves overlap one tile's ranking with the next
-//   tile's scoring.
+// - cube_select keeps a 16 x C score tile in LDS between the two phases, so the scores never reach HBM. A first pass
+//   splits the key cubes into the matrix cores' bf16 operands once (a workspace the caller gives), so its scoring
+//   waves only load and multiply. Its workgroups are persistent (one a CU); scoring waves and ranking waves overlap
+//   one tile's ranking with the next tile's scoring.
 #include "mh3_common.hpp"
 
 #include <algorithm>
@@ -221,15 +222,41 @@ __device__ __forceinline__ uint32_t pad_word(uint32_t j)
 template <int KPL>
 constexpr uint32_t kPaddedRow = 64u * (KPL + 4);
 
-// Scores of query block [i0, i0 + 16) of head h against every key cube; the wave takes key blocks wave, wave + waves...
-// Writes s[r][j] for r < 16, j < cubes into `dst` at r * ld + j, or at r * ld + pad_word<32>(j) when PAD (rows past
-// the last query cube skipped). With DEPTH > 0 the key blocks stream through a DEPTH-deep register ring (block
-// b + DEPTH waves loads while block b's MFMAs run); with DEPTH 0 each block is loaded when it is scored.
-template <bool PAD, int DEPTH>
+// The scores of one key block, stored. A block with a non-finite score (the test is wave-uniform) is scored again by
+// float FMAs (score_block_direct); where `row_flags` is given, rows left with a non-finite score are flagged there.
+// Scores s[r][j] (r < 16, j < cubes) go to `dst` at r * ld + j, or at r * ld + pad_word<32>(j) when PAD (rows past
+// the last query cube skipped).
+template <bool PAD>
+__device__ __forceinline__ void store_block(const CubeGeo& g, const float* __restrict__ qh,
+                                            const float* __restrict__ kh, uint32_t i0, uint32_t b, floatx4 acc,
+                                            float* dst, uint64_t ld, uint32_t* row_flags)
+{
+    const uint32_t lane = threadIdx.x & 63u, j = b * 16u + (lane & 15u);
+    const bool finite = __builtin_isfinite(acc[0]) && __builtin_isfinite(acc[1]) && __builtin_isfinite(acc[2]) &&
+                        __builtin_isfinite(acc[3]);
+    if (__ballot(!finite)) {
+        acc = score_block_direct(qh, kh, i0, b * 16u, g.cubes);
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+            const uint32_t r = (lane >> 4) * 4u + uint32_t(v);
+            if (row_flags && j < g.cubes && i0 + r < g.cubes && !__builtin_isfinite(acc[v]))
+                atomicOr(row_flags + r, 1u);
+        }
+    }
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+        const uint32_t r = (lane >> 4) * 4u + uint32_t(v);
+        if (j < g.cubes && i0 + r < g.cubes)
+            dst[r * ld + (PAD ? pad_word<32>(j) : j)] = acc[v] * kScoreScale;
+    }
+}
+
+// Scores of query block [i0, i0 + 16) of a head against every key cube, from qc and kc as they lie; the wave takes
+// key blocks wave, wave + waves, ..., each split after its load, the next one's loads in flight while a block's MFMAs
+// run (one block ahead: 0.467-0.469 ms at 768p against 0.478 ms for two). Rows go to `dst` at r * ld + j.
 __device__ __forceinline__ void score_rows(const CubeGeo& g, const float* __restrict__ qh, const float* __restrict__ kh,
                                            uint32_t i0, float* dst, uint64_t ld, uint32_t wave, uint32_t waves)
 {
-    const uint32_t lane = threadIdx.x & 63u;
     const uint32_t kblocks = (g.cubes + 15u) / 16u;
     SplitRow qs;
     {
@@ -237,61 +264,85 @@ __device__ __forceinline__ void score_rows(const CubeGeo& g, const float* __rest
         load_raw(qh, i0, g.cubes, qraw);
         split_exchange(qraw, qs);
     }
-    auto finish = [&](uint32_t b, floatx4 acc) {
-        const bool finite = __builtin_isfinite(acc[0]) && __builtin_isfinite(acc[1]) && __builtin_isfinite(acc[2]) &&
-                            __builtin_isfinite(acc[3]);
-        if (__ballot(!finite))
-            acc = score_block_direct(qh, kh, i0, b * 16u, g.cubes);
-        const uint32_t j = b * 16u + (lane & 15u);
-#pragma unroll
-        for (int v = 0; v < 4; ++v) {
-            const uint32_t r = (lane >> 4) * 4u + uint32_t(v);
-            if (j < g.cubes && i0 + r < g.cubes)
-                dst[r * ld + (PAD ? pad_word<32>(j) : j)] = acc[v] * kScoreScale;
-        }
-    };
-    if constexpr (DEPTH == 0) {
-        for (uint32_t b = wave; b < kblocks; b += waves) {
-            SplitRow ks;
-            {
-                RawRows raw;
-                load_raw(kh, b * 16u, g.cubes, raw);
-                split_exchange(raw, ks);
-            }
-            finish(b, score_block(qs, ks));
-        }
-    } else {
-        RawRows kr[DEPTH];
-#pragma unroll
-        for (int d = 0; d < DEPTH; ++d)
-            if (wave + uint32_t(d) * waves < kblocks)
-                load_raw(kh, (wave + uint32_t(d) * waves) * 16u, g.cubes, kr[d]);
-        for (uint32_t b0 = wave; b0 < kblocks; b0 += DEPTH * waves) {
-#pragma unroll
-            for (int d = 0; d < DEPTH; ++d) {
-                const uint32_t b = b0 + uint32_t(d) * waves;
-                if (b >= kblocks)
-                    break;
-                SplitRow ks;
-                split_exchange(kr[d], ks);
-                if (b + DEPTH * waves < kblocks)
-                    load_raw(kh, (b + DEPTH * waves) * 16u, g.cubes, kr[d]);
-                finish(b, score_block(qs, ks));
-            }
-        }
+    RawRows kr;
+    if (wave < kblocks)
+        load_raw(kh, wave * 16u, g.cubes, kr);
+    for (uint32_t b = wave; b < kblocks; b += waves) {
+        SplitRow ks;
+        split_exchange(kr, ks);
+        if (b + waves < kblocks)
+            load_raw(kh, (b + waves) * 16u, g.cubes, kr);
+        store_block<false>(g, qh, kh, i0, b, score_block(qs, ks), dst, ld, nullptr);
     }
 }
 
-// Key blocks in flight a wave in cube_scores: one (0.467-0.469 ms at 768p against 0.478 for two, alternated).
-constexpr int kScoreDepth = 1;
+// The key operands split once for cube_select: block b (16 key cubes) of head h is 8 KiB at ks + (h kblocks + b) 512
+// (16-byte units): unit (2 s + part) 64 + l holds lane l's operands of MFMA step s, part 0 the bf16 high parts and
+// part 1 the low parts, exactly as split_exchange leaves them in the registers. A scoring wave then loads a block with
+// eight 1 KiB contiguous reads and no VALU work, and the scores are the same bits as cube_scores'.
+__global__ __launch_bounds__(256) void cube_split_kernel(CubeGeo g, const float* __restrict__ kc,
+                                                         uint4* __restrict__ ks)
+{
+    const uint32_t kblocks = (g.cubes + 15u) / 16u;
+    const uint32_t item = blockIdx.x * 4u + (threadIdx.x >> 6); // (head, key block), wave-uniform
+    if (item >= g.heads * kblocks)
+        return;
+    const uint32_t h = item / kblocks, b = item - h * kblocks;
+    RawRows raw;
+    load_raw(kc + uint64_t(h) * g.cubes * 128u, b * 16u, g.cubes, raw);
+    SplitRow s;
+    split_exchange(raw, s);
+    uint4* dst = ks + uint64_t(item) * 512u + (threadIdx.x & 63u);
+#pragma unroll
+    for (int st = 0; st < 4; ++st) {
+        dst[(2 * st) * 64] = __builtin_bit_cast(uint4, s.hi[st]);
+        dst[(2 * st + 1) * 64] = __builtin_bit_cast(uint4, s.lo[st]);
+    }
+}
+
+__device__ __forceinline__ void load_split(const uint4* __restrict__ base, uint32_t b, SplitRow& o)
+{
+    const uint4* p = base + uint64_t(b) * 512u + (threadIdx.x & 63u);
+#pragma unroll
+    for (int st = 0; st < 4; ++st) {
+        o.hi[st] = __builtin_bit_cast(bf16x8_t, p[(2 * st) * 64]);
+        o.lo[st] = __builtin_bit_cast(bf16x8_t, p[(2 * st + 1) * 64]);
+    }
+}
+
+// cube_select's scoring: as score_rows, with the key blocks' operands from cube_split_kernel (`ksh`: the head's
+// blocks) and the scores into the padded LDS tile, rows with a non-finite score flagged in `row_flags`. One block in
+// flight a wave: 0.525-0.532 ms at 768p against 0.535-0.551 ms for two (registers spilled) and 1.14 ms for three.
+__device__ __forceinline__ void score_rows_split(const CubeGeo& g, const float* __restrict__ qh,
+                                                 const float* __restrict__ kh, const uint4* __restrict__ ksh,
+                                                 uint32_t i0, float* dst, uint64_t ld, uint32_t wave, uint32_t waves,
+                                                 uint32_t* row_flags)
+{
+    const uint32_t kblocks = (g.cubes + 15u) / 16u;
+    SplitRow qs;
+    {
+        RawRows qraw;
+        load_raw(qh, i0, g.cubes, qraw);
+        split_exchange(qraw, qs);
+    }
+    SplitRow kr;
+    if (wave < kblocks)
+        load_split(ksh, wave, kr);
+    for (uint32_t b = wave; b < kblocks; b += waves) {
+        const floatx4 acc = score_block(qs, kr);
+        if (b + waves < kblocks)
+            load_split(ksh, b + waves, kr);
+        store_block<true>(g, qh, kh, i0, b, acc, dst, ld, row_flags);
+    }
+}
 
 __global__ __launch_bounds__(256) void cube_scores_kernel(CubeGeo g, const float* __restrict__ qc,
                                                           const float* __restrict__ kc, float* __restrict__ s)
 {
     const uint32_t h = blockIdx.y, i0 = blockIdx.x * 16u;
     const uint64_t plane = uint64_t(g.cubes) * 128u;
-    score_rows<false, kScoreDepth>(g, qc + h * plane, kc + h * plane, i0, s + (uint64_t(h) * g.cubes + i0) * g.cubes,
-                                   g.cubes, threadIdx.x >> 6, blockDim.x >> 6);
+    score_rows(g, qc + h * plane, kc + h * plane, i0, s + (uint64_t(h) * g.cubes + i0) * g.cubes, g.cubes,
+               threadIdx.x >> 6, blockDim.x >> 6);
 }
 
 // Order-preserving key of a float score (larger score, larger key); -0 ranks as +0; key 0 is below every score.
@@ -321,168 +372,36 @@ __device__ __forceinline__ float key_value(uint32_t key)
 
 constexpr uint32_t kHistBins = 128; // lanes 0 .. 31 hold four bins each
 
-// Top-k plus local cubes of one (head, query cube i) row of `cubes` scores, by one wavefront. Lane l holds cubes
-// j = l KPL + m (m < KPL), read from `row` in the padded layout of pad_word; entries with j >= cubes are ignored.
-// `cand` (64 words) and `hist` (kHistBins words) are LDS private to the wave.
-// The k-th largest key t is the largest t with #{key >= t} >= k. The search keeps lo (#{key >= lo} = n_lo >= k) and
-// hi (#{key > hi} = n_hi < k), t in [lo, hi]. When the row's scores are finite and not all equal, a histogram sets
-// the first bracket: bin(v) = min(127, (v - vmin) * 128 / (vmax - vmin)) is non-decreasing in v (rounded
-// subtraction, multiplication, minimum and truncation all are), so every key of a higher bin exceeds every key of a
-// lower one. With b the bin where the count from the top first reaches k, lo and hi are the smallest and largest keys
-// of bin b, n_hi the keys above it and n_lo that plus its own. A binary search over the key range then narrows
-// [lo, hi] while more than 64 keys lie in it; the rest are compacted one to a lane and the search finishes over them
-// alone (#{key >= m} = n_hi + #{candidates >= m}).
-// The selection is then a per-lane bit mask: keys above t, the first k - #{key > t} keys equal to t in cube order
-// (ranked by a wave prefix sum of per-lane tie counts) and the local cubes; a prefix sum of the per-lane counts gives
-// each lane its output position, so the indices come out ascending.
-// A row's scores as lane l holds them: keys of cubes j = l KPL + m (m < KPL); bit m of `valid` set when j < cubes
-// (other keys 0).
+// Per-lane bit masks over a lane's KPL cubes.
 template <int KPL>
-struct RowKeys {
-    typedef typename std::conditional<KPL == 32, uint32_t, uint64_t>::type Mask;
-    uint32_t key[KPL];
-    Mask valid;
-};
+using LaneMask = typename std::conditional<KPL == 32, uint32_t, uint64_t>::type;
 
-// Lane l's KPL scores of a row in the padded layout of pad_word, as keys.
+// The selection from the threshold's masks, bit m for cube j0 + m of the lane: gt (scores above the k-th largest t)
+// and eq (scores equal to t). The first k - #gt ties in cube order join gt (a prefix sum of per-lane tie counts ranks
+// them; when there are exactly that many ties they all join), then the local cubes; a prefix sum of the per-lane
+// counts gives each lane its output position, so the indices come out ascending.
 template <int KPL>
-__device__ __forceinline__ void load_keys(const float* row, uint32_t C, RowKeys<KPL>& r)
+__device__ __forceinline__ void select_emit(LaneMask<KPL> gt, LaneMask<KPL> eq, const CubeGeo& g, uint32_t i,
+                                            uint32_t k, uint32_t local, int32_t* __restrict__ out, uint32_t out_stride,
+                                            int32_t* __restrict__ cnt)
 {
-    typedef typename RowKeys<KPL>::Mask Mask;
+    typedef LaneMask<KPL> Mask;
     const uint32_t lane = threadIdx.x & 63u, j0 = lane * KPL;
-    const float4* mine = reinterpret_cast<const float4*>(row + lane * (KPL + 4));
-    const uint32_t nv = C > j0 ? min(C - j0, uint32_t(KPL)) : 0u; // the lane's cubes: keys 0 .. nv - 1
-    r.valid = nv >= uint32_t(KPL) ? ~Mask(0) : (Mask(1) << nv) - Mask(1);
-#pragma unroll
-    for (int v = 0; v < KPL / 4; ++v) {
-        const float4 f = mine[v];
-        const float fv[4] = {f.x, f.y, f.z, f.w};
-#pragma unroll
-        for (int c = 0; c < 4; ++c) {
-            const int m = 4 * v + c;
-            r.key[m] = uint32_t(m) < nv ? score_key(fv[c]) : 0u;
-        }
-    }
-}
-
-template <int KPL>
-__device__ __forceinline__ void topk_keys(const RowKeys<KPL>& rk, const CubeGeo& g, uint32_t i, uint32_t k,
-                                          uint32_t local, int32_t* __restrict__ out, uint32_t out_stride,
-                                          int32_t* __restrict__ cnt, uint32_t* cand, uint32_t* hist)
-{
-    typedef typename RowKeys<KPL>::Mask Mask;
-    const uint32_t lane = threadIdx.x & 63u;
-    const uint32_t C = g.cubes, j0 = lane * KPL;
-    const uint32_t(&key)[KPL] = rk.key;
-    const Mask valid = rk.valid;
-    uint32_t mn = 0xffffffffu, mx = 0u;
-#pragma unroll
-    for (int m = 0; m < KPL; ++m) {
-        const bool ok = (valid >> m) & 1u;
-        mn = ok && key[m] < mn ? key[m] : mn;
-        mx = ok && key[m] > mx ? key[m] : mx;
-    }
-    uint32_t lo = wave_min_u32(mn), hi = wave_max_u32(mx);
-    uint32_t n_lo = C, n_hi = 0u; // every valid key is >= the minimum; padding keys (0) are never counted (mid > 0)
-    constexpr uint32_t kKeyNegInf = 0x007fffffu, kKeyPosInf = 0xff800000u; // score_key(-inf), score_key(+inf)
-    const float vmin = key_value(lo), vmax = key_value(hi);
-    const float inv = float(kHistBins) / (vmax - vmin);
-    if (lo > kKeyNegInf && hi < kKeyPosInf && lo < hi && inv < __builtin_huge_valf()) {
-#pragma unroll
-        for (uint32_t e = lane; e < kHistBins; e += 64u)
-            hist[e] = 0u; // 32-bit stores: a hoisted 16-byte zero vector was spilled under 1024 threads
-        // NaN (padding keys) gives the top bin; padding is never counted or compared.
-        auto bin_of = [&](uint32_t key_m) {
-            return uint32_t(fminf((key_value(key_m) - vmin) * inv, float(kHistBins - 1u)));
-        };
-        // Each key's bin, kept four to a register (byte m % 4 of bins[m / 4]; 0xff for a padding key, which no bin
-        // index equals) for the bracket's pass below.
-        uint32_t bins[KPL / 4];
-#pragma unroll
-        for (int m = 0; m < KPL; ++m) {
-            const bool ok = (valid >> m) & 1u;
-            const uint32_t b_m = ok ? bin_of(key[m]) : 0xffu;
-            if (ok)
-                atomicAdd(hist + b_m, 1u);
-            bins[m / 4] = (m % 4 == 0 ? 0u : bins[m / 4]) | (b_m << (8 * (m % 4)));
-        }
-        __builtin_amdgcn_s_waitcnt(0xC07F); // the wave's own LDS atomics are visible to its reads after lgkmcnt(0)
-        const uint4 h4 = lane < kHistBins / 4u ? reinterpret_cast<const uint4*>(hist)[lane] // bins 4 lane ... + 3
-                                               : uint4{0u, 0u, 0u, 0u};
-        const uint32_t hs[4] = {h4.x, h4.y, h4.z, h4.w};
-        const uint32_t s4 = hs[0] + hs[1] + hs[2] + hs[3];
-        uint32_t above = C - (wave_excl_scan_u32(s4) + s4); // keys in bins above this lane's four
-        uint32_t b = kHistBins, n_above = 0u, n_b = 0u;
-#pragma unroll
-        for (int e = 3; e >= 0; --e) {
-            if (above < k && above + hs[e] >= k)
-                b = 4u * lane + uint32_t(e), n_above = above, n_b = hs[e];
-            above += hs[e];
-        }
-        const uint64_t owner = __ballot(b != kHistBins); // exactly one lane: the counts from the top cross k once
-        const int src = int(__builtin_ctzll(owner));
-        b = uint32_t(__builtin_amdgcn_readlane(int(b), src));
-        n_hi = uint32_t(__builtin_amdgcn_readlane(int(n_above), src));
-        n_lo = n_hi + uint32_t(__builtin_amdgcn_readlane(int(n_b), src));
-        uint32_t bmn = 0xffffffffu, bmx = 0u;
-#pragma unroll
-        for (int m = 0; m < KPL; ++m) {
-            const bool in_b = ((bins[m / 4] >> (8 * (m % 4))) & 0xffu) == b;
-            bmn = in_b && key[m] < bmn ? key[m] : bmn;
-            bmx = in_b && key[m] > bmx ? key[m] : bmx;
-        }
-        lo = wave_min_u32(bmn), hi = wave_max_u32(bmx);
-    }
-    while (lo < hi && n_lo - n_hi > 64u) {
-        const uint32_t d = hi - lo;
-        const uint32_t mid = lo + (d >> 1) + (d & 1u);
-        const uint32_t n = count_ge(key, mid);
-        if (n >= k)
-            lo = mid, n_lo = n;
-        else
-            hi = mid - 1u, n_hi = n;
-    }
-    if (lo < hi) {
-        uint32_t mine_n = 0;
-#pragma unroll
-        for (int m = 0; m < KPL; ++m)
-            mine_n += ((valid >> m) & 1u) && key[m] >= lo && key[m] <= hi ? 1u : 0u;
-        uint32_t slot = wave_excl_scan_u32(mine_n); // the candidates number n_lo - n_hi <= 64
-#pragma unroll
-        for (int m = 0; m < KPL; ++m)
-            if (((valid >> m) & 1u) && key[m] >= lo && key[m] <= hi)
-                cand[slot++] = key[m];
-        __builtin_amdgcn_s_waitcnt(0xC07F); // the wave's own LDS writes are visible to its reads after lgkmcnt(0)
-        const uint32_t c = lane < n_lo - n_hi ? cand[lane] : 0u;
-        const uint32_t need = k - n_hi;
-        while (lo < hi) {
-            const uint32_t d = hi - lo;
-            const uint32_t mid = lo + (d >> 1) + (d & 1u);
-            if (uint32_t(__popcll(__ballot(c >= mid))) >= need)
-                lo = mid;
-            else
-                hi = mid - 1u;
-        }
-    }
-    const uint32_t t = lo;
-    Mask gt = 0, eq = 0;
-#pragma unroll
-    for (int m = 0; m < KPL; ++m) {
-        gt |= key[m] > t ? Mask(1) << m : Mask(0);
-        eq |= key[m] == t ? Mask(1) << m : Mask(0);
-    }
-    gt &= valid;
-    eq &= valid;
     const uint32_t n_gt = uint32_t(__popcll(uint64_t(gt))), n_eq = uint32_t(__popcll(uint64_t(eq)));
     const uint32_t need_eq = k - wave_sum_u32(n_gt); // >= 1
     const uint32_t eq_before = wave_excl_scan_u32(n_eq);
-    uint32_t take = need_eq > eq_before ? min(need_eq - eq_before, n_eq) : 0u;
+    const uint32_t all_eq = uint32_t(__builtin_amdgcn_readlane(int(eq_before + n_eq), 63));
     Mask sel = gt;
+    if (all_eq == need_eq) {
+        sel |= eq;
+    } else {
+        uint32_t take = need_eq > eq_before ? min(need_eq - eq_before, n_eq) : 0u;
 #pragma unroll
-    for (int m = 0; m < KPL; ++m) {
-        const bool tie = (eq >> m) & 1u;
-        sel |= tie && take > 0u ? Mask(1) << m : Mask(0);
-        take -= tie && take > 0u ? 1u : 0u;
+        for (int m = 0; m < KPL; ++m) {
+            const bool tie = (eq >> m) & 1u;
+            sel |= tie && take > 0u ? Mask(1) << m : Mask(0);
+            take -= tie && take > 0u ? 1u : 0u;
+        }
     }
     const uint32_t ct = i / g.plane;
     const uint32_t loc[3] = {local >= 1u ? i : 0xffffffffu, local == 3u && ct > 0u ? i - g.plane : 0xffffffffu,
@@ -509,14 +428,197 @@ __device__ __forceinline__ void topk_keys(const RowKeys<KPL>& rk, const CubeGeo&
         *cnt = int32_t(total);
 }
 
+// A row's scores as lane l holds them: cubes j = l KPL + m (m < KPL) as floats; slots with j >= cubes hold NaN.
 template <int KPL>
-__device__ __forceinline__ void topk_row(const float* row, const CubeGeo& g, uint32_t i, uint32_t k, uint32_t local,
-                                         int32_t* __restrict__ out, uint32_t out_stride, int32_t* __restrict__ cnt,
-                                         uint32_t* cand, uint32_t* hist)
+struct RowVals {
+    float f[KPL];
+};
+
+// Lane l's KPL scores of a row in the padded layout of pad_word.
+template <int KPL>
+__device__ __forceinline__ void load_vals(const float* row, RowVals<KPL>& r)
 {
-    RowKeys<KPL> rk;
-    load_keys<KPL>(row, g.cubes, rk);
-    topk_keys<KPL>(rk, g, i, k, local, out, out_stride, cnt, cand, hist);
+    const uint32_t lane = threadIdx.x & 63u;
+    const float4* mine = reinterpret_cast<const float4*>(row + lane * (KPL + 4));
+#pragma unroll
+    for (int v = 0; v < KPL / 4; ++v) {
+        const float4 x = mine[v];
+        r.f[4 * v] = x.x, r.f[4 * v + 1] = x.y, r.f[4 * v + 2] = x.z, r.f[4 * v + 3] = x.w;
+    }
+}
+
+constexpr int kMaxLevels = 32; // histogram levels of the float search
+
+// Top-k plus local cubes of one (head, query cube i) row of `cubes` scores, by one wavefront. Lane l holds cubes
+// j = l KPL + m (m < KPL) as floats (NaN past the last cube); `cand` (64 words) and `hist` (kHistBins words) are LDS
+// private to the wave. The k-th largest score t is the largest t with #{score >= t} >= k. When every score is finite
+// (`finite`, wave-uniform) it is found on the floats:
+// - A 128-bin histogram, linear in value between the range's lowest and highest score (LDS atomics), brackets t to
+//   one bin: bin(v) = min(127, (v - lo) * 128 / (hi - lo)) is non-decreasing in v (rounded subtraction,
+//   multiplication, minimum and truncation all are), so every score of a higher bin exceeds every score of a lower
+//   one. At the first level the NaN slots fall in the top bin and are taken off its count.
+// - While t's bin holds more than 64 scores, the range narrows to that bin's scores and a new histogram spans them
+//   (a range's lowest and highest scores fall in its bottom and top bins, so each level holds fewer scores); a range
+//   of equal scores is t itself.
+// - The bin's scores are compacted one to a lane and t is selected among them by ballots: the pivot is the lowest
+//   remaining lane's score, and the scores above it, or those below it, remain, so the set shrinks every round.
+// Rows with an infinite or NaN score, and ranges too narrow to scale, rank order-preserving keys (score_key) by a
+// bisection of the key range. Float order is the key order on finite scores (-0 and +0 equal in both).
+template <int KPL>
+__device__ __forceinline__ void topk_vals(RowVals<KPL>& rv, bool finite, const CubeGeo& g, uint32_t i, uint32_t k,
+                                          uint32_t local, int32_t* __restrict__ out, uint32_t out_stride,
+                                          int32_t* __restrict__ cnt, uint32_t* cand, uint32_t* hist)
+{
+    typedef LaneMask<KPL> Mask;
+    const uint32_t lane = threadIdx.x & 63u, C = g.cubes;
+    float(&f)[KPL] = rv.f;
+    bool found = false;
+    float t = 0.0f;
+    if (finite) {
+        float mn = __builtin_inff(), mx = -__builtin_inff();
+#pragma unroll
+        for (int m = 0; m < KPL; ++m) {
+            mn = fminf(mn, f[m]); // NaN slots are ignored
+            mx = fmaxf(mx, f[m]);
+        }
+        float lo = key_value(wave_min_u32(score_key(mn))), hi = key_value(wave_max_u32(score_key(mx)));
+        uint32_t bins[KPL / 4];             // byte m % 4 of bins[m / 4]: score m's bin at the current level
+        uint32_t b = 0u, n_hi = 0u, nb = C; // t's bin; scores above the range [lo, hi]; scores in it
+        // One level: the histogram of the range's scores, then t's bin b, the scores above it and those in it. A score
+        // is in the range when lo <= f <= hi (never a NaN slot).
+        auto level = [&](auto first, float inv) {
+            constexpr bool kFirst = decltype(first)::value;
+#pragma unroll
+            for (uint32_t e = lane; e < kHistBins; e += 64u)
+                hist[e] = 0u;
+#pragma unroll
+            for (int m = 0; m < KPL; ++m) {
+                // NaN slots give the top bin; scores below the range (deeper levels, not counted) bin 0
+                const float x = fminf((f[m] - lo) * inv, float(kHistBins - 1u));
+                const uint32_t b_m = uint32_t(kFirst ? x : fmaxf(x, 0.0f));
+                if (kFirst || (f[m] >= lo && f[m] <= hi))
+                    atomicAdd(hist + b_m, 1u);
+                bins[m / 4] = (m % 4 == 0 ? 0u : bins[m / 4]) | (b_m << (8 * (m % 4)));
+            }
+            __builtin_amdgcn_s_waitcnt(0xC07F); // the wave's own LDS atomics are visible to its reads after lgkmcnt(0)
+            const uint4 h4 =
+                lane < kHistBins / 4u ? reinterpret_cast<const uint4*>(hist)[lane] : uint4{0u, 0u, 0u, 0u};
+            uint32_t hs[4] = {h4.x, h4.y, h4.z, h4.w};
+            if (kFirst && lane == kHistBins / 4u - 1u)
+                hs[3] -= 64u * KPL - C; // the NaN slots
+            const uint32_t s4 = hs[0] + hs[1] + hs[2] + hs[3];
+            uint32_t above = nb - (wave_excl_scan_u32(s4) + s4); // range scores in bins above this lane's four
+            const uint32_t need = k - n_hi;
+            uint32_t bb = kHistBins, n_above = 0u, n_b = 0u;
+#pragma unroll
+            for (int e = 3; e >= 0; --e) {
+                if (above < need && above + hs[e] >= need)
+                    bb = 4u * lane + uint32_t(e), n_above = above, n_b = hs[e];
+                above += hs[e];
+            }
+            const int src = int(__builtin_ctzll(__ballot(bb != kHistBins))); // the counts cross `need` once
+            b = uint32_t(__builtin_amdgcn_readlane(int(bb), src));
+            n_hi += uint32_t(__builtin_amdgcn_readlane(int(n_above), src));
+            nb = uint32_t(__builtin_amdgcn_readlane(int(n_b), src));
+        };
+        // The range's scores in bin b (at most 64) compacted one to a lane, then t selected among them by ballots.
+        auto in_bin = [&](int m) {
+            return f[m] >= lo && f[m] <= hi && ((bins[m / 4] >> (8 * (m % 4))) & 0xffu) == b;
+        };
+        auto pick = [&]() {
+            uint32_t mine_n = 0u;
+#pragma unroll
+            for (int m = 0; m < KPL; ++m)
+                mine_n += in_bin(m) ? 1u : 0u;
+            uint32_t slot = wave_excl_scan_u32(mine_n);
+            // The bin's count from the histogram and from the scores agree; else the key path ranks the row.
+            const bool agree = uint32_t(__builtin_amdgcn_readlane(int(slot + mine_n), 63)) == nb;
+#pragma unroll
+            for (int m = 0; m < KPL; ++m)
+                if (agree && in_bin(m))
+                    cand[slot++] = __float_as_uint(f[m]);
+            __builtin_amdgcn_s_waitcnt(0xC07F); // the wave's own LDS writes are visible to its reads after lgkmcnt(0)
+            const float c = lane < nb ? __uint_as_float(cand[lane]) : __builtin_nanf("");
+            uint64_t rem = agree ? __ballot(lane < nb) : 0u;
+            uint32_t need = k - n_hi; // 1 <= need <= #rem
+            for (int it = 0; it < 64 && rem; ++it) { // at most 64 rounds: each removes a score
+                const float p = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(c), int(__builtin_ctzll(rem))));
+                const uint64_t above_p = __ballot(c > p) & rem, at_p = __ballot(c == p) & rem;
+                const uint32_t n_above_p = uint32_t(__popcll(above_p)), n_at_p = uint32_t(__popcll(at_p));
+                if (need <= n_above_p) {
+                    rem = above_p;
+                } else if (need <= n_above_p + n_at_p) {
+                    t = p, found = true;
+                    break;
+                } else {
+                    need -= n_above_p + n_at_p;
+                    rem &= ~(above_p | at_p);
+                }
+            }
+        };
+        if (!(lo < hi)) {
+            t = lo, found = true; // every score equal
+        } else if (float inv = float(kHistBins) / (hi - lo); inv < __builtin_huge_valf()) {
+            level(std::true_type{}, inv);
+            for (int lv = 1; nb > 64u && lv < kMaxLevels; ++lv) { // beyond kMaxLevels: the key path
+                // The new range: bin b's scores, from its lowest to its highest (monotone bins: exactly those).
+                float mn2 = __builtin_inff(), mx2 = -__builtin_inff();
+#pragma unroll
+                for (int m = 0; m < KPL; ++m) {
+                    const bool in = in_bin(m);
+                    mn2 = in ? fminf(mn2, f[m]) : mn2;
+                    mx2 = in ? fmaxf(mx2, f[m]) : mx2;
+                }
+                lo = key_value(wave_min_u32(score_key(mn2)));
+                hi = key_value(wave_max_u32(score_key(mx2)));
+                if (!(lo < hi)) {
+                    t = lo, found = true; // bin b's scores are equal: t itself
+                    break;
+                }
+                inv = float(kHistBins) / (hi - lo);
+                if (!(inv < __builtin_huge_valf()))
+                    break;
+                level(std::false_type{}, inv);
+            }
+            if (!found && nb <= 64u)
+                pick();
+        }
+    }
+    Mask gt = 0, eq = 0;
+    if (found) {
+#pragma unroll
+        for (int m = 0; m < KPL; ++m) {
+            gt |= f[m] > t ? Mask(1) << m : Mask(0); // NaN slots compare false
+            eq |= f[m] == t ? Mask(1) << m : Mask(0);
+        }
+    } else {
+        const uint32_t j0 = lane * KPL, nv = C > j0 ? min(C - j0, uint32_t(KPL)) : 0u;
+        uint32_t key[KPL];
+        uint32_t kmn = 0xffffffffu, kmx = 0u;
+#pragma unroll
+        for (int m = 0; m < KPL; ++m) {
+            key[m] = uint32_t(m) < nv ? score_key(f[m]) : 0u;
+            kmn = uint32_t(m) < nv ? min(kmn, key[m]) : kmn;
+            kmx = max(kmx, key[m]);
+        }
+        uint32_t klo = wave_min_u32(kmn), khi = wave_max_u32(kmx);
+        while (klo < khi) { // slot keys (0) are never counted: mid > klo
+            const uint32_t d = khi - klo, mid = klo + (d >> 1) + (d & 1u);
+            if (count_ge(key, mid) >= k)
+                klo = mid;
+            else
+                khi = mid - 1u;
+        }
+        const Mask valid = nv >= uint32_t(KPL) ? ~Mask(0) : (Mask(1) << nv) - Mask(1);
+#pragma unroll
+        for (int m = 0; m < KPL; ++m) {
+            gt |= key[m] > klo ? Mask(1) << m : Mask(0);
+            eq |= key[m] == klo ? Mask(1) << m : Mask(0);
+        }
+        gt &= valid;
+        eq &= valid;
+    }
+    select_emit<KPL>(gt, eq, g, i, k, local, out, out_stride, cnt);
 }
 
 // One wavefront per (head, query cube) row of s: the row is staged into LDS in the padded layout (coalesced loads),
@@ -534,50 +636,81 @@ __global__ __launch_bounds__(256) void cube_topk_kernel(CubeGeo g, const float* 
     if (item >= g.heads * g.cubes)
         return;
     const float* src = s + uint64_t(item) * g.cubes;
-#pragma unroll 8
-    for (uint32_t j = lane; j < g.cubes; j += 64u)
-        row[pad_word<KPL>(j)] = src[j];
+    bool bad = false;
+    for (int u0 = 0; u0 < KPL; u0 += 8) {
+        float v[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) // clamped indices: eight loads go out together, unconditionally
+            v[u] = src[min(lane + 64u * uint32_t(u0 + u), g.cubes - 1u)];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+            const uint32_t j = lane + 64u * uint32_t(u0 + u);
+            const float x = j < g.cubes ? v[u] : __builtin_nanf("");
+            bad |= j < g.cubes && !__builtin_isfinite(x);
+            row[pad_word<KPL>(j)] = x; // NaN in the slots past the last cube
+        }
+    }
+    const bool finite = __ballot(bad) == 0u;
     __builtin_amdgcn_s_waitcnt(0xC07F); // the wave reads only what it wrote itself
-    topk_row<KPL>(row, g, item % g.cubes, k, local, idx + uint64_t(item) * out_stride, out_stride, cnt + item, cand,
-                  cand + 64);
+    RowVals<KPL> rv;
+    load_vals<KPL>(row, rv);
+    topk_vals<KPL>(rv, finite, g, item % g.cubes, k, local, idx + uint64_t(item) * out_stride, out_stride, cnt + item,
+                   cand, cand + 64);
 }
 
 // cube_select: a persistent workgroup of 12 waves loops over tiles (16 query cubes of a head, dealt round robin), in
 // two roles: 4 scoring waves (one a SIMD) and 8 ranking waves (two a SIMD, rows r and r + 8 of a tile each).
-// Iteration j: the scoring waves score the key blocks of tile t_j into the LDS tile (split bf16 MFMAs, the next key
-// block's loads in flight while a block's MFMAs run) while the ranking waves rank their rows of t_(j-1) from
-// registers (VALU work); barrier; the ranking waves copy their rows of t_j into registers as keys; barrier (the tile
-// is free again). The roles run side by side on every SIMD, one's loads and MFMAs beside the other's VALU work, and
-// in separate loops with the same barriers, so neither holds the other's registers (168 a wave at 768 threads).
-// Measured at 768p (alternated): 0.585-0.607 ms against 0.611-0.629 for 16 waves that each score and then rank one
-// row (there scoring and ranking barely overlap: the split's VALU work competes with the ranking's); scoring alone
-// 0.51 ms, ranking alone 0.43 ms. Slower: 8 scoring waves at 1024 threads (0.62-0.64 ms, 128 registers a wave with
-// spills), scoring without the one-block ring (0.66-0.68 ms), a two-block ring (0.87 ms: 17 registers spilled in the
-// loop). A timing copy without the split's VALU work and lane exchange (its outputs wrong) ran 0.51-0.56 ms: split
-// copies of qc and kc prepared ahead would gain at most that, less the pass that writes them.
+// Iteration j: the scoring waves score the key blocks of tile t_j into the LDS tile (split bf16 MFMAs on the key
+// operands cube_split_kernel prepared, the next key block's loads in flight while a block's MFMAs run) while the
+// ranking waves rank their rows of t_(j-1) from registers (VALU work); barrier; the ranking waves copy their rows of
+// t_j into registers, with the rows' non-finite flags; barrier (the tile is free again). The roles run side by side
+// on every SIMD, one's loads and MFMAs beside the other's VALU work, and in separate loops with the same barriers, so
+// neither holds the other's registers (168 a wave at 768 threads).
+// Measured at 768p (alternated): 0.420-0.426 ms; scoring alone 0.28 ms. Before: the key blocks split by every tile
+// that scores them (126 times a head at 768p), 0.525-0.548 ms with this ranking and 0.585-0.599 ms with the ranking on
+// order-preserving keys; 16 waves that each score and then rank one row 0.611-0.629 ms; 8 scoring waves at 1024
+// threads 0.62-0.64 ms (128 registers a wave, spills).
 constexpr uint32_t kSelectScorers = 4, kSelectRankers = 8;
 constexpr int kSelectThreads = int(64 * (kSelectScorers + kSelectRankers));
 constexpr uint32_t kSelectRows = 16;
 constexpr uint32_t kSelectMaxCubes = 2048;
 static_assert(2 * kSelectRankers == kSelectRows, "two rows of a tile a ranking wave");
 constexpr size_t kSelectLds =
-    (size_t(kSelectRows) * kPaddedRow<32> + kSelectRankers * (64u + kHistBins)) * sizeof(float);
-static_assert(kSelectLds <= 160 * 1024, "the select tile, candidates and histograms fit gfx950's LDS");
+    (size_t(kSelectRows) * kPaddedRow<32> + kSelectRankers * (64u + kHistBins) + kSelectRows) * sizeof(float);
+static_assert(kSelectLds <= 160 * 1024, "the select tile, candidates, histograms and flags fit gfx950's LDS");
 
 __global__ __launch_bounds__(kSelectThreads) void cube_select_kernel(CubeGeo g, const float* __restrict__ qc,
-                                                                     const float* __restrict__ kc, uint32_t k,
+                                                                     const float* __restrict__ kc,
+                                                                     const uint4* __restrict__ ks, uint32_t k,
                                                                      uint32_t local, uint32_t out_stride,
                                                                      int32_t* __restrict__ idx,
                                                                      int32_t* __restrict__ cnt)
 {
-    extern __shared__ float tile[]; // [16][padded row], then 64 candidate words and a histogram per ranking wave
+    // [16][padded row], then 64 candidate words and a histogram per ranking wave, then a flag word per row (set: the
+    // row has an infinite or NaN score)
+    extern __shared__ float tile[];
     const uint32_t wave = threadIdx.x >> 6;
     const uint64_t plane = uint64_t(g.cubes) * 128u;
     const uint32_t row_tiles = (g.cubes + kSelectRows - 1u) / kSelectRows, tiles = row_tiles * g.heads;
+    uint32_t* row_flags =
+        reinterpret_cast<uint32_t*>(tile + kSelectRows * kPaddedRow<32> + kSelectRankers * (64u + kHistBins));
+    {
+        // NaN in each row's slots past the last cube (never scored: the ranking takes them as no score); flags clear.
+        const uint32_t pad = 64u * 32u - g.cubes;
+        for (uint32_t q = threadIdx.x; q < kSelectRows * pad; q += blockDim.x) {
+            const uint32_t r = q / pad, j = g.cubes + (q - r * pad);
+            tile[r * kPaddedRow<32> + pad_word<32>(j)] = __builtin_nanf("");
+        }
+        if (threadIdx.x < kSelectRows)
+            row_flags[threadIdx.x] = 0u;
+        __syncthreads();
+    }
     if (wave < kSelectScorers) {
+        const uint32_t kblocks = (g.cubes + 15u) / 16u;
         for (uint32_t t = blockIdx.x; t < tiles; t += gridDim.x) {
             const uint32_t h = t / row_tiles, i0 = (t - h * row_tiles) * kSelectRows;
-            score_rows<true, 1>(g, qc + h * plane, kc + h * plane, i0, tile, kPaddedRow<32>, wave, kSelectScorers);
+            score_rows_split(g, qc + h * plane, kc + h * plane, ks + uint64_t(h) * kblocks * 512u, i0, tile,
+                             kPaddedRow<32>, wave, kSelectScorers, row_flags);
             __syncthreads(); // tile t scored
             __syncthreads(); // the ranking waves hold every row of t: the tile is free
         }
@@ -585,25 +718,31 @@ __global__ __launch_bounds__(kSelectThreads) void cube_select_kernel(CubeGeo g, 
     }
     const uint32_t r0 = wave - kSelectScorers; // rows r0 and r0 + 8 of each tile
     uint32_t* cand = reinterpret_cast<uint32_t*>(tile + kSelectRows * kPaddedRow<32>) + r0 * (64u + kHistBins);
-    auto rank_row = [&](uint32_t t, uint32_t r, const RowKeys<32>& keys) {
+    auto rank_row = [&](uint32_t t, uint32_t r, RowVals<32>& vals, bool finite) {
         const uint32_t h = t / row_tiles, i = (t - h * row_tiles) * kSelectRows + r;
         if (i < g.cubes) {
             const uint64_t item = uint64_t(h) * g.cubes + i;
-            topk_keys<32>(keys, g, i, k, local, idx + item * out_stride, out_stride, cnt + item, cand, cand + 64);
+            topk_vals<32>(vals, finite, g, i, k, local, idx + item * out_stride, out_stride, cnt + item, cand,
+                          cand + 64);
         }
     };
-    RowKeys<32> rka, rkb;
+    RowVals<32> rva, rvb;
+    bool fa = true, fb = true;
     for (uint32_t j = 0;; ++j) {
         const uint32_t t = blockIdx.x + j * gridDim.x;
         if (j > 0u) {
-            rank_row(t - gridDim.x, r0, rka);
-            rank_row(t - gridDim.x, r0 + kSelectRankers, rkb);
+            rank_row(t - gridDim.x, r0, rva, fa);
+            rank_row(t - gridDim.x, r0 + kSelectRankers, rvb, fb);
         }
         if (t >= tiles)
             break;
         __syncthreads(); // tile t scored
-        load_keys<32>(tile + r0 * kPaddedRow<32>, g.cubes, rka);
-        load_keys<32>(tile + (r0 + kSelectRankers) * kPaddedRow<32>, g.cubes, rkb);
+        load_vals<32>(tile + r0 * kPaddedRow<32>, rva);
+        load_vals<32>(tile + (r0 + kSelectRankers) * kPaddedRow<32>, rvb);
+        fa = __builtin_amdgcn_readfirstlane(row_flags[r0]) == 0u;
+        fb = __builtin_amdgcn_readfirstlane(row_flags[r0 + kSelectRankers]) == 0u;
+        if ((threadIdx.x & 63u) == 0u)
+            row_flags[r0] = row_flags[r0 + kSelectRankers] = 0u; // after the reads above (same wave, same words)
         __syncthreads(); // every row of t in registers: the tile is free
     }
 }
@@ -804,8 +943,18 @@ int mh3_cube_topk(const MH3CubeArgs* args, const float* s, int32_t* idx, int32_t
     return host::check_launch();
 }
 
-int mh3_cube_select(const MH3CubeArgs* args, const float* qc, const float* kc, int32_t* idx, int32_t* cnt,
-                    mh3_stream_t stream)
+// cube_select's workspace: the key operands split into bf16 parts, 8 KiB a (head, 16-key-cube block).
+uint64_t select_workspace(const CubeGeo& g) { return uint64_t(g.heads) * ((g.cubes + 15u) / 16u) * 8192u; }
+
+int64_t mh3_cube_select_workspace_bytes(const MH3CubeArgs* args)
+{
+    CubeGeo g;
+    const int rc = make_geo(args, g);
+    return rc != MH3_OK ? int64_t(rc) : int64_t(select_workspace(g));
+}
+
+int mh3_cube_select(const MH3CubeArgs* args, const float* qc, const float* kc, void* workspace,
+                    uint64_t workspace_bytes, int32_t* idx, int32_t* cnt, mh3_stream_t stream)
 {
     CubeGeo g;
     int rc = make_geo(args, g);
@@ -813,15 +962,18 @@ int mh3_cube_select(const MH3CubeArgs* args, const float* qc, const float* kc, i
         return rc;
     if ((rc = check_topk_args(args, g)) != MH3_OK)
         return rc;
-    if (!qc || !kc || !idx || !cnt)
+    if (!qc || !kc || !idx || !cnt || !workspace)
         return MH3_ERR_POINTER;
-    if (!host::aligned16(qc) || !host::aligned16(kc))
+    if (!host::aligned16(qc) || !host::aligned16(kc) || !host::aligned16(workspace))
         return MH3_ERR_ALIGN;
+    if (workspace_bytes < select_workspace(g))
+        return MH3_ERR_SHAPE;
     {
         const uint64_t pooled = uint64_t(g.heads) * g.cubes * 128u * 4u;
         const host::Span in[] = {{qc, pooled}, {kc, pooled}};
         const host::Span out[] = {{idx, uint64_t(g.heads) * g.cubes * args->out_stride * 4u},
-                            {cnt, uint64_t(g.heads) * g.cubes * 4u}};
+                                  {cnt, uint64_t(g.heads) * g.cubes * 4u},
+                                  {workspace, select_workspace(g)}};
         if (host::any_overlap(in, out))
             return MH3_ERR_PARAM;
     }
@@ -830,11 +982,17 @@ int mh3_cube_select(const MH3CubeArgs* args, const float* qc, const float* kc, i
     const int lds_ok = set_lds_limit(reinterpret_cast<const void*>(&cube_select_kernel), kSelectLds);
     if (lds_ok != MH3_OK)
         return lds_ok;
+    const hipStream_t st = static_cast<hipStream_t>(stream);
+    uint4* ks = static_cast<uint4*>(workspace);
+    const uint32_t blocks = g.heads * ((g.cubes + 15u) / 16u); // (head, key block) items, one a wave
+    hipLaunchKernelGGL(cube_split_kernel, dim3((blocks + 3u) / 4u), dim3(256), 0, st, g, kc, ks);
+    if ((rc = host::check_launch()) != MH3_OK)
+        return rc;
     // Persistent: one workgroup a CU (the tile takes the LDS), at most one a tile.
     const uint32_t tiles = (g.cubes + kSelectRows - 1) / kSelectRows * g.heads;
     const dim3 grid(std::min<uint32_t>(tiles, uint32_t(host::cu_count())));
-    hipLaunchKernelGGL(cube_select_kernel, grid, dim3(kSelectThreads), kSelectLds, static_cast<hipStream_t>(stream), g,
-                       qc, kc, args->k, args->local, args->out_stride, idx, cnt);
+    hipLaunchKernelGGL(cube_select_kernel, grid, dim3(kSelectThreads), kSelectLds, st, g, qc, kc, ks, args->k,
+                       args->local, args->out_stride, idx, cnt);
     return host::check_launch();
 }
 

@@ -100,7 +100,8 @@ def _load() -> C.CDLL:
         "mh3_cube_pool": (I32, [C.POINTER(CubeArgs), P, P, P, P, P, P]),
         "mh3_cube_scores": (I32, [C.POINTER(CubeArgs), P, P, P, P]),
         "mh3_cube_topk": (I32, [C.POINTER(CubeArgs), P, P, P, P]),
-        "mh3_cube_select": (I32, [C.POINTER(CubeArgs), P, P, P, P, P]),
+        "mh3_cube_select_workspace_bytes": (I64, [C.POINTER(CubeArgs)]),
+        "mh3_cube_select": (I32, [C.POINTER(CubeArgs), P, P, P, C.c_uint64, P, P, P]),
         "mh3_cube_map": (I32, [C.POINTER(CubeMapArgs), P, P, P]),
         "mh3_time_embed_workspace_bytes": (I64, [C.POINTER(TimeArgs)]),
         "mh3_time_embed": (I32, [C.POINTER(TimeArgs), P, P, P, P, P, P, C.c_uint64, P, P, P]),
@@ -386,13 +387,25 @@ def cube_topk(a: CubeArgs, scores, *, idx=None, cnt=None):
     return idx, cnt
 
 
-def cube_select(a: CubeArgs, qc, kc, *, idx=None, cnt=None):
-    """cube_scores and cube_topk fused: the scores stay on chip."""
+def cube_select_workspace_bytes(a: CubeArgs) -> int:
+    n = int(lib.mh3_cube_select_workspace_bytes(C.byref(a)))
+    _check(min(n, 0), "cube_select_workspace_bytes")
+    return n
+
+
+def cube_select(a: CubeArgs, qc, kc, *, workspace=None, idx=None, cnt=None):
+    """cube_scores and cube_topk fused: the scores stay on chip. `workspace` (uint8, at least
+    cube_select_workspace_bytes(a), allocated here when None) holds kc split for the matrix cores."""
     cubes = cube_count(a.grid_t, a.grid_h, a.grid_w)
     _need(qc, "qc", torch.float32, a.heads * cubes * a.head_dim)
     _need(kc, "kc", torch.float32, a.heads * cubes * a.head_dim)
+    nbytes = cube_select_workspace_bytes(a)
+    if workspace is None:
+        workspace = torch.empty(nbytes, dtype=torch.uint8, device=qc.device)
+    _need(workspace, "workspace", torch.uint8, nbytes)
     idx, cnt = _topk_out(a, qc.device, idx, cnt)
-    _check(lib.mh3_cube_select(C.byref(a), _ptr(qc), _ptr(kc), _ptr(idx), _ptr(cnt), _stream()), "cube_select")
+    _check(lib.mh3_cube_select(C.byref(a), _ptr(qc), _ptr(kc), _ptr(workspace), workspace.numel(), _ptr(idx),
+                               _ptr(cnt), _stream()), "cube_select")
     return idx, cnt
 
 

@@ -195,7 +195,8 @@ void cubes()
     k.cube_pool(c, dq.get(), dk.get(), qc.get(), kc.get(), counts.get());
     k.cube_scores(c, qc.get(), kc.get(), s.get());
     k.cube_topk(c, s.get(), idx.get(), cnt.get());
-    k.cube_select(c, qc.get(), kc.get(), idx2.get(), cnt2.get());
+    DeviceBuffer<uint8_t> ws(Kernels::cube_select_workspace_bytes(c));
+    k.cube_select(c, qc.get(), kc.get(), ws.get(), ws.size(), idx2.get(), cnt2.get());
     k.finish();
     std::vector<float> wq(qc.size()), wk(kc.size());
     std::vector<int32_t> wc(C);
@@ -265,7 +266,8 @@ void attn()
     kern.heads_partial(hd, dqkv.get(), dqw.get(), dkw.get(), dcs.get(), dsn.get(), dmap.get(), q.get(), k.get(),
                        v.get());
     kern.cube_pool(c, q.get(), k.get(), qc.get(), kc.get());
-    kern.cube_select(c, qc.get(), kc.get(), idx.get(), cnt.get());
+    DeviceBuffer<uint8_t> ws(Kernels::cube_select_workspace_bytes(c));
+    kern.cube_select(c, qc.get(), kc.get(), ws.get(), ws.size(), idx.get(), cnt.get());
     kern.flash_attn_sparse_128(c, q.get(), k.get(), v.get(), idx.get(), cnt.get(), 64ull * C, n_dense, out.get());
     kern.finish();
     std::vector<uint16_t> oq(tile), ok_(tile), ov(tile), oo(tile, 0);

@@ -164,13 +164,13 @@ def test_swiglu_validation():
 def test_cube_validation():
     a = mh.cube_args(40, (32, 48, 84), k=202, local=1)
     bad = mh.cube_args(40, (32, 48, 84), k=202, local=2)
-    assert mh.lib.mh3_cube_select(C.byref(bad), FAKE, FAKE, FAKE, FAKE, None) == mh.ERR_PARAM
+    assert mh.lib.mh3_cube_select(C.byref(bad), FAKE, FAKE, FAKE, 1 << 30, FAKE, FAKE, None) == mh.ERR_PARAM
     bad = mh.cube_args(40, (32, 48, 84), k=0, local=1)
     assert mh.lib.mh3_cube_topk(C.byref(bad), FAKE, FAKE, FAKE, None) == mh.ERR_PARAM
     bad = mh.cube_args(40, (32, 48, 84), k=2017, local=1)
     assert mh.lib.mh3_cube_topk(C.byref(bad), FAKE, FAKE, FAKE, None) == mh.ERR_PARAM
     bad = mh.cube_args(40, (32, 48, 84), k=202, local=1, out_stride=202)
-    assert mh.lib.mh3_cube_select(C.byref(bad), FAKE, FAKE, FAKE, FAKE, None) == mh.ERR_SHAPE
+    assert mh.lib.mh3_cube_select(C.byref(bad), FAKE, FAKE, FAKE, 1 << 30, FAKE, FAKE, None) == mh.ERR_SHAPE
     bad = mh.cube_args(40, (32, 48, 84), head_dim=64)
     assert mh.lib.mh3_cube_pool(C.byref(bad), FAKE, FAKE, FAKE, FAKE, None, None) == mh.ERR_UNSUPPORTED
     bad = mh.cube_args(40, (0, 48, 84))
@@ -180,6 +180,26 @@ def test_cube_validation():
     assert mh.lib.mh3_cube_pool(C.byref(a), FAKE, None, FAKE, FAKE, None, None) == mh.ERR_POINTER
     big = mh.cube_args(1, (400, 400, 400), k=10, local=1)                 # 10^6 cubes: top-k beyond 4096 cubes
     assert mh.lib.mh3_cube_topk(C.byref(big), FAKE, FAKE, FAKE, None) == mh.ERR_UNSUPPORTED
+
+
+def test_cube_select_workspace():
+    """cube_select's workspace: 8 KiB a (head, 16-key-cube block); refused when missing, misaligned, short, or
+    overlapping an input or output (every check before any GPU call)."""
+    lib = mh.lib
+    a = mh.cube_args(40, (32, 48, 84), k=202, local=1)          # 2016 cubes: 126 key blocks a head
+    need = lib.mh3_cube_select_workspace_bytes(C.byref(a))
+    assert need == 40 * 126 * 8192
+    assert lib.mh3_cube_select_workspace_bytes(C.byref(mh.cube_args(40, (0, 48, 84)))) == mh.ERR_SHAPE
+    assert lib.mh3_cube_select_workspace_bytes(None) == mh.ERR_POINTER
+    qc, kc, idx, cnt, ws = (C.c_void_p(b << 28) for b in (1, 2, 3, 4, 5))  # 256 MiB apart: disjoint
+    sel = lambda w, n, **kw: lib.mh3_cube_select(C.byref(a), kw.get("qc", qc), kw.get("kc", kc), w, n,  # noqa: E731
+                                                 kw.get("idx", idx), cnt, None)
+    assert sel(None, need) == mh.ERR_POINTER
+    assert sel(ODD, need) == mh.ERR_ALIGN
+    assert sel(ws, need - 1) == mh.ERR_SHAPE
+    assert sel(C.c_void_p((2 << 28) + 4096), need) == mh.ERR_PARAM     # inside kc
+    assert sel(C.c_void_p((3 << 28) - 4096), need) == mh.ERR_PARAM     # runs into idx
+    assert sel(ws, need, idx=C.c_void_p((5 << 28) + need - 16)) == mh.ERR_PARAM  # idx starts in its last unit
 
 
 def test_quant_and_gemm_validation():
@@ -327,7 +347,8 @@ def test_selector_refuses_overlapping_outputs():
     s, idx, cnt = C.c_void_p(0x2000000), C.c_void_p(0x3000000), C.c_void_p(0x4000000)
     assert lib.mh3_cube_topk(C.byref(a), s, s, cnt, None) == mh.ERR_PARAM                     # idx = s
     assert lib.mh3_cube_topk(C.byref(a), s, idx, C.c_void_p(0x3000000 + 4), None) == mh.ERR_PARAM
-    assert lib.mh3_cube_select(C.byref(a), qc, kc, idx, qc, None) == mh.ERR_PARAM             # cnt = qc
+    ws = C.c_void_p(0x5000000)
+    assert lib.mh3_cube_select(C.byref(a), qc, kc, ws, 1 << 20, idx, qc, None) == mh.ERR_PARAM  # cnt = qc
     m = mh.CubeMapArgs()
     m.grid_t, m.grid_h, m.grid_w, m.n_dense, m.video_row0, m.dense_row0 = 8, 8, 12, 16, 0, 768
     assert lib.mh3_cube_map(C.byref(m), idx, C.c_void_p(0x3000000 + 64), None) == mh.ERR_PARAM

@@ -117,6 +117,40 @@ def test_cube_scores_special_values(dev):
     assert (cnt.cpu().numpy() == wcnt).all() and (idx.cpu().numpy() == widx).all()
 
 
+def test_select_non_finite_rows_and_workspace_reuse(dev):
+    """cube_select ranks a row whose scores include +-inf or NaN as order-preserving keys (the scoring waves flag
+    such rows), every other row on its floats: the selection equals cube_topk over cube_scores' scores, which takes
+    the same rule from the scores in HBM. NaN in kc[0, 7] makes a NaN column in every row of head 0; +inf in
+    qc[1, 3] makes row 3 of head 1 +-inf; 3.4e38 in qc[1, 10] (bf16-overflowing, scored by float FMAs) leaves row 10
+    finite. Then one workspace sized for the larger call serves a smaller one after it."""
+    rng = np.random.default_rng(23)
+    grid = (16, 16, 32)  # 128 cubes: 8 query tiles and 8 key blocks a head
+    heads, cubes = 2, mh.cube_count(*grid)
+    qc = rng.standard_normal((heads, cubes, 128)).astype(np.float32)
+    kc = rng.standard_normal((heads, cubes, 128)).astype(np.float32)
+    kc[0, 7, 9] = np.nan
+    qc[1, 3, 5] = np.inf
+    qc[1, 10, 0] = 3.4e38
+    kc[1, :, 0] *= 1e-4
+    a = mh.cube_args(heads, grid, k=13, local=1, out_stride=14)
+    tq, tk = torch.from_numpy(qc).to(dev), torch.from_numpy(kc).to(dev)
+    s = mh.cube_scores(a, tq, tk)
+    sn = s.cpu().numpy()
+    assert np.isnan(sn[0]).any(axis=1).all() and np.isinf(sn[1, 3]).any() and np.isfinite(sn[1, 10]).all()
+    idx, cnt = mh.cube_topk(a, s)
+    ws = torch.empty(mh.cube_select_workspace_bytes(a), dtype=torch.uint8, device=dev)
+    sidx, scnt = mh.cube_select(a, tq, tk, workspace=ws)
+    assert torch.equal(scnt, cnt) and torch.equal(sidx, idx)
+    small = (8, 16, 16)  # 32 cubes, in the same workspace
+    a2 = mh.cube_args(1, small, k=5, local=3, out_stride=8)
+    n2 = mh.cube_count(*small)
+    q2, k2 = tq[0, :n2].contiguous(), tk[1, :n2].contiguous()
+    assert mh.cube_select_workspace_bytes(a2) < ws.numel()
+    i2, c2 = mh.cube_select(a2, q2, k2, workspace=ws)
+    w2, wc2 = mh.cube_topk(a2, mh.cube_scores(a2, q2, k2))
+    assert torch.equal(c2, wc2) and torch.equal(i2, w2)
+
+
 @pytest.mark.parametrize("grid", [(8, 8, 12), (5, 7, 9), (16, 16, 16)])
 @pytest.mark.parametrize("local", [0, 1, 3])
 @pytest.mark.parametrize("ratio", [0.0001, 0.1, 0.25, 0.9, 1.0])
