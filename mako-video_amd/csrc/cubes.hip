@@ -482,30 +482,36 @@ __device__ __forceinline__ void topk_vals(RowVals<KPL>& rv, bool finite, const C
             mx = fmaxf(mx, f[m]);
         }
         float lo = key_value(wave_min_u32(score_key(mn))), hi = key_value(wave_max_u32(score_key(mx)));
-        uint32_t bins[KPL / 4];             // byte m % 4 of bins[m / 4]: score m's bin at the current level
+        uint32_t bins[KPL / 4] = {};        // byte m % 4 of bins[m / 4]: score m's bin at the current level
         uint32_t b = 0u, n_hi = 0u, nb = C; // t's bin; scores above the range [lo, hi]; scores in it
         // One level: the histogram of the range's scores, then t's bin b, the scores above it and those in it. A score
         // is in the range when lo <= f <= hi (never a NaN slot).
+        // At the first level only lanes holding a cube count (all of a lane's slots, its NaN slots in the top bin,
+        // taken off afterwards): lanes of NaN slots alone would all add into the top bin at once, and conflicting LDS
+        // atomics serialize (a 400-cube row: 51 of 64 lanes).
+        const bool holds = lane * KPL < C;
         auto level = [&](auto first, float inv) {
             constexpr bool kFirst = decltype(first)::value;
 #pragma unroll
             for (uint32_t e = lane; e < kHistBins; e += 64u)
                 hist[e] = 0u;
+            if (!kFirst || holds) {
 #pragma unroll
-            for (int m = 0; m < KPL; ++m) {
-                // NaN slots give the top bin; scores below the range (deeper levels, not counted) bin 0
-                const float x = fminf((f[m] - lo) * inv, float(kHistBins - 1u));
-                const uint32_t b_m = uint32_t(kFirst ? x : fmaxf(x, 0.0f));
-                if (kFirst || (f[m] >= lo && f[m] <= hi))
-                    atomicAdd(hist + b_m, 1u);
-                bins[m / 4] = (m % 4 == 0 ? 0u : bins[m / 4]) | (b_m << (8 * (m % 4)));
+                for (int m = 0; m < KPL; ++m) {
+                    // NaN slots give the top bin; scores below the range (deeper levels, not counted) bin 0
+                    const float x = fminf((f[m] - lo) * inv, float(kHistBins - 1u));
+                    const uint32_t b_m = uint32_t(kFirst ? x : fmaxf(x, 0.0f));
+                    if (kFirst || (f[m] >= lo && f[m] <= hi))
+                        atomicAdd(hist + b_m, 1u);
+                    bins[m / 4] = (m % 4 == 0 ? 0u : bins[m / 4]) | (b_m << (8 * (m % 4)));
+                }
             }
             __builtin_amdgcn_s_waitcnt(0xC07F); // the wave's own LDS atomics are visible to its reads after lgkmcnt(0)
             const uint4 h4 =
                 lane < kHistBins / 4u ? reinterpret_cast<const uint4*>(hist)[lane] : uint4{0u, 0u, 0u, 0u};
             uint32_t hs[4] = {h4.x, h4.y, h4.z, h4.w};
             if (kFirst && lane == kHistBins / 4u - 1u)
-                hs[3] -= 64u * KPL - C; // the NaN slots
+                hs[3] -= (C + KPL - 1u) / KPL * KPL - C; // the NaN slots of the lane holding the last cube
             const uint32_t s4 = hs[0] + hs[1] + hs[2] + hs[3];
             uint32_t above = nb - (wave_excl_scan_u32(s4) + s4); // range scores in bins above this lane's four
             const uint32_t need = k - n_hi;
