@@ -816,14 +816,41 @@ def bench_fc1(mh, dev, steps, warmup, compare):
         wt = wb.t().contiguous()
         nms, _ = time_launches(lambda: torch.matmul(x, wt, out=y), max(3, steps // 2), 2)
         res["bf16_hipblaslt_gemm_wt_ms"] = nms
-        del wt, y, wb
+        del wt
+        res.update(hipblaslt_tuned_replay(lambda: torch.matmul(x, wb.t(), out=y), flops, max(3, steps // 2)))
+        del y, wb
     return res
 
 
-def bench_hipblaslt_tuned(dev, steps, warmup, max_ms_per_solution=200):
+TUNABLEOP_FC1 = Path(__file__).resolve().parent / "bench_tunableop_fc1.csv"
+
+
+def hipblaslt_tuned_replay(run, flops, steps):
+    """The fc1 GEMM with the solution PyTorch's TunableOp found best for it (`bench.py --only tuned --tunableop-out
+    bench_tunableop_fc1.csv` on this image), read from that file with tuning off, so the default run times it in
+    seconds instead of tuning for minutes. The file's validators (PyTorch, ROCm, hipBLASLt versions, the GPU) must match
+    the running ones, else TunableOp refuses the file and no figure is reported."""
+    if not TUNABLEOP_FC1.exists():
+        return {"bf16_hipblaslt_tuned_ms": None, "bf16_hipblaslt_tuned_note": "no tuning file"}
+    tun = torch.cuda.tunable
+    try:
+        tun.enable(True)
+        tun.tuning_enable(False)
+        if not tun.read_file(str(TUNABLEOP_FC1)):
+            return {"bf16_hipblaslt_tuned_ms": None, "bf16_hipblaslt_tuned_note": "tuning file refused"}
+        sol = [r for r in tun.get_results() if r[0].startswith("GemmTunableOp_BFloat16") and r[2] != "Default"]
+        ms, _ = time_launches(run, steps, 2)
+    finally:
+        tun.enable(False)
+    return {"bf16_hipblaslt_tuned_ms": ms, "bf16_hipblaslt_tuned_tflops": flops / ms / 1e9,
+            "bf16_hipblaslt_tuned_solution": " ".join(map(str, sol[0][:3])) if sol else None}
+
+
+def bench_hipblaslt_tuned(dev, steps, warmup, max_ms_per_solution=200, out_file=None):
     """hipBLASLt's (and rocBLAS's) best solution for fc1's GEMM (x [129,536][5120] bf16 times w^T, w the weight's
     [27,648][5120] rows, no epilogue), found by PyTorch's TunableOp, which times every candidate solution for this
-    shape; beside the default solution torch.matmul picks. The tuning results file goes to a temporary directory."""
+    shape; beside the default solution torch.matmul picks. The tuning results file goes to a temporary directory,
+    and is copied to `out_file` when one is given (the file the default run's fc1 leg replays)."""
     import tempfile
 
     g = torch.Generator(device=dev).manual_seed(9)
@@ -847,6 +874,11 @@ def bench_hipblaslt_tuned(dev, steps, warmup, max_ms_per_solution=200):
         tun.tuning_enable(False)
         tms, _ = time_launches(lambda: torch.matmul(x, wt, out=y), max(3, steps), warmup)
         results = tun.get_results()
+        if out_file:
+            # TunableOp's results-file format: its validators, then one line a tuned GEMM
+            lines = [f"Validator,{k},{v}" for k, v in tun.get_validators()]
+            lines += [",".join(map(str, r)) for r in results]
+            Path(out_file).write_text("\n".join(lines) + "\n")
         tun.enable(False)
     return {"default_ms": dms, "default_tflops": flops / dms / 1e9, "tuned_ms": tms, "tuned_tflops": flops / tms / 1e9,
             "tuned_mfma_util": flops / tms / 1e9 / BF16_PEAK_TFLOPS, "tuning_s": tune_s,
@@ -1076,6 +1108,7 @@ def main() -> int:
                                       "block,ref,share")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-compare", action="store_true")
+    ap.add_argument("--tunableop-out", default=None, help="with --only tuned: where to copy TunableOp's results file")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: these kernels run on a single MI355X and have no multi-GPU path (the row "
@@ -1157,7 +1190,7 @@ def main() -> int:
         done("fc1")
     if "tuned" in ops:
         report["hipblaslt_tuned_fc1"] = bench_hipblaslt_tuned(dev, max(3, args.steps // 2),
-                                                              max(1, args.warmup // 2))
+                                                              max(1, args.warmup // 2), out_file=args.tunableop_out)
         torch.cuda.empty_cache()
         done("tuned")
     if "mfma" in ops:
