@@ -117,6 +117,34 @@ def test_cube_scores_special_values(dev):
     assert (cnt.cpu().numpy() == wcnt).all() and (idx.cpu().numpy() == widx).all()
 
 
+@pytest.mark.parametrize("grid", [(32, 32, 128), (4, 92, 356)])
+def test_select_lane_boundaries_and_outlier_keys(dev, grid):
+    """The float top-k at the edges of its lane layout (32 cubes a lane, 64 lanes): 2048 cubes fill every lane, 2047
+    leave one NaN slot in the last lane. Head 1's key cube 5 has 1000 times the norm of the others, so its scores
+    stretch every row's range and the histogram's first level leaves t's bin over 64 scores: the search narrows to
+    deeper levels. cube_select equals cube_topk over cube_scores bit for bit, and the oracle's top-k over the same
+    scores on sampled rows (all rows of the 2047-cube grid's last tile)."""
+    rng = np.random.default_rng(29)
+    heads, cubes = 2, mh.cube_count(*grid)
+    assert cubes in (2048, 2047)
+    qc = rng.standard_normal((heads, cubes, 128)).astype(np.float32)
+    kc = rng.standard_normal((heads, cubes, 128)).astype(np.float32)
+    kc[1, 5] *= 1000.0
+    k = mh.topk_k(0.1, cubes)
+    a = mh.cube_args(heads, grid, k=k, local=1)
+    tq, tk = torch.from_numpy(qc).to(dev), torch.from_numpy(kc).to(dev)
+    s = mh.cube_scores(a, tq, tk)
+    idx, cnt = mh.cube_topk(a, s)
+    sidx, scnt = mh.cube_select(a, tq, tk)
+    assert torch.equal(scnt, cnt) and torch.equal(sidx, idx)
+    sn = s.cpu().numpy().astype(np.float64)
+    rows = np.unique(np.concatenate([np.arange(cubes - 16, cubes), np.arange(0, cubes, 97)]))
+    for h in range(heads):
+        for i in rows:
+            oi, oc = orc.cube_topk_row(sn[h, i], int(i), grid, k, 1)
+            assert int(cnt[h, i]) == oc and np.array_equal(idx[h, i].cpu().numpy()[:oc], oi[:oc]), f"head {h} row {i}"
+
+
 def test_select_non_finite_rows_and_workspace_reuse(dev):
     """cube_select ranks a row whose scores include +-inf or NaN as order-preserving keys (the scoring waves flag
     such rows), every other row on its floats: the selection equals cube_topk over cube_scores' scores, which takes
