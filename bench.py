@@ -386,7 +386,8 @@ def pass_list_overlap(idx, cnt, cubes):
 
 def bench_attn(mh, dev, steps, warmup, shared=False):
     """flash_attn_sparse_128 at the 768p shape: 40 heads, grid 32 x 48 x 84 (2016 cubes) in the model's row order,
-    512 text rows after the video rows; the pass lists from cube_pool + cube_select at ratio 0.1 (k = 202), local 1.
+    512 text rows after the video rows; the pass lists from cube_pool + cube_select at ratio 0.1 (k = 202), local 1;
+    the query cubes scheduled in cube_order's order, as the block runs them (`plain_order_ms`: without it).
     Algorithmic work: 4 x 128 flops (q.k and p.v) per (query, attended key) pair; K/V bytes: 512 per attended key
     a query tile (one K and one V row per tile that attends it). `shared`: the q/k data whose smooth waves q and k
     share (selector_qk), so neighbouring query cubes' pass lists overlap."""
@@ -401,9 +402,14 @@ def bench_attn(mh, dev, steps, warmup, shared=False):
     a = mh.cube_args(HEADS, GRID, head_stride=rows * 128, k=kk, local=1)
     qc, kc = mh.cube_pool(a, q, k)
     idx, cnt = mh.cube_select(a, qc, kc)
+    order = mh.cube_order(a, idx, cnt)
     out = torch.empty_like(q)
+    # The block's launch: the query cubes in cube_order's order (the plain order timed beside it).
     ms, _ = time_launches(lambda: mh.flash_attn_sparse_128(a, q, k, v, idx, cnt, dense_row0=video, n_dense=n_dense,
-                                                           out=out), steps, warmup)
+                                                           out=out, order=order), steps, warmup)
+    plain_ms, _ = time_launches(lambda: mh.flash_attn_sparse_128(a, q, k, v, idx, cnt, dense_row0=video,
+                                                                 n_dense=n_dense, out=out), steps, warmup)
+    order_ms, _ = time_launches(lambda: mh.cube_order(a, idx, cnt, order=order), steps, warmup)
     sel = int(cnt.to(torch.int64).sum())
     pairs = 64 * (sel * 64 + HEADS * cubes * n_dense) + HEADS * n_dense * rows
     flops = 4.0 * 128 * pairs
@@ -415,6 +421,7 @@ def bench_attn(mh, dev, steps, warmup, shared=False):
     # query tiles), so it is not an HBM figure and is not compared with the HBM peak; the HBM-side rate comes from the
     # counters (bytes past L2, FETCH_SIZE) in the profile summaries.
     res = {"ms": ms, "tflops": flops / ms / 1e9, "mfma_util": flops / ms / 1e9 / BF16_PEAK_TFLOPS,
+           "plain_order_ms": plain_ms, "cube_order_ms": order_ms,
            "flops": flops, "mean_cubes_selected": sel / (HEADS * cubes), "kv_tile_bytes": kv_tile_rows * 512,
            "kv_tile_GBs": kv_tile_rows * 512 / ms / 1e6,
            "flop_per_kv_byte": flops / (kv_tile_rows * 512), "dense_equivalent_flops": dense_flops,
@@ -606,16 +613,19 @@ def bench_reference_shapes(mh, dev, steps, warmup):
     idx = torch.empty((H3_HEADS, cubes, kk + 1), dtype=torch.int32, device=dev)
     cnt = torch.empty((H3_HEADS, cubes), dtype=torch.int32, device=dev)
     ws = torch.empty(mh.cube_select_workspace_bytes(a), dtype=torch.uint8, device=dev)
+    order = torch.empty((H3_HEADS, cubes), dtype=torch.int32, device=dev)
 
     def select():
         mh.cube_pool(a, q, k, qc=qc, kc=kc)
         mh.cube_select(a, qc, kc, workspace=ws, idx=idx, cnt=cnt)
+        mh.cube_order(a, idx, cnt, order=order)
     ms, _ = time_launches(select, steps, warmup)
     out["sparse_selection_per_forward"] = entry(ms * H3_BLOCKS, 300.0,
-                                                "cube_pool + cube_select, 56 heads, 400 cubes, k = 40, x 50 blocks")
+                                                "cube_pool + cube_select + cube_order, 56 heads, 400 cubes, k = 40, "
+                                                "x 50 blocks")
     ao = torch.empty_like(q)
     ms, _ = time_launches(lambda: mh.flash_attn_sparse_128(a, q, k, v, idx, cnt, dense_row0=video, n_dense=n_dense,
-                                                           out=ao), steps, warmup)
+                                                           out=ao, order=order), steps, warmup)
     out["sparse_attention_per_forward"] = entry(ms * H3_BLOCKS, 4700.0,
                                                 "flash_attn_sparse_128 over those pass lists, 19,305 rows, x 50 blocks")
     # Dense attention (docs/performance.md:168-169: 17.2 s a forward) is the same kernel with every cube selected
@@ -686,6 +696,7 @@ def bench_block(mh, dev, steps, warmup):
     idx = torch.empty((HEADS, cubes, kk + 1), dtype=torch.int32, device=dev)
     cnt = torch.empty((HEADS, cubes), dtype=torch.int32, device=dev)
     ws = torch.empty(mh.cube_select_workspace_bytes(a), dtype=torch.uint8, device=dev)
+    order = torch.empty((HEADS, cubes), dtype=torch.int32, device=dev)
     att = torch.empty((ROWS, HEADS * 128), dtype=torch.bfloat16, device=dev)
     f = torch.empty((ROWS, FFN), dtype=torch.bfloat16, device=dev)
 
@@ -695,7 +706,8 @@ def bench_block(mh, dev, steps, warmup):
         mh.heads_partial_pool(qkv, HEADS, GRID, None, None, cs, sn, rot=96, layout="rows", cube_layout=mh.CUBES_GRID,
                               q=q, k=k, v=v, qc=qc, kc=kc)
         mh.cube_select(a, qc, kc, workspace=ws, idx=idx, cnt=cnt)
-        mh.flash_attn_sparse_128(a, q, k, v, idx, cnt, dense_row0=video, n_dense=n_dense, out=att)
+        mh.cube_order(a, idx, cnt, order=order)
+        mh.flash_attn_sparse_128(a, q, k, v, idx, cnt, dense_row0=video, n_dense=n_dense, out=att, order=order)
         mh.gemm_gate_add(att, wo, x, ga_a, w_scale=so)
         mh.rms_mod_rows(x, n2, sh_m, sc_m, out=h)
         mh.gemm_w8a16_swiglu(h, w1, s1, out=f)
@@ -721,7 +733,8 @@ def bench_block(mh, dev, steps, warmup):
         mh.heads_partial_pool(qkv, HEADS, GRID, None, None, cs, sn, rot=96, layout="rows", cube_layout=mh.CUBES_GRID,
                               q=q, k=k, v=v, qc=qc, kc=kc)
         mh.cube_select(a, qc, kc, workspace=ws, idx=idx, cnt=cnt)
-        mh.flash_attn_sparse_128(a, q, k, v, idx, cnt, dense_row0=video, n_dense=n_dense, out=att)
+        mh.cube_order(a, idx, cnt, order=order)
+        mh.flash_attn_sparse_128(a, q, k, v, idx, cnt, dense_row0=video, n_dense=n_dense, out=att, order=order)
         mh.gemm_gate_add(quant(att), wo, x, ga_a, x_scale=xs, w_scale=so)
         mh.rms_mod_rows(x, n2, sh_m, sc_m, out=h)
         mh.gemm_i8_swiglu(quant(h), xs, w1, s1, out=f)
@@ -937,13 +950,15 @@ def bench_share(mh, dev, steps, warmup, gpus=8):
     nb = 2 * heads * video * 128 * 2 + heads * cubes * (kk + 1) * 4
     res["cube_selector"] = {"ms": ms, "GBs": nb / ms / 1e6, "frac": nb / ms / 1e6 / HBM_PEAK_GBS}
     o = torch.empty_like(q)
+    order = mh.cube_order(a, idx, cnt)
     ms, _ = time_launches(lambda: mh.flash_attn_sparse_128(a, q, k, v, idx, cnt, dense_row0=video, n_dense=n_dense,
-                                                           out=o), max(3, steps // 2), max(1, warmup // 2))
+                                                           out=o, order=order), max(3, steps // 2),
+                          max(1, warmup // 2))
     sel = int(cnt.to(torch.int64).sum())
     rows_all = video + n_dense
     fl = 4.0 * 128 * (64 * (sel * 64 + heads * cubes * n_dense) + heads * n_dense * rows_all)
     res["flash_attn_sparse_128"] = {"ms": ms, "tflops": fl / ms / 1e9, "mfma_util": fl / ms / 1e9 / BF16_PEAK_TFLOPS}
-    del q, k, v, o, qc, kc, idx, cnt
+    del q, k, v, o, qc, kc, idx, cnt, order
     torch.cuda.empty_cache()
     return res
 

@@ -29,7 +29,7 @@
 extern "C" {
 #endif
 
-#define MH3_ABI_VERSION 4
+#define MH3_ABI_VERSION 5
 
 /* ---- error codes ------------------------------------------------------------------------------------------------ */
 enum {
@@ -193,6 +193,15 @@ int64_t mh3_cube_select_workspace_bytes(const MH3CubeArgs* args); /* a negative 
 int mh3_cube_select(const MH3CubeArgs* args, const float* qc, const float* kc, void* workspace,
                     uint64_t workspace_bytes, int32_t* idx, int32_t* cnt, mh3_stream_t stream);
 
+/* The query-cube order for mh3_flash_attn_sparse_128_ordered. No counterpart in the reference: a scheduling input for
+ * this library's attention. For each head h, order[h][r] (int32 [heads][cubes]) is the cube of rank r when the head's
+ * cubes are sorted by the middle entry idx[h][c][cnt[h][c] / 2] of their pass lists (the median of the ascending
+ * lists cube_topk and cube_select write; an empty list, or an entry outside [0, cubes), sorts as `cubes`), equal
+ * entries by cube index: a permutation of [0, cubes). Uses heads, grid and out_stride (>= 1) of args; up to 4096
+ * cubes (MH3_ERR_UNSUPPORTED beyond). Pointers 4-byte aligned; order may not overlap idx or cnt (MH3_ERR_PARAM). */
+int mh3_cube_order(const MH3CubeArgs* args, const int32_t* idx, const int32_t* cnt, int32_t* order,
+                   mh3_stream_t stream);
+
 /* H3::Cubes' map (docs/architecture.md:120-125), built in the reference's begin(): the attention's row order, the
  * generated video rows in 4x4x4 cubes of (latent frame, patch row, patch column), the grid padded to multiples of 4
  * with rows that are no token, then the dense rows (text, keyframe and audio), which every query attends. For
@@ -281,6 +290,15 @@ typedef struct MH3AttnArgs {
 } MH3AttnArgs;
 int mh3_flash_attn_sparse_128(const MH3AttnArgs* args, const uint16_t* q, const uint16_t* k, const uint16_t* v,
                               const int32_t* idx, const int32_t* cnt, uint16_t* out, mh3_stream_t stream);
+/* The same attention with the query cubes of each head scheduled in `order` (int32 [heads][cubes], a permutation of
+ * [0, cubes) per head, as mh3_cube_order writes; entries are clamped to [0, cubes), and a non-permutation leaves
+ * cubes unwritten). No counterpart in the reference: it is flash_attn_sparse_128 with a scheduling input. Each XCD
+ * takes a contiguous eighth of a head's cubes in this order, so cubes whose pass lists centre on the same keys run
+ * together and share K/V tiles in that XCD's L2. The outputs equal the plain call's up to the softmax's summation
+ * order. order may not overlap out (MH3_ERR_PARAM) and must be 4-byte aligned. */
+int mh3_flash_attn_sparse_128_ordered(const MH3AttnArgs* args, const uint16_t* q, const uint16_t* k,
+                                      const uint16_t* v, const int32_t* idx, const int32_t* cnt, const int32_t* order,
+                                      uint16_t* out, mh3_stream_t stream);
 
 /* ---- int8 weights: quant_rows_i8 (weight side) ---------------------------------------------------------------------
  * Reference kernel `quant_rows_i8` (mako-common; docs/performance.md:122-123, docs/architecture.md:54-56): each row

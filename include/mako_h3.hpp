@@ -236,6 +236,12 @@ public:
         const MH3CubeArgs a = c.args();
         check(mh3_cube_select(&a, qc, kc, workspace, workspace_bytes, idx, cnt, s_), "cube_scores+cube_topk");
     }
+    // The query-cube order for the ordered attention: each head's cubes sorted by the middle entry of their pass lists.
+    void cube_order(const Cubes& c, const int32_t* idx, const int32_t* cnt, int32_t* order) const
+    {
+        const MH3CubeArgs a = c.args();
+        check(mh3_cube_order(&a, idx, cnt, order, s_), "cube_order");
+    }
 
     // H3::Cubes' map of begin(): attention row -> model row (-1 for a cube's padding slot), the cubes' 64 rows each
     // and then the n_dense dense rows; counts (may be null) the cubes' token counts.
@@ -312,6 +318,14 @@ public:
     {
         const MH3AttnArgs a{c.args(), dense_row0, n_dense, scale};
         check(mh3_flash_attn_sparse_128(&a, q, k, v, idx, cnt, out, s_), "flash_attn_sparse_128");
+    }
+    // The same with the query cubes scheduled in cube_order's order (outputs equal up to summation order).
+    void flash_attn_sparse_128(const Cubes& c, const uint16_t* q, const uint16_t* k, const uint16_t* v,
+                               const int32_t* idx, const int32_t* cnt, const int32_t* order, uint64_t dense_row0,
+                               uint32_t n_dense, uint16_t* out, float scale = 0.0f) const
+    {
+        const MH3AttnArgs a{c.args(), dense_row0, n_dense, scale};
+        check(mh3_flash_attn_sparse_128_ordered(&a, q, k, v, idx, cnt, order, out, s_), "flash_attn_sparse_128");
     }
 
     // Weight rows to int8 with one scale each (at load)

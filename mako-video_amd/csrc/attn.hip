@@ -73,6 +73,7 @@ struct AttnParams {
     FastDiv div_plane, div_cw; // c / plane and c / cw by multiply-high: a key tile's cube coordinates cost a few
                                // scalar instructions instead of integer divisions
     float scale_log2;    // score scale times log2(e): softmax in base 2
+    const int32_t* order; // or null: head h's j-th cube tile takes query cube order[h cubes + j] (clamped)
 };
 
 // A tile of 64 slots. kind 0: dense run (slot l is row base + l, a token while l < lim_t); 1: cube in the grid layout
@@ -175,8 +176,8 @@ __global__ __launch_bounds__(kAttnThreads, STAGES == 2 ? 1 : 2) void attn_sparse
 
     // This workgroup's head and query tile: the dense query tiles of every head first, then the cube tiles. Blocks
     // go to the 8 XCDs round-robin (block b to XCD b % 8); when the counts allow, XCD x takes the x-th eighth of each
-    // head's cubes in raster order, so the workgroups resident on one XCD are neighbouring query cubes, whose pass
-    // lists overlap and meet in that XCD's L2, while all XCDs stay on the same head.
+    // head's cubes in raster order (or in p.order's), so the workgroups resident on one XCD are query cubes whose
+    // pass lists overlap and meet in that XCD's L2, while all XCDs stay on the same head.
     uint32_t h, qt, rank = 0; // rank: the workgroup's place in its XCD's sequence of cube tiles
     {
         const uint32_t b = blockIdx.x, dense_blocks = p.nd * p.heads;
@@ -189,15 +190,17 @@ __global__ __launch_bounds__(kAttnThreads, STAGES == 2 ? 1 : 2) void attn_sparse
             qt = l - h * p.nd;
         } else {
             const uint32_t r = b - dense_blocks;
+            uint32_t j; // the cube tile's place among its head's
             if (p.xcd_slices) {
                 const uint32_t per = p.cubes / 8u, k = r / 8u;
                 h = k / per;
-                qt = p.nd + (r % 8u) * per + (k - h * per);
+                j = (r % 8u) * per + (k - h * per);
                 rank = k;
             } else {
                 h = r / p.cubes;
-                qt = p.nd + (r - h * p.cubes);
+                j = r - h * p.cubes;
             }
+            qt = p.nd + (p.order ? min(uint32_t(p.order[uint64_t(h) * p.cubes + j]), p.cubes - 1u) : j);
         }
     }
     const uint64_t hoff = uint64_t(h) * p.head_stride;
@@ -417,9 +420,11 @@ __global__ __launch_bounds__(kAttnThreads, STAGES == 2 ? 1 : 2) void attn_sparse
 } // namespace
 } // namespace mh3
 
-extern "C" int mh3_flash_attn_sparse_128(const MH3AttnArgs* args, const uint16_t* q, const uint16_t* k,
-                                         const uint16_t* v, const int32_t* idx, const int32_t* cnt, uint16_t* out,
-                                         mh3_stream_t stream)
+namespace {
+
+// order: null for the plain entry point; `ordered`: the ordered one, which needs it.
+int launch_attn(const MH3AttnArgs* args, const uint16_t* q, const uint16_t* k, const uint16_t* v, const int32_t* idx,
+                const int32_t* cnt, const int32_t* order, bool ordered, uint16_t* out, mh3_stream_t stream)
 {
     using namespace mh3;
     if (!args)
@@ -433,12 +438,13 @@ extern "C" int mh3_flash_attn_sparse_128(const MH3AttnArgs* args, const uint16_t
         return MH3_ERR_UNSUPPORTED;
     if (!(args->scale >= 0.0f) || args->scale == __builtin_inff())
         return MH3_ERR_PARAM;
-    if (!q || !k || !v || !idx || !cnt || !out)
+    if (!q || !k || !v || !idx || !cnt || !out || (ordered && !order))
         return MH3_ERR_POINTER;
     if (out == q || out == k || out == v)
         return MH3_ERR_PARAM;
     if (c.row_stride % 8 != 0 || c.head_stride % 8 != 0 || c.row_stride < 128 || !host::aligned16(q) ||
-        !host::aligned16(k) || !host::aligned16(v) || !host::aligned16(out))
+        !host::aligned16(k) || !host::aligned16(v) || !host::aligned16(out) ||
+        reinterpret_cast<uintptr_t>(order) % 4u != 0u)
         return MH3_ERR_ALIGN;
     AttnParams p{};
     p.gt = c.grid_t, p.gh = c.grid_h, p.gw = c.grid_w;
@@ -465,12 +471,13 @@ extern "C" int mh3_flash_attn_sparse_128(const MH3AttnArgs* args, const uint16_t
                                  {k, span},
                                  {v, span},
                                  {idx, uint64_t(c.heads) * cubes * c.out_stride * 4u},
-                                 {cnt, uint64_t(c.heads) * cubes * 4u}};
+                                 {cnt, uint64_t(c.heads) * cubes * 4u},
+                                 {order, uint64_t(c.heads) * cubes * 4u}};
         const host::Span o[] = {{out, span}};
         if (host::any_overlap(in, o))
             return MH3_ERR_PARAM;
     }
-    p.q = q, p.k = k, p.v = v, p.out = out, p.idx = idx, p.cnt = cnt;
+    p.q = q, p.k = k, p.v = v, p.out = out, p.idx = idx, p.cnt = cnt, p.order = order;
     p.row0 = c.row0, p.dense_row0 = args->dense_row0, p.head_stride = c.head_stride, p.row_stride = c.row_stride;
     p.plane = uint32_t(plane), p.cubes = uint32_t(cubes), p.heads = c.heads, p.n_dense = args->n_dense;
     p.div_plane = FastDiv::make(p.plane);
@@ -496,4 +503,20 @@ extern "C" int mh3_flash_attn_sparse_128(const MH3AttnArgs* args, const uint16_t
     hipLaunchKernelGGL(attn_sparse_kernel<kStages>, dim3(uint32_t(blocks)), dim3(kAttnThreads), lds,
                        static_cast<hipStream_t>(stream), p);
     return host::check_launch();
+}
+
+} // namespace
+
+extern "C" int mh3_flash_attn_sparse_128(const MH3AttnArgs* args, const uint16_t* q, const uint16_t* k,
+                                         const uint16_t* v, const int32_t* idx, const int32_t* cnt, uint16_t* out,
+                                         mh3_stream_t stream)
+{
+    return launch_attn(args, q, k, v, idx, cnt, nullptr, false, out, stream);
+}
+
+extern "C" int mh3_flash_attn_sparse_128_ordered(const MH3AttnArgs* args, const uint16_t* q, const uint16_t* k,
+                                                 const uint16_t* v, const int32_t* idx, const int32_t* cnt,
+                                                 const int32_t* order, uint16_t* out, mh3_stream_t stream)
+{
+    return launch_attn(args, q, k, v, idx, cnt, order, true, out, stream);
 }

@@ -782,6 +782,47 @@ __global__ __launch_bounds__(256) void cube_map_kernel(CubeMapParams p, int32_t*
     }
 }
 
+// The attention's query-cube order (flash_attn_sparse_128's ordered form): head h's cubes ranked by the key
+// m(c) cubes + c, where m(c) is the middle entry idx[c][cnt[c] / 2] of cube c's pass list (the median of an ascending
+// list; `cubes` for an empty list or an entry outside [0, cubes)), so the cubes sort by that entry and ties by index;
+// order[h cubes + rank] = c. A workgroup stages one head's keys in LDS and ranks 256 of its cubes, a thread a cube:
+// rank = #{keys below its own} (the keys are distinct), four keys an LDS read, the same for every lane (a broadcast).
+constexpr uint32_t kOrderMaxCubes = 4096;
+
+__global__ __launch_bounds__(256) void cube_order_kernel(uint32_t cubes, uint32_t out_stride,
+                                                         const int32_t* __restrict__ idx,
+                                                         const int32_t* __restrict__ cnt, int32_t* __restrict__ order)
+{
+    __shared__ uint4 keys4[kOrderMaxCubes / 4u];
+    uint32_t* const keys = reinterpret_cast<uint32_t*>(keys4);
+    const uint32_t slices = (cubes + 255u) / 256u, h = blockIdx.x / slices;
+    const uint32_t mine_c = (blockIdx.x - h * slices) * 256u + threadIdx.x, n4 = (cubes + 3u) / 4u;
+    const int32_t* hidx = idx + uint64_t(h) * cubes * out_stride;
+    const int32_t* hcnt = cnt + uint64_t(h) * cubes;
+    for (uint32_t c = threadIdx.x; c < 4u * n4; c += 256u) {
+        uint32_t key = 0xffffffffu; // past the last cube: above every key
+        if (c < cubes) {
+            const int32_t n = min(max(hcnt[c], 0), int32_t(out_stride));
+            const int32_t j = n > 0 ? hidx[uint64_t(c) * out_stride + uint32_t(n) / 2u] : -1;
+            key = (j >= 0 && uint32_t(j) < cubes ? uint32_t(j) : cubes) * cubes + c;
+        }
+        keys[c] = key;
+    }
+    __syncthreads();
+    if (mine_c >= cubes)
+        return;
+    const uint32_t mine = keys[mine_c];
+    uint32_t rank[4] = {0u, 0u, 0u, 0u};
+    for (uint32_t i = 0; i < n4; ++i) {
+        const uint4 kq = keys4[i];
+        rank[0] += kq.x < mine ? 1u : 0u;
+        rank[1] += kq.y < mine ? 1u : 0u;
+        rank[2] += kq.z < mine ? 1u : 0u;
+        rank[3] += kq.w < mine ? 1u : 0u;
+    }
+    order[uint64_t(h) * cubes + (rank[0] + rank[1]) + (rank[2] + rank[3])] = int32_t(mine_c);
+}
+
 } // namespace mh3
 
 // ---- C-ABI ----------------------------------------------------------------------------------------------------------
@@ -999,6 +1040,36 @@ int mh3_cube_select(const MH3CubeArgs* args, const float* qc, const float* kc, v
     const dim3 grid(std::min<uint32_t>(tiles, uint32_t(host::cu_count())));
     hipLaunchKernelGGL(cube_select_kernel, grid, dim3(kSelectThreads), kSelectLds, st, g, qc, kc, ks, args->k,
                        args->local, args->out_stride, idx, cnt);
+    return host::check_launch();
+}
+
+int mh3_cube_order(const MH3CubeArgs* args, const int32_t* idx, const int32_t* cnt, int32_t* order,
+                   mh3_stream_t stream)
+{
+    CubeGeo g;
+    const int rc = make_geo(args, g);
+    if (rc != MH3_OK)
+        return rc;
+    if (args->out_stride == 0)
+        return MH3_ERR_SHAPE;
+    if (!idx || !cnt || !order)
+        return MH3_ERR_POINTER;
+    if ((reinterpret_cast<uintptr_t>(idx) | reinterpret_cast<uintptr_t>(cnt) | reinterpret_cast<uintptr_t>(order)) %
+            4u !=
+        0u)
+        return MH3_ERR_ALIGN;
+    {
+        const uint64_t bytes = uint64_t(g.heads) * g.cubes * 4u; // cnt and order
+        const host::Span in[] = {{idx, bytes * args->out_stride}, {cnt, bytes}};
+        const host::Span out[] = {{order, bytes}};
+        if (host::any_overlap(in, out))
+            return MH3_ERR_PARAM;
+    }
+    if (g.cubes > kOrderMaxCubes)
+        return MH3_ERR_UNSUPPORTED;
+    const uint32_t slices = (g.cubes + 255u) / 256u;
+    hipLaunchKernelGGL(cube_order_kernel, dim3(g.heads * slices), dim3(256), 0, static_cast<hipStream_t>(stream),
+                       g.cubes, args->out_stride, idx, cnt, order);
     return host::check_launch();
 }
 

@@ -20,7 +20,7 @@ import torch
 
 _LIB_PATH = Path(os.environ.get("MAKO_H3_LIB", Path(__file__).resolve().parent.parent / "lib" / "libmako_h3.so"))
 
-ABI_VERSION = 4  # MH3_ABI_VERSION of include/mako_h3.h, whose structs this module mirrors
+ABI_VERSION = 5  # MH3_ABI_VERSION of include/mako_h3.h, whose structs this module mirrors
 OK, ERR_SHAPE, ERR_POINTER, ERR_ALIGN, ERR_PARAM, ERR_HIP, ERR_UNSUPPORTED = 0, -1, -2, -3, -4, -5, -6
 F32, BF16 = 0, 1
 ROWS_NORM_BF16, ROWS_Y_BF16 = 1, 2  # MH3RowsArgs.flags: the float stream's bf16 GEMM rows
@@ -102,6 +102,7 @@ def _load() -> C.CDLL:
         "mh3_cube_topk": (I32, [C.POINTER(CubeArgs), P, P, P, P]),
         "mh3_cube_select_workspace_bytes": (I64, [C.POINTER(CubeArgs)]),
         "mh3_cube_select": (I32, [C.POINTER(CubeArgs), P, P, P, C.c_uint64, P, P, P]),
+        "mh3_cube_order": (I32, [C.POINTER(CubeArgs), P, P, P, P]),
         "mh3_cube_map": (I32, [C.POINTER(CubeMapArgs), P, P, P]),
         "mh3_time_embed_workspace_bytes": (I64, [C.POINTER(TimeArgs)]),
         "mh3_time_embed": (I32, [C.POINTER(TimeArgs), P, P, P, P, P, P, C.c_uint64, P, P, P]),
@@ -111,6 +112,7 @@ def _load() -> C.CDLL:
         "mh3_heads_partial": (I32, [C.POINTER(HeadsArgs), P, P, P, P, P, P, P, P, P, P]),
         "mh3_heads_partial_pool": (I32, [C.POINTER(HeadsArgs), C.POINTER(CubeArgs)] + [P] * 13),
         "mh3_flash_attn_sparse_128": (I32, [C.POINTER(AttnArgs), P, P, P, P, P, P, P]),
+        "mh3_flash_attn_sparse_128_ordered": (I32, [C.POINTER(AttnArgs), P, P, P, P, P, P, P, P]),
         "mh3_quant_rows_i8": (I32, [C.POINTER(QuantArgs), P, P, P, P]),
         "mh3_gemm_w8a16_swiglu": (I32, [C.POINTER(GemmArgs), P, P, P, P, P]),
         "mh3_gemm_bf16_swiglu": (I32, [C.POINTER(GemmArgs), P, P, P, P]),
@@ -409,6 +411,18 @@ def cube_select(a: CubeArgs, qc, kc, *, workspace=None, idx=None, cnt=None):
     return idx, cnt
 
 
+def cube_order(a: CubeArgs, idx, cnt, *, order=None):
+    """The query-cube order for flash_attn_sparse_128(order=...): int32 [heads][cubes], each head's cubes sorted by
+    the middle entry of their pass lists (idx[h][c][cnt / 2]), equal entries by cube index."""
+    cubes = cube_count(a.grid_t, a.grid_h, a.grid_w)
+    _need(idx, "idx", torch.int32, a.heads * cubes * a.out_stride)
+    _need(cnt, "cnt", torch.int32, a.heads * cubes)
+    order = torch.empty((a.heads, cubes), dtype=torch.int32, device=idx.device) if order is None else order
+    _need(order, "order", torch.int32, a.heads * cubes)
+    _check(lib.mh3_cube_order(C.byref(a), _ptr(idx), _ptr(cnt), _ptr(order), _stream()), "cube_order")
+    return order
+
+
 def cube_map(grid, *, n_dense=0, video_row0=None, dense_row0=0, device=None, map=None, counts=None):
     """H3::Cubes' map: int32 [cubes * 64 + n_dense], attention row -> model row (-1 for a cube's padding slot), the
     video grid's tokens at model rows video_row0 + (t * H + y) * W + x (default: right after the dense rows) and the
@@ -591,11 +605,13 @@ def heads_partial_pool(qkv, heads, grid, q_w=None, k_w=None, cos_t=None, sin_t=N
 
 # ---- flash_attn_sparse_128 -------------------------------------------------------------------------------------------
 
-def flash_attn_sparse_128(a: CubeArgs, q, k, v, idx, cnt, *, dense_row0=0, n_dense=0, scale=0.0, out=None):
+def flash_attn_sparse_128(a: CubeArgs, q, k, v, idx, cnt, *, dense_row0=0, n_dense=0, scale=0.0, out=None,
+                          order=None):
     """Sparse attention over the pass lists idx / cnt (as cube_select writes them): the queries of cube i attend the
     tokens of its selected cubes and the dense rows [dense_row0, dense_row0 + n_dense); a dense row's query attends
     every token. q, k, v (and out) bf16 in the cube geometry `a` (grid or gathered layout); scale 0 is 1/sqrt(128).
-    Rows that are not written keep `out`'s values (zero when out is None)."""
+    Rows that are not written keep `out`'s values (zero when out is None). With `order` (cube_order's int32
+    [heads][cubes]) the query cubes are scheduled in that order (mh3_flash_attn_sparse_128_ordered)."""
     cubes = cube_count(a.grid_t, a.grid_h, a.grid_w)
     n = _rows_touched(a)
     if n_dense:
@@ -608,8 +624,13 @@ def flash_attn_sparse_128(a: CubeArgs, q, k, v, idx, cnt, *, dense_row0=0, n_den
     _need(out, "out", torch.bfloat16, n)
     args = AttnArgs()
     args.cubes, args.dense_row0, args.n_dense, args.scale = a, dense_row0, n_dense, scale
-    _check(lib.mh3_flash_attn_sparse_128(C.byref(args), _ptr(q), _ptr(k), _ptr(v), _ptr(idx), _ptr(cnt), _ptr(out),
-                                         _stream()), "flash_attn_sparse_128")
+    if order is None:
+        _check(lib.mh3_flash_attn_sparse_128(C.byref(args), _ptr(q), _ptr(k), _ptr(v), _ptr(idx), _ptr(cnt),
+                                             _ptr(out), _stream()), "flash_attn_sparse_128")
+    else:
+        _need(order, "order", torch.int32, a.heads * cubes)
+        _check(lib.mh3_flash_attn_sparse_128_ordered(C.byref(args), _ptr(q), _ptr(k), _ptr(v), _ptr(idx), _ptr(cnt),
+                                                     _ptr(order), _ptr(out), _stream()), "flash_attn_sparse_128")
     return out
 
 

@@ -284,6 +284,30 @@ void attn()
                      oo.data());
     compare("flash_attn_sparse_128 over the gathered tiles, 2 heads, 7x9x10 grid + 70 text rows",
             of_bf16(out.download()), of_bf16(oo), 128, 1e-2, 3e-3);
+    // cube_order: each head's cubes sorted by the middle entry of their pass lists, ties by index (a host sort); then
+    // the attention with the query cubes in that order, against the same oracle outputs.
+    DeviceBuffer<int32_t> order(size_t(c.heads) * C);
+    DeviceBuffer<uint16_t> out2(tile);
+    kern.cube_order(c, idx.get(), cnt.get(), order.get());
+    kern.flash_attn_sparse_128(c, q.get(), k.get(), v.get(), idx.get(), cnt.get(), order.get(), 64ull * C, n_dense,
+                               out2.get());
+    kern.finish();
+    std::vector<int32_t> want_order(size_t(c.heads) * C);
+    for (uint32_t h = 0; h < c.heads; ++h) {
+        auto mid = [&](int32_t cube) {
+            const size_t item = size_t(h) * C + uint32_t(cube);
+            const int32_t n = std::min(std::max(gc[item], 0), int32_t(c.out_stride()));
+            const int32_t j = n > 0 ? gi[item * c.out_stride() + uint32_t(n) / 2] : -1;
+            return j >= 0 && uint32_t(j) < C ? uint32_t(j) : C;
+        };
+        auto first = want_order.begin() + ptrdiff_t(h) * C;
+        for (uint32_t i = 0; i < C; ++i)
+            first[i] = int32_t(i);
+        std::stable_sort(first, first + C, [&](int32_t a, int32_t b) { return mid(a) < mid(b); });
+    }
+    check(order.download() == want_order, "cube_order: cubes by the middle entry of their pass lists, ties by index");
+    compare("flash_attn_sparse_128 with the query cubes in cube_order's order", of_bf16(out2.download()), of_bf16(oo),
+            128, 1e-2, 3e-3);
     // heads_partial and cube_pool in one pass: the same bits as the two calls above.
     DeviceBuffer<uint16_t> q2(tile), k2(tile), v2(tile);
     DeviceBuffer<float> qc2(qc.size()), kc2(kc.size());

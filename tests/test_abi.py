@@ -47,10 +47,10 @@ def test_stream_probe_library_loads_and_refuses_bad_calls():
 
 
 def test_abi_version_and_strings():
-    assert mh.lib.mh3_abi_version() == 4
+    assert mh.lib.mh3_abi_version() == 5
     # The Python structs mirror the header: its MH3_ABI_VERSION is the module's (import refuses another library's).
     header = (Path(__file__).resolve().parent.parent / "include" / "mako_h3.h").read_text()
-    assert re.search(r"#define MH3_ABI_VERSION (\d+)", header).group(1) == str(mh.ABI_VERSION) == "4"
+    assert re.search(r"#define MH3_ABI_VERSION (\d+)", header).group(1) == str(mh.ABI_VERSION) == "5"
     assert mh.strerror(mh.ERR_SHAPE) == "bad shape"
     assert mh.strerror(123) == "unknown error"
 
@@ -283,6 +283,43 @@ def test_flash_attn_sparse_refuses_an_output_over_q_or_the_pass_lists():
     assert mh.lib.mh3_flash_attn_sparse_128(C.byref(a), q, k, v, idx, cnt, over_idx, None) == mh.ERR_PARAM
     over_cnt = C.c_void_p(0x500000 + 64)
     assert mh.lib.mh3_flash_attn_sparse_128(C.byref(a), q, k, v, idx, cnt, over_cnt, None) == mh.ERR_PARAM
+
+
+def test_flash_attn_sparse_ordered_checks():
+    """The ordered form makes the plain form's checks, needs its order (4-byte aligned) and refuses an out over it."""
+    f = mh.lib.mh3_flash_attn_sparse_128_ordered
+    a = attn_args()
+    q, k, v = C.c_void_p(0x100000), C.c_void_p(0x200000), C.c_void_p(0x300000)
+    idx, cnt, order, out = C.c_void_p(0x400000), C.c_void_p(0x500000), C.c_void_p(0x600000), C.c_void_p(0x700000)
+    assert f(None, q, k, v, idx, cnt, order, out, None) == mh.ERR_POINTER
+    assert f(C.byref(a), q, k, v, idx, cnt, None, out, None) == mh.ERR_POINTER
+    assert f(C.byref(a), q, k, v, idx, cnt, C.c_void_p(0x600002), out, None) == mh.ERR_ALIGN
+    assert f(C.byref(a), q, k, v, idx, cnt, order, C.c_void_p(0x600000 + 32), None) == mh.ERR_PARAM  # out over order
+    assert f(C.byref(a), q, k, v, idx, cnt, order, q, None) == mh.ERR_PARAM
+    for kw, code in [({"heads": 0}, mh.ERR_SHAPE), ({"head_dim": 64}, mh.ERR_UNSUPPORTED),
+                     ({"row_stride": 100}, mh.ERR_ALIGN)]:
+        assert f(C.byref(attn_args(**kw)), q, k, v, idx, cnt, order, out, None) == code
+
+
+def test_cube_order_validation():
+    """cube_order refuses bad geometry, null or misaligned pointers, an order over the pass lists and > 4096 cubes."""
+    f = mh.lib.mh3_cube_order
+    a = mh.cube_args(2, (8, 8, 12), k=3, local=1)
+    idx, cnt, order = C.c_void_p(0x400000), C.c_void_p(0x500000), C.c_void_p(0x600000)
+    assert f(None, idx, cnt, order, None) == mh.ERR_POINTER
+    assert f(C.byref(a), None, cnt, order, None) == mh.ERR_POINTER
+    assert f(C.byref(a), idx, cnt, None, None) == mh.ERR_POINTER
+    assert f(C.byref(a), idx, cnt, C.c_void_p(0x600002), None) == mh.ERR_ALIGN
+    assert f(C.byref(a), idx, cnt, C.c_void_p(0x500000 + 8), None) == mh.ERR_PARAM    # order over cnt
+    assert f(C.byref(a), idx, cnt, C.c_void_p(0x400000 + 16), None) == mh.ERR_PARAM   # order over idx
+    bad = mh.cube_args(2, (8, 8, 12), k=3, local=1)
+    bad.out_stride = 0
+    assert f(C.byref(bad), idx, cnt, order, None) == mh.ERR_SHAPE
+    bad = mh.cube_args(1, (8, 8, 12), k=3, local=1)
+    bad.head_dim = 64
+    assert f(C.byref(bad), idx, cnt, order, None) == mh.ERR_UNSUPPORTED
+    big = mh.cube_args(1, (64, 64, 68), k=3, local=1)   # 16 x 16 x 17 = 4352 cubes
+    assert f(C.byref(big), idx, cnt, order, None) == mh.ERR_UNSUPPORTED
 
 
 def test_quant_refuses_overlapping_outputs():

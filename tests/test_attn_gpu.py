@@ -23,14 +23,24 @@ def check(got_bits, want_bits, what):
     assert rel < 5e-3 and cos > 0.9999, f"{what}: rel {rel:.3g} cos {cos:.6f}"
 
 
-def run(dev, q, k, v, idx, cnt, grid, layout, row0, dense_row0, n_dense, out_init=None):
+def run(dev, q, k, v, idx, cnt, grid, layout, row0, dense_row0, n_dense, out_init=None, order=None):
     heads, rows, _ = q.shape
     a = mh.cube_args(heads, grid, layout=layout, row0=row0, head_stride=rows * 128, out_stride=idx.shape[2])
     out = None if out_init is None else from_bits(out_init, dev)
     t = lambda x: torch.from_numpy(np.ascontiguousarray(x)).to(dev)  # noqa: E731
     got = mh.flash_attn_sparse_128(a, from_bits(q, dev), from_bits(k, dev), from_bits(v, dev), t(idx), t(cnt),
-                                   dense_row0=dense_row0, n_dense=n_dense, out=out)
+                                   dense_row0=dense_row0, n_dense=n_dense, out=out,
+                                   order=None if order is None else t(order))
     return to_bits(got)
+
+
+def order_by_middle_entry(idx, cnt, cubes):
+    """cube_order's result restated with numpy: each head's cubes by the middle entry of their pass lists (entries
+    outside [0, cubes), and empty lists, as `cubes`), equal entries by cube index (a stable sort)."""
+    n = np.clip(cnt, 0, idx.shape[2])
+    mid = np.take_along_axis(idx, (n // 2)[..., None], axis=2)[..., 0]
+    key = np.where((n > 0) & (mid >= 0) & (mid < cubes), mid, cubes)
+    return np.argsort(key, axis=1, kind="stable").astype(np.int32)
 
 
 CASES = [
@@ -73,6 +83,49 @@ def test_flash_attn_sparse_matches_oracle(dev, grid, layout, row0, dense_row0, n
                                for c in range(C)])
         pad = np.setdiff1d(np.arange(row0, row0 + 64 * C), vrow)
         assert len(pad) and (got[:, pad] == 0).all()
+
+
+@pytest.mark.parametrize("grid,layout,row0,dense_row0,n_dense,k_sel,local", CASES)
+def test_flash_attn_sparse_ordered_matches_oracle(dev, grid, layout, row0, dense_row0, n_dense, k_sel, local):
+    """The ordered form, with cube_order's order and with a random permutation of each head's cubes: every row the
+    call writes against the oracle (the output NaN-filled first, so an unwritten row fails)."""
+    rng = np.random.default_rng(7 * sum(grid) + n_dense + layout)
+    C = orc.cube_count(*grid)
+    video = C * 64 if layout == orc.CUBES_GATHERED else grid[0] * grid[1] * grid[2]
+    rows = max(row0 + video, dense_row0 + n_dense)
+    q, k, v = [randn_bf16_bits(rng, (2, rows, 128)) for _ in range(3)]
+    idx, cnt = orc.cube_topk(rng.standard_normal((2, C, C)), grid, k_sel, local, out_stride=k_sel + 3)
+    want = orc.attn_sparse(q, k, v, idx, cnt, grid, dense_row0, n_dense, layout, row0)
+    a = mh.cube_args(2, grid, layout=layout, row0=row0, head_stride=rows * 128, out_stride=idx.shape[2])
+    t = lambda x: torch.from_numpy(np.ascontiguousarray(x)).to(dev)  # noqa: E731
+    order = mh.cube_order(a, t(idx), t(cnt)).cpu().numpy()
+    assert (order == order_by_middle_entry(idx, cnt, C)).all()
+    written = np.concatenate([orc.attn_tile_rows(grid, layout, row0, dense_row0, n_dense, t_)
+                              for t_ in range((n_dense + 63) // 64 + C)])
+    nan = np.full((2, rows, 128), 0x7FC0, np.uint16)
+    for name, o in (("cube_order", order), ("random", np.stack([rng.permutation(C) for _ in range(2)]))):
+        got = run(dev, q, k, v, idx, cnt, grid, layout, row0, dense_row0, n_dense, out_init=nan,
+                  order=o.astype(np.int32))
+        check(got[:, written], want[:, written], f"ordered ({name}) attn {grid} layout {layout}")
+
+
+def test_cube_order_edge_cases(dev):
+    """cube_order against its numpy restatement on pass lists with empty lists, counts above out_stride (clamped),
+    negative counts, middle entries outside [0, cubes), unsorted lists and many equal middle entries; 3 heads of a
+    padded grid (5 x 9 x 13: 2 x 3 x 4 = 24 cubes) and 40 heads of 768p's 2016 cubes."""
+    for heads, grid, stride in ((3, (5, 9, 13), 7), (40, (32, 48, 84), 205)):
+        rng = np.random.default_rng(heads)
+        C = orc.cube_count(*grid)
+        idx = rng.integers(-3, C + 3, (heads, C, stride)).astype(np.int32)
+        idx[:, ::3] = rng.integers(0, 4, (heads, len(range(0, C, 3)), stride))   # many equal middle entries
+        cnt = rng.integers(-2, stride + 4, (heads, C)).astype(np.int32)
+        cnt[:, ::5] = 0
+        a = mh.cube_args(heads, grid, out_stride=stride)
+        t = lambda x: torch.from_numpy(np.ascontiguousarray(x)).to(dev)  # noqa: E731
+        got = mh.cube_order(a, t(idx), t(cnt)).cpu().numpy()
+        want = order_by_middle_entry(idx, cnt, C)
+        assert (got == want).all(), f"cube_order {heads} heads {grid}"
+        assert (np.sort(got, axis=1) == np.arange(C)).all()
 
 
 @pytest.mark.parametrize("grid,layout,row0,dense_row0,n_dense", [((7, 9, 10), orc.CUBES_GRID, 0, 630, 70),
@@ -167,7 +220,8 @@ def test_flash_attn_sparse_768p_sampled(dev):
         check(ob[h, r], want[h, r], f"768p head {h} tile {tile}")
 
 
-def test_flash_attn_sparse_rotated_walk_every_tile(dev):
+@pytest.mark.parametrize("ordered", [False, True])
+def test_flash_attn_sparse_rotated_walk_every_tile(dev, ordered):
     """Enough cube tiles an XCD that most walk their pass lists from a rotated start: 160 heads of a 16 x 16 x 16 grid
     (64 cubes, one dense tile), so each XCD runs 1280 cube tiles in sequence, and tiles from the fourth round of the
     XCD's resident workgroups on (rank 512 and up at 4 workgroups a CU on 256 CUs) start a fraction of the way into
@@ -183,8 +237,9 @@ def test_flash_attn_sparse_rotated_walk_every_tile(dev):
     idx_n, cnt_n = orc.cube_topk(rng.standard_normal((heads, C, C)), grid, 6, 1, out_stride=8)
     idx, cnt = torch.from_numpy(idx_n).to(dev), torch.from_numpy(cnt_n).to(dev)
     a = mh.cube_args(heads, grid, head_stride=rows * 128, out_stride=8)
+    order = mh.cube_order(a, idx, cnt) if ordered else None
     out = mh.flash_attn_sparse_128(a, q, k, v, idx, cnt, dense_row0=video, n_dense=n_dense,
-                                   out=nan_filled((heads, rows, 128), dev))
+                                   out=nan_filled((heads, rows, 128), dev), order=order)
     torch.cuda.synchronize()
     assert bool(torch.isfinite(out).all()), "an output row left unwritten"
     worst = (0.0, 0.0)
@@ -205,7 +260,8 @@ def test_flash_attn_sparse_rotated_walk_every_tile(dev):
         check(ob[lh, r], want[lh, r], f"rotated walk: head {hs[lh]} tile {tile}")
 
 
-def test_flash_attn_sparse_768p_40_heads(dev):
+@pytest.mark.parametrize("ordered", [False, True])
+def test_flash_attn_sparse_768p_40_heads(dev, ordered):
     """The launch bench.py times: 40 heads of the 768p shape (2016 cubes, 512 text rows after the video rows), whose
     tile count lets each XCD take a contiguous eighth of every head's query cubes with rotated pass lists, the pass
     lists from cube_select at ratio 0.1 (k = 202), local 1. The output buffer is NaN-filled first and every row is
@@ -228,8 +284,9 @@ def test_flash_attn_sparse_768p_40_heads(dev):
     a = mh.cube_args(heads, grid, head_stride=rows * 128, k=kk, local=1)
     qc, kc = mh.cube_pool(a, q, k)
     idx, cnt = mh.cube_select(a, qc, kc)
+    order = mh.cube_order(a, idx, cnt) if ordered else None
     out = mh.flash_attn_sparse_128(a, q, k, v, idx, cnt, dense_row0=video, n_dense=n_dense,
-                                   out=nan_filled((heads, rows, 128), dev))
+                                   out=nan_filled((heads, rows, 128), dev), order=order)
     torch.cuda.synchronize()
     assert bool(torch.isfinite(out).all()), "an output row left unwritten"
     # Every dense tile of every head, and every cube tile of three whole heads (head 0's tiles are among each XCD's
