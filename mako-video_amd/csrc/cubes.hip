@@ -813,7 +813,8 @@ __global__ __launch_bounds__(256) void cube_order_kernel(uint32_t cubes, uint32_
         return;
     const uint32_t mine = keys[mine_c];
     uint32_t rank[4] = {0u, 0u, 0u, 0u};
-    for (uint32_t i = 0; i < n4; ++i) {
+#pragma unroll 8
+    for (uint32_t i = 0; i < n4; ++i) { // eight reads in flight: the loop is bound by the LDS latency otherwise
         const uint4 kq = keys4[i];
         rank[0] += kq.x < mine ? 1u : 0u;
         rank[1] += kq.y < mine ? 1u : 0u;
