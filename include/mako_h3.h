@@ -195,9 +195,10 @@ int mh3_cube_select(const MH3CubeArgs* args, const float* qc, const float* kc, v
 
 /* The query-cube order for mh3_flash_attn_sparse_128_ordered. No counterpart in the reference: a scheduling input for
  * this library's attention. For each head h, order[h][r] (int32 [heads][cubes]) is the cube of rank r when the head's
- * cubes are sorted by the middle entry idx[h][c][cnt[h][c] / 2] of their pass lists (the median of the ascending
- * lists cube_topk and cube_select write; an empty list, or an entry outside [0, cubes), sorts as `cubes`), equal
- * entries by cube index: a permutation of [0, cubes). Uses heads, grid and out_stride (>= 1) of args; up to 4096
+ * cubes are sorted by the middle entry idx[h][c][n / 2] of their pass lists, n = cnt[h][c] clamped to
+ * [0, out_stride] as the attention clamps it (the median of the ascending lists cube_topk and cube_select write; an
+ * empty list, or an entry outside [0, cubes), sorts as `cubes`), equal entries by cube index: a permutation of
+ * [0, cubes). Uses heads, grid and out_stride (>= 1) of args; up to 4096
  * cubes (MH3_ERR_UNSUPPORTED beyond). Pointers 4-byte aligned; order may not overlap idx or cnt (MH3_ERR_PARAM). */
 int mh3_cube_order(const MH3CubeArgs* args, const int32_t* idx, const int32_t* cnt, int32_t* order,
                    mh3_stream_t stream);
@@ -292,9 +293,10 @@ int mh3_flash_attn_sparse_128(const MH3AttnArgs* args, const uint16_t* q, const 
                               const int32_t* idx, const int32_t* cnt, uint16_t* out, mh3_stream_t stream);
 /* The same attention with the query cubes of each head scheduled in `order` (int32 [heads][cubes], a permutation of
  * [0, cubes) per head, as mh3_cube_order writes; entries are clamped to [0, cubes), and a non-permutation leaves
- * cubes unwritten). No counterpart in the reference: it is flash_attn_sparse_128 with a scheduling input. Each XCD
- * takes a contiguous eighth of a head's cubes in this order, so cubes whose pass lists centre on the same keys run
- * together and share K/V tiles in that XCD's L2. The outputs equal the plain call's up to the softmax's summation
+ * some cubes unwritten and computes others twice). No counterpart in the reference: it is flash_attn_sparse_128 with
+ * a scheduling input. When the cubes and the heads' dense tiles divide into eighths, each XCD takes a contiguous
+ * eighth of a head's cubes in this order (otherwise the cube tiles simply follow it), so cubes whose pass lists
+ * centre on the same keys run together and share K/V tiles in that XCD's L2. The outputs equal the plain call's up to the softmax's summation
  * order. order may not overlap out (MH3_ERR_PARAM) and must be 4-byte aligned. */
 int mh3_flash_attn_sparse_128_ordered(const MH3AttnArgs* args, const uint16_t* q, const uint16_t* k,
                                       const uint16_t* v, const int32_t* idx, const int32_t* cnt, const int32_t* order,
