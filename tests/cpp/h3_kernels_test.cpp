@@ -535,6 +535,17 @@ void errors()
     Cubes c;
     c.heads = 1, c.t = 4, c.h = 4, c.w = 4, c.local = 2;
     check(throws([&] { (void)c.args(); }), "local 2 throws (H3::set_sparse's domain is 0, 1, 3)");
+    c.local = 1;
+    DeviceBuffer<int32_t> lists(64), counts(16), order(16);
+    check(throws([&] { k.cube_order(c, lists.get(), counts.get(), nullptr); }), "cube_order without an order throws");
+    check(throws([&] { k.cube_order(c, lists.get(), counts.get(), counts.get()); }),
+          "cube_order writing over the counts throws");
+    Cubes big = c;
+    big.t = 64, big.h = 64, big.w = 68; // 16 x 16 x 17 = 4352 cubes, above cube_order's 4096
+    DeviceBuffer<int32_t> big_lists(size_t(big.count()) * big.out_stride()), big_counts(big.count()),
+        big_order(big.count());
+    check(throws([&] { k.cube_order(big, big_lists.get(), big_counts.get(), big_order.get()); }),
+          "cube_order beyond 4096 cubes throws");
     check(parse_int8("fc1,qkv") == std::optional<uint32_t>(MH3_INT8_FC1 | MH3_INT8_QKV), "parse_int8 fc1,qkv");
     check(!parse_int8("fc3"), "parse_int8 fc3 has no value");
 }
