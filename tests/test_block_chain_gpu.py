@@ -139,8 +139,8 @@ def test_one_block_through_the_library(dev):
 def test_one_block_in_the_models_row_order(dev):
     """The same block with no gather or scatter, as bench.py's `block` leg runs it: heads_partial writes q, k and v as
     the model's rows ([rows][heads x 128]) with cube_pool in its pass over the grid layout, the selection and the
-    attention read those rows where they lie, and the attention's output rows are the out projection's input. The
-    video grid's rows come first here and the dense rows after them."""
+    attention read those rows where they lie (its query cubes in cube_order's order), and the attention's output rows
+    are the out projection's input. The video grid's rows come first here and the dense rows after them."""
     rng = np.random.default_rng(43)
     t = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(dev)  # noqa: E731
     npv = lambda a: a.cpu().numpy()  # noqa: E731
@@ -168,7 +168,8 @@ def test_one_block_in_the_models_row_order(dev):
     kk = mh.topk_k(0.25, mh.cube_count(*GRID))
     a = mh.cube_args(HEADS, GRID, head_stride=128, row_stride=HEADS * 128, k=kk, local=1)
     idx, cnt = mh.cube_select(a, qc, kc)
-    att = mh.flash_attn_sparse_128(a, q, k, v, idx, cnt, dense_row0=video, n_dense=N_DENSE)
+    order = mh.cube_order(a, idx, cnt)   # the query cubes scheduled as bench.py's block schedules them
+    att = mh.flash_attn_sparse_128(a, q, k, v, idx, cnt, dense_row0=video, n_dense=N_DENSE, order=order)
     x1 = mh.gemm_gate_add(att, wo, x, t(ga_a[0]), w_scale=so)
     h2 = mh.rms_mod_rows(x1, t(n2), t(sh_m[0]), t(sc_m[0]))
     f = mh.gemm_w8a16_swiglu(h2, w1, s1)
